@@ -1,0 +1,111 @@
+"""The C-ABI library loads and exports every entry point include/uwc.h declares; argument checks
+reject bad calls before any GPU work (so these run without a GPU)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "uwc.h")
+
+
+def declared() -> list[str]:
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(uwc_\w+)\s*\(", src)))
+
+
+def test_header_declares_expected_surface():
+    names = declared()
+    for must in ("uwc_noisy_gemm", "uwc_igemm_i32", "uwc_igemm_dequant_f32", "uwc_b3_root_and_seed",
+                 "uwc_noise_uniform", "uwc_noise_perm", "uwc_noise_rows", "uwc_quant_act_f32", "uwc_dequant_f32",
+                 "uwc_last_error", "uwc_version"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    from uwc_amd import _lib
+    L = _lib.lib()
+    for name in declared():
+        assert hasattr(L, name), name
+        assert name in _lib.SIGNATURES, name
+    assert L.uwc_version() == 1
+
+
+def test_scratch_words_host_only():
+    from uwc_amd import _lib
+    L = _lib.lib()
+    assert L.uwc_b3_scratch_words(1024) == 8
+    assert L.uwc_b3_scratch_words(64 * 1024) == 8
+    assert L.uwc_b3_scratch_words(65 * 1024) == 16
+    # 16 MiB: 256 workgroup values
+    assert L.uwc_b3_scratch_words(16 << 20) == 256 * 8
+    # 1 GiB: 16384 values, then one level of 16 groups
+    assert L.uwc_b3_scratch_words(1 << 30) == 16384 * 8 + 16 * 8
+
+
+@pytest.mark.parametrize("kwargs,msg", [
+    (dict(k=100), "multiple of 64"),
+    (dict(flags=1, m=100), "mining needs"),
+    (dict(flags=1, r=96), "power of two"),
+    (dict(flags=2, corr=False), "needs corrA"),
+    (dict(out_mode=7), "unknown out_mode"),
+    (dict(out_mode=3, scales=False), "a_scale and b_scale"),
+    (dict(flags=8), "unknown flags"),
+])
+def test_noisy_gemm_rejects_bad_arguments(kwargs, msg):
+    from uwc_amd import _lib
+    L = _lib.lib()
+    a = dict(m=128, n=128, k=256, r=64, flags=0, out_mode=1, corr=True, scales=True)
+    a.update(kwargs)
+    fake = ctypes.c_void_p(1 << 20)  # aligned, never dereferenced: validation fails first
+    corr = fake if a["corr"] else None
+    sc = fake if a["scales"] else None
+    st = L.uwc_noisy_gemm(fake, fake, a["m"], a["n"], a["k"], a["r"], corr, corr, corr, 2, fake, fake, None, 0, sc, sc,
+                          fake, a["out_mode"], a["flags"], None, None)
+    assert st == -1
+    assert msg in L.uwc_last_error().decode()
+
+
+def test_other_entry_points_reject_bad_arguments():
+    from uwc_amd import _lib
+    L = _lib.lib()
+    fake = ctypes.c_void_p(1 << 20)
+    assert L.uwc_b3_root_and_seed(fake, 1000, fake, None, None, 0, None, None, fake, 100, None) == -1
+    assert "multiple of 1024" in L.uwc_last_error().decode()
+    assert L.uwc_noise_perm(fake, 64, 96, fake, fake, None) == -1
+    assert L.uwc_noise_rows(fake, 12, 64, 64, None, None, None, None, None, -1, -1, None, 0, None) == -1
+    assert L.uwc_quant_act_f32(fake, 4, 96, 64, 64, fake, fake, None) == -1
+    assert "power of two" in L.uwc_last_error().decode()
+    assert L.uwc_quant_act_f32(fake, 4, 64, 0, 200, fake, fake, None) == -1
+
+
+def test_python_surface_matches_reference_names():
+    """The reference's ops.py / detrt names a caller imports are all here."""
+    from uwc_amd import detrt, ops
+    for name in ("BM", "BN", "BK", "limbs_for", "WIN_WORDS", "CHUNKS_PER_CTA", "FLAG_HASH", "FLAG_DENOISE", "OUT_NONE",
+                 "OUT_I32", "OUT_BF16", "CONFIGS", "DEFAULT_CFG", "words", "words_to_bytes", "LABEL_A", "LABEL_B",
+                 "SALT_A", "SALT_B", "consts", "b3_root_and_seed", "noise_uniform", "noise_perm", "noise_rows", "gemm",
+                 "MinedWeight", "GraphedForward"):
+        assert hasattr(ops, name), name
+    for name in ("quant_act", "DetLinear"):
+        assert hasattr(detrt, name), name
+
+
+def test_salt_constants_match_oracle():
+    import oracle as O
+    from uwc_amd import ops
+    assert ops.SEED_SALT_A == O.SEED_SALT_A and ops.SEED_SALT_B == O.SEED_SALT_B
+    assert ops.SEED_LABEL_A == O.SEED_LABEL_A and ops.SEED_LABEL_B == O.SEED_LABEL_B
+
+
+def test_product_does_not_import_oracle():
+    """The product path never routes through the CPU oracle."""
+    pkg = os.path.join(ROOT, "useful-work-coin_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".hip", ".h", ".cpp")):
+                src = open(os.path.join(dirpath, f)).read()
+                assert "oracle" not in re.sub(r"#.*|//.*", "", src).lower() or f == "_lib.py", f

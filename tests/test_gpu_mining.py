@@ -1,0 +1,188 @@
+"""GPU parity of the cuPOW miner path (libuwc_hip.so through uwc_amd.ops) against the CPU oracle:
+bit-exact commitment, noise, noising/projections, every tile's message and digest, the winner
+set, and the exact denoised output. Mirrors miner/ampere/tests/test_kernels.py,
+test_gemm_cfgs.py and test_proj_gemm.py."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _ops():
+    from uwc_amd import ops
+    return ops
+
+
+def _u32(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().numpy().view(np.uint32)
+
+
+@pytest.mark.parametrize("nchunks", [1, 2, 3, 63, 64, 65, 130, 1000, 4097, 65536, 65537, 300_001])
+def test_tree_hash_matches_oracle(dev, nchunks):
+    ops = _ops()
+    rng = np.random.default_rng(nchunks)
+    data = rng.integers(0, 256, size=nchunks * 1024, dtype=np.uint8)
+    key = rng.bytes(32)
+    root = torch.zeros(8, dtype=torch.int32, device=dev)
+    ops.b3_root_and_seed(torch.from_numpy(data).to(dev), ops.words(key), root_out=root)
+    assert ops.words_to_bytes(root) == O.b3(data.tobytes(), key)
+
+
+def test_seed_derivation_matches_oracle(dev):
+    ops = _ops()
+    rng = np.random.default_rng(1)
+    m, n, k = 256, 512, 2048
+    A = rng.integers(-64, 65, size=(m, k), dtype=np.int8)
+    Bt = rng.integers(-64, 65, size=(n, k), dtype=np.int8)
+    job_key = rng.bytes(32)
+    a_seed, b_seed, _, _ = O.commitment(job_key, A, Bt)
+    jk = ops.words(job_key)
+    bs = torch.zeros(8, dtype=torch.int32, device=dev)
+    ops.b3_root_and_seed(torch.from_numpy(Bt).to(dev).view(-1), jk, prefix=jk, salt=ops.SALT_B.to(dev), dim=n, seed_out=bs)
+    assert ops.words_to_bytes(bs) == b_seed
+    as_ = torch.zeros(8, dtype=torch.int32, device=dev)
+    ops.b3_root_and_seed(torch.from_numpy(A).to(dev).view(-1), jk, prefix=bs, salt=ops.SALT_A.to(dev), dim=m, seed_out=as_)
+    assert ops.words_to_bytes(as_) == a_seed
+
+
+@pytest.mark.parametrize("r", [64, 128])
+def test_noise_generation_matches_oracle(dev, r):
+    ops = _ops()
+    rng = np.random.default_rng(2)
+    key = rng.bytes(32)
+    rows, k = 256, 3072 + 5
+    E = torch.empty((rows, r), dtype=torch.int8, device=dev)
+    zero = torch.full((3,), 7, dtype=torch.int32, device=dev)
+    ops.noise_uniform(E, ops.LABEL_A.to(dev), ops.words(key), zero_me=zero, zero_n=2)
+    assert np.array_equal(E.cpu().numpy(), O.uniform_matrix(O.SEED_LABEL_A, key, rows, r))
+    assert zero.cpu().tolist() == [0, 0, 7]
+    P = torch.empty(k, dtype=torch.int32, device=dev)
+    ops.noise_perm(P, k, r, ops.LABEL_B.to(dev), ops.words(key))
+    assert np.array_equal(_u32(P), O.perm_packed(O.SEED_LABEL_B, key, k, r))
+
+
+def test_noise_rows_noising_and_projection(dev):
+    ops = _ops()
+    rng = np.random.default_rng(3)
+    rows, k, r = 128, 2048, 128
+    A = rng.integers(-64, 65, size=(rows, k), dtype=np.int8)
+    E = rng.integers(-32, 32, size=(rows, r), dtype=np.int8)
+    Pn = O.perm_packed(O.SEED_LABEL_A, b"\x01" * 32, k, r)
+    Pp = O.perm_packed(O.SEED_LABEL_B, b"\x02" * 32, k, r)
+    pack = lambda P: torch.from_numpy(P.view(np.int32).copy()).to(dev)
+    dst = torch.empty((rows, k), dtype=torch.int8, device=dev)
+    L = ops.limbs_for(k)
+    corr = torch.zeros((L, rows, 2 * r), dtype=torch.int8, device=dev)
+    mx = torch.zeros(1, dtype=torch.int32, device=dev)
+    ops.noise_rows(torch.from_numpy(A).to(dev), rows, k, r, E=torch.from_numpy(E).to(dev), Pn=pack(Pn), dst=dst,
+                   Pp=pack(Pp), corr=corr, corr_off=0, ecopy_off=r, maxabs=mx)
+    assert np.array_equal(dst.cpu().numpy(), O.noise_apply(A, E, Pn))
+    proj = O.project(A, Pp, r)
+    want = np.zeros((L, rows, 2 * r), np.int8)
+    O.write_limbs(proj, want, 0)
+    for li in range(L):
+        want[li, :, r:] = E
+    assert np.array_equal(corr.cpu().numpy(), want)
+    assert int(mx.item()) == int(np.abs(proj).max())
+
+
+@pytest.mark.parametrize("m,n,k,r", [(128, 128, 1024, 64), (256, 256, 2048, 64), (256, 384, 2048, 128),
+                                     (128, 256, 1280, 64)])
+def test_mined_forward_exact_and_every_tile_matches(dev, m, n, k, r):
+    """Full per-call path: output == A @ Bt^T exactly; every tile's 16-word message and digest
+    and the winner set equal the oracle's (miner/ampere/tests/test_kernels.py:94-125)."""
+    ops = _ops()
+    rng = np.random.default_rng(m + n + k + r)
+    A = rng.integers(-64, 65, size=(m, k), dtype=np.int8)
+    Bt = rng.integers(-64, 65, size=(n, k), dtype=np.int8)
+    job_key = rng.bytes(32)
+    target = O.bound_for_wins(m, n, 12)
+    ref = O.mined_forward(A, Bt, job_key, target, r)
+
+    w = ops.MinedWeight(Bt=torch.from_numpy(Bt).to(dev), b_scale=torch.ones(n, device=dev), r=r, max_wins=4096)
+    w.setup_block(job_key, target)
+    dump = torch.zeros((m // 64) * 8 * (n // 64) * 4 * ops.DUMP_WORDS, dtype=torch.int32, device=dev)
+    out = w._forward(torch.from_numpy(A).to(dev), torch.ones(m, device=dev), None, ops.OUT_I32, True, dump=dump)
+    b = w._buf(m)
+    assert ops.words_to_bytes(w.b_seed) == ref["b_seed"]
+    assert ops.words_to_bytes(b["a_seed"]) == ref["a_seed"]
+    assert np.array_equal(w.EBRt.cpu().numpy(), ref["EBRt"]) and np.array_equal(_u32(w.PB), ref["PB"])
+    assert np.array_equal(w.BpEBt.cpu().numpy(), ref["BpEBt"])
+    assert np.array_equal(b["EAL"].cpu().numpy(), ref["EAL"]) and np.array_equal(_u32(b["PA"]), ref["PA"])
+    assert np.array_equal(b["ApEA"].cpu().numpy(), ref["ApEA"])
+    assert np.array_equal(b["corrA"].cpu().numpy(), ref["corrA"])
+    assert np.array_equal(w.corrB.cpu().numpy(), ref["corrB"])
+    assert np.array_equal(b["maxabs"].cpu().numpy(), ref["maxabs"])
+    d = _u32(dump).reshape(m // 64, 8, n // 64, 4, ops.DUMP_WORDS)
+    assert np.array_equal(d[..., :16], ref["msgs"]), "tile messages differ"
+    assert np.array_equal(d[..., 16:], ref["digests"]), "tile digests differ"
+    assert np.array_equal(out.cpu().numpy(), ref["out"]), "denoised output is not the exact product"
+    got = set(w.winners(m))
+    assert ref["winners"] and got == ref["winners"]
+
+
+def test_noise_mine_matches_and_out_modes(dev):
+    """noise_mine (hash only) gives the same winners; bf16 / fp32 epilogues match the oracle."""
+    ops = _ops()
+    rng = np.random.default_rng(11)
+    m, n, k, r = 256, 256, 1024, 64
+    A = rng.integers(-64, 65, size=(m, k), dtype=np.int8)
+    Bt = rng.integers(-64, 65, size=(n, k), dtype=np.int8)
+    job_key = rng.bytes(32)
+    target = O.bound_for_wins(m, n, 12)
+    ref = O.mined_forward(A, Bt, job_key, target, r)
+    w = ops.MinedWeight(Bt=torch.from_numpy(Bt).to(dev), b_scale=torch.ones(n, device=dev), r=r, max_wins=4096)
+    w.setup_block(job_key, target)
+    Ad = torch.from_numpy(A).to(dev)
+    w.noise_mine(Ad)
+    assert set(w.winners(m)) == ref["winners"]
+    a_scale = torch.from_numpy(rng.random(m).astype(np.float32) * 0.01).to(dev)
+    w.b_scale = torch.from_numpy(rng.random(n).astype(np.float32) * 0.01).to(dev)
+    yb = w.forward(Ad, a_scale, out_mode=ops.OUT_BF16)
+    assert set(w.winners(m)) == ref["winners"]
+    want = O.scale_bf16(ref["out"], a_scale.cpu().numpy(), w.b_scale.cpu().numpy())
+    assert np.array_equal(yb.view(torch.int16).cpu().numpy().view(np.uint16), want)
+    yf = w.forward(Ad, a_scale, out_mode=ops.OUT_F32)
+    wf = O.dequant(ref["out"], a_scale.cpu().numpy(), w.b_scale.cpu().numpy())
+    assert np.array_equal(yf.cpu().numpy().view(np.uint32), wf.view(np.uint32))
+
+
+def test_graphed_forward_matches_eager_every_replay(dev):
+    ops = _ops()
+    rng = np.random.default_rng(5)
+    m, n, k = 256, 512, 2048
+    Bt = torch.from_numpy(rng.integers(-64, 65, size=(n, k), dtype=np.int8)).to(dev)
+    w = ops.MinedWeight(Bt=Bt, b_scale=torch.ones(n, device=dev), r=128, max_wins=4096)
+    w.setup_block(rng.bytes(32), O.bound_for_wins(m, n, 20))
+    gf = ops.GraphedForward(w, m, out_mode=ops.OUT_I32)
+    for rep in range(3):
+        A = torch.from_numpy(rng.integers(-64, 65, size=(m, k), dtype=np.int8)).to(dev)
+        gf.A.copy_(A)
+        got = gf().clone()
+        torch.cuda.synchronize()
+        wins_graph = sorted(w.winners(m))
+        eager = w.forward(A, torch.ones(m, device=dev), out_mode=ops.OUT_I32)
+        torch.cuda.synchronize()
+        assert torch.equal(got, eager), rep
+        assert torch.equal(got.cpu(), torch.from_numpy(O.igemm(A.cpu().numpy(), Bt.cpu().numpy()))), rep
+        assert wins_graph == sorted(w.winners(m)), rep
+
+
+def test_win_records_capped(dev):
+    """More winners than max_wins: the count keeps growing, records stop at the cap."""
+    ops = _ops()
+    rng = np.random.default_rng(12)
+    m, n, k, r = 128, 128, 512, 64
+    A = torch.from_numpy(rng.integers(-64, 65, size=(m, k), dtype=np.int8)).to(dev)
+    B = torch.from_numpy(rng.integers(-64, 65, size=(n, k), dtype=np.int8)).to(dev)
+    key = ops.words(rng.bytes(32))
+    target = torch.full((8,), -1, dtype=torch.int32, device=dev)  # every tile wins
+    wins = torch.zeros(1 + 5 * ops.WIN_WORDS, dtype=torch.int32, device=dev)
+    ops.gemm(A, B, r=r, flags=ops.FLAG_HASH, key=key, target=target, wins=wins, max_wins=5)
+    w = _u32(wins)
+    assert w[0] == (m // 8) * (n // 16)
+    recs = w[1:].reshape(5, ops.WIN_WORDS)
+    assert all(rr[0] % 64 < 8 and rr[1] % 2 == 0 for rr in recs)

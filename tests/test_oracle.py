@@ -1,0 +1,247 @@
+"""The CPU oracle pinned before it is trusted: known answers, golden fixtures, independent
+restatements and brute force, chosen so that a dropped term, a wrong index or a transposed
+operand fails at least one check."""
+import hashlib
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+from oracle.blake3_py import blake3 as py_b3
+from conftest import GOLDEN
+
+
+# ------------------------------------------------------------------ BLAKE3
+def test_blake3_published_digests():
+    # BLAKE3's published digests of the empty input and of "abc"
+    assert O.b3(b"").hex() == "af1349b9f5f9a1a6a0404dea36dcc9499bcb25c9adc112b7cc9a93cae41f3262"
+    assert O.b3(b"abc").hex() == "6437b3ac38465133ffb63b75273a8db548c558465d79db03fd359c6cd5bd9d85"
+    assert py_b3(b"").hex() == "af1349b9f5f9a1a6a0404dea36dcc9499bcb25c9adc112b7cc9a93cae41f3262"
+
+
+@pytest.mark.parametrize("nchunks", list(range(1, 40)) + [63, 64, 65, 127, 128, 129])
+def test_blake3_tree_shapes_agree(nchunks):
+    """Recursive (C) and streaming-stack (Python) trees agree on every shape, keyed and plain."""
+    rng = np.random.default_rng(nchunks)
+    data = rng.bytes(nchunks * 1024)
+    key = rng.bytes(32)
+    assert O.b3(data, key) == py_b3(data, key)
+    assert O.b3(data) == py_b3(data)
+
+
+@pytest.mark.parametrize("n", [1, 63, 64, 65, 1023, 1025, 2047, 3000, 5121])
+def test_blake3_ragged_lengths(n):
+    rng = np.random.default_rng(n)
+    data = rng.bytes(n)
+    assert O.b3(data) == py_b3(data)
+    assert O.b3(data, b"\x07" * 32) == py_b3(data, b"\x07" * 32)
+
+
+def test_blake3_keyed_differs_and_counter_matters():
+    # a dropped key flag or a chunk counter fixed at 0 would make these collide
+    d = bytes(2048)
+    assert O.b3(d) != O.b3(d, bytes(32))
+    a = bytes(1024) + bytes([1]) + bytes(1023)
+    b = bytes([1]) + bytes(1023) + bytes(1024)
+    assert O.b3(a) != O.b3(b)
+
+
+def test_seed_constants():
+    # Pearl's salts: BLAKE3 of their ASCII names (reference.py:25-26)
+    assert O.SEED_SALT_A == py_b3(b"pearl/cert-v3/noise-seed/A")
+    assert O.SEED_SALT_B == py_b3(b"pearl/cert-v3/noise-seed/B")
+
+
+# ------------------------------------------------------------------ noise
+def _py_random_hash(index, label, key, prepend):
+    msg = bytearray(64)
+    msg[prepend * 4:prepend * 4 + 4] = (1 + index).to_bytes(4, "little")
+    msg[32:64] = label
+    return py_b3(bytes(msg), key)
+
+
+def test_noise_uniform_matches_python_random_hash():
+    key = bytes(range(32))
+    E = O.uniform_matrix(O.SEED_LABEL_A, key, 8, 64)
+    raw = b"".join(_py_random_hash(b, O.SEED_LABEL_A, key, 0) for b in range(16))
+    want = ((np.frombuffer(raw, np.uint8) & 63).astype(np.int16) - 32).astype(np.int8).reshape(8, 64)
+    assert np.array_equal(E, want)
+    assert E.min() >= -32 and E.max() <= 31
+
+
+@pytest.mark.parametrize("r", [64, 128])
+def test_noise_perm_matches_python_and_invariants(r):
+    key = bytes(range(1, 33))
+    k = 1000
+    P = O.perm_packed(O.SEED_LABEL_B, key, k, r)
+    first, second = P & 0xFFFF, P >> 16
+    assert (first < r).all() and (second < r).all() and (first != second).all()
+    for i in range(0, (k + 7) // 8, 17):
+        u = np.frombuffer(_py_random_hash(i, O.SEED_LABEL_B, key, 1), "<u4").astype(np.uint64)
+        f = u & (r - 1)
+        s = f ^ (1 + ((np.uint64(r - 1) * u) >> np.uint64(32)))
+        n = min(8, k - 8 * i)
+        assert np.array_equal(first[8 * i:8 * i + n], f[:n]) and np.array_equal(second[8 * i:8 * i + n], s[:n])
+
+
+def test_noise_apply_and_projection_brute_force():
+    rng = np.random.default_rng(3)
+    rows, k, r = 16, 256, 64
+    A = rng.integers(-128, 128, size=(rows, k), dtype=np.int8)
+    E = rng.integers(-32, 32, size=(rows, r), dtype=np.int8)
+    P = O.perm_packed(O.SEED_LABEL_A, b"\x01" * 32, k, r)
+    f, s = (P & 0xFFFF).astype(np.int64), (P >> 16).astype(np.int64)
+    want = (A.astype(np.int64) + E[:, f] - E[:, s]) & 0xFF
+    assert np.array_equal(O.noise_apply(A, E, P).view(np.uint8), want.astype(np.uint8))
+    S = np.zeros((r, k), np.int64)
+    S[f, np.arange(k)] += 1
+    S[s, np.arange(k)] -= 1
+    assert np.array_equal(O.project(A, P, r), A.astype(np.int64) @ S.T)
+
+
+def test_limbs_reconstruct_and_limb_count():
+    rng = np.random.default_rng(4)
+    k = 4096
+    L = O.limbs_for(k)
+    proj = rng.integers(-127 * k, 127 * k + 1, size=(8, 64)).astype(np.int32)
+    proj[0, 0], proj[0, 1] = 127 * k, -127 * k
+    corr = np.zeros((L, 8, 128), np.int8)
+    O.write_limbs(proj, corr, 64)
+    c = corr[:, :, 64:].astype(np.int64)
+    assert c.min() >= -64 and c.max() <= 63
+    assert np.array_equal(sum(c[i] * 128 ** i for i in range(L)), proj)
+    assert not corr[:, :, :64].any()
+    for mx, want in ((0, 1), (63, 1), (64, 2), (8127, 2), (8128, 3), (1040319, 3), (1040320, 4)):
+        assert O.limbs_needed(mx) == want
+
+
+# ------------------------------------------------------------------ GEMM and transcript
+def test_gemm_known_answer_L1():
+    """results/xc_cpu.json:4 (miner/ampere/bench/crosscheck.py:62-76)."""
+    rng = np.random.default_rng(2026)
+    A = rng.integers(-64, 65, size=(1024, 4096), dtype=np.int8)
+    Bt = rng.integers(-64, 65, size=(3072, 4096), dtype=np.int8)
+    C = O.igemm(A, Bt)
+    assert hashlib.sha256(C.tobytes()).hexdigest()[:20] == "bf9394d180bda5b0412c"
+
+
+def test_gemm_ragged_and_extremes():
+    rng = np.random.default_rng(5)
+    for m, n, k in ((1, 1, 1), (3, 70, 130), (65, 1, 257)):
+        A = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+        B = rng.integers(-128, 128, size=(n, k), dtype=np.int8)
+        assert np.array_equal(O.igemm(A, B), (A.astype(np.int64) @ B.astype(np.int64).T).astype(np.int32))
+    A = np.full((2, 4096), -128, np.int8)
+    assert O.igemm(A, A)[0, 0] == 128 * 128 * 4096
+    # int32 accumulation wraps mod 2^32 like the reference's .astype(np.int32)
+    A = np.full((1, 2 ** 18 + 64), -128, np.int8)
+    assert O.igemm(A, A)[0, 0] == np.int64(128 * 128 * (2 ** 18 + 64)).astype(np.int32)
+
+
+def _transcript_brute(Ap, Bp, r):
+    """Per tile, straight from the definition: cumulative sums of exactly its 128 elements."""
+    m, k = Ap.shape
+    n = Bp.shape[0]
+    out = np.zeros((m // 64, 8, n // 64, 4, 16), np.uint32)
+    for rb in range(m // 64):
+        for cb in range(n // 64):
+            for g in range(8):
+                for t in range(4):
+                    rows = [rb * 64 + g + 8 * i for i in range(8)]
+                    cols = sorted(cb * 64 + 2 * t + e + 8 * j for j in range(8) for e in (0, 1))
+                    a = Ap[rows].astype(np.int64)
+                    b = Bp[cols].astype(np.int64)
+                    msg = [0] * 16
+                    for c in range(k // r):
+                        acc = a[:, :(c + 1) * r] @ b[:, :(c + 1) * r].T
+                        x = 0
+                        for v in (acc & 0xFFFFFFFF).ravel():
+                            x ^= int(v)
+                        s = c % 16
+                        msg[s] = (((msg[s] << 13) | (msg[s] >> 19)) & 0xFFFFFFFF) ^ x
+                    out[rb, g, cb, t] = msg
+    return out
+
+
+@pytest.mark.parametrize("k,r", [(128, 64), (1280, 64), (256, 128)])
+def test_transcript_brute_force(k, r):
+    # k = 1280, r = 64: 20 folds, so slots wrap past 16 and rotate twice
+    rng = np.random.default_rng(k + r)
+    Ap = rng.integers(-127, 128, size=(128, k), dtype=np.int8)
+    Bp = rng.integers(-127, 128, size=(64, k), dtype=np.int8)
+    assert np.array_equal(O.transcript(Ap, Bp, r), _transcript_brute(Ap, Bp, r))
+
+
+def test_tile_hash_and_winner_rule():
+    key = bytes(range(32))
+    msgs = np.arange(2 * 8 * 1 * 4 * 16, dtype=np.uint32).reshape(2, 8, 1, 4, 16)
+    dig = O.tile_hashes(msgs, key)
+    for idx in [(0, 0, 0, 0), (1, 7, 0, 3)]:
+        want = py_b3(O.to_bytes(msgs[idx]), key)
+        assert O.to_bytes(dig[idx]) == want
+    # a target at one digest's value: exactly that tile and the smaller ones win
+    d = dig.reshape(-1, 8)
+    vals = [int.from_bytes(O.to_bytes(x), "little") for x in d]
+    tgt = sorted(vals)[5]
+    target = np.array([(tgt >> (32 * i)) & 0xFFFFFFFF for i in range(8)], np.uint32)
+    assert len(O.winners(dig, target)) == 6
+
+
+def test_mined_forward_denoise_exact():
+    """(A + EAL S_A)(Bt + EBRt S_B)^T minus the limb correction is A @ Bt^T exactly."""
+    rng = np.random.default_rng(7)
+    m, n, k, r = 128, 128, 1024, 64
+    A = rng.integers(-64, 65, size=(m, k), dtype=np.int8)
+    Bt = rng.integers(-64, 65, size=(n, k), dtype=np.int8)
+    res = O.mined_forward(A, Bt, rng.bytes(32), O.bound_for_wins(m, n, 12), r)
+    assert np.array_equal(res["out"], O.igemm(A, Bt))
+    # the correction rebuilt from the limb tensors equals the one from the projections
+    L = res["corrA"].shape[0]
+    corr = sum((res["corrA"][li].astype(np.int64) @ res["corrB"][li].astype(np.int64).T) * 128 ** li for li in range(L))
+    noisy = O.igemm(res["ApEA"], res["BpEBt"]).astype(np.int64)
+    assert np.array_equal(((noisy - corr) & 0xFFFFFFFF).astype(np.uint32).view(np.int32), res["out"])
+    assert 0 < len(res["winners"]) < 64
+
+
+# ------------------------------------------------------------------ detrt golden fixtures
+FIXTURES = ["detrt_tiny_qwen3", "detrt_tiny_llama", "detrt_qwen3_1p7b"]
+
+
+@pytest.mark.parametrize("name", FIXTURES)
+def test_quant_act_fixtures(name):
+    """Go-referee fixtures (chain/patches/0003, 0021): N1->QA1, O->QA2, N2->QA3, SM->QA4."""
+    z = np.load(os.path.join(GOLDEN, name + ".npz"))
+    Bs = int(z["cfg"][5])
+    n = 0
+    for l in (0, 1):
+        for src, qa in (("N1", "QA1"), ("O", "QA2"), ("N2", "QA3"), ("SM", "QA4")):
+            x = z[f"l{l}_{src}"]
+            q, s = O.quant_act(x, O.hadamard_bs(Bs, x.shape[1]))
+            assert np.array_equal(q, z[f"l{l}_{qa}_q"]), (name, l, qa)
+            assert np.array_equal(s.view(np.uint32), z[f"l{l}_{qa}_s"].view(np.uint32)), (name, l, qa)
+            n += x.shape[0]
+    assert n >= 64
+
+
+@pytest.mark.parametrize("name", FIXTURES)
+def test_linear_element_rule_fixtures(name):
+    """QA x W -> (f32(acc) * s_x) * s_w equals the referee's linearElem bit for bit."""
+    z = np.load(os.path.join(GOLDEN, name + ".npz"))
+    for l in (0, 1):
+        for lin, qa, op in (("qkv", "QA1", "QKV"), ("o", "QA2", "OP"), ("gu", "QA3", "GU"), ("down", "QA4", "DN")):
+            acc = O.igemm(z[f"l{l}_{qa}_q"], z[f"l{l}_W_{lin}_q"])
+            y = O.dequant(acc, z[f"l{l}_{qa}_s"], z[f"l{l}_W_{lin}_s"])
+            assert np.array_equal(y.view(np.uint32), z[f"l{l}_{op}"].view(np.uint32)), (name, l, lin)
+
+
+def test_dequant_order_matters():
+    # (acc * sx) * sw and acc * (sx * sw) differ for some inputs: the fixture test above would
+    # catch a reassociated product; show that such inputs exist
+    rng = np.random.default_rng(9)
+    acc = rng.integers(-2 ** 20, 2 ** 20, size=(64, 64)).astype(np.int32)
+    sx = rng.random(64).astype(np.float32)
+    sw = rng.random(64).astype(np.float32)
+    y = O.dequant(acc, sx, sw)
+    alt = (acc.astype(np.float32) * (sx[:, None] * sw[None, :]).astype(np.float32)).astype(np.float32)
+    assert not np.array_equal(y, alt)

@@ -1,0 +1,27 @@
+// C-ABI plumbing: last-error message, launch status, library version.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "uwc_common.h"
+
+static thread_local char g_last_error[512] = "";
+
+int uwc_fail(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof g_last_error, fmt, ap);
+  va_end(ap);
+  return UWC_EINVAL;
+}
+
+int uwc_launch_status(const char* kernel) {
+  const hipError_t e = hipGetLastError();
+  if (e == hipSuccess) return UWC_OK;
+  snprintf(g_last_error, sizeof g_last_error, "%s launch failed: %s", kernel, hipGetErrorString(e));
+  return (int)e;
+}
+
+extern "C" const char* uwc_last_error(void) { return g_last_error; }
+
+extern "C" int uwc_version(void) { return 1; }

@@ -1,0 +1,373 @@
+// gfx950 int8 x int8 -> int32 GEMM with the cuPOW transcript: C = A * B^T, A m x k, B n x k
+// (both k-contiguous). One kernel serves the miner (FLAG_HASH: fold + BLAKE3 tile digests +
+// win records; FLAG_DENOISE: exact low-rank correction) and the detrt linear (plain GEMM with
+// an int32, bf16 or fp32-dequant epilogue).
+//
+// Semantics follow miner/ampere/uwc_ampere/kernels.cu:482-715 (noisy_gemm) and
+// reference.py:111-125 (jackpot transcript); the design is CDNA4's own:
+//   * workgroup tile 128 x 128 x 64, 4 wave64s in 2 x 2, each wave owns one 64 x 64 block;
+//     v_mfma_i32_32x32x32_i8 (2 x 2 MFMA blocks per wave, 64 int32 accumulators per lane);
+//   * the consensus hash tile (rows g + 8i, cols 2t + e + 8j inside a 64 x 64 block,
+//     miner/ampere/uwc_ampere/pearl_glue.py:14-15) is spread by the MFMA C layout
+//     (row = 8(e>>2) + 4(lane>>5) + (e&3), col = lane&31) over lane bits 0, 3, 4 and
+//     accumulator index e>>2. Each fold XORs a lane's accumulators into 4 per-lane partials
+//     (one per g&3) and folds them into per-lane partial messages; rotl13 and XOR are linear
+//     over GF(2), so the cross-lane XOR of the partial messages, done once after the k loop,
+//     equals the reference's per-fold tile XOR;
+//   * k is reduced in a fixed order (k tiles ascending, 32 k per MFMA): int32 sums are exact,
+//     so every tiling gives identical accumulators at every r boundary.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "uwc_common.h"
+
+#define G_BM 128
+#define G_BN 128
+#define G_BK 64
+#define G_PITCH 80  // LDS bytes per tile row: 64 data + 16 pad, conflict-free 16-byte fragment reads
+#define G_THREADS 256
+#define G_TILE_BYTES (G_BM * G_PITCH)          // one operand tile in LDS
+#define G_STAGE_BYTES (2 * G_TILE_BYTES)       // A + B
+#define G_MSG_BYTES (4 * 4 * 16 * 64 * 4)      // 4 waves x 4 partials x 16 words x 64 lanes
+#define G_LDS_BYTES (G_MSG_BYTES > 2 * G_STAGE_BYTES ? G_MSG_BYTES : 2 * G_STAGE_BYTES)
+
+#define FLAG_HASH 1
+#define FLAG_DENOISE 2
+#define OUT_NONE 0
+#define OUT_I32 1
+#define OUT_BF16 2
+#define OUT_F32 3
+#define WIN_WORDS 10
+#define DUMP_WORDS 24  // per tile: 16 message words + 8 digest words
+
+struct GemmParams {
+  const i8* A;
+  const i8* B;
+  int m, n, k, r;
+  const i8* corrA;
+  const i8* corrB;
+  const i32* maxabs;
+  int lmax;
+  const u32* key;
+  const u32* target;
+  u32* wins;
+  int max_wins;
+  const float* a_scale;
+  const float* b_scale;
+  void* out;
+  u32* dump;
+};
+
+// Global -> register prefetch of one 128 x 64 operand tile: 512 16-byte pieces, 2 per thread.
+struct TileRegs {
+  v4i a[2], b[2];
+};
+
+__device__ __forceinline__ v4i load16(const i8* base, long row, int rows, long ld, int col) {
+  if (row < rows) return *reinterpret_cast<const v4i*>(base + row * ld + col);
+  return v4i{0, 0, 0, 0};
+}
+
+__device__ __forceinline__ void tile_load(TileRegs& t, const i8* A, long lda, int arows, const i8* B, long ldb,
+                                          int brows, int bm0, int bn0, int k0, int tid) {
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int idx = tid + i * G_THREADS, row = idx >> 2, c = idx & 3;
+    t.a[i] = load16(A, (long)bm0 + row, arows, lda, k0 + c * 16);
+    t.b[i] = load16(B, (long)bn0 + row, brows, ldb, k0 + c * 16);
+  }
+}
+
+__device__ __forceinline__ void tile_store(const TileRegs& t, u8* stage, int tid) {
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int idx = tid + i * G_THREADS, row = idx >> 2, c = idx & 3;
+    *reinterpret_cast<v4i*>(stage + row * G_PITCH + c * 16) = t.a[i];
+    *reinterpret_cast<v4i*>(stage + G_TILE_BYTES + row * G_PITCH + c * 16) = t.b[i];
+  }
+}
+
+// 64 k of MFMA work for one wave's 64 x 64 block from an LDS stage.
+__device__ __forceinline__ void tile_mma(v16i acc[2][2], const u8* stage, int wm, int wn, int lane) {
+  const u8* sA = stage + (wm * 64 + (lane & 31)) * G_PITCH + (lane >> 5) * 16;
+  const u8* sB = stage + G_TILE_BYTES + (wn * 64 + (lane & 31)) * G_PITCH + (lane >> 5) * 16;
+#pragma unroll
+  for (int ks = 0; ks < 2; ks++) {
+    v4i a0 = *reinterpret_cast<const v4i*>(sA + ks * 32);
+    v4i a1 = *reinterpret_cast<const v4i*>(sA + 32 * G_PITCH + ks * 32);
+    v4i b0 = *reinterpret_cast<const v4i*>(sB + ks * 32);
+    v4i b1 = *reinterpret_cast<const v4i*>(sB + 32 * G_PITCH + ks * 32);
+    acc[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, acc[0][0], 0, 0, 0);
+    acc[0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b1, acc[0][1], 0, 0, 0);
+    acc[1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b0, acc[1][0], 0, 0, 0);
+    acc[1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b1, acc[1][1], 0, 0, 0);
+  }
+}
+
+// Runs k tiles [kt_begin, kt_end) of a double-buffered pipeline whose stage (kt_begin & 1)
+// already holds tile kt_begin. On return stage (kt_end & 1) holds tile kt_end (if < kt_total).
+__device__ __forceinline__ void run_ktiles(v16i acc[2][2], u8* smem, const i8* A, long lda, int arows, const i8* B,
+                                           long ldb, int brows, int bm0, int bn0, int kt_begin, int kt_end,
+                                           int kt_total, int tid, int wm, int wn, int lane) {
+  for (int kt = kt_begin; kt < kt_end; kt++) {
+    TileRegs t;
+    const bool more = kt + 1 < kt_total;
+    if (more) tile_load(t, A, lda, arows, B, ldb, brows, bm0, bn0, (kt + 1) * G_BK, tid);
+    tile_mma(acc, smem + (kt & 1) * G_STAGE_BYTES, wm, wn, lane);
+    if (more) tile_store(t, smem + ((kt + 1) & 1) * G_STAGE_BYTES, tid);
+    __syncthreads();
+  }
+}
+
+__device__ __forceinline__ u32 xor3(u32 a, u32 b, u32 c) { return a ^ b ^ c; }
+
+// Per-lane partial tile XOR: x[p] = XOR of this lane's accumulators with (e & 3) == p.
+__device__ __forceinline__ void fold_partials(const v16i acc[2][2], u32 x[4]) {
+#pragma unroll
+  for (int p = 0; p < 4; p++) {
+    u32 v = 0;
+#pragma unroll
+    for (int mb = 0; mb < 2; mb++)
+#pragma unroll
+      for (int nb = 0; nb < 2; nb++)
+        v = xor3(v, (u32)acc[mb][nb][p] ^ (u32)acc[mb][nb][4 + p], (u32)acc[mb][nb][8 + p] ^ (u32)acc[mb][nb][12 + p]);
+    x[p] = v;
+  }
+}
+
+__device__ __forceinline__ u32 rotl13(u32 x) { return __builtin_amdgcn_alignbit(x, x, 19); }
+
+__device__ __forceinline__ u32 bf16_rne(float f) {
+  const u32 u = __float_as_uint(f);
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+// Workgroup id -> (bm0, bn0). Consecutive ids are dispatched round-robin over the 8 XCDs;
+// regrouping them gives each XCD a contiguous run, rastered in column groups of GROUP_M row
+// tiles so neighbouring workgroups on one XCD share A and B tiles in that XCD's L2.
+__device__ __forceinline__ void tile_coords(int m, int n, int& bm0, int& bn0) {
+  const int npm = (m + G_BM - 1) / G_BM, npn = (n + G_BN - 1) / G_BN, total = npm * npn;
+  int pid = blockIdx.x;
+  if ((total & 7) == 0) pid = (pid & 7) * (total >> 3) + (pid >> 3);
+  constexpr int GROUP_M = 8;
+  const int grp = GROUP_M * npn, gid = pid / grp, first = gid * GROUP_M;
+  const int gsz = min(npm - first, GROUP_M), in = pid - gid * grp;
+  bm0 = (first + in % gsz) * G_BM;
+  bn0 = (in / gsz) * G_BN;
+}
+
+template <bool HASH, bool DENOISE, int OUT>
+__global__ void __launch_bounds__(G_THREADS) noisy_gemm_kernel(GemmParams p) {
+  __shared__ __attribute__((aligned(16))) u8 smem[G_LDS_BYTES];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
+  int bm0, bn0;
+  tile_coords(p.m, p.n, bm0, bn0);
+  const long k = p.k;
+  const int KT = p.k / G_BK;
+
+  v16i acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++) acc[i][j] = v16i{};
+
+  {
+    TileRegs t;
+    tile_load(t, p.A, k, p.m, p.B, k, p.n, bm0, bn0, 0, tid);
+    tile_store(t, smem, tid);
+    __syncthreads();
+  }
+
+  if constexpr (HASH) {
+    u32 msg[4][16];
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+#pragma unroll
+      for (int w = 0; w < 16; w++) msg[q][w] = 0;
+    const int tpc = p.r / G_BK, nchunks = p.k / p.r;
+    int kt = 0;
+    for (int c0 = 0; c0 < nchunks; c0 += 16) {
+#pragma unroll
+      for (int s = 0; s < 16; s++) {
+        if (c0 + s < nchunks) {
+          run_ktiles(acc, smem, p.A, k, p.m, p.B, k, p.n, bm0, bn0, kt, kt + tpc, KT, tid, wm, wn, lane);
+          kt += tpc;
+          u32 x[4];
+          fold_partials(acc, x);
+#pragma unroll
+          for (int q = 0; q < 4; q++) msg[q][s] = rotl13(msg[q][s]) ^ x[q];
+        }
+      }
+    }
+    // Cross-lane combine of the partial messages through LDS (the pipeline buffers are free:
+    // the last iteration ended with a barrier and loaded nothing).
+    u32* ms = reinterpret_cast<u32*>(smem);
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+#pragma unroll
+      for (int w = 0; w < 16; w++) ms[((wave * 4 + q) * 16 + w) * 64 + lane] = msg[q][w];
+    __syncthreads();
+    if (tid < 128) {
+      // thread h digests tile (g, t) of wave wv's 64 x 64 block
+      const int wv = tid >> 5, j = tid & 31, g = j >> 2, t = j & 3, q = g & 3;
+      const int base = (g >> 2) * 32 + 2 * t;
+      u32 mw[16];
+#pragma unroll
+      for (int w = 0; w < 16; w++) {
+        const u32* src = ms + ((wv * 4 + q) * 16 + w) * 64 + base;
+        u32 v = 0;
+#pragma unroll
+        for (int b34 = 0; b34 < 4; b34++) v ^= src[8 * b34] ^ src[8 * b34 + 1];
+        mw[w] = v;
+      }
+      u32 key[8], h[8];
+#pragma unroll
+      for (int i = 0; i < 8; i++) key[i] = p.key[i];
+      b3_keyed64(key, mw, h);
+      const int row = bm0 + (wv >> 1) * 64 + g, col = bn0 + (wv & 1) * 64 + 2 * t;
+      if (p.dump) {
+        const long NB = p.n / 64;
+        u32* d = p.dump + ((((long)(row >> 6) * 8 + g) * NB + (col >> 6)) * 4 + t) * DUMP_WORDS;
+#pragma unroll
+        for (int w = 0; w < 16; w++) d[w] = mw[w];
+#pragma unroll
+        for (int w = 0; w < 8; w++) d[16 + w] = h[w];
+      }
+      if (p.wins && u256_le(h, p.target)) {
+        const u32 slot = atomicAdd(p.wins, 1u);
+        if (slot < (u32)p.max_wins) {
+          u32* rec = p.wins + 1 + slot * WIN_WORDS;
+          rec[0] = row;
+          rec[1] = col;
+#pragma unroll
+          for (int i = 0; i < 8; i++) rec[2 + i] = h[i];
+        }
+      }
+    }
+    __syncthreads();
+  } else {
+    run_ktiles(acc, smem, p.A, k, p.m, p.B, k, p.n, bm0, bn0, 0, KT, KT, tid, wm, wn, lane);
+  }
+
+  if constexpr (DENOISE) {
+    // acc -= sum_li 128^li [X_li | EAL] [EBRt | Y_li]^T, Horner over limbs, exact mod 2^32
+    // (kernels.cu:598-673). Operands: corrA (lmax, m, 2r), corrB (lmax, n, 2r) int8.
+    const int mx = max(p.maxabs[0], p.maxabs[1]);
+    int L = mx > 1040319 ? 4 : mx > 8127 ? 3 : mx > 63 ? 2 : 1;
+    L = min(L, p.lmax);
+    const long R2 = 2L * p.r;
+    const int CKT = (int)(R2 / G_BK);
+    v16i tmp[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int j = 0; j < 2; j++) tmp[i][j] = v16i{};
+    for (int li = L - 1; li >= 0; li--) {
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) tmp[i][j] = tmp[i][j] << 7;
+      const i8* cA = p.corrA + (long)li * p.m * R2;
+      const i8* cB = p.corrB + (long)li * p.n * R2;
+      TileRegs t;
+      tile_load(t, cA, R2, p.m, cB, R2, p.n, bm0, bn0, 0, tid);
+      tile_store(t, smem, tid);
+      __syncthreads();
+      run_ktiles(tmp, smem, cA, R2, p.m, cB, R2, p.n, bm0, bn0, 0, CKT, CKT, tid, wm, wn, lane);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int j = 0; j < 2; j++) acc[i][j] -= tmp[i][j];
+  }
+
+  if constexpr (OUT != OUT_NONE) {
+    // lane holds col (lane & 31) of rows 8(e>>2) + 4(lane>>5) + (e&3) of each 32 x 32 block
+#pragma unroll
+    for (int mb = 0; mb < 2; mb++) {
+#pragma unroll
+      for (int nb = 0; nb < 2; nb++) {
+        const int col = bn0 + wn * 64 + nb * 32 + (lane & 31);
+        if (col >= p.n) continue;
+        float bsc = 0.f;
+        if constexpr (OUT == OUT_BF16 || OUT == OUT_F32) bsc = p.b_scale[col];
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+          const int row = bm0 + wm * 64 + mb * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+          if (row >= p.m) continue;
+          const long o = (long)row * p.n + col;
+          const int v = acc[mb][nb][e];
+          if constexpr (OUT == OUT_I32) {
+            reinterpret_cast<i32*>(p.out)[o] = v;
+          } else {
+            const float y = __fmul_rn(__fmul_rn((float)v, p.a_scale[row]), bsc);
+            if constexpr (OUT == OUT_F32)
+              reinterpret_cast<float*>(p.out)[o] = y;
+            else
+              reinterpret_cast<uint16_t*>(p.out)[o] = (uint16_t)bf16_rne(y);
+          }
+        }
+      }
+    }
+  }
+}
+
+template <bool H, bool D>
+static void launch_out(int out_mode, dim3 grid, hipStream_t s, const GemmParams& p) {
+  switch (out_mode) {
+    case OUT_NONE: hipLaunchKernelGGL((noisy_gemm_kernel<H, D, OUT_NONE>), grid, dim3(G_THREADS), 0, s, p); break;
+    case OUT_I32: hipLaunchKernelGGL((noisy_gemm_kernel<H, D, OUT_I32>), grid, dim3(G_THREADS), 0, s, p); break;
+    case OUT_BF16: hipLaunchKernelGGL((noisy_gemm_kernel<H, D, OUT_BF16>), grid, dim3(G_THREADS), 0, s, p); break;
+    default: hipLaunchKernelGGL((noisy_gemm_kernel<H, D, OUT_F32>), grid, dim3(G_THREADS), 0, s, p); break;
+  }
+}
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+extern "C" int uwc_noisy_gemm(const int8_t* A, const int8_t* B, int m, int n, int k, int r, const int8_t* corrA,
+                              const int8_t* corrB, const int32_t* maxabs, int lmax, const uint32_t* key,
+                              const uint32_t* target, uint32_t* wins, int max_wins, const float* a_scale,
+                              const float* b_scale, void* out, int out_mode, int flags, uint32_t* tile_dump,
+                              hipStream_t stream) {
+  const bool hash = flags & FLAG_HASH, denoise = flags & FLAG_DENOISE;
+  if (flags & ~(FLAG_HASH | FLAG_DENOISE)) return uwc_fail("uwc_noisy_gemm: unknown flags %d", flags);
+  if (!A || !B || m <= 0 || n <= 0 || k <= 0) return uwc_fail("uwc_noisy_gemm: empty or null operands (m=%d n=%d k=%d)", m, n, k);
+  if (k % G_BK) return uwc_fail("uwc_noisy_gemm: k=%d must be a multiple of %d", k, G_BK);
+  if (!aligned16(A) || !aligned16(B)) return uwc_fail("uwc_noisy_gemm: A and B must be 16-byte aligned");
+  if (out_mode < OUT_NONE || out_mode > OUT_F32) return uwc_fail("uwc_noisy_gemm: unknown out_mode %d", out_mode);
+  if (out_mode != OUT_NONE && !out) return uwc_fail("uwc_noisy_gemm: out is null for out_mode %d", out_mode);
+  if ((out_mode == OUT_BF16 || out_mode == OUT_F32) && (!a_scale || !b_scale))
+    return uwc_fail("uwc_noisy_gemm: a_scale and b_scale are required for out_mode %d", out_mode);
+  if (hash || denoise) {
+    if (m % G_BM || n % G_BN)
+      return uwc_fail("uwc_noisy_gemm: mining needs m %% %d == 0 and n %% %d == 0 (m=%d n=%d)", G_BM, G_BN, m, n);
+    if (r <= 0 || r % G_BK || k % r || (r & (r - 1)))
+      return uwc_fail("uwc_noisy_gemm: r=%d must be a power of two, a multiple of %d and divide k=%d", r, G_BK, k);
+  }
+  if (hash && (!key || !target)) return uwc_fail("uwc_noisy_gemm: FLAG_HASH needs key and target");
+  if (hash && wins && max_wins < 0) return uwc_fail("uwc_noisy_gemm: max_wins=%d < 0", max_wins);
+  if (denoise) {
+    if (!corrA || !corrB || !maxabs) return uwc_fail("uwc_noisy_gemm: FLAG_DENOISE needs corrA, corrB and maxabs");
+    if (lmax < 1 || lmax > 4) return uwc_fail("uwc_noisy_gemm: lmax=%d outside 1..4", lmax);
+    if (!aligned16(corrA) || !aligned16(corrB)) return uwc_fail("uwc_noisy_gemm: corrA/corrB must be 16-byte aligned");
+  }
+  GemmParams p{A, B, m, n, k, r, corrA, corrB, maxabs, lmax, key, target, wins, max_wins, a_scale, b_scale, out,
+               hash ? tile_dump : nullptr};
+  const dim3 grid(((m + G_BM - 1) / G_BM) * ((n + G_BN - 1) / G_BN));
+  if (hash && denoise) launch_out<true, true>(out_mode, grid, stream, p);
+  else if (hash) launch_out<true, false>(out_mode, grid, stream, p);
+  else if (denoise) launch_out<false, true>(out_mode, grid, stream, p);
+  else launch_out<false, false>(out_mode, grid, stream, p);
+  return uwc_launch_status("noisy_gemm");
+}
+
+extern "C" int uwc_igemm_i32(const int8_t* A, const int8_t* B, int m, int n, int k, int32_t* C, hipStream_t stream) {
+  return uwc_noisy_gemm(A, B, m, n, k, 0, nullptr, nullptr, nullptr, 0, nullptr, nullptr, nullptr, 0, nullptr,
+                        nullptr, C, OUT_I32, 0, nullptr, stream);
+}
+
+extern "C" int uwc_igemm_dequant_f32(const int8_t* A, const int8_t* B, int m, int n, int k, const float* sx,
+                                     const float* sw, float* Y, hipStream_t stream) {
+  return uwc_noisy_gemm(A, B, m, n, k, 0, nullptr, nullptr, nullptr, 0, nullptr, nullptr, nullptr, 0, sx, sw, Y,
+                        OUT_F32, 0, nullptr, stream);
+}

@@ -1,0 +1,63 @@
+"""ctypes binding of libuwc_hip.so (the C-ABI declared in include/uwc.h).
+
+The library is built in-tree by useful-work-coin_amd/csrc/build.sh (or __graft_entry__.build()).
+There is no fallback: if the library is missing or a call fails, this module raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libuwc_hip.so")
+
+vp = ctypes.c_void_p
+i32 = ctypes.c_int
+u32 = ctypes.c_uint32
+u64 = ctypes.c_uint64
+
+# name -> argument types (every function returns int status unless listed in _RESTYPE)
+SIGNATURES = {
+    "uwc_version": [],
+    "uwc_last_error": [],
+    "uwc_noisy_gemm": [vp, vp, i32, i32, i32, i32, vp, vp, vp, i32, vp, vp, vp, i32, vp, vp, vp, i32, i32, vp, vp],
+    "uwc_igemm_i32": [vp, vp, i32, i32, i32, vp, vp],
+    "uwc_igemm_dequant_f32": [vp, vp, i32, i32, i32, vp, vp, vp, vp],
+    "uwc_b3_scratch_words": [u64],
+    "uwc_b3_root_and_seed": [vp, u64, vp, vp, vp, u32, vp, vp, vp, u64, vp],
+    "uwc_noise_uniform": [vp, u32, vp, vp, vp, i32, vp],
+    "uwc_noise_perm": [vp, u32, u32, vp, vp, vp],
+    "uwc_noise_rows": [vp, i32, i32, i32, vp, vp, vp, vp, vp, i32, i32, vp, i32, vp],
+    "uwc_quant_act_f32": [vp, i32, i32, i32, i32, vp, vp, vp],
+    "uwc_dequant_f32": [vp, vp, vp, i32, i32, vp, vp],
+}
+_RESTYPE = {"uwc_last_error": ctypes.c_char_p}
+
+_LIB = None
+
+
+class UwcError(RuntimeError):
+    """A libuwc_hip call rejected its arguments or failed to launch."""
+
+
+def lib() -> ctypes.CDLL:
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is not built: run useful-work-coin_amd/csrc/build.sh "
+                              "(or __graft_entry__.build()); there is no CPU fallback")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, args in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = _RESTYPE.get(name, ctypes.c_int)
+        _LIB = L
+    return _LIB
+
+
+def call(name: str, *args) -> None:
+    """Call an int-status entry point; raise UwcError with uwc_last_error() on failure."""
+    st = getattr(lib(), name)(*args)
+    if st != 0:
+        msg = lib().uwc_last_error().decode(errors="replace")
+        raise UwcError(f"{name} failed (status {st}): {msg}")

@@ -1,0 +1,316 @@
+"""MI355X launchers for the cuPOW NoisyGEMM hot path, on torch ROCm tensors and torch's current
+stream: the call surface of the reference's miner/ampere/uwc_ampere/ops.py (same names,
+argument meaning and error behaviour), over libuwc_hip.so's C-ABI (include/uwc.h).
+
+Differences a caller can see: the GEMM tile is 128 x 128 (so m and n of hashed GEMMs must be
+multiples of 128, not of the reference's BN), `cfg` is accepted and ignored (one tiling), and
+gemm() can also dump every tile's message and digest (`dump`). OUT_F32 is an extra output mode
+(the fused detrt dequant epilogue).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from . import _lib
+
+BM, BN, BK = 128, 128, 64
+
+
+def limbs_for(k: int) -> int:
+    """Balanced base-128 limbs that always cover |projection| <= 127 * k (ops.py:18-24)."""
+    bound, L, cap = 127 * k, 1, 63
+    while cap < bound:
+        L += 1
+        cap = cap * 128 + 63
+    return L
+
+
+WIN_WORDS = 10
+DUMP_WORDS = 24
+CHUNKS_PER_CTA = 64
+FLAG_HASH, FLAG_DENOISE = 1, 2
+OUT_NONE, OUT_I32, OUT_BF16, OUT_F32 = 0, 1, 2, 3
+CONFIGS = {"128x128": (128, 2, 2)}
+DEFAULT_CFG = "128x128"
+
+# Pearl's v3 noise labels and salts (miner/ampere/uwc_ampere/reference.py:23-26):
+# SEED_SALT_X = BLAKE3(b"pearl/cert-v3/noise-seed/X").
+SEED_LABEL_A = b"A_tensor" + b"\x00" * 24
+SEED_LABEL_B = b"B_tensor" + b"\x00" * 24
+SEED_SALT_A = bytes.fromhex("8249406ca0ed15169616f692fcf076f892dbdb2a7023b852f0d47719c390017b")
+SEED_SALT_B = bytes.fromhex("11300632ec6301ca2be2af718b3f4d4f1ae9c63988e8cc044844301d71b89aa9")
+
+
+def _check(cond: bool, msg) -> None:
+    # the reference asserts its preconditions; keep AssertionError, but independent of -O
+    if not cond:
+        raise AssertionError(msg)
+
+
+def _p(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def words(b: bytes, device="cuda") -> torch.Tensor:
+    return torch.from_numpy(np.frombuffer(b, dtype="<u4").view(np.int32).copy()).to(device)
+
+
+def words_to_bytes(t: torch.Tensor) -> bytes:
+    return t.detach().cpu().numpy().view(np.uint32).astype("<u4").tobytes()
+
+
+LABEL_A = words(SEED_LABEL_A, "cpu")
+LABEL_B = words(SEED_LABEL_B, "cpu")
+SALT_A = words(SEED_SALT_A, "cpu")
+SALT_B = words(SEED_SALT_B, "cpu")
+_CONSTS: dict = {}
+
+
+def consts(device) -> dict:
+    """Device copies of the label/salt constants (made once; forward() must not copy H2D)."""
+    key = str(torch.device(device))
+    c = _CONSTS.get(key)
+    if c is None:
+        c = _CONSTS[key] = {n: t.to(device) for n, t in
+                            dict(LABEL_A=LABEL_A, LABEL_B=LABEL_B, SALT_A=SALT_A, SALT_B=SALT_B).items()}
+    return c
+
+
+# ------------------------------------------------------------------ BLAKE3
+def b3_scratch_words(nbytes: int) -> int:
+    return _lib.lib().uwc_b3_scratch_words(nbytes)
+
+
+def b3_root_and_seed(data: torch.Tensor, key: torch.Tensor, *, prefix=None, salt=None, dim: int = 0,
+                     root_out=None, seed_out=None, scratch=None):
+    """Keyed BLAKE3 of `data` (uint8/int8, length a multiple of 1024) -> root, optional salted seed."""
+    nbytes = data.numel() * data.element_size()
+    _check(nbytes % 1024 == 0 and nbytes > 0, f"b3_root_and_seed: {nbytes} bytes is not a positive multiple of 1024")
+    _check(data.is_contiguous(), "b3_root_and_seed: data must be contiguous")
+    need = b3_scratch_words(nbytes)
+    if scratch is None or scratch.numel() < need:
+        scratch = torch.empty(need, dtype=torch.int32, device=data.device)
+    _lib.call("uwc_b3_root_and_seed", _p(data), nbytes, _p(key), _p(prefix), _p(salt), dim, _p(root_out), _p(seed_out),
+              _p(scratch), scratch.numel(), _stream())
+    return scratch
+
+
+# ------------------------------------------------------------------ noise
+def noise_uniform(out: torch.Tensor, label: torch.Tensor, key: torch.Tensor, zero_me=None, zero_n: int = 0):
+    _check(out.numel() % 32 == 0, "noise_uniform: out size must be a multiple of 32")
+    _lib.call("uwc_noise_uniform", _p(out), out.numel() // 32, _p(label), _p(key), _p(zero_me), zero_n, _stream())
+
+
+def noise_perm(out: torch.Tensor, k: int, r: int, label: torch.Tensor, key: torch.Tensor):
+    _check(out.numel() >= k, "noise_perm: out too small")
+    _lib.call("uwc_noise_perm", _p(out), k, r, _p(label), _p(key), _stream())
+
+
+def noise_rows(src, rows, k, r, *, E=None, Pn=None, dst=None, Pp=None, corr=None, corr_off=-1, ecopy_off=-1,
+               maxabs=None, lmax=None):
+    lmax = corr.shape[0] if corr is not None else 0
+    _check(rows % 8 == 0 and k % 4 == 0, f"noise_rows: rows={rows} % 8 and k={k} % 4 must be 0")
+    _lib.call("uwc_noise_rows", _p(src), rows, k, r, _p(E), _p(Pn), _p(dst), _p(Pp), _p(corr), corr_off, ecopy_off,
+              _p(maxabs), lmax, _stream())
+
+
+# ------------------------------------------------------------------ GEMM
+def gemm(A, B, *, r=128, flags=0, corrA=None, corrB=None, maxabs=None, key=None, target=None, wins=None,
+         max_wins=0, a_scale=None, b_scale=None, out=None, out_mode=OUT_NONE, cfg=None, dump=None):
+    """C = A @ B^T (int8, k contiguous) with the optional mining transcript / denoise / epilogue."""
+    m, k = A.shape
+    n = B.shape[0]
+    if flags:
+        _check(m % BM == 0 and n % BN == 0 and k % BK == 0 and r % BK == 0 and k % r == 0, (m, n, k, r))
+    else:
+        _check(k % BK == 0, (m, n, k))
+    _check(A.dtype == torch.int8 and B.dtype == torch.int8 and A.is_contiguous() and B.is_contiguous(),
+           "gemm: A and B must be contiguous int8")
+    _lib.call("uwc_noisy_gemm", _p(A), _p(B), m, n, k, r, _p(corrA), _p(corrB), _p(maxabs),
+              corrA.shape[0] if corrA is not None else 0, _p(key), _p(target), _p(wins), max_wins, _p(a_scale),
+              _p(b_scale), _p(out), out_mode, flags, _p(dump), _stream())
+
+
+def igemm_i32(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Exact int32 A @ B^T for any m, n (k % 64 == 0)."""
+    m, k = A.shape
+    n = B.shape[0]
+    _check(A.is_contiguous() and B.is_contiguous() and A.dtype == torch.int8 and B.dtype == torch.int8,
+           "igemm_i32: A and B must be contiguous int8")
+    out = torch.empty((m, n), dtype=torch.int32, device=A.device) if out is None else out
+    _lib.call("uwc_igemm_i32", _p(A), _p(B), m, n, k, _p(out), _stream())
+    return out
+
+
+# ------------------------------------------------------------------ one mined linear layer
+_WORKSPACE: dict = {}
+
+
+@dataclass
+class MinedWeight:
+    """A weight B^T (n x k int8, values in [-64, 64]) prepared for mining under one block template.
+
+    setup_block() runs once per (block header, k); forward() runs per call and needs no host sync.
+    (miner/ampere/uwc_ampere/ops.py:205-371)
+    """
+    Bt: torch.Tensor
+    b_scale: torch.Tensor
+    r: int = 128
+    max_wins: int = 64
+    job_key: torch.Tensor | None = None
+    b_seed: torch.Tensor | None = None
+    target: torch.Tensor | None = None
+    BpEBt: torch.Tensor | None = None
+    PB: torch.Tensor | None = None
+    EBRt: torch.Tensor | None = None
+    corrB: torch.Tensor | None = None
+    _bufs: dict = field(default_factory=dict)
+
+    @property
+    def n(self):
+        return self.Bt.shape[0]
+
+    @property
+    def k(self):
+        return self.Bt.shape[1]
+
+    @property
+    def device(self):
+        return self.b_scale.device
+
+    def setup_block(self, job_key: bytes, target_words: np.ndarray):
+        dev = self.device
+        n, k, r = self.n, self.k, self.r
+        _check(n % BN == 0 and k % r == 0 and r % BK == 0, f"MinedWeight: n={n} k={k} r={r} unsupported")
+        Bt = self.Bt if self.Bt.device == dev else self.Bt.to(dev, non_blocking=True)
+        Bt = Bt.contiguous()
+        self.job_key = words(job_key, dev)
+        self.target = torch.from_numpy(np.asarray(target_words).astype(np.uint32).view(np.int32).copy()).to(dev)
+        self.b_seed = torch.empty(8, dtype=torch.int32, device=dev)
+        c = consts(dev)
+        b3_root_and_seed(Bt.view(-1), self.job_key, prefix=self.job_key, salt=c["SALT_B"], dim=n, seed_out=self.b_seed)
+        self.EBRt = torch.empty((n, r), dtype=torch.int8, device=dev)
+        noise_uniform(self.EBRt, c["LABEL_B"], self.b_seed)
+        self.PB = torch.empty(k, dtype=torch.int32, device=dev)
+        noise_perm(self.PB, k, r, c["LABEL_B"], self.b_seed)
+        if self.BpEBt is None:
+            self.BpEBt = torch.empty((n, k), dtype=torch.int8, device=dev)
+            self.corrB = torch.zeros((limbs_for(k), n, 2 * r), dtype=torch.int8, device=dev)
+        noise_rows(Bt, n, k, r, E=self.EBRt, Pn=self.PB, dst=self.BpEBt, corr=self.corrB, ecopy_off=0)
+        del Bt
+
+    def _buf(self, m: int):
+        """Per-call buffers. The large ones are a workspace shared by every weight with the same
+        (m, k, r): layers run one after another on one stream. Win records are per weight."""
+        dev, k, r = self.device, self.k, self.r
+        key = (str(dev), m, k, r)
+        ws = _WORKSPACE.get(key)
+        if ws is None:
+            ws = _WORKSPACE[key] = dict(
+                a_seed=torch.empty(8, dtype=torch.int32, device=dev),
+                EAL=torch.empty((m, r), dtype=torch.int8, device=dev),
+                PA=torch.empty(k, dtype=torch.int32, device=dev),
+                ApEA=torch.empty((m, k), dtype=torch.int8, device=dev),
+                corrA=torch.zeros((limbs_for(k), m, 2 * r), dtype=torch.int8, device=dev),
+                maxabs=torch.zeros(2, dtype=torch.int32, device=dev),
+                scratch=torch.empty(max(8, b3_scratch_words(m * k)), dtype=torch.int32, device=dev),
+            )
+        wins = self._bufs.get(m)
+        if wins is None:
+            wins = self._bufs[m] = torch.zeros(1 + self.max_wins * WIN_WORDS, dtype=torch.int32, device=dev)
+        return {**ws, "wins": wins}
+
+    def forward(self, A: torch.Tensor, a_scale: torch.Tensor, out: torch.Tensor | None = None,
+                out_mode: int = OUT_BF16, hash_tiles: bool = True) -> torch.Tensor:
+        """A: m x k int8 (values in [-64, 64]). Returns A @ Bt^T scaled (bf16/f32) or exact int32."""
+        return self._forward(A, a_scale, out, out_mode, hash_tiles)
+
+    def _forward(self, A, a_scale, out, out_mode, hash_tiles, cfg=None, proj=None, dump=None):
+        m, k = A.shape
+        n, r = self.n, self.r
+        _check(k == self.k and m % BM == 0, f"MinedWeight.forward: A is {tuple(A.shape)}, need m % {BM} == 0, k == {self.k}")
+        _check(A.is_contiguous() and A.dtype == torch.int8, "MinedWeight.forward: A must be contiguous int8")
+        dev = A.device
+        b = self._buf(m)
+        c = consts(dev)
+        if out is None and out_mode != OUT_NONE:
+            dt = {OUT_BF16: torch.bfloat16, OUT_I32: torch.int32, OUT_F32: torch.float32}[out_mode]
+            out = torch.empty((m, n), dtype=dt, device=dev)
+        # 1. commit to A, derive a_seed = H(b_seed || bind_a(root_A, m))
+        b3_root_and_seed(A.view(-1), self.job_key, prefix=self.b_seed, salt=c["SALT_A"], dim=m,
+                         seed_out=b["a_seed"], scratch=b["scratch"])
+        # 2. A-side noise (the same launch zeroes maxabs); the win counter restarts at 0
+        noise_uniform(b["EAL"], c["LABEL_A"], b["a_seed"], zero_me=b["maxabs"], zero_n=2)
+        b["wins"][:1].zero_()
+        noise_perm(b["PA"], k, r, c["LABEL_A"], b["a_seed"])
+        # 3. ApEA = A + EAL*P_A ; X = A * P_B^T (limbs) ; EAL copy
+        noise_rows(A, m, k, r, E=b["EAL"], Pn=b["PA"], dst=b["ApEA"], Pp=self.PB, corr=b["corrA"], corr_off=0,
+                   ecopy_off=r, maxabs=b["maxabs"][0:1])
+        # 4. Y = BpEBt * P_A^T (limbs)
+        noise_rows(self.BpEBt, n, k, r, Pp=b["PA"], corr=self.corrB, corr_off=r, maxabs=b["maxabs"][1:2])
+        # 5. noisy GEMM: hash every tile, denoise exactly, scale
+        gemm(b["ApEA"], self.BpEBt, r=r, flags=(FLAG_HASH if hash_tiles else 0) | FLAG_DENOISE,
+             corrA=b["corrA"], corrB=self.corrB, maxabs=b["maxabs"], key=b["a_seed"], target=self.target,
+             wins=b["wins"], max_wins=self.max_wins, a_scale=a_scale, b_scale=self.b_scale, out=out, out_mode=out_mode,
+             dump=dump)
+        return out
+
+    def noise_mine(self, A: torch.Tensor, dump=None):
+        """What a pure noise miner runs per attempt batch: commit A, noise it, hashed GEMM, no output.
+        No projections (X, Y) and no denoise, since nobody needs C."""
+        m, k = A.shape
+        n, r = self.n, self.r
+        _check(k == self.k and m % BM == 0, f"MinedWeight.noise_mine: A is {tuple(A.shape)}")
+        dev = A.device
+        b = self._buf(m)
+        c = consts(dev)
+        b3_root_and_seed(A.view(-1), self.job_key, prefix=self.b_seed, salt=c["SALT_A"], dim=m,
+                         seed_out=b["a_seed"], scratch=b["scratch"])
+        noise_uniform(b["EAL"], c["LABEL_A"], b["a_seed"], zero_me=b["wins"], zero_n=1)
+        noise_perm(b["PA"], k, r, c["LABEL_A"], b["a_seed"])
+        noise_rows(A, m, k, r, E=b["EAL"], Pn=b["PA"], dst=b["ApEA"])
+        gemm(b["ApEA"], self.BpEBt, r=r, flags=FLAG_HASH, key=b["a_seed"], target=self.target, wins=b["wins"],
+             max_wins=self.max_wins, dump=dump)
+
+    def winners(self, m: int) -> list[tuple[int, int, bytes]]:
+        """(row_offset, col_offset, hash) for winning tiles of the last forward with this m (syncs)."""
+        w = self._buf(m)["wins"].cpu().numpy().view(np.uint32)
+        cnt = min(int(w[0]), self.max_wins)
+        recs = w[1:1 + cnt * WIN_WORDS].reshape(cnt, WIN_WORDS)
+        return [(int(x[0]), int(x[1]), x[2:].astype("<u4").tobytes()) for x in recs]
+
+
+class GraphedForward:
+    """MinedWeight.forward captured as one HIP graph for a fixed m (static input/output buffers).
+
+    The graph records no memset node: the win counter and maxabs are cleared by kernels
+    (torch's zero_ fill and noise_uniform's zero_me)."""
+
+    def __init__(self, w: MinedWeight, m: int, out_mode: int = OUT_BF16):
+        dev = w.device
+        self.w, self.m = w, m
+        self.A = torch.zeros((m, w.k), dtype=torch.int8, device=dev)
+        self.a_scale = torch.ones(m, dtype=torch.float32, device=dev)
+        dt = {OUT_BF16: torch.bfloat16, OUT_I32: torch.int32, OUT_F32: torch.float32}[out_mode]
+        self.out = torch.empty((m, w.n), dtype=dt, device=dev)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                w.forward(self.A, self.a_scale, out=self.out, out_mode=out_mode)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            w.forward(self.A, self.a_scale, out=self.out, out_mode=out_mode)
+
+    def __call__(self):
+        self.graph.replay()
+        return self.out
