@@ -1,0 +1,251 @@
+// Keyed BLAKE3 tree commitment of an operand and Pearl's salted seed derivation on gfx950
+// (miner/ampere/uwc_ampere/kernels.cu:138-244, reference.py:41-64, ops.py:99-118).
+//
+// BLAKE3 over 16 MiB is 16384 independent chunk chains of 16 compressions each, then a
+// 14-level tree: the work is latency-bound, not throughput-bound. One compression is therefore
+// spread over the 4 lanes of a quad: lane q holds column q of the 4 x 4 state
+// (a = v[q], b = v[4+q], c = v[8+q], d = v[12+q]), runs the column G on it, and the diagonal
+// step rotates b, c, d across the quad with DPP quad permutes (v0 v5 v10 v15 ... become one
+// lane's a b c d). Message words reach each lane from LDS at precomputed per-lane offsets
+// (lane q of round r reads words S[r][2q], S[r][2q+1], S[r][8+2q], S[r][9+2q]).
+// This quarters the dependent instruction chain per compression and gives 4x the waves.
+#include "uwc_common.h"
+
+#define QROT1 0x39  // quad_perm [1,2,3,0]: lane q takes lane (q+1) & 3
+#define QROT2 0x4E  // quad_perm [2,3,0,1]
+#define QROT3 0x93  // quad_perm [3,0,1,2]
+
+template <int CTRL>
+__device__ __forceinline__ u32 qperm(u32 x) {
+  return (u32)__builtin_amdgcn_mov_dpp((int)x, CTRL, 0xF, 0xF, false);
+}
+
+__device__ __forceinline__ void b3_g1(u32& a, u32& b, u32& c, u32& d, u32 x, u32 y) {
+  a = a + b + x; d = rotr32(d ^ a, 16);
+  c = c + d;     b = rotr32(b ^ c, 12);
+  a = a + b + y; d = rotr32(d ^ a, 8);
+  c = c + d;     b = rotr32(b ^ c, 7);
+}
+
+// Byte offsets, within a 16-word message, of the 28 words lane q consumes (round-major:
+// column pair then diagonal pair).
+struct QuadMsgOffsets {
+  u32 o[28];
+};
+
+__device__ __forceinline__ QuadMsgOffsets quad_offsets(int q) {
+  QuadMsgOffsets t;
+#pragma unroll
+  for (int r = 0; r < 7; r++) {
+    t.o[4 * r + 0] = 4u * kB3Sched[r][2 * q];
+    t.o[4 * r + 1] = 4u * kB3Sched[r][2 * q + 1];
+    t.o[4 * r + 2] = 4u * kB3Sched[r][8 + 2 * q];
+    t.o[4 * r + 3] = 4u * kB3Sched[r][9 + 2 * q];
+  }
+  return t;
+}
+
+// One compression by a quad. msg: the 16-word message in LDS. (ca, cb): this lane's chaining
+// value words cv[q], cv[4+q]. Returns this lane's output words out[q] = a ^ c, out[4+q] = b ^ d.
+__device__ __forceinline__ void quad_compress(const u8* msg, const QuadMsgOffsets& off, int q, u32 ca, u32 cb,
+                                              u64 counter, u32 blen, u32 flags, u32& lo, u32& hi) {
+  u32 m[28];
+#pragma unroll
+  for (int j = 0; j < 28; j++) m[j] = *reinterpret_cast<const u32*>(msg + off.o[j]);
+  u32 a = ca, b = cb, c = b3_iv(0), d = (u32)counter;
+  // c = IV[q], d = (counter lo, counter hi, blen, flags)[q]
+  if (q == 1) { c = b3_iv(1); d = (u32)(counter >> 32); }
+  if (q == 2) { c = b3_iv(2); d = blen; }
+  if (q == 3) { c = b3_iv(3); d = flags; }
+#pragma unroll
+  for (int r = 0; r < 7; r++) {
+    b3_g1(a, b, c, d, m[4 * r], m[4 * r + 1]);
+    b = qperm<QROT1>(b); c = qperm<QROT2>(c); d = qperm<QROT3>(d);
+    b3_g1(a, b, c, d, m[4 * r + 2], m[4 * r + 3]);
+    b = qperm<QROT3>(b); c = qperm<QROT2>(c); d = qperm<QROT1>(d);
+  }
+  lo = a ^ c;
+  hi = b ^ d;
+}
+
+// Level-wise pairwise reduction, by quads, of `count` chaining values in LDS (8 words each):
+// pairs (2i, 2i+1) merge, an odd last value carries up. Over a group that starts at a multiple
+// of a power of two covering it, this is exactly BLAKE3's left-complete tree.
+__device__ void quad_level_reduce(u32* cvs, int count, u32 k_lo, u32 k_hi, u32 kflag, bool root_at_end,
+                                  const QuadMsgOffsets& off) {
+  const int tid = threadIdx.x, q = tid & 3, quad = tid >> 2, nquads = blockDim.x >> 2;
+  while (count > 1) {
+    const int pairs = count >> 1;
+    const bool last = (count == 2) && root_at_end;
+    // up to 2 pairs per quad (groups of at most 4 * blockDim / 4 values)
+    u32 lo0 = 0, hi0 = 0, lo1 = 0, hi1 = 0;
+    if (quad < pairs)
+      quad_compress(reinterpret_cast<const u8*>(cvs + quad * 16), off, q, k_lo, k_hi, 0, 64,
+                    B3_PARENT | kflag | (last ? B3_ROOT : 0u), lo0, hi0);
+    if (quad + nquads < pairs)
+      quad_compress(reinterpret_cast<const u8*>(cvs + (quad + nquads) * 16), off, q, k_lo, k_hi, 0, 64,
+                    B3_PARENT | kflag, lo1, hi1);
+    u32 carry = 0;
+    const bool has_carry = (count & 1) && tid < 8;
+    if (has_carry) carry = cvs[(count - 1) * 8 + tid];
+    __syncthreads();
+    if (quad < pairs) { cvs[quad * 8 + q] = lo0; cvs[quad * 8 + 4 + q] = hi0; }
+    if (quad + nquads < pairs) { cvs[(quad + nquads) * 8 + q] = lo1; cvs[(quad + nquads) * 8 + 4 + q] = hi1; }
+    if (has_carry) cvs[pairs * 8 + tid] = carry;
+    __syncthreads();
+    count = pairs + (count & 1);
+  }
+}
+
+#define B3_CHUNKS_PER_WG 64
+#define B3_QSTRIDE 80  // LDS bytes per quad's message block (64 + 16 pad: fewer bank conflicts)
+
+// 64 chunks per workgroup (256 threads, one quad per chunk). Each lane fetches 16 bytes of
+// its chunk's next block from HBM while the quad compresses the current one; the block goes
+// through the quad's own LDS slot, so only wave-local ordering is needed there.
+__global__ void __launch_bounds__(256) b3_chunks_kernel(const u8* __restrict__ data, u64 nchunks,
+                                                        const u32* __restrict__ key, u32* __restrict__ wg_cvs) {
+  __shared__ __attribute__((aligned(16))) u8 blk[B3_CHUNKS_PER_WG * B3_QSTRIDE];
+  __shared__ u32 cvs[B3_CHUNKS_PER_WG * 8];
+  const int tid = threadIdx.x, q = tid & 3, c = tid >> 2;
+  const u64 base = (u64)blockIdx.x * B3_CHUNKS_PER_WG;
+  const int count = (int)min((u64)B3_CHUNKS_PER_WG, nchunks - base);
+  const QuadMsgOffsets off = quad_offsets(q);
+  const u32 k_lo = key[q], k_hi = key[4 + q];
+  const bool active = c < count;
+  const v4i* src = reinterpret_cast<const v4i*>(data + (base + (active ? c : 0)) * 1024ull) + q;
+  u8* my = blk + c * B3_QSTRIDE;
+  v4i nxt = active ? src[0] : v4i{0, 0, 0, 0};
+  u32 lo = k_lo, hi = k_hi;
+  for (int b = 0; b < 16; b++) {
+    *reinterpret_cast<v4i*>(my + q * 16) = nxt;
+    __builtin_amdgcn_wave_barrier();
+    if (b + 1 < 16 && active) nxt = src[(b + 1) * 4];
+    const u32 flags = B3_KEYED | (b == 0 ? B3_CHUNK_START : 0u) | (b == 15 ? B3_CHUNK_END : 0u) |
+                      ((b == 15 && nchunks == 1) ? B3_ROOT : 0u);
+    quad_compress(my, off, q, lo, hi, base + c, 64, flags, lo, hi);
+    __builtin_amdgcn_wave_barrier();
+  }
+  if (active) { cvs[c * 8 + q] = lo; cvs[c * 8 + 4 + q] = hi; }
+  __syncthreads();
+  quad_level_reduce(cvs, count, k_lo, k_hi, B3_KEYED, gridDim.x == 1, off);
+  if (tid < 8) wg_cvs[blockIdx.x * 8 + tid] = cvs[tid];
+}
+
+#define B3_GROUP 1024
+// Reduces aligned groups of up to 1024 chaining values (256 threads = 64 quads). With a single
+// group (final), the last merge carries ROOT and the salted seed may follow:
+//   seed = BLAKE3(prefix || keyed_BLAKE3(salt, root || dim_le32 || 0^28))
+// (Pearl's v3 derivation: b_seed with prefix = job_key, a_seed with prefix = b_seed).
+__global__ void __launch_bounds__(256) b3_reduce_kernel(const u32* __restrict__ in_cvs, int count,
+                                                        const u32* __restrict__ key, u32* __restrict__ out_cvs,
+                                                        int final_level, const u32* __restrict__ prefix,
+                                                        const u32* __restrict__ salt, u32 dim,
+                                                        u32* __restrict__ root_out, u32* __restrict__ seed_out) {
+  __shared__ __attribute__((aligned(16))) u32 cvs[B3_GROUP * 8];
+  const int tid = threadIdx.x, q = tid & 3;
+  const int base = blockIdx.x * B3_GROUP, cnt = min(B3_GROUP, count - base);
+  for (int i = tid; i < cnt * 8; i += blockDim.x) cvs[i] = in_cvs[(u64)base * 8 + i];
+  __syncthreads();
+  const QuadMsgOffsets off = quad_offsets(q);
+  const u32 k_lo = key[q], k_hi = key[4 + q];
+  // level 0 has up to 512 pairs for 64 quads: reduce in passes of 128 pairs (2 per quad)
+  int c2 = cnt;
+  while (c2 > 256) {
+    // pairwise merge of the first 256 values, then of the next 256, ... keeping order
+    const int pairs = c2 >> 1;
+    for (int p0 = 0; p0 < pairs; p0 += 128) {
+      const int quad = tid >> 2;
+      u32 lo0 = 0, hi0 = 0, lo1 = 0, hi1 = 0;
+      const int pa = p0 + quad, pb = p0 + quad + 64;
+      if (pa < pairs)
+        quad_compress(reinterpret_cast<const u8*>(cvs + pa * 16), off, q, k_lo, k_hi, 0, 64, B3_PARENT | B3_KEYED, lo0,
+                      hi0);
+      if (pb < pairs)
+        quad_compress(reinterpret_cast<const u8*>(cvs + pb * 16), off, q, k_lo, k_hi, 0, 64, B3_PARENT | B3_KEYED, lo1,
+                      hi1);
+      __syncthreads();
+      // pair p's output goes to slot p: slots below p0 are final already, slots >= p0 are
+      // read only by pairs >= p0, which this pass has consumed
+      if (pa < pairs) { cvs[pa * 8 + q] = lo0; cvs[pa * 8 + 4 + q] = hi0; }
+      if (pb < pairs) { cvs[pb * 8 + q] = lo1; cvs[pb * 8 + 4 + q] = hi1; }
+      __syncthreads();
+    }
+    if (c2 & 1) {
+      u32 carry = tid < 8 ? cvs[(c2 - 1) * 8 + tid] : 0u;
+      __syncthreads();
+      if (tid < 8) cvs[pairs * 8 + tid] = carry;
+      __syncthreads();
+    }
+    c2 = pairs + (c2 & 1);
+  }
+  quad_level_reduce(cvs, c2, k_lo, k_hi, B3_KEYED, final_level != 0, off);
+  if (!final_level) {
+    if (tid < 8) out_cvs[blockIdx.x * 8 + tid] = cvs[tid];
+    return;
+  }
+  // root, then the seed: two one-block hashes by quad 0 (messages staged in LDS)
+  u32* msg = cvs + 16;
+  if (tid < 8) {
+    if (root_out) root_out[tid] = cvs[tid];
+    msg[tid] = cvs[tid];
+    msg[8 + tid] = tid == 0 ? dim : 0u;
+  }
+  if (!seed_out) return;
+  __syncthreads();
+  u32 lo = 0, hi = 0;
+  if (tid < 4)
+    quad_compress(reinterpret_cast<const u8*>(msg), off, q, salt[q], salt[4 + q], 0, 64,
+                  B3_CHUNK_START | B3_CHUNK_END | B3_ROOT | B3_KEYED, lo, hi);
+  __syncthreads();
+  if (tid < 4) { msg[8 + q] = lo; msg[12 + q] = hi; }
+  if (tid < 8) msg[tid] = prefix[tid];
+  __syncthreads();
+  if (tid < 4) {
+    quad_compress(reinterpret_cast<const u8*>(msg), off, q, b3_iv(q), b3_iv(4 + q), 0, 64,
+                  B3_CHUNK_START | B3_CHUNK_END | B3_ROOT, lo, hi);
+    seed_out[q] = lo;
+    seed_out[4 + q] = hi;
+  }
+}
+
+extern "C" int uwc_b3_scratch_words(uint64_t nbytes) {
+  const u64 nch = nbytes / 1024, nwg = (nch + B3_CHUNKS_PER_WG - 1) / B3_CHUNKS_PER_WG;
+  u64 words = nwg * 8, cnt = nwg;
+  while (cnt > B3_GROUP) {  // intermediate levels are kept after the first one
+    cnt = (cnt + B3_GROUP - 1) / B3_GROUP;
+    words += cnt * 8;
+  }
+  return words > 0x7fffffff ? -1 : (int)words;
+}
+
+extern "C" int uwc_b3_root_and_seed(const uint8_t* data, uint64_t nbytes, const uint32_t* key, const uint32_t* prefix,
+                                    const uint32_t* salt, uint32_t dim, uint32_t* root_out, uint32_t* seed_out,
+                                    uint32_t* scratch, uint64_t scratch_words, hipStream_t stream) {
+  if (!data || !key || !scratch) return uwc_fail("uwc_b3_root_and_seed: null data, key or scratch");
+  if (nbytes == 0 || nbytes % 1024) return uwc_fail("uwc_b3_root_and_seed: nbytes=%llu must be a positive multiple of 1024",
+                                                    (unsigned long long)nbytes);
+  if (((uintptr_t)data & 15u) != 0) return uwc_fail("uwc_b3_root_and_seed: data must be 16-byte aligned");
+  if (seed_out && (!prefix || !salt)) return uwc_fail("uwc_b3_root_and_seed: a seed needs prefix and salt");
+  const int need = uwc_b3_scratch_words(nbytes);
+  if (need < 0 || scratch_words < (u64)need)
+    return uwc_fail("uwc_b3_root_and_seed: scratch has %llu words, needs %d", (unsigned long long)scratch_words, need);
+  const u64 nch = nbytes / 1024;
+  int cnt = (int)((nch + B3_CHUNKS_PER_WG - 1) / B3_CHUNKS_PER_WG);
+  hipLaunchKernelGGL(b3_chunks_kernel, dim3(cnt), dim3(256), 0, stream, data, nch, key, scratch);
+  int st = uwc_launch_status("b3_chunks");
+  if (st) return st;
+  u32* cur = scratch;
+  while (cnt > B3_GROUP) {
+    const int groups = (cnt + B3_GROUP - 1) / B3_GROUP;
+    u32* nxt = cur + (u64)cnt * 8;
+    hipLaunchKernelGGL(b3_reduce_kernel, dim3(groups), dim3(256), 0, stream, cur, cnt, key, nxt, 0, nullptr, nullptr,
+                       0u, nullptr, nullptr);
+    if ((st = uwc_launch_status("b3_reduce"))) return st;
+    cur = nxt;
+    cnt = groups;
+  }
+  hipLaunchKernelGGL(b3_reduce_kernel, dim3(1), dim3(256), 0, stream, cur, cnt, key, nullptr, 1, prefix, salt, dim,
+                     root_out, seed_out);
+  return uwc_launch_status("b3_reduce_final");
+}

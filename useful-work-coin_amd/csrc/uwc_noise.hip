@@ -1,188 +1,8 @@
-// Per-nonce commitment and noise kernels of the cuPOW miner on gfx950:
-//   keyed BLAKE3 tree commitment of an operand and the salted seed derivation
-//   (miner/ampere/uwc_ampere/kernels.cu:138-244, reference.py:41-64);
+// Per-nonce noise kernels of the cuPOW miner on gfx950 (the commitment is uwc_commit.hip):
 //   uniform noise E and the noise pairs P (kernels.cu:246-301, reference.py:67-93);
 //   operand noising + rank-r projections in balanced base-128 limbs + max |projection|
 //   (kernels.cu:303-372).
 #include "uwc_common.h"
-
-// ------------------------------------------------------------------ BLAKE3 tree
-// Level-wise pairwise reduction of `count` chaining values in LDS (8 words each): pairs
-// (2i, 2i+1) merge, an odd last value carries up. Applied to a group that starts at a
-// multiple of a power of two covering it, this is exactly BLAKE3's left-complete tree.
-__device__ void b3_level_reduce(u32* cvs, int count, const u32 key[8], u32 kflag, bool root_at_end) {
-  const int tid = threadIdx.x;
-  while (count > 1) {
-    const int pairs = count >> 1;
-    const bool last = (count == 2) && root_at_end;
-    u32 res[8];
-    // callers size groups so that pairs <= blockDim.x: one pair per thread
-    if (tid < pairs) {
-      u32 msg[16];
-#pragma unroll
-      for (int i = 0; i < 16; i++) msg[i] = cvs[(2 * tid) * 8 + i];
-      b3_compress(key, msg, 0, 64, B3_PARENT | kflag | (last ? B3_ROOT : 0u), res);
-    }
-    u32 carry[8];
-    const bool has_carry = (count & 1) && tid == 0;
-    if (has_carry) {
-#pragma unroll
-      for (int i = 0; i < 8; i++) carry[i] = cvs[(count - 1) * 8 + i];
-    }
-    __syncthreads();
-    if (tid < pairs) {
-#pragma unroll
-      for (int i = 0; i < 8; i++) cvs[tid * 8 + i] = res[i];
-    }
-    if (has_carry) {
-#pragma unroll
-      for (int i = 0; i < 8; i++) cvs[pairs * 8 + i] = carry[i];
-    }
-    __syncthreads();
-    count = pairs + (count & 1);
-  }
-}
-
-#define B3_CHUNKS_PER_WG 64
-
-// One thread per 1 KiB chunk; the workgroup's 64 chunks are staged block by block through
-// LDS (each 64-byte block row is read by 4 neighbouring lanes) and reduced to one value.
-__global__ void __launch_bounds__(B3_CHUNKS_PER_WG) b3_chunks_kernel(const u8* __restrict__ data, u64 nchunks,
-                                                                      const u32* __restrict__ key,
-                                                                      u32* __restrict__ wg_cvs) {
-  __shared__ u32 cvs[B3_CHUNKS_PER_WG * 8];
-  __shared__ v4i stage[2][B3_CHUNKS_PER_WG * 4];
-  u32 k8[8];
-#pragma unroll
-  for (int i = 0; i < 8; i++) k8[i] = key[i];
-  const u64 base = (u64)blockIdx.x * B3_CHUNKS_PER_WG;
-  const int count = (int)min((u64)B3_CHUNKS_PER_WG, nchunks - base);
-  const int tid = threadIdx.x;
-  const v4i* g = reinterpret_cast<const v4i*>(data + base * 1024ull);
-  auto fetch = [&](int buf, int b) {
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-      const int idx = tid + q * B3_CHUNKS_PER_WG, c = idx >> 2, part = idx & 3;
-      if (c < count) stage[buf][idx] = g[(u64)c * 64 + b * 4 + part];
-    }
-  };
-  u32 cv[8];
-#pragma unroll
-  for (int i = 0; i < 8; i++) cv[i] = k8[i];
-  fetch(0, 0);
-  __syncthreads();
-  for (int b = 0; b < 16; b++) {
-    if (b + 1 < 16) fetch((b + 1) & 1, b + 1);
-    if (tid < count) {
-      u32 msg[16];
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const v4i w = stage[b & 1][tid * 4 + q];
-        msg[4 * q] = w[0]; msg[4 * q + 1] = w[1]; msg[4 * q + 2] = w[2]; msg[4 * q + 3] = w[3];
-      }
-      const u32 flags = B3_KEYED | (b == 0 ? B3_CHUNK_START : 0u) | (b == 15 ? B3_CHUNK_END : 0u) |
-                        ((b == 15 && nchunks == 1) ? B3_ROOT : 0u);
-      u32 out[8];
-      b3_compress(cv, msg, base + tid, 64, flags, out);
-#pragma unroll
-      for (int i = 0; i < 8; i++) cv[i] = out[i];
-    }
-    __syncthreads();
-  }
-  if (tid < count) {
-#pragma unroll
-    for (int i = 0; i < 8; i++) cvs[tid * 8 + i] = cv[i];
-  }
-  __syncthreads();
-  b3_level_reduce(cvs, count, k8, B3_KEYED, gridDim.x == 1);
-  if (tid < 8) wg_cvs[blockIdx.x * 8 + tid] = cvs[tid];
-}
-
-#define B3_GROUP 1024
-// Reduces aligned groups of up to 1024 chaining values (512 threads, one pair each). With a
-// single group (final), the last merge carries ROOT and the salted seed may follow:
-//   seed = BLAKE3(prefix || keyed_BLAKE3(salt, root || dim_le32 || 0^28))
-// (Pearl's v3 derivation: b_seed with prefix = job_key, a_seed with prefix = b_seed).
-__global__ void __launch_bounds__(512) b3_reduce_kernel(const u32* __restrict__ in_cvs, int count,
-                                                        const u32* __restrict__ key, u32* __restrict__ out_cvs,
-                                                        int final_level, const u32* __restrict__ prefix,
-                                                        const u32* __restrict__ salt, u32 dim,
-                                                        u32* __restrict__ root_out, u32* __restrict__ seed_out) {
-  __shared__ u32 cvs[B3_GROUP * 8];
-  const int base = blockIdx.x * B3_GROUP, cnt = min(B3_GROUP, count - base);
-  for (int i = threadIdx.x; i < cnt * 8; i += blockDim.x) cvs[i] = in_cvs[(u64)base * 8 + i];
-  __syncthreads();
-  u32 k8[8];
-#pragma unroll
-  for (int i = 0; i < 8; i++) k8[i] = key[i];
-  b3_level_reduce(cvs, cnt, k8, B3_KEYED, final_level != 0);
-  if (!final_level) {
-    if (threadIdx.x < 8) out_cvs[blockIdx.x * 8 + threadIdx.x] = cvs[threadIdx.x];
-    return;
-  }
-  if (threadIdx.x == 0) {
-    u32 root[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) root[i] = cvs[i];
-    if (root_out) {
-#pragma unroll
-      for (int i = 0; i < 8; i++) root_out[i] = root[i];
-    }
-    if (seed_out) {
-      u32 msg[16], bound[8], s8[8], seed[8];
-#pragma unroll
-      for (int i = 0; i < 8; i++) { msg[i] = root[i]; msg[8 + i] = 0; s8[i] = salt[i]; }
-      msg[8] = dim;
-      b3_keyed64(s8, msg, bound);
-#pragma unroll
-      for (int i = 0; i < 8; i++) { msg[i] = prefix[i]; msg[8 + i] = bound[i]; }
-      b3_plain64(msg, seed);
-#pragma unroll
-      for (int i = 0; i < 8; i++) seed_out[i] = seed[i];
-    }
-  }
-}
-
-extern "C" int uwc_b3_scratch_words(uint64_t nbytes) {
-  const u64 nch = nbytes / 1024, nwg = (nch + B3_CHUNKS_PER_WG - 1) / B3_CHUNKS_PER_WG;
-  u64 words = nwg * 8, cnt = nwg;
-  while (cnt > B3_GROUP) {  // intermediate levels are kept after the first one
-    cnt = (cnt + B3_GROUP - 1) / B3_GROUP;
-    words += cnt * 8;
-  }
-  return words > 0x7fffffff ? -1 : (int)words;
-}
-
-extern "C" int uwc_b3_root_and_seed(const uint8_t* data, uint64_t nbytes, const uint32_t* key, const uint32_t* prefix,
-                                    const uint32_t* salt, uint32_t dim, uint32_t* root_out, uint32_t* seed_out,
-                                    uint32_t* scratch, uint64_t scratch_words, hipStream_t stream) {
-  if (!data || !key || !scratch) return uwc_fail("uwc_b3_root_and_seed: null data, key or scratch");
-  if (nbytes == 0 || nbytes % 1024) return uwc_fail("uwc_b3_root_and_seed: nbytes=%llu must be a positive multiple of 1024",
-                                                    (unsigned long long)nbytes);
-  if (((uintptr_t)data & 15u) != 0) return uwc_fail("uwc_b3_root_and_seed: data must be 16-byte aligned");
-  if (seed_out && (!prefix || !salt)) return uwc_fail("uwc_b3_root_and_seed: a seed needs prefix and salt");
-  const int need = uwc_b3_scratch_words(nbytes);
-  if (need < 0 || scratch_words < (u64)need)
-    return uwc_fail("uwc_b3_root_and_seed: scratch has %llu words, needs %d", (unsigned long long)scratch_words, need);
-  const u64 nch = nbytes / 1024;
-  int cnt = (int)((nch + B3_CHUNKS_PER_WG - 1) / B3_CHUNKS_PER_WG);
-  hipLaunchKernelGGL(b3_chunks_kernel, dim3(cnt), dim3(B3_CHUNKS_PER_WG), 0, stream, data, nch, key, scratch);
-  int st = uwc_launch_status("b3_chunks");
-  if (st) return st;
-  u32* cur = scratch;
-  while (cnt > B3_GROUP) {
-    const int groups = (cnt + B3_GROUP - 1) / B3_GROUP;
-    u32* nxt = cur + (u64)cnt * 8;
-    hipLaunchKernelGGL(b3_reduce_kernel, dim3(groups), dim3(512), 0, stream, cur, cnt, key, nxt, 0, nullptr, nullptr,
-                       0u, nullptr, nullptr);
-    if ((st = uwc_launch_status("b3_reduce"))) return st;
-    cur = nxt;
-    cnt = groups;
-  }
-  hipLaunchKernelGGL(b3_reduce_kernel, dim3(1), dim3(512), 0, stream, cur, cnt, key, nullptr, 1, prefix, salt, dim,
-                     root_out, seed_out);
-  return uwc_launch_status("b3_reduce_final");
-}
 
 // ------------------------------------------------------------------ noise generation
 // random_hash(index, label, key, prepend): keyed digest of msg with msg[prepend] = 1 + index,
