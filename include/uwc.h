@@ -95,6 +95,14 @@ int uwc_noise_uniform(int8_t* out, uint32_t nblocks, const uint32_t* label, cons
 int uwc_noise_perm(uint32_t* out, uint32_t k, uint32_t r, const uint32_t* label, const uint32_t* key,
                    hipStream_t stream);
 
+/* One launch for a nonce's noise: E (rows x r) as uwc_noise_uniform, P (k pairs) as
+ * uwc_noise_perm with the same label and key, St (r x k, optional) as uwc_proj_matrix(P), and
+ * zeroes zero0[0..n0) and zero1[0..n1) (n <= 256 each, pointers may be NULL with n = 0).
+ * Fuses ops.noise_uniform + ops.noise_perm + ops.proj_matrix of MinedWeight._forward
+ * (ops.py:328-336). */
+int uwc_nonce_noise(int8_t* E, int rows, int r, uint32_t* P, int k, int8_t* St, const uint32_t* label,
+                    const uint32_t* key, int32_t* zero0, int n0, int32_t* zero1, int n1, hipStream_t stream);
+
 /* For rows (multiple of 8) x k (multiple of 4) int8 src, each part optional (NULL = skip):
  *   dst = int8(src + E[row][Pn.first] - E[row][Pn.second]);
  *   projection src * S^T (S from Pp) in lmax base-128 limbs at corr[li][row][corr_off + j];
@@ -104,6 +112,26 @@ int uwc_noise_perm(uint32_t* out, uint32_t k, uint32_t r, const uint32_t* label,
 int uwc_noise_rows(const int8_t* src, int rows, int k, int r, const int8_t* E, const uint32_t* Pn, int8_t* dst,
                    const uint32_t* Pp, int8_t* corr, int corr_off, int ecopy_off, int32_t* maxabs, int lmax,
                    hipStream_t stream);
+
+/* St (r x k int8, k % 16 == 0) = the selection matrix of a noise permutation:
+ * St[j][l] = [P.first(l) == j] - [P.second(l) == j].
+ * Replaces ops.proj_matrix: ops.py:152-158, kernels.cu:397-404. */
+int uwc_proj_matrix(const uint32_t* P, int k, int r, int8_t* St, hipStream_t stream);
+
+/* Projection src * St^T (rows x r, exact int32 on the matrix cores) written as lmax balanced
+ * base-128 limbs to corr[li][row][corr_off + j] (corr_off 0 or r), max |projection| into *maxabs
+ * (atomic max; may be NULL). rows % 16 == 0, k % 64 == 0, r % 16 == 0, r <= 128.
+ * Replaces ops.project (torch._int_mm + proj_corr): ops.py:161-168, kernels.cu:374-395. */
+int uwc_project(const int8_t* src, int rows, int k, int r, const int8_t* St, int8_t* corr, int corr_off,
+                int32_t* maxabs, int lmax, hipStream_t stream);
+
+/* One pass over src: dst = int8(src + E[row][Pn.first] - E[row][Pn.second]); if St is given the
+ * projection src * St^T in limbs at corr_off (as uwc_project); E rows copied to
+ * corr[li][row][ecopy_off + j] if ecopy_off >= 0. Shapes as uwc_project; Pn and dst 16-byte aligned.
+ * Fuses noise_rows' noising (kernels.cu:303-345) with ops.project (ops.py:332-334). */
+int uwc_noise_project(const int8_t* src, int rows, int k, int r, const int8_t* E, const uint32_t* Pn, int8_t* dst,
+                      const int8_t* St, int8_t* corr, int corr_off, int ecopy_off, int32_t* maxabs, int lmax,
+                      hipStream_t stream);
 
 /* detrt quant_act per row of x (rows x k fp32): q = clamp(rint(fwht_bs(x) / s), -qmax, qmax),
  * s = max(max|y|, 1e-8) / qmax, scale = s * (1 / sqrt(bs)) if bs > 1 else s (bs a power of two

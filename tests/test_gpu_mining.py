@@ -186,3 +186,89 @@ def test_win_records_capped(dev):
     assert w[0] == (m // 8) * (n // 16)
     recs = w[1:].reshape(5, ops.WIN_WORDS)
     assert all(rr[0] % 64 < 8 and rr[1] % 2 == 0 for rr in recs)
+
+
+@pytest.mark.parametrize("r", [64, 128])
+def test_proj_matrix_project_and_noise_project(dev, r):
+    """The matrix-core projection path (proj_matrix + project / noise_project) against the oracle."""
+    ops = _ops()
+    rng = np.random.default_rng(31 + r)
+    rows, k = 96, 1536
+    A = rng.integers(-64, 65, size=(rows, k), dtype=np.int8)
+    E = rng.integers(-32, 32, size=(rows, r), dtype=np.int8)
+    Pn = O.perm_packed(O.SEED_LABEL_A, b"\x05" * 32, k, r)
+    Pp = O.perm_packed(O.SEED_LABEL_B, b"\x06" * 32, k, r)
+    pack = lambda P: torch.from_numpy(P.view(np.int32).copy()).to(dev)
+    St = ops.proj_matrix(pack(Pp), k, r)
+    S = np.zeros((r, k), np.int64)
+    S[(Pp & 0xFFFF).astype(np.int64), np.arange(k)] += 1
+    S[(Pp >> 16).astype(np.int64), np.arange(k)] -= 1
+    assert np.array_equal(St.cpu().numpy().astype(np.int64), S)
+    L = ops.limbs_for(k)
+    proj = O.project(A, Pp, r)
+    Ad = torch.from_numpy(A).to(dev)
+    corr = torch.zeros((L, rows, 2 * r), dtype=torch.int8, device=dev)
+    mx = torch.zeros(1, dtype=torch.int32, device=dev)
+    ops.project(Ad, St, corr, r, mx)
+    want = np.zeros((L, rows, 2 * r), np.int8)
+    O.write_limbs(proj, want, r)
+    assert np.array_equal(corr.cpu().numpy(), want)
+    assert int(mx.item()) == int(np.abs(proj).max())
+    # fused noising + projection + E copy
+    dst = torch.empty_like(Ad)
+    corr2 = torch.zeros_like(corr)
+    mx2 = torch.zeros(1, dtype=torch.int32, device=dev)
+    ops.noise_project(Ad, rows, k, r, E=torch.from_numpy(E).to(dev), Pn=pack(Pn), dst=dst, St=St, corr=corr2, corr_off=0,
+                      ecopy_off=r, maxabs=mx2)
+    assert np.array_equal(dst.cpu().numpy(), O.noise_apply(A, E, Pn))
+    want2 = np.zeros((L, rows, 2 * r), np.int8)
+    O.write_limbs(proj, want2, 0)
+    for li in range(L):
+        want2[li, :, r:] = E
+    assert np.array_equal(corr2.cpu().numpy(), want2)
+    assert int(mx2.item()) == int(np.abs(proj).max())
+
+
+def test_projection_paths_identical(dev):
+    """The matrix-core projections leave the mined forward bit-identical to the LDS-atomic path:
+    output, both correction tensors, maxabs and winning tiles (miner/ampere/tests/test_proj_gemm.py)."""
+    ops = _ops()
+    torch.manual_seed(0)
+    for (n, k, m) in ((512, 2048, 128), (256, 1024, 384)):
+        Bt = torch.randint(-64, 65, (n, k), dtype=torch.int8, device=dev)
+        A = torch.randint(-64, 65, (m, k), dtype=torch.int8, device=dev)
+        ones = torch.ones(m, dtype=torch.float32, device=dev)
+        res = {}
+        for mode in (False, True):
+            w = ops.MinedWeight(Bt=Bt, b_scale=torch.ones(n, device=dev), r=128, max_wins=4096)
+            w.setup_block(bytes(range(32)), O.bound_for_wins(m, n, 12))
+            out = w._forward(A, ones, None, ops.OUT_I32, True, None, mode)
+            b = w._buf(m)
+            res[mode] = (out.clone(), b["corrA"].clone(), w.corrB.clone(), b["maxabs"].clone(), sorted(w.winners(m)))
+            assert torch.equal(out.cpu(), (A.cpu().long() @ Bt.cpu().long().t()).int())
+        for name, x, y in zip(("out", "corrA", "corrB", "maxabs"), res[False][:4], res[True][:4]):
+            assert torch.equal(x, y), (n, k, m, name)
+        assert res[False][4] == res[True][4] and 0 < len(res[True][4])
+
+
+@pytest.mark.parametrize("rows,k,r", [(256, 4096, 64), (128, 1000, 128), (32, 8, 64)])
+def test_nonce_noise_fused_matches_oracle(dev, rows, k, r):
+    """One launch: E as uniform_matrix, P as perm_matrix, St as the dense selection matrix,
+    and both counter ranges zeroed."""
+    ops = _ops()
+    rng = np.random.default_rng(rows + k + r)
+    key = rng.bytes(32)
+    E = torch.empty((rows, r), dtype=torch.int8, device=dev)
+    P = torch.empty(k, dtype=torch.int32, device=dev)
+    St = torch.full((r, k), 5, dtype=torch.int8, device=dev)
+    z0 = torch.full((2,), 9, dtype=torch.int32, device=dev)
+    z1 = torch.full((3,), 9, dtype=torch.int32, device=dev)
+    ops.nonce_noise(E, P, k, r, ops.LABEL_A.to(dev), ops.words(key), St=St, zero0=z0, zero1=z1[:1])
+    assert np.array_equal(E.cpu().numpy(), O.uniform_matrix(O.SEED_LABEL_A, key, rows, r))
+    Pw = O.perm_packed(O.SEED_LABEL_A, key, k, r)
+    assert np.array_equal(_u32(P), Pw)
+    S = np.zeros((r, k), np.int64)
+    S[(Pw & 0xFFFF).astype(np.int64), np.arange(k)] += 1
+    S[(Pw >> 16).astype(np.int64), np.arange(k)] -= 1
+    assert np.array_equal(St.cpu().numpy().astype(np.int64), S)
+    assert z0.cpu().tolist() == [0, 0] and z1.cpu().tolist() == [0, 9, 9]

@@ -249,3 +249,76 @@ extern "C" int uwc_b3_root_and_seed(const uint8_t* data, uint64_t nbytes, const 
                      root_out, seed_out);
   return uwc_launch_status("b3_reduce_final");
 }
+
+// ------------------------------------------------------------------ per-nonce noise in one launch
+// E (rows x r, the uniform_matrix), P (k pairs) and optionally St (the r x k selection matrix
+// of P) from one keyed random_hash per quad (reference.py:67-93, kernels.cu:246-301,
+// ops.py:152-158), and zeroes two counter ranges, in a single latency-bound launch instead of
+// four. Quads [0, rows*r/32) make E blocks; the next ceil(k/8) quads make 8 pairs each and
+// write St's columns for them in full (so St needs no clearing).
+__global__ void __launch_bounds__(256) nonce_noise_kernel(i8* __restrict__ E, u32 eblocks, u32* __restrict__ P, u32 k,
+                                                          u32 r, i8* __restrict__ St, const u32* __restrict__ label,
+                                                          const u32* __restrict__ key, i32* __restrict__ z0, int n0,
+                                                          i32* __restrict__ z1, int n1) {
+  __shared__ __attribute__((aligned(16))) u8 msgs[64 * B3_QSTRIDE];
+  const int tid = threadIdx.x, q = tid & 3, lq = tid >> 2;
+  if (blockIdx.x == 0) {
+    if (z0 && tid < n0) z0[tid] = 0;
+    if (z1 && tid < n1) z1[tid] = 0;
+  }
+  const u32 quad = blockIdx.x * 64 + lq;
+  const u32 pblocks = (k + 7) / 8;
+  const bool is_e = quad < eblocks, is_p = !is_e && quad < eblocks + pblocks;
+  const u32 index = is_e ? quad : quad - eblocks;
+  const int prepend = is_e ? 0 : 1;
+  // message words 4q..4q+3 of msg: 0 except word `prepend` = 1 + index; words 8..15 = label
+  u32* mw = reinterpret_cast<u32*>(msgs + lq * B3_QSTRIDE);
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int w = 4 * q + i;
+    mw[w] = w >= 8 ? label[w - 8] : (w == prepend ? 1u + index : 0u);
+  }
+  __builtin_amdgcn_wave_barrier();
+  const QuadMsgOffsets off = quad_offsets(q);
+  u32 lo, hi;
+  quad_compress(msgs + lq * B3_QSTRIDE, off, q, key[q], key[4 + q], 0, 64,
+                B3_CHUNK_START | B3_CHUNK_END | B3_ROOT | B3_KEYED, lo, hi);
+  if (is_e) {
+    // digest bytes -> (y & 63) - 32: the 6-bit value (y & 63) ^ 32 sign-extended per byte
+    u32 z = (lo & 0x3F3F3F3Fu) ^ 0x20202020u, s = z & 0x20202020u;
+    const u32 elo = z | (s << 1) | (s << 2);
+    z = (hi & 0x3F3F3F3Fu) ^ 0x20202020u; s = z & 0x20202020u;
+    const u32 ehi = z | (s << 1) | (s << 2);
+    u32* dst = reinterpret_cast<u32*>(E + (u64)index * 32);
+    dst[q] = elo;
+    dst[4 + q] = ehi;
+  } else if (is_p) {
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const u32 l = index * 8 + q + 4 * h;
+      if (l < k) {
+        const u32 u = h ? hi : lo, first = u & (r - 1);
+        const u32 second = first ^ (1u + __umulhi(r - 1, u));
+        P[l] = first | (second << 16);
+        if (St)
+          for (u32 j = 0; j < r; j++) St[(u64)j * k + l] = (i8)((int)(first == j) - (int)(second == j));
+      }
+    }
+  }
+}
+
+extern "C" int uwc_nonce_noise(int8_t* E, int rows, int r, uint32_t* P, int k, int8_t* St, const uint32_t* label,
+                               const uint32_t* key, int32_t* zero0, int n0, int32_t* zero1, int n1, hipStream_t stream) {
+  if (!E || !P || !label || !key || rows < 0 || k < 0) return uwc_fail("uwc_nonce_noise: null or negative arguments");
+  if (r < 2 || r > 65536 || (r & (r - 1))) return uwc_fail("uwc_nonce_noise: r=%d must be a power of two", r);
+  if (((u64)rows * r) % 32) return uwc_fail("uwc_nonce_noise: rows * r must be a multiple of 32");
+  if (((uintptr_t)E & 3u)) return uwc_fail("uwc_nonce_noise: E must be 4-byte aligned");
+  if (n0 < 0 || n1 < 0 || n0 > 256 || n1 > 256 || (n0 && !zero0) || (n1 && !zero1))
+    return uwc_fail("uwc_nonce_noise: zero ranges must be 0..256 words with pointers");
+  const u64 quads = (u64)rows * r / 32 + ((u64)k + 7) / 8;
+  const u64 blocks = quads ? (quads + 63) / 64 : 1;
+  if (blocks > 0x7fffffff) return uwc_fail("uwc_nonce_noise: too large");
+  hipLaunchKernelGGL(nonce_noise_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, E, (u32)((u64)rows * r / 32), P,
+                     (u32)k, (u32)r, St, label, key, zero0, n0, zero1, n1);
+  return uwc_launch_status("nonce_noise");
+}

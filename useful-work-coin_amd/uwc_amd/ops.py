@@ -113,11 +113,47 @@ def noise_perm(out: torch.Tensor, k: int, r: int, label: torch.Tensor, key: torc
     _lib.call("uwc_noise_perm", _p(out), k, r, _p(label), _p(key), _stream())
 
 
+def nonce_noise(E: torch.Tensor, P: torch.Tensor, k: int, r: int, label: torch.Tensor, key: torch.Tensor,
+                St: torch.Tensor | None = None, zero0=None, zero1=None):
+    """noise_uniform(E) + noise_perm(P) + proj_matrix(P) -> St in one launch; zeroes zero0 and zero1."""
+    rows = E.shape[0]
+    _check(E.shape[1] == r and P.numel() >= k, "nonce_noise: E must be rows x r and P hold k words")
+    n0 = zero0.numel() if zero0 is not None else 0
+    n1 = zero1.numel() if zero1 is not None else 0
+    _lib.call("uwc_nonce_noise", _p(E), rows, r, _p(P), k, _p(St), _p(label), _p(key), _p(zero0), n0, _p(zero1), n1,
+              _stream())
+
+
 def noise_rows(src, rows, k, r, *, E=None, Pn=None, dst=None, Pp=None, corr=None, corr_off=-1, ecopy_off=-1,
                maxabs=None, lmax=None):
     lmax = corr.shape[0] if corr is not None else 0
     _check(rows % 8 == 0 and k % 4 == 0, f"noise_rows: rows={rows} % 8 and k={k} % 4 must be 0")
     _lib.call("uwc_noise_rows", _p(src), rows, k, r, _p(E), _p(Pn), _p(dst), _p(Pp), _p(corr), corr_off, ecopy_off,
+              _p(maxabs), lmax, _stream())
+
+
+# ------------------------------------------------------------------ projections as int8 GEMMs
+def proj_matrix(P: torch.Tensor, k: int, r: int, St: torch.Tensor | None = None) -> torch.Tensor:
+    """S^T for a noise permutation P (k entries, +index in the low 16 bits, -index in the high 16):
+    r x k int8 with S^T[lo(l), l] += 1 and S^T[hi(l), l] -= 1, so src @ S = noise_rows' projection."""
+    St = torch.empty((r, k), dtype=torch.int8, device=P.device) if St is None else St
+    _lib.call("uwc_proj_matrix", _p(P), k, r, _p(St), _stream())
+    return St
+
+
+def project(src: torch.Tensor, St: torch.Tensor, corr: torch.Tensor, corr_off: int, maxabs: torch.Tensor):
+    """noise_rows' projection part (corr limbs at corr_off, maxabs) with the sum on the matrix cores:
+    exact, since every term is an integer and int8 x int8 products accumulate exactly in int32."""
+    rows, k = src.shape
+    r = St.shape[0]
+    _check(src.is_contiguous() and St.is_contiguous(), "project: src and St must be contiguous")
+    _lib.call("uwc_project", _p(src), rows, k, r, _p(St), _p(corr), corr_off, _p(maxabs), corr.shape[0], _stream())
+
+
+def noise_project(src, rows, k, r, *, E, Pn, dst, St=None, corr=None, corr_off=-1, ecopy_off=-1, maxabs=None):
+    """One pass over src: noising (dst) + optional projection with St into limbs + optional E copy."""
+    lmax = corr.shape[0] if corr is not None else 0
+    _lib.call("uwc_noise_project", _p(src), rows, k, r, _p(E), _p(Pn), _p(dst), _p(St), _p(corr), corr_off, ecopy_off,
               _p(maxabs), lmax, _stream())
 
 
@@ -171,6 +207,7 @@ class MinedWeight:
     PB: torch.Tensor | None = None
     EBRt: torch.Tensor | None = None
     corrB: torch.Tensor | None = None
+    SBt: torch.Tensor | None = None
     _bufs: dict = field(default_factory=dict)
 
     @property
@@ -203,7 +240,11 @@ class MinedWeight:
         if self.BpEBt is None:
             self.BpEBt = torch.empty((n, k), dtype=torch.int8, device=dev)
             self.corrB = torch.zeros((limbs_for(k), n, 2 * r), dtype=torch.int8, device=dev)
-        noise_rows(Bt, n, k, r, E=self.EBRt, Pn=self.PB, dst=self.BpEBt, corr=self.corrB, ecopy_off=0)
+        if n % 16 == 0 and k % 64 == 0 and r <= 128:
+            noise_project(Bt, n, k, r, E=self.EBRt, Pn=self.PB, dst=self.BpEBt, corr=self.corrB, ecopy_off=0)
+        else:
+            noise_rows(Bt, n, k, r, E=self.EBRt, Pn=self.PB, dst=self.BpEBt, corr=self.corrB, ecopy_off=0)
+        self.SBt = proj_matrix(self.PB, k, r)
         del Bt
 
     def _buf(self, m: int):
@@ -218,6 +259,7 @@ class MinedWeight:
                 EAL=torch.empty((m, r), dtype=torch.int8, device=dev),
                 PA=torch.empty(k, dtype=torch.int32, device=dev),
                 ApEA=torch.empty((m, k), dtype=torch.int8, device=dev),
+                SA=torch.empty((r, k), dtype=torch.int8, device=dev),
                 corrA=torch.zeros((limbs_for(k), m, 2 * r), dtype=torch.int8, device=dev),
                 maxabs=torch.zeros(2, dtype=torch.int32, device=dev),
                 scratch=torch.empty(max(8, b3_scratch_words(m * k)), dtype=torch.int32, device=dev),
@@ -232,7 +274,7 @@ class MinedWeight:
         """A: m x k int8 (values in [-64, 64]). Returns A @ Bt^T scaled (bf16/f32) or exact int32."""
         return self._forward(A, a_scale, out, out_mode, hash_tiles)
 
-    def _forward(self, A, a_scale, out, out_mode, hash_tiles, cfg=None, proj=None, dump=None):
+    def _forward(self, A, a_scale, out, out_mode, hash_tiles, cfg=None, proj=True, dump=None):
         m, k = A.shape
         n, r = self.n, self.r
         _check(k == self.k and m % BM == 0, f"MinedWeight.forward: A is {tuple(A.shape)}, need m % {BM} == 0, k == {self.k}")
@@ -246,15 +288,23 @@ class MinedWeight:
         # 1. commit to A, derive a_seed = H(b_seed || bind_a(root_A, m))
         b3_root_and_seed(A.view(-1), self.job_key, prefix=self.b_seed, salt=c["SALT_A"], dim=m,
                          seed_out=b["a_seed"], scratch=b["scratch"])
-        # 2. A-side noise (the same launch zeroes maxabs); the win counter restarts at 0
-        noise_uniform(b["EAL"], c["LABEL_A"], b["a_seed"], zero_me=b["maxabs"], zero_n=2)
-        b["wins"][:1].zero_()
-        noise_perm(b["PA"], k, r, c["LABEL_A"], b["a_seed"])
+        # 2. A-side noise E_AL, P_A (and its selection matrix); the same launch zeroes maxabs and
+        #    the win counter
         # 3. ApEA = A + EAL*P_A ; X = A * P_B^T (limbs) ; EAL copy
-        noise_rows(A, m, k, r, E=b["EAL"], Pn=b["PA"], dst=b["ApEA"], Pp=self.PB, corr=b["corrA"], corr_off=0,
-                   ecopy_off=r, maxabs=b["maxabs"][0:1])
         # 4. Y = BpEBt * P_A^T (limbs)
-        noise_rows(self.BpEBt, n, k, r, Pp=b["PA"], corr=self.corrB, corr_off=r, maxabs=b["maxabs"][1:2])
+        if proj:  # projections on the matrix cores (the reference's PROJ_GEMM path)
+            nonce_noise(b["EAL"], b["PA"], k, r, c["LABEL_A"], b["a_seed"], St=b["SA"], zero0=b["maxabs"],
+                        zero1=b["wins"][:1])
+            noise_project(A, m, k, r, E=b["EAL"], Pn=b["PA"], dst=b["ApEA"], St=self.SBt, corr=b["corrA"], corr_off=0,
+                          ecopy_off=r, maxabs=b["maxabs"][0:1])
+            project(self.BpEBt, b["SA"], self.corrB, r, b["maxabs"][1:2])
+        else:     # projections by LDS atomics (noise_rows with Pp)
+            noise_uniform(b["EAL"], c["LABEL_A"], b["a_seed"], zero_me=b["maxabs"], zero_n=2)
+            b["wins"][:1].zero_()
+            noise_perm(b["PA"], k, r, c["LABEL_A"], b["a_seed"])
+            noise_rows(A, m, k, r, E=b["EAL"], Pn=b["PA"], dst=b["ApEA"], Pp=self.PB, corr=b["corrA"], corr_off=0,
+                       ecopy_off=r, maxabs=b["maxabs"][0:1])
+            noise_rows(self.BpEBt, n, k, r, Pp=b["PA"], corr=self.corrB, corr_off=r, maxabs=b["maxabs"][1:2])
         # 5. noisy GEMM: hash every tile, denoise exactly, scale
         gemm(b["ApEA"], self.BpEBt, r=r, flags=(FLAG_HASH if hash_tiles else 0) | FLAG_DENOISE,
              corrA=b["corrA"], corrB=self.corrB, maxabs=b["maxabs"], key=b["a_seed"], target=self.target,
@@ -273,9 +323,11 @@ class MinedWeight:
         c = consts(dev)
         b3_root_and_seed(A.view(-1), self.job_key, prefix=self.b_seed, salt=c["SALT_A"], dim=m,
                          seed_out=b["a_seed"], scratch=b["scratch"])
-        noise_uniform(b["EAL"], c["LABEL_A"], b["a_seed"], zero_me=b["wins"], zero_n=1)
-        noise_perm(b["PA"], k, r, c["LABEL_A"], b["a_seed"])
-        noise_rows(A, m, k, r, E=b["EAL"], Pn=b["PA"], dst=b["ApEA"])
+        nonce_noise(b["EAL"], b["PA"], k, r, c["LABEL_A"], b["a_seed"], zero0=b["wins"][:1])
+        if m % 16 == 0 and k % 64 == 0 and r <= 128:
+            noise_project(A, m, k, r, E=b["EAL"], Pn=b["PA"], dst=b["ApEA"])
+        else:
+            noise_rows(A, m, k, r, E=b["EAL"], Pn=b["PA"], dst=b["ApEA"])
         gemm(b["ApEA"], self.BpEBt, r=r, flags=FLAG_HASH, key=b["a_seed"], target=self.target, wins=b["wins"],
              max_wins=self.max_wins, dump=dump)
 
