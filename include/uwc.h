@@ -29,6 +29,7 @@ extern "C" {
  * fused detrt dequant epilogue fmul(fmul(f32(acc), a_scale[i]), b_scale[j])). */
 #define UWC_FLAG_HASH 1
 #define UWC_FLAG_DENOISE 2
+#define UWC_FLAG_TILE128 0x100  /* force the 128 x 128 tiling (identical results) */
 #define UWC_OUT_NONE 0
 #define UWC_OUT_I32 1
 #define UWC_OUT_BF16 2

@@ -272,3 +272,37 @@ def test_nonce_noise_fused_matches_oracle(dev, rows, k, r):
     S[(Pw >> 16).astype(np.int64), np.arange(k)] -= 1
     assert np.array_equal(St.cpu().numpy().astype(np.int64), S)
     assert z0.cpu().tolist() == [0, 0] and z1.cpu().tolist() == [0, 9, 9]
+
+
+@pytest.mark.parametrize("m,n,k,r", [(256, 256, 1024, 64), (512, 768, 2048, 128), (256, 512, 1280, 64)])
+def test_tile_configs_identical(dev, m, n, k, r):
+    """Every GEMM tiling gives the same mined result: exact output, the same tile messages and
+    digests, the same winners (miner/ampere/tests/test_gemm_cfgs.py)."""
+    ops = _ops()
+    rng = np.random.default_rng(m * 3 + n + k + r)
+    A = torch.from_numpy(rng.integers(-64, 65, size=(m, k), dtype=np.int8)).to(dev)
+    Bt = torch.from_numpy(rng.integers(-64, 65, size=(n, k), dtype=np.int8)).to(dev)
+    w = ops.MinedWeight(Bt=Bt, b_scale=torch.ones(n, device=dev), r=r, max_wins=4096)
+    w.setup_block(rng.bytes(32), O.bound_for_wins(m, n, 12))
+    ones = torch.ones(m, dtype=torch.float32, device=dev)
+    ref = torch.from_numpy(O.igemm(A.cpu().numpy(), Bt.cpu().numpy()))
+    got = {}
+    for cfg in ops.CONFIGS:
+        dump = torch.zeros((m // 64) * 8 * (n // 64) * 4 * ops.DUMP_WORDS, dtype=torch.int32, device=dev)
+        out = w._forward(A, ones, None, ops.OUT_I32, True, cfg, True, dump=dump)
+        assert torch.equal(out.cpu(), ref), (cfg, "output")
+        got[cfg] = (sorted(w.winners(m)), dump.cpu())
+    base = got["128x128"]
+    assert 0 < len(base[0]) < w.max_wins
+    for cfg, (wins, dump) in got.items():
+        assert wins == base[0] and torch.equal(dump, base[1]), cfg
+
+
+@pytest.mark.parametrize("m,n,k", [(256, 256, 64), (512, 256, 4096), (2048, 4096, 2048)])
+def test_large_tile_plain_gemm(dev, m, n, k):
+    ops, = (_ops(),)
+    rng = np.random.default_rng(m + 7 * n + k)
+    A = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, size=(n, k), dtype=np.int8)
+    C = ops.igemm_i32(torch.from_numpy(A).to(dev), torch.from_numpy(B).to(dev))
+    assert np.array_equal(C.cpu().numpy(), O.igemm(A, B))

@@ -33,6 +33,7 @@
 
 #define FLAG_HASH 1
 #define FLAG_DENOISE 2
+#define FLAG_TILE128 0x100  // force the 128 x 128 kernel (same results; for tests and small shapes)
 #define OUT_NONE 0
 #define OUT_I32 1
 #define OUT_BF16 2
@@ -312,6 +313,11 @@ __global__ void __launch_bounds__(G_THREADS) noisy_gemm_kernel(GemmParams p) {
   }
 }
 
+int uwc_noisy_gemm256(const int8_t* A, const int8_t* B, int m, int n, int k, int r, const int8_t* corrA,
+                      const int8_t* corrB, const int32_t* maxabs, int lmax, const uint32_t* key,
+                      const uint32_t* target, uint32_t* wins, int max_wins, const float* a_scale, const float* b_scale,
+                      void* out, int out_mode, int flags, uint32_t* tile_dump, hipStream_t stream);
+
 template <bool H, bool D>
 static void launch_out(int out_mode, dim3 grid, hipStream_t s, const GemmParams& p) {
   switch (out_mode) {
@@ -330,7 +336,7 @@ extern "C" int uwc_noisy_gemm(const int8_t* A, const int8_t* B, int m, int n, in
                               const float* b_scale, void* out, int out_mode, int flags, uint32_t* tile_dump,
                               hipStream_t stream) {
   const bool hash = flags & FLAG_HASH, denoise = flags & FLAG_DENOISE;
-  if (flags & ~(FLAG_HASH | FLAG_DENOISE)) return uwc_fail("uwc_noisy_gemm: unknown flags %d", flags);
+  if (flags & ~(FLAG_HASH | FLAG_DENOISE | FLAG_TILE128)) return uwc_fail("uwc_noisy_gemm: unknown flags %d", flags);
   if (!A || !B || m <= 0 || n <= 0 || k <= 0) return uwc_fail("uwc_noisy_gemm: empty or null operands (m=%d n=%d k=%d)", m, n, k);
   if (k % G_BK) return uwc_fail("uwc_noisy_gemm: k=%d must be a multiple of %d", k, G_BK);
   if (!aligned16(A) || !aligned16(B)) return uwc_fail("uwc_noisy_gemm: A and B must be 16-byte aligned");
@@ -351,6 +357,9 @@ extern "C" int uwc_noisy_gemm(const int8_t* A, const int8_t* B, int m, int n, in
     if (lmax < 1 || lmax > 4) return uwc_fail("uwc_noisy_gemm: lmax=%d outside 1..4", lmax);
     if (!aligned16(corrA) || !aligned16(corrB)) return uwc_fail("uwc_noisy_gemm: corrA/corrB must be 16-byte aligned");
   }
+  if (m % 256 == 0 && n % 256 == 0 && !(flags & FLAG_TILE128))
+    return uwc_noisy_gemm256(A, B, m, n, k, r, corrA, corrB, maxabs, lmax, key, target, wins, max_wins, a_scale,
+                             b_scale, out, out_mode, flags & ~FLAG_TILE128, tile_dump, stream);
   GemmParams p{A, B, m, n, k, r, corrA, corrB, maxabs, lmax, key, target, wins, max_wins, a_scale, b_scale, out,
                hash ? tile_dump : nullptr};
   const dim3 grid(((m + G_BM - 1) / G_BM) * ((n + G_BN - 1) / G_BN));

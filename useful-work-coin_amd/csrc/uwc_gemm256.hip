@@ -1,0 +1,376 @@
+// gfx950 noisy GEMM, large-tile variant for m % 256 == 0 and n % 256 == 0: the same contract
+// as noisy_gemm_kernel (uwc_gemm.hip; miner/ampere/uwc_ampere/kernels.cu:482-715), built for
+// throughput at the mining and detrt-prefill shapes.
+//
+//   * Workgroup tile 256 x 256, k step 64, 8 wave64s in 2 (M) x 4 (N); each wave owns 128 x 64
+//     = two consensus 64 x 64 hash blocks, as 4 x 2 v_mfma_i32_32x32x32_i8 blocks
+//     (128 int32 accumulators per lane, in VGPRs so the fold reads them directly).
+//   * Operand tiles go HBM -> LDS with global_load_lds_dwordx4 (no VGPR staging) into a 4-stage
+//     ring, three k steps in flight; one barrier per k step.
+//   * LDS rows are 64 bytes; the 16-byte chunk c of row r sits at chunk c ^ f(r),
+//     f(r) = ((r >> 1) ^ (r >> 2)) & 3, so the 32-row fragment reads are conflict-free with
+//     32 or 64 banks. The swizzle is applied on the global side (each lane of a DMA writes a
+//     fixed LDS slot and fetches the bytes that belong there).
+//   * Transcript fold every r along k: a lane XORs its accumulators into 8 partials (hash block
+//     x g & 3), then a reduce-scatter over lane bits 0, 3, 4 (DPP quad_perm, DPP row_ror:8,
+//     ds_swizzle) leaves every lane with the full tile XOR of exactly one tile, which it folds
+//     into that tile's 16-word message (message slots are static: the fold loop is unrolled
+//     over the 16 slots). After the k loop every lane digests its own tile.
+//   * Denoise in two passes over the wave's two 32-column halves (a 64-register Horner
+//     accumulator), streaming [X_li | EAL] and [EBRt | Y_li] through the same ring.
+#include "uwc_common.h"
+
+#define W_BM 256
+#define W_BN 256
+#define W_BK 64
+#define W_STAGES 4
+#define W_THREADS 512
+#define W_TILE (W_BM * W_BK)                 // bytes of one operand tile
+#define W_STAGE (2 * W_TILE)                 // A + B
+#define W_LDS (W_STAGES * W_STAGE)           // 128 KiB
+#define W_SEGS_PER_WAVE 4                    // 1 KiB DMA segments per wave per k step
+
+#define FLAG_HASH 1
+#define FLAG_DENOISE 2
+#define OUT_NONE 0
+#define OUT_I32 1
+#define OUT_BF16 2
+#define OUT_F32 3
+#define WIN_WORDS 10
+#define DUMP_WORDS 24
+
+struct Gemm256Params {
+  const i8* A;
+  const i8* B;
+  int m, n, k, r;
+  const i8* corrA;
+  const i8* corrB;
+  const i32* maxabs;
+  int lmax;
+  const u32* key;
+  const u32* target;
+  u32* wins;
+  int max_wins;
+  const float* a_scale;
+  const float* b_scale;
+  void* out;
+  u32* dump;
+};
+
+typedef const void __attribute__((address_space(1)))* gptr_t;
+typedef void __attribute__((address_space(3)))* lptr_t;
+
+// Per-lane DMA source: lane i of a segment fills LDS bytes [16 i, 16 i + 16) of it, i.e. row
+// 16 s + i / 4 (s = the segment) at physical chunk i & 3, logical chunk (i & 3) ^ swz(i / 4)
+// (swz of a row depends only on its low 4 bits).
+struct DmaLane {
+  const i8* a;  // A + (bm0 + lane / 4) * lda + chunk * 16
+  const i8* b;
+};
+
+__device__ __forceinline__ DmaLane dma_lane(const i8* A, long lda, const i8* B, long ldb, int bm0, int bn0, int lane) {
+  const int rin = lane >> 2, c = (lane & 3) ^ ((((rin >> 1) ^ (rin >> 2))) & 3);
+  return DmaLane{A + (long)(bm0 + rin) * lda + c * 16, B + (long)(bn0 + rin) * ldb + c * 16};
+}
+
+// Issue this wave's 4 DMA segments of one k step: segments 2w, 2w+1 of A and of B.
+__device__ __forceinline__ void dma_step(u8* stage, const DmaLane& d, long lda, long ldb, long k0, int wave) {
+#pragma unroll
+  for (int t = 0; t < 2; t++) {
+    const int s = 2 * wave + t;
+    __builtin_amdgcn_global_load_lds((gptr_t)(d.a + 16L * s * lda + k0), (lptr_t)(stage + s * 1024), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((gptr_t)(d.b + 16L * s * ldb + k0), (lptr_t)(stage + W_TILE + s * 1024), 16, 0, 0);
+  }
+}
+
+// Wait until at most `younger` of this wave's k steps are still loading, then barrier.
+__device__ __forceinline__ void wait_step(int younger) {
+  if (younger >= 2) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  else if (younger == 1) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+}
+
+__device__ __forceinline__ v4i lds16(const u8* p) { return *reinterpret_cast<const v4i*>(p); }
+
+// Per-lane fragment offset within a tile for k32 pass kp: row (lane & 31) of the 32-row block,
+// logical chunk 2 kp + (lane >> 5). Block row bases are multiples of 32, which leave swz alone.
+__device__ __forceinline__ int frag_off(int lane, int kp) {
+  const int r = lane & 31, c = 2 * kp + (lane >> 5);
+  return r * 64 + ((c ^ (((r >> 1) ^ (r >> 2)) & 3)) << 4);
+}
+
+// One k step of MFMA work for the wave's 128 x 64 block from a stage.
+__device__ __forceinline__ void step_mma(v16i acc[4][2], const u8* stage, int wm, int wn, const int fo[2]) {
+  const u8* sa = stage + wm * 128 * 64;
+  const u8* sb = stage + W_TILE + wn * 64 * 64;
+#pragma unroll
+  for (int kp = 0; kp < 2; kp++) {
+    v4i a[4], b[2];
+#pragma unroll
+    for (int mb = 0; mb < 4; mb++) a[mb] = lds16(sa + mb * 32 * 64 + fo[kp]);
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++) b[nb] = lds16(sb + nb * 32 * 64 + fo[kp]);
+#pragma unroll
+    for (int mb = 0; mb < 4; mb++)
+#pragma unroll
+      for (int nb = 0; nb < 2; nb++) acc[mb][nb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[mb], b[nb], acc[mb][nb], 0, 0, 0);
+  }
+}
+
+// Denoise k step for one quarter of the wave's block: M blocks 2h, 2h+1 of column half nb.
+__device__ __forceinline__ void step_mma_quarter(v16i tmp[2], const u8* stage, int wm, int wn, int h, int nb,
+                                                 const int fo[2]) {
+  const u8* sa = stage + (wm * 128 + h * 64) * 64;
+  const u8* sb = stage + W_TILE + (wn * 64 + nb * 32) * 64;
+#pragma unroll
+  for (int kp = 0; kp < 2; kp++) {
+    const v4i a0 = lds16(sa + fo[kp]), a1 = lds16(sa + 32 * 64 + fo[kp]), b = lds16(sb + fo[kp]);
+    tmp[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b, tmp[0], 0, 0, 0);
+    tmp[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b, tmp[1], 0, 0, 0);
+  }
+}
+
+__device__ __forceinline__ u32 xor3(u32 a, u32 b, u32 c) { return a ^ b ^ c; }
+__device__ __forceinline__ u32 rotl13(u32 x) { return __builtin_amdgcn_alignbit(x, x, 19); }
+
+template <int CTRL>
+__device__ __forceinline__ u32 dpp(u32 x) {
+  return (u32)__builtin_amdgcn_mov_dpp((int)x, CTRL, 0xF, 0xF, false);
+}
+
+// Tile XOR of the one tile this lane owns after the reduce-scatter (see the file comment).
+__device__ __forceinline__ u32 fold_owned(const v16i acc[4][2], int lane) {
+  u32 x[8];
+#pragma unroll
+  for (int hb = 0; hb < 2; hb++)
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+      u32 v = 0;
+#pragma unroll
+      for (int mb = 2 * hb; mb < 2 * hb + 2; mb++)
+#pragma unroll
+        for (int nb = 0; nb < 2; nb++)
+          v = xor3(v, (u32)acc[mb][nb][p] ^ (u32)acc[mb][nb][4 + p], (u32)acc[mb][nb][8 + p] ^ (u32)acc[mb][nb][12 + p]);
+      x[hb * 4 + p] = v;
+    }
+  const bool b0 = lane & 1, b3 = (lane >> 3) & 1, b4 = (lane >> 4) & 1;
+  u32 y[4], z[2];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {  // lane bit 0: keep hash block b0
+    const u32 keep = b0 ? x[4 + i] : x[i], send = b0 ? x[i] : x[4 + i];
+    y[i] = keep ^ dpp<0xB1>(send);  // quad_perm [1,0,3,2]: partner lane ^ 1
+  }
+#pragma unroll
+  for (int j = 0; j < 2; j++) {  // lane bit 3: keep g & 3 in {2 b3, 2 b3 + 1}
+    const u32 keep = b3 ? y[2 + j] : y[j], send = b3 ? y[j] : y[2 + j];
+    z[j] = keep ^ dpp<0x128>(send);  // row_ror:8 within a 16-lane row: partner lane ^ 8
+  }
+  const u32 keep = b4 ? z[1] : z[0], send = b4 ? z[0] : z[1];
+  return keep ^ (u32)__builtin_amdgcn_ds_swizzle((int)send, 0x401F);  // partner lane ^ 16
+}
+
+__device__ __forceinline__ u32 bf16_rne(float f) {
+  const u32 u = __float_as_uint(f);
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+// Workgroup id -> tile: XCD-contiguous runs (ids are dispatched round-robin over 8 XCDs),
+// rastered in groups of 4 tile rows.
+__device__ __forceinline__ void tile256(int m, int n, int& bm0, int& bn0) {
+  const int npm = m / W_BM, npn = n / W_BN, total = npm * npn;
+  int pid = blockIdx.x;
+  if ((total & 7) == 0) pid = (pid & 7) * (total >> 3) + (pid >> 3);
+  constexpr int GROUP_M = 4;
+  const int grp = GROUP_M * npn, gid = pid / grp, first = gid * GROUP_M;
+  const int gsz = min(npm - first, GROUP_M), in = pid - gid * grp;
+  bm0 = (first + in % gsz) * W_BM;
+  bn0 = (in / gsz) * W_BN;
+}
+
+template <bool HASH, bool DENOISE, int OUT>
+__global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params p) {
+  extern __shared__ __attribute__((aligned(1024))) u8 wsm[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave >> 2, wn = wave & 3;
+  int bm0, bn0;
+  tile256(p.m, p.n, bm0, bn0);
+  const long k = p.k;
+  const int KT = p.k / W_BK;
+
+  v16i acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++) acc[i][j] = v16i{};
+
+  const int fo[2] = {frag_off(lane, 0), frag_off(lane, 1)};
+  const DmaLane dl = dma_lane(p.A, k, p.B, k, bm0, bn0, lane);
+  // prologue: k steps 0..2 in flight
+#pragma unroll
+  for (int s = 0; s < W_STAGES - 1; s++)
+    if (s < KT) dma_step(wsm + s * W_STAGE, dl, k, k, (long)s * W_BK, wave);
+
+  auto kstep = [&](int kt) {
+    wait_step(min(KT - 1 - kt, W_STAGES - 2));
+    if (kt + W_STAGES - 1 < KT)
+      dma_step(wsm + ((kt + W_STAGES - 1) % W_STAGES) * W_STAGE, dl, k, k, (long)(kt + W_STAGES - 1) * W_BK, wave);
+    step_mma(acc, wsm + (kt % W_STAGES) * W_STAGE, wm, wn, fo);
+  };
+
+  if constexpr (HASH) {
+    u32 msg[16];
+#pragma unroll
+    for (int w = 0; w < 16; w++) msg[w] = 0;
+    const int tpc = p.r / W_BK, nchunks = p.k / p.r;
+    int kt = 0;
+    for (int c0 = 0; c0 < nchunks; c0 += 16) {
+#pragma unroll
+      for (int s = 0; s < 16; s++) {
+        if (c0 + s < nchunks) {
+          for (int i = 0; i < tpc; i++, kt++) kstep(kt);
+          msg[s] = rotl13(msg[s]) ^ fold_owned(acc, lane);
+        }
+      }
+    }
+    // every lane digests the tile it owns: hash block b0, g = 4 (lane >> 5) + 2 b3 + b4, t
+    const int hb = lane & 1, g = 4 * (lane >> 5) + 2 * ((lane >> 3) & 1) + ((lane >> 4) & 1), t = (lane >> 1) & 3;
+    u32 key[8], h[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) key[i] = p.key[i];
+    b3_keyed64(key, msg, h);
+    const int row = bm0 + wm * 128 + hb * 64 + g, col = bn0 + wn * 64 + 2 * t;
+    if (p.dump) {
+      const long NB = p.n / 64;
+      u32* d = p.dump + ((((long)(row >> 6) * 8 + g) * NB + (col >> 6)) * 4 + t) * DUMP_WORDS;
+#pragma unroll
+      for (int w = 0; w < 16; w++) d[w] = msg[w];
+#pragma unroll
+      for (int w = 0; w < 8; w++) d[16 + w] = h[w];
+    }
+    if (p.wins && u256_le(h, p.target)) {
+      const u32 slot = atomicAdd(p.wins, 1u);
+      if (slot < (u32)p.max_wins) {
+        u32* rec = p.wins + 1 + slot * WIN_WORDS;
+        rec[0] = row;
+        rec[1] = col;
+#pragma unroll
+        for (int i = 0; i < 8; i++) rec[2 + i] = h[i];
+      }
+    }
+  } else {
+    for (int kt = 0; kt < KT; kt++) kstep(kt);
+  }
+
+  // epilogue of one 32 x 32 MFMA block: lane holds col (lane & 31) of rows
+  // 8 (e >> 2) + 4 (lane >> 5) + (e & 3)
+  auto store_block = [&](int mb, int nb, const v16i& v) {
+    if constexpr (OUT != OUT_NONE) {
+      const int col = bn0 + wn * 64 + nb * 32 + (lane & 31);
+      float bsc = 0.f;
+      if constexpr (OUT == OUT_BF16 || OUT == OUT_F32) bsc = p.b_scale[col];
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const int row = bm0 + wm * 128 + mb * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        const long o = (long)row * p.n + col;
+        if constexpr (OUT == OUT_I32) {
+          reinterpret_cast<i32*>(p.out)[o] = v[e];
+        } else {
+          const float y = __fmul_rn(__fmul_rn((float)v[e], p.a_scale[row]), bsc);
+          if constexpr (OUT == OUT_F32)
+            reinterpret_cast<float*>(p.out)[o] = y;
+          else
+            reinterpret_cast<uint16_t*>(p.out)[o] = (uint16_t)bf16_rne(y);
+        }
+      }
+    }
+  };
+
+  if constexpr (DENOISE) {
+    // acc -= sum_li 128^li [X_li | EAL] [EBRt | Y_li]^T, exact mod 2^32, Horner over limbs
+    // (kernels.cu:598-673). Four passes over quarters of the wave's block keep the Horner
+    // accumulator at 32 registers; each quarter is stored as soon as it is final. The corr k
+    // steps (limb L-1 down to 0, each 2r / 64 chunks) stream through one continuous ring for all
+    // passes: global step g is corr step g mod CT.
+    const int mx = max(p.maxabs[0], p.maxabs[1]);
+    int L = mx > 1040319 ? 4 : mx > 8127 ? 3 : mx > 63 ? 2 : 1;
+    L = min(L, p.lmax);
+    const long R2 = 2L * p.r;
+    const int CPL = (int)(R2 / W_BK), CT = L * CPL, GT = 4 * CT;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // gfx9 counts stores in vmcnt: drain the hash phase
+    __syncthreads();
+    // next corr step to issue: global index ig, limb li, chunk kc
+    int ig = 0, li = L - 1, kc = 0;
+    auto cissue = [&]() {
+      const DmaLane cl = dma_lane(p.corrA + (long)li * p.m * R2, R2, p.corrB + (long)li * p.n * R2, R2, bm0, bn0, lane);
+      dma_step(wsm + (ig & (W_STAGES - 1)) * W_STAGE, cl, R2, R2, (long)kc * W_BK, wave);
+      ig++;
+      if (++kc == CPL) {
+        kc = 0;
+        li = li == 0 ? L - 1 : li - 1;
+      }
+    };
+#pragma unroll
+    for (int g = 0; g < W_STAGES - 1; g++)
+      if (g < GT) cissue();
+    int g = 0;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int h = q >> 1, nb = q & 1;
+      v16i tmp[2] = {v16i{}, v16i{}};
+      for (int t = 0, c = 0; t < CT; t++, g++) {
+        wait_step(min(GT - 1 - g, W_STAGES - 2));
+        if (ig < GT) cissue();
+        if (c == 0) {
+          tmp[0] = tmp[0] << 7;
+          tmp[1] = tmp[1] << 7;
+        }
+        if (++c == CPL) c = 0;
+        step_mma_quarter(tmp, wsm + (g & (W_STAGES - 1)) * W_STAGE, wm, wn, h, nb, fo);
+      }
+      store_block(2 * h, nb, acc[2 * h][nb] - tmp[0]);
+      store_block(2 * h + 1, nb, acc[2 * h + 1][nb] - tmp[1]);
+    }
+  } else {
+#pragma unroll
+    for (int mb = 0; mb < 4; mb++)
+#pragma unroll
+      for (int nb = 0; nb < 2; nb++) store_block(mb, nb, acc[mb][nb]);
+  }
+}
+
+template <bool H, bool D, int OUT>
+static void go256(dim3 grid, hipStream_t s, const Gemm256Params& p) {
+  auto kern = noisy_gemm256_kernel<H, D, OUT>;
+  static bool attr = false;  // one attribute call per instantiation (the library is process-wide)
+  if (!attr) {
+    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, W_LDS);
+    attr = true;
+  }
+  hipLaunchKernelGGL(kern, grid, dim3(W_THREADS), W_LDS, s, p);
+}
+
+template <bool H, bool D>
+static void out256(int out_mode, dim3 grid, hipStream_t s, const Gemm256Params& p) {
+  switch (out_mode) {
+    case OUT_NONE: go256<H, D, OUT_NONE>(grid, s, p); break;
+    case OUT_I32: go256<H, D, OUT_I32>(grid, s, p); break;
+    case OUT_BF16: go256<H, D, OUT_BF16>(grid, s, p); break;
+    default: go256<H, D, OUT_F32>(grid, s, p); break;
+  }
+}
+
+// Called by uwc_noisy_gemm after argument checks when m % 256 == 0 and n % 256 == 0.
+int uwc_noisy_gemm256(const int8_t* A, const int8_t* B, int m, int n, int k, int r, const int8_t* corrA,
+                      const int8_t* corrB, const int32_t* maxabs, int lmax, const uint32_t* key,
+                      const uint32_t* target, uint32_t* wins, int max_wins, const float* a_scale, const float* b_scale,
+                      void* out, int out_mode, int flags, uint32_t* tile_dump, hipStream_t stream) {
+  const bool hash = flags & FLAG_HASH, denoise = flags & FLAG_DENOISE;
+  Gemm256Params p{A, B, m, n, k, r, corrA, corrB, maxabs, lmax, key, target, wins, max_wins, a_scale, b_scale, out,
+                  hash ? tile_dump : nullptr};
+  const dim3 grid((m / W_BM) * (n / W_BN));
+  if (hash && denoise) out256<true, true>(out_mode, grid, stream, p);
+  else if (hash) out256<true, false>(out_mode, grid, stream, p);
+  else if (denoise) out256<false, true>(out_mode, grid, stream, p);
+  else out256<false, false>(out_mode, grid, stream, p);
+  return uwc_launch_status("noisy_gemm256");
+}

@@ -32,9 +32,12 @@ WIN_WORDS = 10
 DUMP_WORDS = 24
 CHUNKS_PER_CTA = 64
 FLAG_HASH, FLAG_DENOISE = 1, 2
+FLAG_TILE128 = 0x100  # force the 128 x 128 tiling (identical results)
 OUT_NONE, OUT_I32, OUT_BF16, OUT_F32 = 0, 1, 2, 3
-CONFIGS = {"128x128": (128, 2, 2)}
-DEFAULT_CFG = "128x128"
+# GEMM tilings: (tile M = N, pipeline stages, waves per SIMD). "256x256" serves m, n % 256 == 0
+# and falls back to "128x128" otherwise; every tiling gives identical outputs and winners.
+CONFIGS = {"256x256": (256, 4, 2), "128x128": (128, 2, 2)}
+DEFAULT_CFG = "256x256"
 
 # Pearl's v3 noise labels and salts (miner/ampere/uwc_ampere/reference.py:23-26):
 # SEED_SALT_X = BLAKE3(b"pearl/cert-v3/noise-seed/X").
@@ -161,6 +164,8 @@ def noise_project(src, rows, k, r, *, E, Pn, dst, St=None, corr=None, corr_off=-
 def gemm(A, B, *, r=128, flags=0, corrA=None, corrB=None, maxabs=None, key=None, target=None, wins=None,
          max_wins=0, a_scale=None, b_scale=None, out=None, out_mode=OUT_NONE, cfg=None, dump=None):
     """C = A @ B^T (int8, k contiguous) with the optional mining transcript / denoise / epilogue."""
+    cfg = cfg or DEFAULT_CFG
+    _check(cfg in CONFIGS, f"gemm: unknown cfg {cfg!r}")
     m, k = A.shape
     n = B.shape[0]
     if flags:
@@ -171,7 +176,7 @@ def gemm(A, B, *, r=128, flags=0, corrA=None, corrB=None, maxabs=None, key=None,
            "gemm: A and B must be contiguous int8")
     _lib.call("uwc_noisy_gemm", _p(A), _p(B), m, n, k, r, _p(corrA), _p(corrB), _p(maxabs),
               corrA.shape[0] if corrA is not None else 0, _p(key), _p(target), _p(wins), max_wins, _p(a_scale),
-              _p(b_scale), _p(out), out_mode, flags, _p(dump), _stream())
+              _p(b_scale), _p(out), out_mode, flags | (FLAG_TILE128 if cfg == "128x128" else 0), _p(dump), _stream())
 
 
 def igemm_i32(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
@@ -309,7 +314,7 @@ class MinedWeight:
         gemm(b["ApEA"], self.BpEBt, r=r, flags=(FLAG_HASH if hash_tiles else 0) | FLAG_DENOISE,
              corrA=b["corrA"], corrB=self.corrB, maxabs=b["maxabs"], key=b["a_seed"], target=self.target,
              wins=b["wins"], max_wins=self.max_wins, a_scale=a_scale, b_scale=self.b_scale, out=out, out_mode=out_mode,
-             dump=dump)
+             cfg=cfg, dump=dump)
         return out
 
     def noise_mine(self, A: torch.Tensor, dump=None):
