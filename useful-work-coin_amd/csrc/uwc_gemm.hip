@@ -357,7 +357,7 @@ extern "C" int uwc_noisy_gemm(const int8_t* A, const int8_t* B, int m, int n, in
     if (lmax < 1 || lmax > 4) return uwc_fail("uwc_noisy_gemm: lmax=%d outside 1..4", lmax);
     if (!aligned16(corrA) || !aligned16(corrB)) return uwc_fail("uwc_noisy_gemm: corrA/corrB must be 16-byte aligned");
   }
-  if (m % 256 == 0 && n % 256 == 0 && !(flags & FLAG_TILE128))
+  if (m % 256 == 0 && n % 256 == 0 && k % 128 == 0 && !(flags & FLAG_TILE128))
     return uwc_noisy_gemm256(A, B, m, n, k, r, corrA, corrB, maxabs, lmax, key, target, wins, max_wins, a_scale,
                              b_scale, out, out_mode, flags & ~FLAG_TILE128, tile_dump, stream);
   GemmParams p{A, B, m, n, k, r, corrA, corrB, maxabs, lmax, key, target, wins, max_wins, a_scale, b_scale, out,

@@ -22,13 +22,18 @@
 
 #define W_BM 256
 #define W_BN 256
-#define W_BK 64
-#define W_STAGES 4
+#ifndef W_BK
+#define W_BK 128
+#endif
+#define W_STAGES (W_BK == 64 ? 4 : 2)
+#define W_CH (W_BK / 16)                    // 16-byte chunks per LDS row
+#define W_KP (W_BK / 32)                    // k32 MFMA passes per k step
 #define W_THREADS 512
 #define W_TILE (W_BM * W_BK)                 // bytes of one operand tile
 #define W_STAGE (2 * W_TILE)                 // A + B
 #define W_LDS (W_STAGES * W_STAGE)           // 128 KiB
-#define W_SEGS_PER_WAVE 4                    // 1 KiB DMA segments per wave per k step
+#define W_WAVES (W_THREADS / 64)
+#define W_SEGS_PER_WAVE (W_TILE / 1024 / W_WAVES)  // 1 KiB DMA segments per wave per operand per k step
 
 #define FLAG_HASH 1
 #define FLAG_DENOISE 2
@@ -60,72 +65,106 @@ struct Gemm256Params {
 typedef const void __attribute__((address_space(1)))* gptr_t;
 typedef void __attribute__((address_space(3)))* lptr_t;
 
-// Per-lane DMA source: lane i of a segment fills LDS bytes [16 i, 16 i + 16) of it, i.e. row
-// 16 s + i / 4 (s = the segment) at physical chunk i & 3, logical chunk (i & 3) ^ swz(i / 4)
-// (swz of a row depends only on its low 4 bits).
+// LDS tile rows are W_BK bytes; 16-byte chunk c of tile row r sits at chunk c ^ swz(r):
+//   64-byte rows  (4 chunks): swz(r) = ((r >> 1) ^ (r >> 2)) & 3
+//   128-byte rows (8 chunks): swz(r) = (r ^ (r >> 3)) & 7
+// Either way 16 consecutive rows read at one logical chunk hit 16 distinct 16-byte bank groups
+// (64 banks) and any 8 consecutive rows hit 8 distinct ones (32 banks).
+__device__ __forceinline__ int swz(int r) {
+  if constexpr (W_BK == 64) return ((r >> 1) ^ (r >> 2)) & 3;
+  else return (r ^ (r >> 3)) & 7;
+}
+
+// A 1 KiB DMA segment holds 1024 / W_BK tile rows; lane i fills LDS bytes [16 i, 16 i + 16) of
+// it: row RPS s + i / W_CH (RPS = rows per segment), physical chunk i % W_CH, so it fetches
+// logical chunk (i % W_CH) ^ swz(row).
+#define W_RPS (1024 / W_BK)
+
 struct DmaLane {
-  const i8* a;  // A + (bm0 + lane / 4) * lda + chunk * 16
+  const i8* a;  // A + (bm0 + i / W_CH) * lda
   const i8* b;
+  int rin, phys;
 };
 
 __device__ __forceinline__ DmaLane dma_lane(const i8* A, long lda, const i8* B, long ldb, int bm0, int bn0, int lane) {
-  const int rin = lane >> 2, c = (lane & 3) ^ ((((rin >> 1) ^ (rin >> 2))) & 3);
-  return DmaLane{A + (long)(bm0 + rin) * lda + c * 16, B + (long)(bn0 + rin) * ldb + c * 16};
+  const int rin = lane / W_CH, phys = lane % W_CH;
+  return DmaLane{A + (long)(bm0 + rin) * lda, B + (long)(bn0 + rin) * ldb, rin, phys};
 }
 
-// Issue this wave's 4 DMA segments of one k step: segments 2w, 2w+1 of A and of B.
+// Issue this wave's DMA segments of one k step (segments wave * SPW .. of A and of B).
 __device__ __forceinline__ void dma_step(u8* stage, const DmaLane& d, long lda, long ldb, long k0, int wave) {
 #pragma unroll
-  for (int t = 0; t < 2; t++) {
-    const int s = 2 * wave + t;
-    __builtin_amdgcn_global_load_lds((gptr_t)(d.a + 16L * s * lda + k0), (lptr_t)(stage + s * 1024), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds((gptr_t)(d.b + 16L * s * ldb + k0), (lptr_t)(stage + W_TILE + s * 1024), 16, 0, 0);
+  for (int t = 0; t < W_SEGS_PER_WAVE; t++) {
+    const int s = W_SEGS_PER_WAVE * wave + t;
+    const int c = d.phys ^ swz(W_RPS * s + d.rin);
+    const long off = (long)W_RPS * s;
+    __builtin_amdgcn_global_load_lds((gptr_t)(d.a + off * lda + k0 + c * 16), (lptr_t)(stage + s * 1024), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((gptr_t)(d.b + off * ldb + k0 + c * 16), (lptr_t)(stage + W_TILE + s * 1024), 16, 0, 0);
   }
 }
 
 // Wait until at most `younger` of this wave's k steps are still loading, then barrier.
 __device__ __forceinline__ void wait_step(int younger) {
-  if (younger >= 2) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-  else if (younger == 1) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+  constexpr int per = 2 * W_SEGS_PER_WAVE;  // DMA instructions per wave per k step
+  if (younger >= 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * per) : "memory");
+  else if (younger == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(per) : "memory");
   else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
 }
 
 __device__ __forceinline__ v4i lds16(const u8* p) { return *reinterpret_cast<const v4i*>(p); }
 
-// Per-lane fragment offset within a tile for k32 pass kp: row (lane & 31) of the 32-row block,
-// logical chunk 2 kp + (lane >> 5). Block row bases are multiples of 32, which leave swz alone.
-__device__ __forceinline__ int frag_off(int lane, int kp) {
+// Per-lane fragment offset within a tile for k32 pass kp and block parity par (the 32-row
+// block index mb & 1 reaches swz through row bit 5 when rows are 128 bytes): row (lane & 31)
+// of the block, logical chunk 2 kp + (lane >> 5).
+__device__ __forceinline__ int frag_off(int lane, int kp, int par) {
   const int r = lane & 31, c = 2 * kp + (lane >> 5);
-  return r * 64 + ((c ^ (((r >> 1) ^ (r >> 2)) & 3)) << 4);
+  return r * W_BK + ((c ^ swz(r + 32 * par)) << 4);
 }
 
-// One k step of MFMA work for the wave's 128 x 64 block from a stage.
-__device__ __forceinline__ void step_mma(v16i acc[4][2], const u8* stage, int wm, int wn, const int fo[2]) {
-  const u8* sa = stage + wm * 128 * 64;
-  const u8* sb = stage + W_TILE + wn * 64 * 64;
+struct FragOff {
+  int o[W_KP][2];
+};
+
+__device__ __forceinline__ FragOff frag_offsets(int lane) {
+  FragOff f;
 #pragma unroll
-  for (int kp = 0; kp < 2; kp++) {
+  for (int kp = 0; kp < W_KP; kp++)
+#pragma unroll
+    for (int par = 0; par < 2; par++) f.o[kp][par] = frag_off(lane, kp, par);
+  return f;
+}
+
+// k32 passes [KP0, KP1) of a k step of MFMA work for the wave's 128 x 64 block from a stage:
+// per pass, the six fragments are requested before its eight MFMAs (LDS returns in order).
+template <int KP0 = 0, int KP1 = W_KP>
+__device__ __forceinline__ void step_mma(v16i acc[4][2], const u8* stage, int wm, int wn, const FragOff& fo) {
+  const u8* sa = stage + wm * 128 * W_BK;
+  const u8* sb = stage + W_TILE + wn * 64 * W_BK;
+#pragma unroll
+  for (int kp = KP0; kp < KP1; kp++) {
     v4i a[4], b[2];
 #pragma unroll
-    for (int mb = 0; mb < 4; mb++) a[mb] = lds16(sa + mb * 32 * 64 + fo[kp]);
+    for (int nb = 0; nb < 2; nb++) b[nb] = lds16(sb + nb * 32 * W_BK + fo.o[kp][nb & 1]);
 #pragma unroll
-    for (int nb = 0; nb < 2; nb++) b[nb] = lds16(sb + nb * 32 * 64 + fo[kp]);
+    for (int mb = 0; mb < 4; mb++) a[mb] = lds16(sa + mb * 32 * W_BK + fo.o[kp][mb & 1]);
 #pragma unroll
     for (int mb = 0; mb < 4; mb++)
 #pragma unroll
       for (int nb = 0; nb < 2; nb++) acc[mb][nb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[mb], b[nb], acc[mb][nb], 0, 0, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
   }
 }
 
 // Denoise k step for one quarter of the wave's block: M blocks 2h, 2h+1 of column half nb.
 __device__ __forceinline__ void step_mma_quarter(v16i tmp[2], const u8* stage, int wm, int wn, int h, int nb,
-                                                 const int fo[2]) {
-  const u8* sa = stage + (wm * 128 + h * 64) * 64;
-  const u8* sb = stage + W_TILE + (wn * 64 + nb * 32) * 64;
+                                                 const FragOff& fo) {
+  const u8* sa = stage + (wm * 128 + h * 64) * W_BK;
+  const u8* sb = stage + W_TILE + (wn * 64 + nb * 32) * W_BK;
 #pragma unroll
-  for (int kp = 0; kp < 2; kp++) {
-    const v4i a0 = lds16(sa + fo[kp]), a1 = lds16(sa + 32 * 64 + fo[kp]), b = lds16(sb + fo[kp]);
+  for (int kp = 0; kp < W_KP; kp++) {
+    const v4i a0 = lds16(sa + fo.o[kp][0]), a1 = lds16(sa + 32 * W_BK + fo.o[kp][1]), b = lds16(sb + fo.o[kp][nb & 1]);
     tmp[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b, tmp[0], 0, 0, 0);
     tmp[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b, tmp[1], 0, 0, 0);
   }
@@ -203,17 +242,20 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
 #pragma unroll
     for (int j = 0; j < 2; j++) acc[i][j] = v16i{};
 
-  const int fo[2] = {frag_off(lane, 0), frag_off(lane, 1)};
+  const FragOff fo = frag_offsets(lane);
   const DmaLane dl = dma_lane(p.A, k, p.B, k, bm0, bn0, lane);
   // prologue: k steps 0..2 in flight
 #pragma unroll
   for (int s = 0; s < W_STAGES - 1; s++)
     if (s < KT) dma_step(wsm + s * W_STAGE, dl, k, k, (long)s * W_BK, wave);
 
-  auto kstep = [&](int kt) {
+  auto kwait = [&](int kt) {
     wait_step(min(KT - 1 - kt, W_STAGES - 2));
     if (kt + W_STAGES - 1 < KT)
       dma_step(wsm + ((kt + W_STAGES - 1) % W_STAGES) * W_STAGE, dl, k, k, (long)(kt + W_STAGES - 1) * W_BK, wave);
+  };
+  auto kstep = [&](int kt) {
+    kwait(kt);
     step_mma(acc, wsm + (kt % W_STAGES) * W_STAGE, wm, wn, fo);
   };
 
@@ -221,14 +263,34 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
     u32 msg[16];
 #pragma unroll
     for (int w = 0; w < 16; w++) msg[w] = 0;
-    const int tpc = p.r / W_BK, nchunks = p.k / p.r;
+    const int nchunks = p.k / p.r;
     int kt = 0;
-    for (int c0 = 0; c0 < nchunks; c0 += 16) {
+    if (p.r >= W_BK) {
+      const int tpc = p.r / W_BK;
+      for (int c0 = 0; c0 < nchunks; c0 += 16) {
 #pragma unroll
-      for (int s = 0; s < 16; s++) {
-        if (c0 + s < nchunks) {
-          for (int i = 0; i < tpc; i++, kt++) kstep(kt);
-          msg[s] = rotl13(msg[s]) ^ fold_owned(acc, lane);
+        for (int s = 0; s < 16; s++) {
+          if (c0 + s < nchunks) {
+            for (int i = 0; i < tpc; i++, kt++) kstep(kt);
+            msg[s] = rotl13(msg[s]) ^ fold_owned(acc, lane);
+          }
+        }
+      }
+    } else {
+      // r = W_BK / 2: two transcript chunks per k step (even slot: first half, odd: second)
+      for (int c0 = 0; c0 < nchunks; c0 += 16) {
+#pragma unroll
+        for (int s = 0; s < 16; s++) {
+          if (c0 + s < nchunks) {
+            if ((s & 1) == 0) {
+              kwait(kt);
+              step_mma<0, W_KP / 2>(acc, wsm + (kt % W_STAGES) * W_STAGE, wm, wn, fo);
+            } else {
+              step_mma<W_KP / 2, W_KP>(acc, wsm + (kt % W_STAGES) * W_STAGE, wm, wn, fo);
+              kt++;
+            }
+            msg[s] = rotl13(msg[s]) ^ fold_owned(acc, lane);
+          }
         }
       }
     }
