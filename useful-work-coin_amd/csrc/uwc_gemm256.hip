@@ -2,21 +2,27 @@
 // as noisy_gemm_kernel (uwc_gemm.hip; miner/ampere/uwc_ampere/kernels.cu:482-715), built for
 // throughput at the mining and detrt-prefill shapes.
 //
-//   * Workgroup tile 256 x 256, k step 64, 8 wave64s in 2 (M) x 4 (N); each wave owns 128 x 64
-//     = two consensus 64 x 64 hash blocks, as 4 x 2 v_mfma_i32_32x32x32_i8 blocks
+//   * Workgroup tile 256 x 256, k step W_BK (128), 8 wave64s in 2 (M) x 4 (N); each wave owns
+//     128 x 64 = two consensus 64 x 64 hash blocks, as 4 x 2 v_mfma_i32_32x32x32_i8 blocks
 //     (128 int32 accumulators per lane, in VGPRs so the fold reads them directly).
-//   * Operand tiles go HBM -> LDS with global_load_lds_dwordx4 (no VGPR staging) into a 4-stage
-//     ring, three k steps in flight; one barrier per k step.
-//   * LDS rows are 64 bytes; the 16-byte chunk c of row r sits at chunk c ^ f(r),
-//     f(r) = ((r >> 1) ^ (r >> 2)) & 3, so the 32-row fragment reads are conflict-free with
-//     32 or 64 banks. The swizzle is applied on the global side (each lane of a DMA writes a
-//     fixed LDS slot and fetches the bytes that belong there).
+//   * Operand tiles go HBM -> LDS with global_load_lds_dwordx4 (no VGPR staging) into a ring of
+//     W_STAGES k steps (128 KiB); one barrier per k step.
+//   * Software pipeline at k32-pass granularity: the six LDS fragments of pass p + 1 are read
+//     while the eight MFMAs of pass p run (two fragment sets in registers). The step barrier and
+//     the next DMA issue sit before the MFMAs of a step's last pass, whose fragments are already
+//     in registers, so the barrier wait overlaps MFMA work.
+//   * LDS rows are W_BK bytes; the 16-byte chunk c of row r sits at chunk c ^ swz(r), so the
+//     32-row fragment reads are conflict-free with 32 or 64 banks. The swizzle is applied on the
+//     global side (each lane of a DMA writes a fixed LDS slot and fetches the bytes that belong
+//     there).
 //   * Transcript fold every r along k: a lane XORs its accumulators into 8 partials (hash block
-//     x g & 3), then a reduce-scatter over lane bits 0, 3, 4 (DPP quad_perm, DPP row_ror:8,
-//     ds_swizzle) leaves every lane with the full tile XOR of exactly one tile, which it folds
-//     into that tile's 16-word message (message slots are static: the fold loop is unrolled
-//     over the 16 slots). After the k loop every lane digests its own tile.
-//   * Denoise in two passes over the wave's two 32-column halves (a 64-register Horner
+//     x g & 3) with 3-input v_bitop3 XORs, block by block right before that block's next MFMA
+//     (the fold of chunk c runs inside the first pass of chunk c + 1), then a reduce-scatter
+//     over lane bits 0, 3, 4 (DPP quad_perm and row_ror:8 fused into v_xor, ds_swizzle) leaves
+//     every lane with the full tile XOR of exactly one tile, which it folds into that tile's
+//     16-word message (message slots are static: the chunk loop is unrolled over the 16 slots).
+//     After the k loop every lane digests its own tile.
+//   * Denoise in four passes over quarters of the wave's block (a 32-register Horner
 //     accumulator), streaming [X_li | EAL] and [EBRt | Y_li] through the same ring.
 #include "uwc_common.h"
 
@@ -25,13 +31,16 @@
 #ifndef W_BK
 #define W_BK 128
 #endif
+#ifndef W_STAGES
 #define W_STAGES (W_BK == 64 ? 4 : 2)
+#endif
 #define W_CH (W_BK / 16)                    // 16-byte chunks per LDS row
 #define W_KP (W_BK / 32)                    // k32 MFMA passes per k step
 #define W_THREADS 512
 #define W_TILE (W_BM * W_BK)                 // bytes of one operand tile
 #define W_STAGE (2 * W_TILE)                 // A + B
-#define W_LDS (W_STAGES * W_STAGE)           // 128 KiB
+#define W_LDS (W_STAGES * W_STAGE)           // at most 160 KiB (gfx950 LDS per workgroup)
+static_assert(W_LDS <= 160 * 1024, "LDS ring exceeds 160 KiB");
 #define W_WAVES (W_THREADS / 64)
 #define W_SEGS_PER_WAVE (W_TILE / 1024 / W_WAVES)  // 1 KiB DMA segments per wave per operand per k step
 
@@ -91,22 +100,40 @@ __device__ __forceinline__ DmaLane dma_lane(const i8* A, long lda, const i8* B, 
   return DmaLane{A + (long)(bm0 + rin) * lda, B + (long)(bn0 + rin) * ldb, rin, phys};
 }
 
+// One wave-wide 16-byte-per-lane DMA: lane i's 16 bytes at g land at LDS byte lds + 16 i
+// (lds is wave-uniform and goes in M0). Written as asm rather than the global_load_lds builtin
+// so that the compiler's wait-count model does not see an LDS write in flight: with one pending
+// it waits for every outstanding LDS read (lgkmcnt(0)) before each use of a fragment, instead
+// of only for the reads that use needs. The kernel tracks these loads itself: wait_step waits
+// on vmcnt and barriers before any stage is read, and the loads issue only after the barrier
+// that ends every read of the stage they fill.
+__device__ __forceinline__ void dma16(const void* g, u32 lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+
+__device__ __forceinline__ u32 lds_addr(const u8* p) { return (u32)(uintptr_t)(lptr_t)p; }
+
 // Issue this wave's DMA segments of one k step (segments wave * SPW .. of A and of B).
 __device__ __forceinline__ void dma_step(u8* stage, const DmaLane& d, long lda, long ldb, long k0, int wave) {
+  const u32 base = __builtin_amdgcn_readfirstlane(lds_addr(stage));
 #pragma unroll
   for (int t = 0; t < W_SEGS_PER_WAVE; t++) {
     const int s = W_SEGS_PER_WAVE * wave + t;
     const int c = d.phys ^ swz(W_RPS * s + d.rin);
     const long off = (long)W_RPS * s;
-    __builtin_amdgcn_global_load_lds((gptr_t)(d.a + off * lda + k0 + c * 16), (lptr_t)(stage + s * 1024), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds((gptr_t)(d.b + off * ldb + k0 + c * 16), (lptr_t)(stage + W_TILE + s * 1024), 16, 0, 0);
+    const u32 ls = __builtin_amdgcn_readfirstlane(base + s * 1024);
+    dma16(d.a + off * lda + k0 + c * 16, ls);
+    dma16(d.b + off * ldb + k0 + c * 16, ls + W_TILE);
   }
 }
 
 // Wait until at most `younger` of this wave's k steps are still loading, then barrier.
 __device__ __forceinline__ void wait_step(int younger) {
   constexpr int per = 2 * W_SEGS_PER_WAVE;  // DMA instructions per wave per k step
-  if (younger >= 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * per) : "memory");
+  static_assert((W_STAGES - 1) * per < 64, "vmcnt is 6 bits");
+  if (younger >= 4) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * per) : "memory");
+  else if (younger == 3) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * per) : "memory");
+  else if (younger == 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * per) : "memory");
   else if (younger == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(per) : "memory");
   else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
@@ -122,91 +149,147 @@ __device__ __forceinline__ int frag_off(int lane, int kp, int par) {
   return r * W_BK + ((c ^ swz(r + 32 * par)) << 4);
 }
 
+// Offsets of one lane's fragment reads for the k32 passes of a step, for even 32-row blocks;
+// odd blocks (row bit 5 set) read o[kp ^ 2] with 128-byte rows (swz then flips chunk bit 2)
+// and o[kp] with 64-byte rows (swz does not see row bit 5).
 struct FragOff {
-  int o[W_KP][2];
+  int o[W_KP];
+  __device__ __forceinline__ int at(int kp, int par) const {
+    if constexpr (W_BK == 128) return o[par ? kp ^ 2 : kp];
+    else return o[kp];
+  }
 };
 
 __device__ __forceinline__ FragOff frag_offsets(int lane) {
   FragOff f;
 #pragma unroll
-  for (int kp = 0; kp < W_KP; kp++)
-#pragma unroll
-    for (int par = 0; par < 2; par++) f.o[kp][par] = frag_off(lane, kp, par);
+  for (int kp = 0; kp < W_KP; kp++) f.o[kp] = frag_off(lane, kp, 0);
   return f;
 }
 
-// k32 passes [KP0, KP1) of a k step of MFMA work for the wave's 128 x 64 block from a stage:
-// per pass, the six fragments are requested before its eight MFMAs (LDS returns in order).
-template <int KP0 = 0, int KP1 = W_KP>
-__device__ __forceinline__ void step_mma(v16i acc[4][2], const u8* stage, int wm, int wn, const FragOff& fo) {
-  const u8* sa = stage + wm * 128 * W_BK;
-  const u8* sb = stage + W_TILE + wn * 64 * W_BK;
+// The operand fragments of one k32 pass of the wave's 128 x 64 block.
+struct Frag {
+  v4i a[4], b[2];
+};
+
+__device__ __forceinline__ v4i frag_a(const u8* stage, int wm, const FragOff& fo, int kp, int mb) {
+  return lds16(stage + (wm * 128 + mb * 32) * W_BK + fo.at(kp, mb & 1));
+}
+__device__ __forceinline__ v4i frag_b(const u8* stage, int wn, const FragOff& fo, int kp, int nb) {
+  return lds16(stage + W_TILE + (wn * 64 + nb * 32) * W_BK + fo.at(kp, nb & 1));
+}
+
+__device__ __forceinline__ void frag_read(Frag& f, const u8* stage, int wm, int wn, const FragOff& fo, int kp) {
 #pragma unroll
-  for (int kp = KP0; kp < KP1; kp++) {
-    v4i a[4], b[2];
+  for (int nb = 0; nb < 2; nb++) f.b[nb] = frag_b(stage, wn, fo, kp, nb);
 #pragma unroll
-    for (int nb = 0; nb < 2; nb++) b[nb] = lds16(sb + nb * 32 * W_BK + fo.o[kp][nb & 1]);
+  for (int mb = 0; mb < 4; mb++) f.a[mb] = frag_a(stage, wm, fo, kp, mb);
+}
+
+__device__ __forceinline__ u32 xor3(u32 a, u32 b, u32 c) { return __builtin_amdgcn_bitop3_b32(a, b, c, 0x96); }
+
+// XOR one 32 x 32 block's 16 accumulators into the lane's 4 partials of its hash block:
+// x[p] collects elements e with e % 4 == p (rows g + 8 i of one tile).
+__device__ __forceinline__ void fold_block(const v16i& v, u32* x, bool first) {
 #pragma unroll
-    for (int mb = 0; mb < 4; mb++) a[mb] = lds16(sa + mb * 32 * W_BK + fo.o[kp][mb & 1]);
-#pragma unroll
-    for (int mb = 0; mb < 4; mb++)
-#pragma unroll
-      for (int nb = 0; nb < 2; nb++) acc[mb][nb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[mb], b[nb], acc[mb][nb], 0, 0, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+  for (int p = 0; p < 4; p++) {
+    if (first) x[p] = xor3(v[p], v[4 + p], v[8 + p]) ^ (u32)v[12 + p];
+    else x[p] = xor3(xor3(x[p], v[p], v[4 + p]), v[8 + p], v[12 + p]);
   }
+}
+
+// The eight MFMAs of one pass, column half 0 first. With FOLD, each block's accumulators are
+// first XORed into the fold partials x[8] (the cumulative sums of the chunk that ended with the
+// previous pass), so the fold's VALU work interleaves with the MFMAs. With READ, f is refilled
+// with the fragments of pass nkp of stage nst as the current ones retire: b[0] after the four
+// half-0 MFMAs, a[mb] after MFMA (mb, 1), b[1] last; one fragment set stays in registers and
+// each read still has several MFMAs to land before its first use in the next pass.
+template <bool FOLD, bool READ>
+__device__ __forceinline__ void pass_mma(v16i acc[4][2], Frag& f, u32 x[8], const u8* nst, int wm, int wn,
+                                         const FragOff& fo, int nkp) {
+#pragma unroll
+  for (int mb = 0; mb < 4; mb++) {
+    if constexpr (FOLD) fold_block(acc[mb][0], x + (mb >> 1) * 4, (mb & 1) == 0);
+    acc[mb][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[mb], f.b[0], acc[mb][0], 0, 0, 0);
+  }
+  if constexpr (READ) f.b[0] = frag_b(nst, wn, fo, nkp, 0);
+#pragma unroll
+  for (int mb = 0; mb < 4; mb++) {
+    if constexpr (FOLD) fold_block(acc[mb][1], x + (mb >> 1) * 4, false);
+    acc[mb][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[mb], f.b[1], acc[mb][1], 0, 0, 0);
+    if constexpr (READ) f.a[mb] = frag_a(nst, wm, fo, nkp, mb);
+  }
+  if constexpr (READ) f.b[1] = frag_b(nst, wn, fo, nkp, 1);
+  // pin the interleave: [fold VALU,] MFMA ... with the reads after the MFMAs that free them
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    if constexpr (FOLD) __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+  }
+  if constexpr (READ) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    if constexpr (FOLD) __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if constexpr (READ) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+  }
+  if constexpr (READ) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
 }
 
 // Denoise k step for one quarter of the wave's block: M blocks 2h, 2h+1 of column half nb.
 __device__ __forceinline__ void step_mma_quarter(v16i tmp[2], const u8* stage, int wm, int wn, int h, int nb,
                                                  const FragOff& fo) {
-  const u8* sa = stage + (wm * 128 + h * 64) * W_BK;
-  const u8* sb = stage + W_TILE + (wn * 64 + nb * 32) * W_BK;
 #pragma unroll
   for (int kp = 0; kp < W_KP; kp++) {
-    const v4i a0 = lds16(sa + fo.o[kp][0]), a1 = lds16(sa + 32 * W_BK + fo.o[kp][1]), b = lds16(sb + fo.o[kp][nb & 1]);
+    const v4i a0 = frag_a(stage, wm, fo, kp, 2 * h), a1 = frag_a(stage, wm, fo, kp, 2 * h + 1);
+    const v4i b = frag_b(stage, wn, fo, kp, nb);
     tmp[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b, tmp[0], 0, 0, 0);
     tmp[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b, tmp[1], 0, 0, 0);
   }
 }
 
-__device__ __forceinline__ u32 xor3(u32 a, u32 b, u32 c) { return a ^ b ^ c; }
 __device__ __forceinline__ u32 rotl13(u32 x) { return __builtin_amdgcn_alignbit(x, x, 19); }
 
+// Lane-permuted copy of x (DPP control CTRL). bound_ctrl with a zero old value lets the compiler
+// fuse the permutation into the consuming v_xor as a DPP operand (every source lane is in range
+// for the two controls used here, so the result is the plain permutation).
 template <int CTRL>
 __device__ __forceinline__ u32 dpp(u32 x) {
-  return (u32)__builtin_amdgcn_mov_dpp((int)x, CTRL, 0xF, 0xF, false);
+  return (u32)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xF, 0xF, true);
 }
 
-// Tile XOR of the one tile this lane owns after the reduce-scatter (see the file comment).
-__device__ __forceinline__ u32 fold_owned(const v16i acc[4][2], int lane) {
-  u32 x[8];
-#pragma unroll
-  for (int hb = 0; hb < 2; hb++)
-#pragma unroll
-    for (int p = 0; p < 4; p++) {
-      u32 v = 0;
-#pragma unroll
-      for (int mb = 2 * hb; mb < 2 * hb + 2; mb++)
-#pragma unroll
-        for (int nb = 0; nb < 2; nb++)
-          v = xor3(v, (u32)acc[mb][nb][p] ^ (u32)acc[mb][nb][4 + p], (u32)acc[mb][nb][8 + p] ^ (u32)acc[mb][nb][12 + p]);
-      x[hb * 4 + p] = v;
-    }
+// Reduce-scatter of the 8 fold partials over lane bits 0, 3, 4: afterwards the tile XOR of the
+// one tile this lane owns is keep ^ other.
+__device__ __forceinline__ void fold_scatter(const u32 x[8], int lane, u32& keep, u32& other) {
   const bool b0 = lane & 1, b3 = (lane >> 3) & 1, b4 = (lane >> 4) & 1;
   u32 y[4], z[2];
 #pragma unroll
   for (int i = 0; i < 4; i++) {  // lane bit 0: keep hash block b0
-    const u32 keep = b0 ? x[4 + i] : x[i], send = b0 ? x[i] : x[4 + i];
-    y[i] = keep ^ dpp<0xB1>(send);  // quad_perm [1,0,3,2]: partner lane ^ 1
+    const u32 kp = b0 ? x[4 + i] : x[i], send = b0 ? x[i] : x[4 + i];
+    y[i] = kp ^ dpp<0xB1>(send);  // quad_perm [1,0,3,2]: partner lane ^ 1
   }
 #pragma unroll
   for (int j = 0; j < 2; j++) {  // lane bit 3: keep g & 3 in {2 b3, 2 b3 + 1}
-    const u32 keep = b3 ? y[2 + j] : y[j], send = b3 ? y[j] : y[2 + j];
-    z[j] = keep ^ dpp<0x128>(send);  // row_ror:8 within a 16-lane row: partner lane ^ 8
+    const u32 kp = b3 ? y[2 + j] : y[j], send = b3 ? y[j] : y[2 + j];
+    z[j] = kp ^ dpp<0x128>(send);  // row_ror:8 within a 16-lane row: partner lane ^ 8
   }
-  const u32 keep = b4 ? z[1] : z[0], send = b4 ? z[0] : z[1];
-  return keep ^ (u32)__builtin_amdgcn_ds_swizzle((int)send, 0x401F);  // partner lane ^ 16
+  keep = b4 ? z[1] : z[0];
+  other = (u32)__builtin_amdgcn_ds_swizzle((int)(b4 ? z[0] : z[1]), 0x401F);  // partner lane ^ 16
+}
+
+// msg = rotl13(msg) ^ (tile XOR), from the partials.
+__device__ __forceinline__ void fold_into(u32& msg, const u32 x[8], int lane) {
+  u32 keep, other;
+  fold_scatter(x, lane, keep, other);
+  msg = xor3(rotl13(msg), keep, other);
+}
+
+// Tile XOR partials of the current accumulators (no MFMA interleave).
+__device__ __forceinline__ void fold_partials(const v16i acc[4][2], u32 x[8]) {
+#pragma unroll
+  for (int mb = 0; mb < 4; mb++)
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++) fold_block(acc[mb][nb], x + (mb >> 1) * 4, (mb & 1) == 0 && nb == 0);
 }
 
 __device__ __forceinline__ u32 bf16_rne(float f) {
@@ -227,6 +310,19 @@ __device__ __forceinline__ void tile256(int m, int n, int& bm0, int& bn0) {
   bn0 = (in / gsz) * W_BN;
 }
 
+// f(std::integral_constant<int, i>) for i = 0 .. N - 1, each i a compile-time constant.
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for_(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for_<I + 1, N>(f);
+  }
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_<0, N>(f);
+}
+
 template <bool HASH, bool DENOISE, int OUT>
 __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params p) {
   extern __shared__ __attribute__((aligned(1024))) u8 wsm[];
@@ -244,20 +340,42 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
 
   const FragOff fo = frag_offsets(lane);
   const DmaLane dl = dma_lane(p.A, k, p.B, k, bm0, bn0, lane);
-  // prologue: k steps 0..2 in flight
+  // prologue: every stage of the ring loading, then step 0 resident and its first pass read
 #pragma unroll
-  for (int s = 0; s < W_STAGES - 1; s++)
+  for (int s = 0; s < W_STAGES; s++)
     if (s < KT) dma_step(wsm + s * W_STAGE, dl, k, k, (long)s * W_BK, wave);
+  wait_step(min(KT - 1, W_STAGES - 1));
+  Frag cur;
+  frag_read(cur, wsm, wm, wn, fo, 0);
 
-  auto kwait = [&](int kt) {
-    wait_step(min(KT - 1 - kt, W_STAGES - 2));
-    if (kt + W_STAGES - 1 < KT)
-      dma_step(wsm + ((kt + W_STAGES - 1) % W_STAGES) * W_STAGE, dl, k, k, (long)(kt + W_STAGES - 1) * W_BK, wave);
+  // One k step. Pass kp runs its MFMAs on the fragments in `cur` while reading those of pass
+  // kp + 1. Before the last pass the wave waits for step kt + 1 (vmcnt + barrier: every wave is
+  // then done reading step kt's stage) and refills that stage with step kt + W_STAGES; the last
+  // pass reads the next step's first fragments (on the final step that read of a resident stage
+  // is unused, which keeps the MFMA code free of branches). Bit kp of FM: pass kp first folds
+  // the chunk that ended with the previous pass into m0 (kp == 0) or m1 (kp > 0).
+  auto step = [&](auto fm, int kt, u32& m0, u32& m1) {
+    constexpr int FM = decltype(fm)::value;
+    const u8* st = wsm + (kt % W_STAGES) * W_STAGE;
+    static_for<W_KP>([&](auto kpc) {
+      constexpr int kp = decltype(kpc)::value;
+      constexpr bool fold = ((FM >> kp) & 1) != 0;
+      u32 x[8];
+      if constexpr (kp + 1 < W_KP) {
+        pass_mma<fold, true>(acc, cur, x, st, wm, wn, fo, kp + 1);
+      } else {
+        if (kt + 1 < KT) {
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this stage's reads are complete
+          wait_step(min(KT - 2 - kt, W_STAGES - 2));
+          if (kt + W_STAGES < KT)
+            dma_step(wsm + (kt % W_STAGES) * W_STAGE, dl, k, k, (long)(kt + W_STAGES) * W_BK, wave);
+        }
+        pass_mma<fold, true>(acc, cur, x, wsm + ((kt + 1) % W_STAGES) * W_STAGE, wm, wn, fo, 0);
+      }
+      if constexpr (fold) fold_into(kp == 0 ? m0 : m1, x, lane);
+    });
   };
-  auto kstep = [&](int kt) {
-    kwait(kt);
-    step_mma(acc, wsm + (kt % W_STAGES) * W_STAGE, wm, wn, fo);
-  };
+  using NoFold = std::integral_constant<int, 0>;
 
   if constexpr (HASH) {
     u32 msg[16];
@@ -265,34 +383,38 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
     for (int w = 0; w < 16; w++) msg[w] = 0;
     const int nchunks = p.k / p.r;
     int kt = 0;
+    u32 unused = 0;
+    // The fold of chunk c runs in the first pass of chunk c + 1 (slot (c - 1) mod 16 for the
+    // chunk starting at slot c). For chunk 0 that folds the all-zero accumulators into the
+    // all-zero slot 15, which leaves it zero.
     if (p.r >= W_BK) {
       const int tpc = p.r / W_BK;
       for (int c0 = 0; c0 < nchunks; c0 += 16) {
 #pragma unroll
         for (int s = 0; s < 16; s++) {
           if (c0 + s < nchunks) {
-            for (int i = 0; i < tpc; i++, kt++) kstep(kt);
-            msg[s] = rotl13(msg[s]) ^ fold_owned(acc, lane);
+            step(std::integral_constant<int, 1>{}, kt++, msg[(s + 15) & 15], unused);
+            for (int i = 1; i < tpc; i++) step(NoFold{}, kt++, unused, unused);
           }
         }
       }
-    } else {
-      // r = W_BK / 2: two transcript chunks per k step (even slot: first half, odd: second)
+    } else if constexpr (W_KP == 4) {
+      // r = 64 = W_BK / 2: k step j holds chunks 2j (passes 0, 1) and 2j + 1 (passes 2, 3)
       for (int c0 = 0; c0 < nchunks; c0 += 16) {
 #pragma unroll
-        for (int s = 0; s < 16; s++) {
-          if (c0 + s < nchunks) {
-            if ((s & 1) == 0) {
-              kwait(kt);
-              step_mma<0, W_KP / 2>(acc, wsm + (kt % W_STAGES) * W_STAGE, wm, wn, fo);
-            } else {
-              step_mma<W_KP / 2, W_KP>(acc, wsm + (kt % W_STAGES) * W_STAGE, wm, wn, fo);
-              kt++;
-            }
-            msg[s] = rotl13(msg[s]) ^ fold_owned(acc, lane);
-          }
+        for (int s = 0; s < 16; s += 2) {
+          if (c0 + s < nchunks) step(std::integral_constant<int, 0b0101>{}, kt++, msg[(s + 15) & 15], msg[s]);
         }
       }
+    }
+    {  // the last chunk
+      u32 x[8], keep, other;
+      fold_partials(acc, x);
+      fold_scatter(x, lane, keep, other);
+      const int last = (nchunks - 1) & 15;
+#pragma unroll
+      for (int s = 0; s < 16; s++)
+        if (s == last) msg[s] = xor3(rotl13(msg[s]), keep, other);
     }
     // every lane digests the tile it owns: hash block b0, g = 4 (lane >> 5) + 2 b3 + b4, t
     const int hb = lane & 1, g = 4 * (lane >> 5) + 2 * ((lane >> 3) & 1) + ((lane >> 4) & 1), t = (lane >> 1) & 3;
@@ -320,7 +442,8 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
       }
     }
   } else {
-    for (int kt = 0; kt < KT; kt++) kstep(kt);
+    u32 unused = 0;
+    for (int kt = 0; kt < KT; kt++) step(NoFold{}, kt, unused, unused);
   }
 
   // epilogue of one 32 x 32 MFMA block: lane holds col (lane & 31) of rows
@@ -364,7 +487,7 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
     int ig = 0, li = L - 1, kc = 0;
     auto cissue = [&]() {
       const DmaLane cl = dma_lane(p.corrA + (long)li * p.m * R2, R2, p.corrB + (long)li * p.n * R2, R2, bm0, bn0, lane);
-      dma_step(wsm + (ig & (W_STAGES - 1)) * W_STAGE, cl, R2, R2, (long)kc * W_BK, wave);
+      dma_step(wsm + (ig % W_STAGES) * W_STAGE, cl, R2, R2, (long)kc * W_BK, wave);
       ig++;
       if (++kc == CPL) {
         kc = 0;
@@ -387,7 +510,7 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
           tmp[1] = tmp[1] << 7;
         }
         if (++c == CPL) c = 0;
-        step_mma_quarter(tmp, wsm + (g & (W_STAGES - 1)) * W_STAGE, wm, wn, h, nb, fo);
+        step_mma_quarter(tmp, wsm + (g % W_STAGES) * W_STAGE, wm, wn, h, nb, fo);
       }
       store_block(2 * h, nb, acc[2 * h][nb] - tmp[0]);
       store_block(2 * h + 1, nb, acc[2 * h + 1][nb] - tmp[1]);
