@@ -97,11 +97,12 @@ int uwc_noise_perm(uint32_t* out, uint32_t k, uint32_t r, const uint32_t* label,
                    hipStream_t stream);
 
 /* One launch for a nonce's noise: E (rows x r) as uwc_noise_uniform, P (k pairs) as
- * uwc_noise_perm with the same label and key, St (r x k, optional) as uwc_proj_matrix(P), and
- * zeroes zero0[0..n0) and zero1[0..n1) (n <= 256 each, pointers may be NULL with n = 0).
+ * uwc_noise_perm with the same label and key, St (r x k, optional) as uwc_proj_matrix(P), SpT
+ * (optional, r <= 64, 16-byte aligned) = St transposed as k rows of 64 bytes, zero past r,
+ * and zeroes zero0[0..n0) and zero1[0..n1) (n <= 256 each, pointers may be NULL with n = 0).
  * Fuses ops.noise_uniform + ops.noise_perm + ops.proj_matrix of MinedWeight._forward
  * (ops.py:328-336). */
-int uwc_nonce_noise(int8_t* E, int rows, int r, uint32_t* P, int k, int8_t* St, const uint32_t* label,
+int uwc_nonce_noise(int8_t* E, int rows, int r, uint32_t* P, int k, int8_t* St, int8_t* SpT, const uint32_t* label,
                     const uint32_t* key, int32_t* zero0, int n0, int32_t* zero1, int n1, hipStream_t stream);
 
 /* For rows (multiple of 8) x k (multiple of 4) int8 src, each part optional (NULL = skip):
@@ -133,6 +134,21 @@ int uwc_project(const int8_t* src, int rows, int k, int r, const int8_t* St, int
 int uwc_noise_project(const int8_t* src, int rows, int k, int r, const int8_t* E, const uint32_t* Pn, int8_t* dst,
                       const int8_t* St, int8_t* corr, int corr_off, int ecopy_off, int32_t* maxabs, int lmax,
                       hipStream_t stream);
+
+/* The per-nonce operand side of a mined forward in one launch:
+ *   ApEA = int8(A + EA[row][P.first] - EA[row][P.second]), given as A + (SpA * EA^T)^T with
+ *   SpA (k x 64) = uwc_nonce_noise's SpT of those pairs;
+ *   X = A * StB^T -> lmax limbs at corrA[li][row][corr_a_off + j], EA rows copied to
+ *   corrA[li][row][ecopy_off + j] (if ecopy_off >= 0), maxabs[0] = max(maxabs[0], max |X|);
+ *   Y = Bp * StA^T -> lmax limbs at corrB[li][col][corr_b_off + j], maxabs[1] likewise.
+ * A m x k, Bp n x k, StA/StB r x k selection matrices (uwc_proj_matrix / uwc_nonce_noise);
+ * m % 32 == 0, n % 32 == 0, k % 256 == 0, r in {16, 32, 64}, lmax 1..4; A, ApEA, Bp, StA,
+ * StB, SpA, EA 16-byte aligned.
+ * Replaces MinedWeight._forward's noise_rows(A) + project(A) + project(BpEBt) (ops.py:331-336; the
+ * operand noising, both projections and their limbs, kernels.cu:303-404). */
+int uwc_side_project(const int8_t* A, int m, const int8_t* EA, const int8_t* SpA, int8_t* ApEA, const int8_t* StB,
+                     int8_t* corrA, int corr_a_off, int ecopy_off, const int8_t* Bp, int n, const int8_t* StA,
+                     int8_t* corrB, int corr_b_off, int k, int r, int32_t* maxabs, int lmax, hipStream_t stream);
 
 /* detrt quant_act per row of x (rows x k fp32): q = clamp(rint(fwht_bs(x) / s), -qmax, qmax),
  * s = max(max|y|, 1e-8) / qmax, scale = s * (1 / sqrt(bs)) if bs > 1 else s (bs a power of two

@@ -229,6 +229,46 @@ def test_proj_matrix_project_and_noise_project(dev, r):
     assert int(mx2.item()) == int(np.abs(proj).max())
 
 
+@pytest.mark.parametrize("m,n,k,r", [(128, 192, 1536, 64), (64, 32, 4096, 64), (256, 128, 768, 16),
+                                     (96, 64, 256, 32)])
+def test_side_project_matches_oracle(dev, m, n, k, r):
+    """One launch for the operand side: ApEA (noise on the matrix cores from SpA), X limbs + EAL
+    copy (corrA), Y limbs (corrB) and both maxima equal the oracle (1 to 16 chunks of 256
+    columns); maxabs is an atomic max into what the buffer held; a second call gives the same
+    bytes."""
+    ops = _ops()
+    rng = np.random.default_rng(m * 7 + n + k + r)
+    A = rng.integers(-64, 65, size=(m, k), dtype=np.int8)
+    Bp = rng.integers(-64, 65, size=(n, k), dtype=np.int8)
+    E = rng.integers(-32, 32, size=(m, r), dtype=np.int8)
+    PA = O.perm_packed(O.SEED_LABEL_A, rng.bytes(32), k, r)
+    PB = O.perm_packed(O.SEED_LABEL_B, rng.bytes(32), k, r)
+    pack = lambda P: torch.from_numpy(P.view(np.int32).copy()).to(dev)
+    L = ops.limbs_for(k)
+    StA, StB = ops.proj_matrix(pack(PA), k, r), ops.proj_matrix(pack(PB), k, r)
+    SpA = torch.zeros((k, 64), dtype=torch.int8, device=dev)
+    SpA[:, :r] = StA.t()
+    X, Y = O.project(A, PB, r), O.project(Bp, PA, r)
+    wantA = np.zeros((L, m, 2 * r), np.int8)
+    O.write_limbs(X, wantA, 0)
+    for li in range(L):
+        wantA[li, :, r:] = E
+    wantB = np.full((L, n, 2 * r), 7, np.int8)
+    O.write_limbs(Y, wantB, r)
+    Ad, Bd = torch.from_numpy(A).to(dev), torch.from_numpy(Bp).to(dev)
+    for call in range(2):
+        ApEA = torch.empty_like(Ad)
+        corrA = torch.zeros((L, m, 2 * r), dtype=torch.int8, device=dev)
+        corrB = torch.full((L, n, 2 * r), 7, dtype=torch.int8, device=dev)
+        mx = torch.tensor([0, 3], dtype=torch.int32, device=dev)
+        ops.side_project(Ad, torch.from_numpy(E).to(dev), SpA, ApEA, StB, corrA, Bd, StA, corrB, maxabs=mx,
+                         corr_a_off=0, ecopy_off=r, corr_b_off=r)
+        assert np.array_equal(ApEA.cpu().numpy(), O.noise_apply(A, E, PA)), call
+        assert np.array_equal(corrA.cpu().numpy(), wantA), call
+        assert np.array_equal(corrB.cpu().numpy(), wantB), call
+        assert mx.cpu().tolist() == [int(np.abs(X).max()), max(3, int(np.abs(Y).max()))], call
+
+
 def test_projection_paths_identical(dev):
     """The matrix-core projections leave the mined forward bit-identical to the LDS-atomic path:
     output, both correction tensors, maxabs and winning tiles (miner/ampere/tests/test_proj_gemm.py)."""
@@ -261,9 +301,10 @@ def test_nonce_noise_fused_matches_oracle(dev, rows, k, r):
     E = torch.empty((rows, r), dtype=torch.int8, device=dev)
     P = torch.empty(k, dtype=torch.int32, device=dev)
     St = torch.full((r, k), 5, dtype=torch.int8, device=dev)
+    SpT = torch.full((k, 64), 5, dtype=torch.int8, device=dev) if r <= 64 else None
     z0 = torch.full((2,), 9, dtype=torch.int32, device=dev)
     z1 = torch.full((3,), 9, dtype=torch.int32, device=dev)
-    ops.nonce_noise(E, P, k, r, ops.LABEL_A.to(dev), ops.words(key), St=St, zero0=z0, zero1=z1[:1])
+    ops.nonce_noise(E, P, k, r, ops.LABEL_A.to(dev), ops.words(key), St=St, zero0=z0, zero1=z1[:1], SpT=SpT)
     assert np.array_equal(E.cpu().numpy(), O.uniform_matrix(O.SEED_LABEL_A, key, rows, r))
     Pw = O.perm_packed(O.SEED_LABEL_A, key, k, r)
     assert np.array_equal(_u32(P), Pw)
@@ -271,6 +312,10 @@ def test_nonce_noise_fused_matches_oracle(dev, rows, k, r):
     S[(Pw & 0xFFFF).astype(np.int64), np.arange(k)] += 1
     S[(Pw >> 16).astype(np.int64), np.arange(k)] -= 1
     assert np.array_equal(St.cpu().numpy().astype(np.int64), S)
+    if SpT is not None:  # the transpose as 64-byte rows, zero past r
+        want = np.zeros((k, 64), np.int64)
+        want[:, :r] = S.T
+        assert np.array_equal(SpT.cpu().numpy().astype(np.int64), want)
     assert z0.cpu().tolist() == [0, 0] and z1.cpu().tolist() == [0, 9, 9]
 
 

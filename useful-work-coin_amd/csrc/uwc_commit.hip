@@ -252,12 +252,14 @@ extern "C" int uwc_b3_root_and_seed(const uint8_t* data, uint64_t nbytes, const 
 
 // ------------------------------------------------------------------ per-nonce noise in one launch
 // E (rows x r, the uniform_matrix), P (k pairs) and optionally St (the r x k selection matrix
-// of P) from one keyed random_hash per quad (reference.py:67-93, kernels.cu:246-301,
-// ops.py:152-158), and zeroes two counter ranges, in a single latency-bound launch instead of
-// four. Quads [0, rows*r/32) make E blocks; the next ceil(k/8) quads make 8 pairs each and
-// write St's columns for them in full (so St needs no clearing).
+// of P) and SpT (its transpose as k rows of 64 bytes, zero past r) from one keyed random_hash
+// per quad (reference.py:67-93, kernels.cu:246-301, ops.py:152-158), and zeroes two counter
+// ranges, in a single latency-bound launch instead of four. Quads [0, rows*r/32) make E
+// blocks; the next ceil(k/8) quads make 8 pairs each and write St's columns and SpT's rows for
+// them in full (so neither needs clearing).
 __global__ void __launch_bounds__(256) nonce_noise_kernel(i8* __restrict__ E, u32 eblocks, u32* __restrict__ P, u32 k,
-                                                          u32 r, i8* __restrict__ St, const u32* __restrict__ label,
+                                                          u32 r, i8* __restrict__ St, i8* __restrict__ SpT,
+                                                          const u32* __restrict__ label,
                                                           const u32* __restrict__ key, i32* __restrict__ z0, int n0,
                                                           i32* __restrict__ z1, int n1) {
   __shared__ __attribute__((aligned(16))) u8 msgs[64 * B3_QSTRIDE];
@@ -302,14 +304,28 @@ __global__ void __launch_bounds__(256) nonce_noise_kernel(i8* __restrict__ E, u3
         P[l] = first | (second << 16);
         if (St)
           for (u32 j = 0; j < r; j++) St[(u64)j * k + l] = (i8)((int)(first == j) - (int)(second == j));
+        if (SpT) {  // row l: +1 at byte first, -1 at byte second (r <= 64)
+          v4i* row = reinterpret_cast<v4i*>(SpT + (u64)l * 64);
+          const u32 b0 = 1u << (8 * (first & 3)), b1 = 0xFFu << (8 * (second & 3));
+#pragma unroll
+          for (int c = 0; c < 4; c++) {
+            v4i w;
+#pragma unroll
+            for (int d = 0; d < 4; d++)
+              w[d] = (int)(((first >> 2) == (u32)(4 * c + d) ? b0 : 0u) | ((second >> 2) == (u32)(4 * c + d) ? b1 : 0u));
+            row[c] = w;
+          }
+        }
       }
     }
   }
 }
 
-extern "C" int uwc_nonce_noise(int8_t* E, int rows, int r, uint32_t* P, int k, int8_t* St, const uint32_t* label,
-                               const uint32_t* key, int32_t* zero0, int n0, int32_t* zero1, int n1, hipStream_t stream) {
+extern "C" int uwc_nonce_noise(int8_t* E, int rows, int r, uint32_t* P, int k, int8_t* St, int8_t* SpT,
+                               const uint32_t* label, const uint32_t* key, int32_t* zero0, int n0, int32_t* zero1, int n1,
+                               hipStream_t stream) {
   if (!E || !P || !label || !key || rows < 0 || k < 0) return uwc_fail("uwc_nonce_noise: null or negative arguments");
+  if (SpT && (r > 64 || ((uintptr_t)SpT & 15u))) return uwc_fail("uwc_nonce_noise: SpT needs r <= 64 and 16-byte alignment");
   if (r < 2 || r > 65536 || (r & (r - 1))) return uwc_fail("uwc_nonce_noise: r=%d must be a power of two", r);
   if (((u64)rows * r) % 32) return uwc_fail("uwc_nonce_noise: rows * r must be a multiple of 32");
   if (((uintptr_t)E & 3u)) return uwc_fail("uwc_nonce_noise: E must be 4-byte aligned");
@@ -319,6 +335,6 @@ extern "C" int uwc_nonce_noise(int8_t* E, int rows, int r, uint32_t* P, int k, i
   const u64 blocks = quads ? (quads + 63) / 64 : 1;
   if (blocks > 0x7fffffff) return uwc_fail("uwc_nonce_noise: too large");
   hipLaunchKernelGGL(nonce_noise_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, E, (u32)((u64)rows * r / 32), P,
-                     (u32)k, (u32)r, St, label, key, zero0, n0, zero1, n1);
+                     (u32)k, (u32)r, St, SpT, label, key, zero0, n0, zero1, n1);
   return uwc_launch_status("nonce_noise");
 }

@@ -43,6 +43,9 @@
 static_assert(W_LDS <= 160 * 1024, "LDS ring exceeds 160 KiB");
 #define W_WAVES (W_THREADS / 64)
 #define W_SEGS_PER_WAVE (W_TILE / 1024 / W_WAVES)  // 1 KiB DMA segments per wave per operand per k step
+#ifndef W_DB_HASH
+#define W_DB_HASH 0  // double-buffered fragments in the hashing kernels too
+#endif
 
 #define FLAG_HASH 1
 #define FLAG_DENOISE 2
@@ -236,15 +239,47 @@ __device__ __forceinline__ void pass_mma(v16i acc[4][2], Frag& f, u32 x[8], cons
   if constexpr (READ) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
 }
 
+// Double-buffered form of pass_mma: with READ, the six fragments of pass nkp go into nxt
+// before the MFMAs on cur, so they have the whole pass to land. Costs a second fragment set
+// (24 VGPRs); used where registers allow.
+template <bool FOLD, bool READ>
+__device__ __forceinline__ void pass_mma_db(v16i acc[4][2], const Frag& cur, Frag& nxt, u32 x[8], const u8* nst,
+                                            int wm, int wn, const FragOff& fo, int nkp) {
+  if constexpr (READ) frag_read(nxt, nst, wm, wn, fo, nkp);
+#pragma unroll
+  for (int mb = 0; mb < 4; mb++)
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++) {
+      if constexpr (FOLD) fold_block(acc[mb][nb], x + (mb >> 1) * 4, (mb & 1) == 0 && nb == 0);
+      acc[mb][nb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.a[mb], cur.b[nb], acc[mb][nb], 0, 0, 0);
+    }
+  if constexpr (READ) __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    if constexpr (FOLD) __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+  }
+}
+
 // Denoise k step for one quarter of the wave's block: M blocks 2h, 2h+1 of column half nb.
+// The fragments of two passes are requested before their MFMAs, so each MFMA waits only for
+// its own reads and the second pass's reads overlap the first pass's MFMAs.
 __device__ __forceinline__ void step_mma_quarter(v16i tmp[2], const u8* stage, int wm, int wn, int h, int nb,
                                                  const FragOff& fo) {
 #pragma unroll
-  for (int kp = 0; kp < W_KP; kp++) {
-    const v4i a0 = frag_a(stage, wm, fo, kp, 2 * h), a1 = frag_a(stage, wm, fo, kp, 2 * h + 1);
-    const v4i b = frag_b(stage, wn, fo, kp, nb);
-    tmp[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b, tmp[0], 0, 0, 0);
-    tmp[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b, tmp[1], 0, 0, 0);
+  for (int k2 = 0; k2 < W_KP; k2 += 2) {
+    v4i a0[2], a1[2], b[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      b[j] = frag_b(stage, wn, fo, k2 + j, nb);
+      a0[j] = frag_a(stage, wm, fo, k2 + j, 2 * h);
+      a1[j] = frag_a(stage, wm, fo, k2 + j, 2 * h + 1);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      tmp[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0[j], b[j], tmp[0], 0, 0, 0);
+      tmp[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1[j], b[j], tmp[1], 0, 0, 0);
+    }
   }
 }
 
@@ -345,8 +380,10 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
   for (int s = 0; s < W_STAGES; s++)
     if (s < KT) dma_step(wsm + s * W_STAGE, dl, k, k, (long)s * W_BK, wave);
   wait_step(min(KT - 1, W_STAGES - 1));
-  Frag cur;
-  frag_read(cur, wsm, wm, wn, fo, 0);
+  // fragment sets: single set streamed (pass_mma) or two alternating sets (pass_mma_db)
+  constexpr bool DB = !HASH || W_DB_HASH;
+  Frag fb[DB ? 2 : 1];
+  frag_read(fb[0], wsm, wm, wn, fo, 0);
 
   // One k step. Pass kp runs its MFMAs on the fragments in `cur` while reading those of pass
   // kp + 1. Before the last pass the wave waits for step kt + 1 (vmcnt + barrier: every wave is
@@ -361,17 +398,20 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
       constexpr int kp = decltype(kpc)::value;
       constexpr bool fold = ((FM >> kp) & 1) != 0;
       u32 x[8];
-      if constexpr (kp + 1 < W_KP) {
-        pass_mma<fold, true>(acc, cur, x, st, wm, wn, fo, kp + 1);
-      } else {
+      const u8* nst = st;
+      int nkp = kp + 1;
+      if constexpr (kp + 1 == W_KP) {
         if (kt + 1 < KT) {
           asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this stage's reads are complete
           wait_step(min(KT - 2 - kt, W_STAGES - 2));
           if (kt + W_STAGES < KT)
             dma_step(wsm + (kt % W_STAGES) * W_STAGE, dl, k, k, (long)(kt + W_STAGES) * W_BK, wave);
         }
-        pass_mma<fold, true>(acc, cur, x, wsm + ((kt + 1) % W_STAGES) * W_STAGE, wm, wn, fo, 0);
+        nst = wsm + ((kt + 1) % W_STAGES) * W_STAGE;
+        nkp = 0;
       }
+      if constexpr (DB) pass_mma_db<fold, true>(acc, fb[kp & 1], fb[(kp + 1) & 1], x, nst, wm, wn, fo, nkp);
+      else pass_mma<fold, true>(acc, fb[0], x, nst, wm, wn, fo, nkp);
       if constexpr (fold) fold_into(kp == 0 ? m0 : m1, x, lane);
     });
   };
@@ -450,21 +490,26 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
   // 8 (e >> 2) + 4 (lane >> 5) + (e & 3)
   auto store_block = [&](int mb, int nb, const v16i& v) {
     if constexpr (OUT != OUT_NONE) {
-      const int col = bn0 + wn * 64 + nb * 32 + (lane & 31);
+      constexpr int ES = OUT == OUT_BF16 ? 2 : 4;  // output element bytes
+      // element e of the block is row row0 + 8 (e >> 2) + (e & 3) + lr, column col0 + lc: a
+      // wave-uniform base per e plus one 32-bit lane offset (scalar-base addressing)
+      const int row0 = bm0 + wm * 128 + mb * 32, col0 = bn0 + wn * 64 + nb * 32;
+      const int lr = 4 * (lane >> 5), lc = lane & 31;
+      const u32 loff = (u32)(lr * p.n + lc) * ES;
       float bsc = 0.f;
-      if constexpr (OUT == OUT_BF16 || OUT == OUT_F32) bsc = p.b_scale[col];
+      if constexpr (OUT == OUT_BF16 || OUT == OUT_F32) bsc = p.b_scale[col0 + lc];
 #pragma unroll
       for (int e = 0; e < 16; e++) {
-        const int row = bm0 + wm * 128 + mb * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-        const long o = (long)row * p.n + col;
+        const int re = row0 + 8 * (e >> 2) + (e & 3);
+        u8* base = reinterpret_cast<u8*>(p.out) + ((long)re * p.n + col0) * ES;
         if constexpr (OUT == OUT_I32) {
-          reinterpret_cast<i32*>(p.out)[o] = v[e];
+          *reinterpret_cast<i32*>(base + loff) = v[e];
         } else {
-          const float y = __fmul_rn(__fmul_rn((float)v[e], p.a_scale[row]), bsc);
+          const float y = __fmul_rn(__fmul_rn((float)v[e], p.a_scale[re + lr]), bsc);
           if constexpr (OUT == OUT_F32)
-            reinterpret_cast<float*>(p.out)[o] = y;
+            *reinterpret_cast<float*>(base + loff) = y;
           else
-            reinterpret_cast<uint16_t*>(p.out)[o] = (uint16_t)bf16_rne(y);
+            *reinterpret_cast<uint16_t*>(base + loff) = (uint16_t)bf16_rne(y);
         }
       }
     }
@@ -474,8 +519,10 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
     // acc -= sum_li 128^li [X_li | EAL] [EBRt | Y_li]^T, exact mod 2^32, Horner over limbs
     // (kernels.cu:598-673). Four passes over quarters of the wave's block keep the Horner
     // accumulator at 32 registers; each quarter is stored as soon as it is final. The corr k
-    // steps (limb L-1 down to 0, each 2r / 64 chunks) stream through one continuous ring for all
-    // passes: global step g is corr step g mod CT.
+    // steps run limb L-1 down to 0, each limb 2r / W_BK steps. When all CT of them fit in the
+    // ring (L * 2r <= W_STAGES * W_BK: the mining shapes) they are loaded once in one burst and
+    // the four passes read them without further barriers; otherwise they stream through the ring
+    // continuously across the passes (global step g is corr step g mod CT).
     const int mx = max(p.maxabs[0], p.maxabs[1]);
     int L = mx > 1040319 ? 4 : mx > 8127 ? 3 : mx > 63 ? 2 : 1;
     L = min(L, p.lmax);
@@ -494,6 +541,27 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
         li = li == 0 ? L - 1 : li - 1;
       }
     };
+    if (CT <= W_STAGES) {
+      for (int t = 0; t < CT; t++) cissue();  // corr step t -> stage t
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int h = q >> 1, nb = q & 1;
+        v16i tmp[2] = {v16i{}, v16i{}};
+        for (int t = 0, c = 0; t < CT; t++) {
+          if (c == 0) {
+            tmp[0] = tmp[0] << 7;
+            tmp[1] = tmp[1] << 7;
+          }
+          if (++c == CPL) c = 0;
+          step_mma_quarter(tmp, wsm + t * W_STAGE, wm, wn, h, nb, fo);
+        }
+        store_block(2 * h, nb, acc[2 * h][nb] - tmp[0]);
+        store_block(2 * h + 1, nb, acc[2 * h + 1][nb] - tmp[1]);
+      }
+      return;
+    }
 #pragma unroll
     for (int g = 0; g < W_STAGES - 1; g++)
       if (g < GT) cissue();

@@ -28,10 +28,11 @@ SIGNATURES = {
     "uwc_noise_uniform": [vp, u32, vp, vp, vp, i32, vp],
     "uwc_noise_perm": [vp, u32, u32, vp, vp, vp],
     "uwc_noise_rows": [vp, i32, i32, i32, vp, vp, vp, vp, vp, i32, i32, vp, i32, vp],
-    "uwc_nonce_noise": [vp, i32, i32, vp, i32, vp, vp, vp, vp, i32, vp, i32, vp],
+    "uwc_nonce_noise": [vp, i32, i32, vp, i32, vp, vp, vp, vp, vp, i32, vp, i32, vp],
     "uwc_proj_matrix": [vp, i32, i32, vp, vp],
     "uwc_project": [vp, i32, i32, i32, vp, vp, i32, vp, i32, vp],
     "uwc_noise_project": [vp, i32, i32, i32, vp, vp, vp, vp, vp, i32, i32, vp, i32, vp],
+    "uwc_side_project": [vp, i32, vp, vp, vp, vp, vp, i32, i32, vp, i32, vp, vp, i32, i32, i32, vp, i32, vp],
     "uwc_quant_act_f32": [vp, i32, i32, i32, i32, vp, vp, vp],
     "uwc_dequant_f32": [vp, vp, vp, i32, i32, vp, vp],
 }

@@ -117,14 +117,15 @@ def noise_perm(out: torch.Tensor, k: int, r: int, label: torch.Tensor, key: torc
 
 
 def nonce_noise(E: torch.Tensor, P: torch.Tensor, k: int, r: int, label: torch.Tensor, key: torch.Tensor,
-                St: torch.Tensor | None = None, zero0=None, zero1=None):
-    """noise_uniform(E) + noise_perm(P) + proj_matrix(P) -> St in one launch; zeroes zero0 and zero1."""
+                St: torch.Tensor | None = None, zero0=None, zero1=None, SpT: torch.Tensor | None = None):
+    """noise_uniform(E) + noise_perm(P) + proj_matrix(P) -> St (and its transpose SpT, k x 64) in
+    one launch; zeroes zero0 and zero1."""
     rows = E.shape[0]
     _check(E.shape[1] == r and P.numel() >= k, "nonce_noise: E must be rows x r and P hold k words")
     n0 = zero0.numel() if zero0 is not None else 0
     n1 = zero1.numel() if zero1 is not None else 0
-    _lib.call("uwc_nonce_noise", _p(E), rows, r, _p(P), k, _p(St), _p(label), _p(key), _p(zero0), n0, _p(zero1), n1,
-              _stream())
+    _lib.call("uwc_nonce_noise", _p(E), rows, r, _p(P), k, _p(St), _p(SpT), _p(label), _p(key), _p(zero0), n0,
+              _p(zero1), n1, _stream())
 
 
 def noise_rows(src, rows, k, r, *, E=None, Pn=None, dst=None, Pp=None, corr=None, corr_off=-1, ecopy_off=-1,
@@ -158,6 +159,27 @@ def noise_project(src, rows, k, r, *, E, Pn, dst, St=None, corr=None, corr_off=-
     lmax = corr.shape[0] if corr is not None else 0
     _lib.call("uwc_noise_project", _p(src), rows, k, r, _p(E), _p(Pn), _p(dst), _p(St), _p(corr), corr_off, ecopy_off,
               _p(maxabs), lmax, _stream())
+
+
+def side_ok(m: int, n: int, k: int, r: int) -> bool:
+    """Shapes uwc_side_project takes."""
+    return m % 32 == 0 and n % 32 == 0 and k % 256 == 0 and r in (16, 32, 64)
+
+
+def side_project(A, EA, SpA, ApEA, StB, corrA, Bp, StA, corrB, *, maxabs, corr_a_off=0, ecopy_off=-1, corr_b_off=0):
+    """One launch for a nonce's operand side (ops.py:331-336): ApEA = A noised with EA and the
+    pairs whose transposed selection matrix is SpA (k x 64, nonce_noise's SpT), X = A StB^T and
+    Y = Bp StA^T into their limbs (corrA / corrB), EA copied into corrA at ecopy_off,
+    maxabs[0..1] = max(maxabs, max |X|), max(maxabs, max |Y|)."""
+    m, k = A.shape
+    n, r = Bp.shape[0], StA.shape[0]
+    _check(side_ok(m, n, k, r), f"side_project: m={m} n={n} k={k} r={r} unsupported")
+    _check(all(t.is_contiguous() for t in (A, EA, SpA, ApEA, StB, corrA, Bp, StA, corrB)),
+           "side_project: tensors must be contiguous")
+    _check(SpA.shape == (k, 64), "side_project: SpA must be k x 64")
+    _check(corrA.shape[0] == corrB.shape[0], "side_project: corrA and corrB need the same limb count")
+    _lib.call("uwc_side_project", _p(A), m, _p(EA), _p(SpA), _p(ApEA), _p(StB), _p(corrA), corr_a_off, ecopy_off,
+              _p(Bp), n, _p(StA), _p(corrB), corr_b_off, k, r, _p(maxabs), corrA.shape[0], _stream())
 
 
 # ------------------------------------------------------------------ GEMM
@@ -265,6 +287,7 @@ class MinedWeight:
                 PA=torch.empty(k, dtype=torch.int32, device=dev),
                 ApEA=torch.empty((m, k), dtype=torch.int8, device=dev),
                 SA=torch.empty((r, k), dtype=torch.int8, device=dev),
+                SpA=torch.empty((k, 64), dtype=torch.int8, device=dev) if r <= 64 else None,
                 corrA=torch.zeros((limbs_for(k), m, 2 * r), dtype=torch.int8, device=dev),
                 maxabs=torch.zeros(2, dtype=torch.int32, device=dev),
                 scratch=torch.empty(max(8, b3_scratch_words(m * k)), dtype=torch.int32, device=dev),
@@ -298,11 +321,16 @@ class MinedWeight:
         # 3. ApEA = A + EAL*P_A ; X = A * P_B^T (limbs) ; EAL copy
         # 4. Y = BpEBt * P_A^T (limbs)
         if proj:  # projections on the matrix cores (the reference's PROJ_GEMM path)
+            side = side_ok(m, n, k, r)
             nonce_noise(b["EAL"], b["PA"], k, r, c["LABEL_A"], b["a_seed"], St=b["SA"], zero0=b["maxabs"],
-                        zero1=b["wins"][:1])
-            noise_project(A, m, k, r, E=b["EAL"], Pn=b["PA"], dst=b["ApEA"], St=self.SBt, corr=b["corrA"], corr_off=0,
-                          ecopy_off=r, maxabs=b["maxabs"][0:1])
-            project(self.BpEBt, b["SA"], self.corrB, r, b["maxabs"][1:2])
+                        zero1=b["wins"][:1], SpT=b["SpA"] if side else None)
+            if side:
+                side_project(A, b["EAL"], b["SpA"], b["ApEA"], self.SBt, b["corrA"], self.BpEBt, b["SA"], self.corrB,
+                             maxabs=b["maxabs"], corr_a_off=0, ecopy_off=r, corr_b_off=r)
+            else:
+                noise_project(A, m, k, r, E=b["EAL"], Pn=b["PA"], dst=b["ApEA"], St=self.SBt, corr=b["corrA"],
+                              corr_off=0, ecopy_off=r, maxabs=b["maxabs"][0:1])
+                project(self.BpEBt, b["SA"], self.corrB, r, b["maxabs"][1:2])
         else:     # projections by LDS atomics (noise_rows with Pp)
             noise_uniform(b["EAL"], c["LABEL_A"], b["a_seed"], zero_me=b["maxabs"], zero_n=2)
             b["wins"][:1].zero_()
