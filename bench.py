@@ -171,6 +171,89 @@ def detrt_layer(args, torch, np):
     return out
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "noisy_gemm256_mining_4096_traffic.txt")
+COPY_BYTES = 256 << 20  # the calibration copy: reads and writes exactly this many bytes
+
+
+def traffic_probe(args, torch, ops, O, np):
+    """What the two rocprofv3 --pmc passes (FETCH_SIZE, then WRITE_SIZE) profile: a few mined
+    forwards at the bench shape, then a plain device copy of COPY_BYTES three times, whose
+    counter readings calibrate the KiB units of both counters."""
+    args.steps, args.warmup = 4, 2
+    mining(args, torch, np, ops, O)
+    x = torch.empty(COPY_BYTES, dtype=torch.int8, device="cuda").fill_(1)
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    log("traffic probe: done")
+
+
+def summarize_pmc(fetch_csv, write_csv, cmd):
+    """Per-dispatch FETCH_SIZE / WRITE_SIZE of the noisy GEMM, each scaled by COPY_BYTES over the
+    counter's reading for the calibration copy, into TRAFFIC_FILE."""
+    import csv
+    import statistics
+
+    def per_kernel(path, counter):
+        vals = {}
+        for row in csv.DictReader(open(path)):
+            if row["Counter_Name"].startswith(counter):
+                vals.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+        return vals
+
+    out = {}
+    for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        v = per_kernel(path, counter)
+        gemm = [x for name, xs in v.items() if "noisy_gemm256_kernel<true, true, 1>" in name for x in xs]
+        copy = [x for name, xs in v.items() if "copy" in name.lower() for x in xs]  # the runtime's blit kernel
+        copy = [x for x in copy if x > 0.5 * COPY_BYTES / 1024]  # the 256 MiB copies, not tensor setup
+        gk, ck = statistics.median(gemm), statistics.median(copy)
+        factor = COPY_BYTES / (ck * 1024.0)
+        out[counter] = dict(gemm_kib=gk, copy_kib=ck, factor=factor, bytes=gk * 1024.0 * factor, n=len(gemm))
+    traffic = out["FETCH_SIZE"]["bytes"] + out["WRITE_SIZE"]["bytes"]
+    with open(TRAFFIC_FILE, "w") as f:
+        f.write("HBM traffic of noisy_gemm256_kernel<true, true, 1> (mining, 4096^3, r=64, L=2), bytes per dispatch\n")
+        f.write(f"commands: {cmd}\n")
+        for c in ("FETCH_SIZE", "WRITE_SIZE"):
+            d = out[c]
+            f.write(f"{c}: median {d['gemm_kib']:.1f} KiB per dispatch over {d['n']} dispatches; calibration copy of "
+                    f"{COPY_BYTES} B reads {d['copy_kib']:.1f} KiB -> factor {d['factor']:.4f} -> {d['bytes']:.0f} B\n")
+        f.write(f"traffic_bytes_per_launch: {traffic:.0f}\n")
+    print(open(TRAFFIC_FILE).read())
+
+
+def summarize_trace(stats_csv, out_path, cmd, nonces):
+    """A kernel-trace --stats table (per kernel: calls, average, share) as text, per nonce."""
+    import csv
+    import re
+    rows = list(csv.DictReader(open(stats_csv)))
+    with open(out_path, "w") as f:
+        f.write(f"rocprofv3 kernel trace, mined forward 4096x4096x4096 r=64 (bench.py workload), {nonces} timed nonces\n")
+        f.write(f"command: {cmd}\n\n")
+        f.write(f"{'kernel':58s} {'calls':>6s} {'avg_us':>9s} {'min_us':>9s} {'max_us':>9s} {'share':>6s}\n")
+        for r in rows:
+            name = re.sub(r"\(.*", "", r["Name"])[:58]
+            f.write(f"{name:58s} {int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:9.2f} {float(r['MinNs']) / 1e3:9.2f} "
+                    f"{float(r['MaxNs']) / 1e3:9.2f} {float(r['Percentage']):5.1f}%\n")
+        f.write("\nPer nonce: b3_chunks + b3_reduce (commitment of A), nonce_noise (E_A, P_A, selection matrices),\n"
+                "side_kernel (noised A, both projections in limbs), noisy_gemm256_kernel<true, true, 1> (hashed GEMM,\n"
+                "exact denoise, int32 out). at::native random kernels = the bench's setup of its distinct A inputs,\n"
+                "outside the timed region; the rest = setup_block and the warm-up.\n")
+    print(open(out_path).read())
+
+
+def read_traffic():
+    """traffic_bytes_per_launch from the committed summary, or None."""
+    try:
+        for line in open(TRAFFIC_FILE):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -183,7 +266,18 @@ def main():
     ap.add_argument("--cpu-max-nonces", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-detrt", action="store_true")
+    ap.add_argument("--traffic-probe", action="store_true", help="the workload of the FETCH_SIZE / WRITE_SIZE passes")
+    ap.add_argument("--summarize-pmc", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "CMD"),
+                    help="write the traffic summary under profiles/ from two counter_collection.csv files")
+    ap.add_argument("--summarize-trace", nargs=4, metavar=("STATS_CSV", "OUT", "CMD", "NONCES"),
+                    help="write a kernel-trace summary under profiles/ from a kernel_stats.csv")
     args = ap.parse_args()
+    if args.summarize_trace:
+        summarize_trace(*args.summarize_trace)
+        return
+    if args.summarize_pmc:
+        summarize_pmc(*args.summarize_pmc)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the multi-GPU layout "
               "is a design in DESIGN.md, not a measured path", file=sys.stderr)
@@ -195,6 +289,9 @@ def main():
     import oracle as O
     from uwc_amd import ops
 
+    if args.traffic_probe:
+        traffic_probe(args, torch, ops, O, np)
+        return
     res = mining(args, torch, np, ops, O)
     parity, cpu = (None, None) if args.no_cpu else parity_and_cpu(args, res, torch, np, ops, O)
     det = None if args.no_detrt else detrt_layer(args, torch, np)
@@ -217,8 +314,8 @@ def main():
                                f"{m}x{n}x{k}, r={r}, one nonce per step, {args.steps}-nonce sweep",
                    "m": m, "n": n, "k": k, "r": r, "noise": "reference rules (E in [-32,31], +-1 pairs)"},
         "roofline": {"bound": "mfma", "achieved": round(res["kern_tops"], 2), "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
-                     "frac": round(res["kern_tops"] / PEAK_INT8_TOPS, 4), "traffic": None,
-                     "kernel": "noisy_gemm_kernel<HASH,DENOISE,OUT_I32>", "avg_us": round(res["kern_ms"] * 1e3, 2),
+                     "frac": round(res["kern_tops"] / PEAK_INT8_TOPS, 4), "traffic": read_traffic(),
+                     "kernel": "noisy_gemm256_kernel<HASH=true, DENOISE=true, OUT_I32>", "avg_us": round(res["kern_ms"] * 1e3, 2),
                      "ops_per_launch": 2 * m * n * k + 2 * m * n * 2 * r * res["L"]},
         "cpu_baseline": cpu,
         "parity": parity,
