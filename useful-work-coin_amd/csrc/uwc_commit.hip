@@ -254,25 +254,33 @@ extern "C" int uwc_b3_root_and_seed(const uint8_t* data, uint64_t nbytes, const 
 // E (rows x r, the uniform_matrix), P (k pairs) and optionally St (the r x k selection matrix
 // of P) and SpT (its transpose as k rows of 64 bytes, zero past r) from one keyed random_hash
 // per quad (reference.py:67-93, kernels.cu:246-301, ops.py:152-158), and zeroes two counter
-// ranges, in a single latency-bound launch instead of four. Quads [0, rows*r/32) make E
-// blocks; the next ceil(k/8) quads make 8 pairs each and write St's columns and SpT's rows for
-// them in full (so neither needs clearing).
-__global__ void __launch_bounds__(256) nonce_noise_kernel(i8* __restrict__ E, u32 eblocks, u32* __restrict__ P, u32 k,
-                                                          u32 r, i8* __restrict__ St, i8* __restrict__ SpT,
+// ranges, in a single latency-bound launch instead of four. Workgroups [0, nE) make E blocks
+// (one quad per 32-byte block); the rest make 8 pairs per quad. A P wave owns 128 consecutive
+// columns: it builds their St rows (r x 128 bytes) and SpT rows (128 x 64 bytes) in LDS by a
+// zero fill and a 2-byte scatter per pair, then writes them with 16-byte stores (column-wise
+// byte stores of St cost several times more).
+#define NN_COLS 128  // columns per P wave
+
+__device__ __forceinline__ void pair_of(u32 u, u32 r, u32& first, u32& second) {
+  first = u & (r - 1);
+  second = first ^ (1u + __umulhi(r - 1, u));
+}
+
+__global__ void __launch_bounds__(256) nonce_noise_kernel(i8* __restrict__ E, u32 eblocks, u32 nE, u32* __restrict__ P,
+                                                          u32 k, u32 r, i8* __restrict__ St, i8* __restrict__ SpT,
                                                           const u32* __restrict__ label,
                                                           const u32* __restrict__ key, i32* __restrict__ z0, int n0,
                                                           i32* __restrict__ z1, int n1) {
   __shared__ __attribute__((aligned(16))) u8 msgs[64 * B3_QSTRIDE];
-  const int tid = threadIdx.x, q = tid & 3, lq = tid >> 2;
+  extern __shared__ __attribute__((aligned(16))) u8 nn_blk[];  // per P wave: St [r][128], SpT [128][64]
+  const int tid = threadIdx.x, q = tid & 3, lq = tid >> 2, lane = tid & 63, wave = tid >> 6;
   if (blockIdx.x == 0) {
     if (z0 && tid < n0) z0[tid] = 0;
     if (z1 && tid < n1) z1[tid] = 0;
   }
-  const u32 quad = blockIdx.x * 64 + lq;
-  const u32 pblocks = (k + 7) / 8;
-  const bool is_e = quad < eblocks, is_p = !is_e && quad < eblocks + pblocks;
-  const u32 index = is_e ? quad : quad - eblocks;
-  const int prepend = is_e ? 0 : 1;
+  const bool pblk = blockIdx.x >= nE;
+  const u32 index = pblk ? (blockIdx.x - nE) * 64 + lq : blockIdx.x * 64 + lq;  // E block or pair octet
+  const int prepend = pblk ? 1 : 0;
   // message words 4q..4q+3 of msg: 0 except word `prepend` = 1 + index; words 8..15 = label
   u32* mw = reinterpret_cast<u32*>(msgs + lq * B3_QSTRIDE);
 #pragma unroll
@@ -285,40 +293,72 @@ __global__ void __launch_bounds__(256) nonce_noise_kernel(i8* __restrict__ E, u3
   u32 lo, hi;
   quad_compress(msgs + lq * B3_QSTRIDE, off, q, key[q], key[4 + q], 0, 64,
                 B3_CHUNK_START | B3_CHUNK_END | B3_ROOT | B3_KEYED, lo, hi);
-  if (is_e) {
-    // digest bytes -> (y & 63) - 32: the 6-bit value (y & 63) ^ 32 sign-extended per byte
-    u32 z = (lo & 0x3F3F3F3Fu) ^ 0x20202020u, s = z & 0x20202020u;
-    const u32 elo = z | (s << 1) | (s << 2);
-    z = (hi & 0x3F3F3F3Fu) ^ 0x20202020u; s = z & 0x20202020u;
-    const u32 ehi = z | (s << 1) | (s << 2);
-    u32* dst = reinterpret_cast<u32*>(E + (u64)index * 32);
-    dst[q] = elo;
-    dst[4 + q] = ehi;
-  } else if (is_p) {
+  if (!pblk) {
+    if (index < eblocks) {
+      // digest bytes -> (y & 63) - 32: the 6-bit value (y & 63) ^ 32 sign-extended per byte
+      u32 z = (lo & 0x3F3F3F3Fu) ^ 0x20202020u, sg = z & 0x20202020u;
+      const u32 elo = z | (sg << 1) | (sg << 2);
+      z = (hi & 0x3F3F3F3Fu) ^ 0x20202020u; sg = z & 0x20202020u;
+      const u32 ehi = z | (sg << 1) | (sg << 2);
+      u32* dst = reinterpret_cast<u32*>(E + (u64)index * 32);
+      dst[q] = elo;
+      dst[4 + q] = ehi;
+    }
+    return;
+  }
+  // pairs l = 8 index + q + 4 h
+  u32 f[2], sc[2];
+  bool v[2];
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
-      const u32 l = index * 8 + q + 4 * h;
-      if (l < k) {
-        const u32 u = h ? hi : lo, first = u & (r - 1);
-        const u32 second = first ^ (1u + __umulhi(r - 1, u));
-        P[l] = first | (second << 16);
-        if (St)
-          for (u32 j = 0; j < r; j++) St[(u64)j * k + l] = (i8)((int)(first == j) - (int)(second == j));
-        if (SpT) {  // row l: +1 at byte first, -1 at byte second (r <= 64)
-          v4i* row = reinterpret_cast<v4i*>(SpT + (u64)l * 64);
-          const u32 b0 = 1u << (8 * (first & 3)), b1 = 0xFFu << (8 * (second & 3));
+  for (int h = 0; h < 2; h++) {
+    const u32 l = index * 8 + q + 4 * h;
+    v[h] = l < k;
+    pair_of(h ? hi : lo, r, f[h], sc[h]);
+    if (v[h]) P[l] = f[h] | (sc[h] << 16);
+  }
+  if (!St && !SpT) return;
+  if (r > 128) {  // large r: St column by column (SpT needs r <= 64)
 #pragma unroll
-          for (int c = 0; c < 4; c++) {
-            v4i w;
+    for (int h = 0; h < 2; h++)
+      if (v[h] && St)
+        for (u32 j = 0; j < r; j++)
+          St[(u64)j * k + index * 8 + q + 4 * h] = (i8)((int)(f[h] == j) - (int)(sc[h] == j));
+    return;
+  }
+  const int stb = St ? (int)r * NN_COLS : 0, blk = stb + (SpT ? NN_COLS * 64 : 0);
+  u8* wst = nn_blk + wave * blk;  // this wave's St block, then its SpT block
+  u8* wsp = wst + stb;
+  for (int i = lane * 16; i < blk; i += 64 * 16) *reinterpret_cast<v4i*>(wst + i) = v4i{0, 0, 0, 0};
+  __builtin_amdgcn_wave_barrier();  // a wave's LDS accesses complete in order
 #pragma unroll
-            for (int d = 0; d < 4; d++)
-              w[d] = (int)(((first >> 2) == (u32)(4 * c + d) ? b0 : 0u) | ((second >> 2) == (u32)(4 * c + d) ? b1 : 0u));
-            row[c] = w;
-          }
-        }
+  for (int h = 0; h < 2; h++) {
+    if (!v[h]) continue;
+    const int c = (lq & 15) * 8 + q + 4 * h;  // column within the wave's 128
+    if (St) { wst[f[h] * NN_COLS + c] = 1; wst[sc[h] * NN_COLS + c] = 0xFF; }
+    if (SpT) { wsp[c * 64 + f[h]] = 1; wsp[c * 64 + sc[h]] = 0xFF; }
+  }
+  __builtin_amdgcn_wave_barrier();
+  const u32 l0 = ((blockIdx.x - nE) * 64 + wave * 16) * 8;
+  if (St) {
+    const bool vec = (k % 16) == 0;
+    for (int idx = lane; idx < (int)r * 8; idx += 64) {
+      const int j = idx >> 3, cc = idx & 7;
+      const u32 col = l0 + 16 * cc;
+      if (col >= k) continue;
+      const v4i d = *reinterpret_cast<const v4i*>(wst + j * NN_COLS + 16 * cc);
+      if (vec) {
+        *reinterpret_cast<v4i*>(St + (u64)j * k + col) = d;
+      } else {
+        for (int b = 0; b < 16 && col + b < k; b++) St[(u64)j * k + col + b] = (i8)(((u32)d[b >> 2] >> (8 * (b & 3))) & 0xFF);
       }
     }
   }
+  if (SpT)
+    for (int idx = lane; idx < NN_COLS * 4; idx += 64) {
+      const int c = idx >> 2, cc = idx & 3;
+      if (l0 + c < k)
+        *reinterpret_cast<v4i*>(SpT + (u64)(l0 + c) * 64 + 16 * cc) = *reinterpret_cast<const v4i*>(wsp + c * 64 + 16 * cc);
+    }
 }
 
 extern "C" int uwc_nonce_noise(int8_t* E, int rows, int r, uint32_t* P, int k, int8_t* St, int8_t* SpT,
@@ -331,10 +371,17 @@ extern "C" int uwc_nonce_noise(int8_t* E, int rows, int r, uint32_t* P, int k, i
   if (((uintptr_t)E & 3u)) return uwc_fail("uwc_nonce_noise: E must be 4-byte aligned");
   if (n0 < 0 || n1 < 0 || n0 > 256 || n1 > 256 || (n0 && !zero0) || (n1 && !zero1))
     return uwc_fail("uwc_nonce_noise: zero ranges must be 0..256 words with pointers");
-  const u64 quads = (u64)rows * r / 32 + ((u64)k + 7) / 8;
-  const u64 blocks = quads ? (quads + 63) / 64 : 1;
+  const u64 eblocks = (u64)rows * r / 32, nE = (eblocks + 63) / 64, nP = (((u64)k + 7) / 8 + 63) / 64;
+  const u64 blocks = nE + nP > 0 ? nE + nP : 1;
   if (blocks > 0x7fffffff) return uwc_fail("uwc_nonce_noise: too large");
-  hipLaunchKernelGGL(nonce_noise_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, E, (u32)((u64)rows * r / 32), P,
+  const size_t smem = r <= 128 ? (size_t)4 * ((St ? (size_t)r * NN_COLS : 0) + (SpT ? NN_COLS * 64 : 0)) : 0;
+  static bool attr = false;  // one attribute call (96 KiB at r = 128 with SpT absent, 64 KiB + 32 KiB max)
+  if (!attr) {
+    (void)hipFuncSetAttribute((const void*)nonce_noise_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              4 * (128 * NN_COLS + NN_COLS * 64));
+    attr = true;
+  }
+  hipLaunchKernelGGL(nonce_noise_kernel, dim3((unsigned)blocks), dim3(256), smem, stream, E, (u32)eblocks, (u32)nE, P,
                      (u32)k, (u32)r, St, SpT, label, key, zero0, n0, zero1, n1);
   return uwc_launch_status("nonce_noise");
 }
