@@ -152,7 +152,7 @@ int uwc_side_project(const int8_t* A, int m, const int8_t* EA, const int8_t* SpA
 
 /* detrt quant_act per row of x (rows x k fp32): q = clamp(rint(fwht_bs(x) / s), -qmax, qmax),
  * s = max(max|y|, 1e-8) / qmax, scale = s * (1 / sqrt(bs)) if bs > 1 else s (bs a power of two
- * dividing k, or 0/1 for none; k <= 40960).
+ * dividing k, or 0/1 for none; k % 512 == 0 with bs <= 512, else k <= 40960).
  * Replaces core.quant_act / detgpu quant_act_f32: runtime/detrt/core.py:162-195,
  * runtime/detgpu/kernels.py:75-114. */
 int uwc_quant_act_f32(const float* x, int rows, int k, int bs, int qmax, int8_t* q, float* scale, hipStream_t stream);

@@ -86,7 +86,8 @@ def test_linear_fixtures(dev, name):
             assert torch.equal(y, y2)
 
 
-@pytest.mark.parametrize("k,bs", [(2048, 512), (6144, 512), (4096, 128), (14336, 128), (2048, 0), (128, 64)])
+@pytest.mark.parametrize("k,bs", [(2048, 512), (6144, 512), (4096, 128), (14336, 128), (2048, 0), (128, 64),
+                                  (4096, 512), (4608, 512), (1536, 1), (512, 8), (640, 128), (4096, 1024)])
 def test_quant_act_random_rows(dev, k, bs):
     """fp32 sweep: IEEE adds, max, divide, rint and sqrt on gfx950 equal x86 SSE bit for bit,
     including tiny, huge and all-zero rows (runtime/tests/test_fp32_native.py)."""

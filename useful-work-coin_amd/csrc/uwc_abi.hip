@@ -25,3 +25,16 @@ int uwc_launch_status(const char* kernel) {
 extern "C" const char* uwc_last_error(void) { return g_last_error; }
 
 extern "C" int uwc_version(void) { return 1; }
+
+// Compute units of the current device, queried once per device (256 on MI355X).
+int uwc_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+    cached[dev] = v;
+  }
+  return cached[dev];
+}

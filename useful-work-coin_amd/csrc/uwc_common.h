@@ -19,6 +19,8 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 int uwc_fail(const char* fmt, ...);
 // hipGetLastError() after a launch, converted to a status (and a message on failure).
 int uwc_launch_status(const char* kernel);
+// Compute units of the current device (cached per device).
+int uwc_cu_count();
 
 // ------------------------------------------------------------------ BLAKE3
 // The keyed one-block compression used for tile digests, noise words and tree nodes.

@@ -318,6 +318,9 @@ int uwc_noisy_gemm256(const int8_t* A, const int8_t* B, int m, int n, int k, int
                       const uint32_t* target, uint32_t* wins, int max_wins, const float* a_scale, const float* b_scale,
                       void* out, int out_mode, int flags, uint32_t* tile_dump, hipStream_t stream);
 
+int uwc_skinny_gemm(const int8_t* X, const int8_t* W, int m, int n, int k, const float* sx, const float* sw,
+                    void* out, int out_mode, hipStream_t stream);
+
 template <bool H, bool D>
 static void launch_out(int out_mode, dim3 grid, hipStream_t s, const GemmParams& p) {
   switch (out_mode) {
@@ -357,7 +360,13 @@ extern "C" int uwc_noisy_gemm(const int8_t* A, const int8_t* B, int m, int n, in
     if (lmax < 1 || lmax > 4) return uwc_fail("uwc_noisy_gemm: lmax=%d outside 1..4", lmax);
     if (!aligned16(corrA) || !aligned16(corrB)) return uwc_fail("uwc_noisy_gemm: corrA/corrB must be 16-byte aligned");
   }
-  if (m % 256 == 0 && n % 256 == 0 && k % 128 == 0 && !(flags & FLAG_TILE128))
+  const bool plain = !hash && !denoise;
+  if (plain && m <= 64 && out_mode != OUT_NONE && !(flags & FLAG_TILE128))
+    return uwc_skinny_gemm(A, B, m, n, k, a_scale, b_scale, out, out_mode, stream);
+  // 256 x 256 tiles when they fill the 256 CUs (or when hashing: one tiling per nonce shape);
+  // a plain GEMM with fewer 256 x 256 tiles than CUs runs faster on 128 x 128 tiles.
+  const bool fills = (long)(m / 256) * (n / 256) >= 256;
+  if (m % 256 == 0 && n % 256 == 0 && k % 128 == 0 && !(flags & FLAG_TILE128) && (!plain || fills))
     return uwc_noisy_gemm256(A, B, m, n, k, r, corrA, corrB, maxabs, lmax, key, target, wins, max_wins, a_scale,
                              b_scale, out, out_mode, flags & ~FLAG_TILE128, tile_dump, stream);
   GemmParams p{A, B, m, n, k, r, corrA, corrB, maxabs, lmax, key, target, wins, max_wins, a_scale, b_scale, out,

@@ -48,6 +48,103 @@ __global__ void __launch_bounds__(256) quant_act_kernel(const float* __restrict_
   if (tid == 0) scale[row] = bs > 1 ? __fmul_rn(s, __fdiv_rn(1.0f, __fsqrt_rn((float)bs))) : s;
 }
 
+// The same quant_act with one wave per row and no LDS: for k % 512 == 0 and bs <= 512. A row is
+// processed in groups of 512 elements, lane L holding elements 8 L .. 8 L + 7 of a group as
+// registers. Stages h = 1, 2, 4 pair elements inside a lane; stages h = 8 .. 256 pair lane L
+// with lane L ^ (h / 8): the lane holding index i (bit h clear) keeps a + b, its partner
+// keeps a - b, with a = y[i] and b = y[i + h]. Each output of a stage is one rounded add or
+// subtract of the same two inputs as in the reference's stage order, so the result is
+// bit-identical to the LDS form. With STASH the row's transformed values stay in registers
+// (k <= 512 * QA_GMAX); otherwise the quantizing pass reloads and transforms again.
+#define QA_GMAX 8
+
+__device__ __forceinline__ void fwht512(float v[8], int lane, int lbs) {
+#pragma unroll
+  for (int lh = 0; lh < 3; lh++) {
+    if (lh < lbs) {
+      const int h = 1 << lh;
+#pragma unroll
+      for (int j = 0; j < 8; j++)
+        if (!(j & h)) {
+          const float a = v[j], b = v[j + h];
+          v[j] = __fadd_rn(a, b);
+          v[j + h] = __fsub_rn(a, b);
+        }
+    }
+  }
+#pragma unroll
+  for (int lh = 3; lh < 9; lh++) {
+    if (lh < lbs) {
+      const int d = 1 << (lh - 3);
+      const bool hi = lane & d;
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const float o = __shfl_xor(v[j], d, 64);
+        v[j] = hi ? __fsub_rn(o, v[j]) : __fadd_rn(v[j], o);
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ void load8(const float* p, float v[8]) {
+  const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+template <bool STASH>
+__global__ void __launch_bounds__(256) quant_act_wave_kernel(const float* __restrict__ x, int rows, int k, int lbs,
+                                                             int qmax, i8* __restrict__ q, float* __restrict__ scale) {
+  const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;  // whole waves only; no barriers below
+  const int G = k >> 9;
+  const float* xr = x + (u64)row * k + lane * 8;
+  float y[STASH ? QA_GMAX : 1][8];
+  float mx = 0.f;
+  if constexpr (STASH) {
+#pragma unroll
+    for (int g = 0; g < QA_GMAX; g++)
+      if (g < G) {
+        load8(xr + g * 512, y[g]);
+        fwht512(y[g], lane, lbs);
+#pragma unroll
+        for (int j = 0; j < 8; j++) mx = fmaxf(mx, fabsf(y[g][j]));
+      }
+  } else {
+    for (int g = 0; g < G; g++) {
+      load8(xr + g * 512, y[0]);
+      fwht512(y[0], lane, lbs);
+#pragma unroll
+      for (int j = 0; j < 8; j++) mx = fmaxf(mx, fabsf(y[0][j]));
+    }
+  }
+#pragma unroll
+  for (int s = 32; s > 0; s >>= 1) mx = fmaxf(mx, __shfl_xor(mx, s, 64));
+  const float fq = (float)qmax;
+  const float s = __fdiv_rn(fmaxf(mx, 1e-8f), fq);
+  i8* qr = q + (u64)row * k + lane * 8;
+  auto emit = [&](const float v[8], int g) {
+    u64 packed = 0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const float t = fminf(fmaxf(rintf(__fdiv_rn(v[j], s)), -fq), fq);
+      packed |= (u64)(u8)(i8)(int)t << (8 * j);
+    }
+    *reinterpret_cast<u64*>(qr + g * 512) = packed;
+  };
+  if constexpr (STASH) {
+#pragma unroll
+    for (int g = 0; g < QA_GMAX; g++)
+      if (g < G) emit(y[g], g);
+  } else {
+    for (int g = 0; g < G; g++) {
+      load8(xr + g * 512, y[0]);
+      fwht512(y[0], lane, lbs);
+      emit(y[0], g);
+    }
+  }
+  if (lane == 0) scale[row] = lbs > 0 ? __fmul_rn(s, __fdiv_rn(1.0f, __fsqrt_rn((float)(1 << lbs)))) : s;
+}
+
 // y = (f32(acc) * sx[row]) * sw[col], each product rounded once (qwen3.py:125).
 __global__ void dequant_kernel(const i32* __restrict__ acc, const float* __restrict__ sx, const float* __restrict__ sw,
                                int n, u64 total, float* __restrict__ y) {
@@ -63,9 +160,19 @@ extern "C" int uwc_quant_act_f32(const float* x, int rows, int k, int bs, int qm
   if (!x || !q || !scale || rows < 0 || k <= 0) return uwc_fail("uwc_quant_act_f32: null or empty arguments");
   if (bs > 1 && ((bs & (bs - 1)) || k % bs)) return uwc_fail("uwc_quant_act_f32: bs=%d must be a power of two dividing k=%d", bs, k);
   if (qmax < 1 || qmax > 127) return uwc_fail("uwc_quant_act_f32: qmax=%d outside 1..127", qmax);
+  if (rows == 0) return UWC_OK;
+  const int bse = bs > 1 ? bs : 1;
+  if (k % 512 == 0 && bse <= 512 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)q & 7) == 0) {
+    const int lbs = 31 - __builtin_clz((unsigned)bse);
+    const dim3 grid((unsigned)((rows + 3) / 4));
+    if (k <= 512 * QA_GMAX)
+      hipLaunchKernelGGL(quant_act_wave_kernel<true>, grid, dim3(256), 0, stream, x, rows, k, lbs, qmax, q, scale);
+    else
+      hipLaunchKernelGGL(quant_act_wave_kernel<false>, grid, dim3(256), 0, stream, x, rows, k, lbs, qmax, q, scale);
+    return uwc_launch_status("quant_act_wave");
+  }
   const size_t smem = (size_t)k * 4;
   if (smem > 160 * 1024) return uwc_fail("uwc_quant_act_f32: a row of k=%d floats exceeds LDS", k);
-  if (rows == 0) return UWC_OK;
   if (smem > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute((const void*)quant_act_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
     if (e != hipSuccess) return uwc_fail("uwc_quant_act_f32: cannot raise LDS to %zu bytes: %s", smem, hipGetErrorString(e));
