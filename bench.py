@@ -14,6 +14,10 @@ miner/ampere/bench/bench_gemm.py:37-56). The line also carries:
                 work) per launch / its average duration, against 5.0 POP/s dense int8;
   detrt_layer   BASELINE configs[1]: the four linears of a Qwen3-1.7B layer at M = 2048
                 (quant_act -> exact GEMM -> fused dequant), TOPS of the GEMMs;
+  detrt_skinny  BASELINE configs[0] (64 x 2048 -> 6144) and configs[3]'s decode shapes (Llama-3.1-8B
+                linears at M = 1, 8, 32): device time from graph replays over > 1.2 GB of rotated
+                weights, algorithmic bytes / time against 8 TB/s HBM;
+  llama_prefill configs[3]'s prefill shapes (M = 8192), TOPS of the four GEMMs;
   cpu_baseline  the CPU oracle (this repo's C restatement, OpenMP) on a bounded sample of the
                 same workload: full mined forwards of whole nonces at the same shape;
   parity        the sampled nonce's GPU output, every tile digest and the winner set compared
@@ -171,6 +175,109 @@ def detrt_layer(args, torch, np):
     return out
 
 
+def _graph_time_us(torch, launches, reps=3):
+    """Average device time per launch of a list of zero-argument launch closures, captured once
+    into a HIP graph and replayed (so host launch overhead is not measured), HIP events on the
+    capturing stream."""
+    for f in launches:  # eager warm-up: one-time attribute setup happens outside the capture
+        assert f() == 0, "launch failed"
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for f in launches:
+                assert f() == 0, "launch failed during capture"
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (reps * len(launches))
+
+
+def skinny_linears(args, torch, np):
+    """BASELINE configs[0] (detrt MLP-up, 64 x 2048 -> 6144) and the decode half of configs[3]
+    (Llama-3.1-8B layer linears at M = 1, 8, 32): exact GEMM + fused fp32 dequant through
+    uwc_igemm_dequant_f32, weights rotated over > 1.2 GB of distinct buffers so the 256 MB
+    Infinity Cache cannot serve them. Algorithmic bytes = W + X + fp32 out + scales; roofline =
+    those bytes / device time vs 8 TB/s."""
+    from uwc_amd import _lib
+    dev = "cuda"
+    L = _lib.lib()
+    stream_of = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+
+    def run(m, shapes, reps_cap=48):
+        """time per layer (sum over shapes) for token count m."""
+        total_us, total_bytes, per = 0.0, 0, {}
+        for name, (n, k) in shapes.items():
+            wb = n * k
+            nw = max(2, -(-(1200 << 20) // wb))
+            Ws = [torch.randint(-64, 65, (n, k), dtype=torch.int8, device=dev) for _ in range(nw)]
+            X = torch.randint(-64, 65, (m, k), dtype=torch.int8, device=dev)
+            sx, sw = torch.rand(m, device=dev) + 0.5, torch.rand(n, device=dev) * 1e-3
+            Y = torch.empty((m, n), dtype=torch.float32, device=dev)
+
+            def mk(W):
+                return lambda: L.uwc_igemm_dequant_f32(X.data_ptr(), W.data_ptr(), m, n, k, sx.data_ptr(),
+                                                       sw.data_ptr(), Y.data_ptr(), stream_of())
+            launches = [mk(Ws[i % nw]) for i in range(min(max(2 * nw, 16), reps_cap))]
+            us = _graph_time_us(torch, launches)
+            byt = wb + m * k + 4 * m * n + 4 * (m + n)
+            per[name] = dict(us=round(us, 2), gbs=round(byt / us / 1e3, 1))
+            total_us += us
+            total_bytes += byt
+            del Ws
+            torch.cuda.empty_cache()
+        return total_us, total_bytes, per
+
+    out = {}
+    us, byt, per = run(64, {"mlp_up": (6144, 2048)})
+    out["config1_mlp_up_64x2048x6144"] = dict(us=round(us, 2), bytes=byt, gbs=round(byt / us / 1e3, 1),
+                                              hbm_frac=round(byt / us / 1e3 / PEAK_HBM_GBS, 4))
+    llama = {"qkv": (6144, 4096), "o": (4096, 4096), "gu": (28672, 4096), "down": (4096, 14336)}
+    dec = {}
+    for m in (1, 8, 32):
+        us, byt, per = run(m, llama)
+        dec[f"M{m}"] = dict(us_per_layer=round(us, 2), bytes_per_layer=byt, gbs=round(byt / us / 1e3, 1),
+                            hbm_frac=round(byt / us / 1e3 / PEAK_HBM_GBS, 4), per_linear=per)
+    out["config4_llama8b_decode"] = dec
+    log(f"skinny linears: {json.dumps(out)}")
+    return out
+
+
+def llama_prefill(args, torch, np):
+    """The prefill half of BASELINE configs[3]: Llama-3.1-8B layer linears at M = 8192, exact
+    GEMM + fused fp32 dequant (uwc_igemm_dequant_f32), TOPS of the four GEMMs."""
+    from uwc_amd import _lib
+    dev = "cuda"
+    L = _lib.lib()
+    M = 8192
+    shapes = {"qkv": (6144, 4096), "o": (4096, 4096), "gu": (28672, 4096), "down": (4096, 14336)}
+    per, total_us, ops = {}, 0.0, 0.0
+    for name, (n, k) in shapes.items():
+        X = torch.randint(-64, 65, (M, k), dtype=torch.int8, device=dev)
+        W = torch.randint(-64, 65, (n, k), dtype=torch.int8, device=dev)
+        sx, sw = torch.rand(M, device=dev), torch.rand(n, device=dev)
+        Y = torch.empty((M, n), dtype=torch.float32, device=dev)
+        f = lambda: L.uwc_igemm_dequant_f32(X.data_ptr(), W.data_ptr(), M, n, k, sx.data_ptr(), sw.data_ptr(),  # noqa: E731
+                                            Y.data_ptr(), torch.cuda.current_stream().cuda_stream)
+        us = _graph_time_us(torch, [f] * 4)
+        per[name] = dict(us=round(us, 2), tops=round(2.0 * M * n * k / us / 1e6, 1))
+        total_us += us
+        ops += 2.0 * M * n * k
+        del X, W, Y
+        torch.cuda.empty_cache()
+    out = dict(us_per_layer=round(total_us, 1), tops=round(ops / total_us / 1e6, 1),
+               frac_of_peak=round(ops / total_us / 1e6 / PEAK_INT8_TOPS, 4), per_linear=per)
+    log(f"llama prefill: {out}")
+    return out
+
+
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "noisy_gemm256_mining_4096_traffic.txt")
 COPY_BYTES = 256 << 20  # the calibration copy: reads and writes exactly this many bytes
 
@@ -295,6 +402,8 @@ def main():
     res = mining(args, torch, np, ops, O)
     parity, cpu = (None, None) if args.no_cpu else parity_and_cpu(args, res, torch, np, ops, O)
     det = None if args.no_detrt else detrt_layer(args, torch, np)
+    skinny = None if args.no_detrt else skinny_linears(args, torch, np)
+    prefill = None if args.no_detrt else llama_prefill(args, torch, np)
     m, n, k, r = res["m"], res["n"], res["k"], res["r"]
     line = {
         "metric": METRIC,
@@ -320,6 +429,8 @@ def main():
         "cpu_baseline": cpu,
         "parity": parity,
         "detrt_layer": det,
+        "detrt_skinny": skinny,
+        "llama_prefill": prefill,
     }
     print(json.dumps(line), flush=True)
 

@@ -169,6 +169,11 @@ __device__ __forceinline__ void s2_dma16(const void* g, u32 lds) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
 }
 
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS operations, not for its
+// global loads and stores (__syncthreads() also fences global memory, which would drain the
+// prefetched W loads and the epilogue's output stores at every barrier).
+__device__ __forceinline__ void s2_lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 template <int MT, int RG, int U, int OUT>
 __global__ void __launch_bounds__(512) skinny2_kernel(const i8* __restrict__ X, const i8* __restrict__ W, int m,
                                                       int n, int k, int ks_log, int xpitch,
@@ -176,6 +181,7 @@ __global__ void __launch_bounds__(512) skinny2_kernel(const i8* __restrict__ X, 
                                                       void* __restrict__ out) {
   extern __shared__ __attribute__((aligned(16))) u8 s2_lds[];
   i32* red = reinterpret_cast<i32*>(s2_lds + (((long)m * xpitch + 15) & ~15L));  // [8 waves][RG][4][64]
+  float* sxl = reinterpret_cast<float*>(red + 8 * RG * 256);                           // [m] token scales
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int KS = 1 << ks_log, RR = 8 >> ks_log;
   const int ks = wave & (KS - 1), rr = wave >> ks_log;
@@ -185,11 +191,12 @@ __global__ void __launch_bounds__(512) skinny2_kernel(const i8* __restrict__ X, 
   // steps of this wave: s(j) = (j / SG) KS SG + ks SG + j % SG; every wave runs nbat batches
   const int nj = SK_SG * ((ksteps + KS * SK_SG - 1) / (KS * SK_SG));
   const int nbat = (nj + U - 1) / U;
-  const int nmine = blockIdx.x < nblk ? (nblk - 1 - blockIdx.x) / gridDim.x + 1 : 0;
+  const int G = gridDim.x, bid = blockIdx.x;
+  const int nmine = bid < nblk ? (nblk - 1 - bid) / G + 1 : 0;
   const int T = nmine * nbat;
   auto step_of = [&](int j) { return (j / SK_SG) * KS * SK_SG + ks * SK_SG + (j % SK_SG); };
   auto load_unit = [&](int t, v4i w[U][RG]) {
-    const int b = t % nbat, rb = blockIdx.x + (t / nbat) * gridDim.x;
+    const int b = t % nbat, rb = bid + (t / nbat) * G;
 #pragma unroll
     for (int g = 0; g < RG; g++) {
       const i8* wp = W + (long)min(rb * rows_blk + rr * 16 * RG + 16 * g + lr, n - 1) * k + kb;
@@ -208,11 +215,22 @@ __global__ void __launch_bounds__(512) skinny2_kernel(const i8* __restrict__ X, 
       if (sg * 64 + lane < cpr) s2_dma16(X + (long)r * k + sg * 1024 + lane * 16, l);
     }
   }
+  // scales for the dequant epilogue, requested now so no epilogue waits on memory: the token
+  // scales go to LDS; a thread's output column is the same in every pass of a row block
+  // (512 % rows_blk == 0), so it holds that column's weight scale for the current block
+  constexpr bool SCALED = OUT != UWC_OUT_I32;
+  float sxv = 0.f, swv = 0.f;
+  if constexpr (SCALED) {
+    if (threadIdx.x < m) sxv = sx[threadIdx.x];
+    if (T > 0) swv = sw[min(bid * rows_blk + (int)threadIdx.x % rows_blk, n - 1)];
+  }
   v4i wa[U][RG];
   if (T > 0) load_unit(0, wa);
+  if constexpr (SCALED)
+    if (threadIdx.x < m) sxl[threadIdx.x] = sxv;
   // the DMAs are older than the U * RG loads just issued: wait for them, then every wave's
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(U * RG) : "memory");
-  __syncthreads();
+  s2_lds_barrier();
   int xoff[MT];
 #pragma unroll
   for (int tg = 0; tg < MT; tg++) xoff[tg] = min(16 * tg + lr, m - 1) * xpitch + kb;
@@ -223,10 +241,12 @@ __global__ void __launch_bounds__(512) skinny2_kernel(const i8* __restrict__ X, 
 #pragma unroll
     for (int tg = 0; tg < MT; tg++) acc[g][tg] = v4i{0, 0, 0, 0};
 
-  for (int t = 0; t < T; t++) {
-    v4i wb[U][RG];
-    if (t + 1 < T) load_unit(t + 1, wb);
+  // unit t: MFMAs on its W registers; after a row block's last unit, the cross-wave reduction
+  // and the epilogue
+  auto process = [&](int t, const v4i w[U][RG]) {
     const int b = t % nbat;
+    if constexpr (SCALED)
+      if (b == 0 && t > 0) swv = sw[min((bid + (t / nbat) * G) * rows_blk + (int)threadIdx.x % rows_blk, n - 1)];
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int s = step_of(b * U + u);
@@ -237,19 +257,19 @@ __global__ void __launch_bounds__(512) skinny2_kernel(const i8* __restrict__ X, 
 #pragma unroll
         for (int g = 0; g < RG; g++)
 #pragma unroll
-          for (int tg = 0; tg < MT; tg++) acc[g][tg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa[u][g], xr[tg], acc[g][tg], 0, 0, 0);
+          for (int tg = 0; tg < MT; tg++) acc[g][tg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w[u][g], xr[tg], acc[g][tg], 0, 0, 0);
       }
     }
     if (b == nbat - 1) {
       // row block done: sum the KS partials of each row group, one token group at a time
-      const int rb = blockIdx.x + (t / nbat) * gridDim.x;
+      const int rb = bid + (t / nbat) * G;
 #pragma unroll
       for (int tg = 0; tg < MT; tg++) {
 #pragma unroll
         for (int g = 0; g < RG; g++)
 #pragma unroll
           for (int i = 0; i < 4; i++) red[((wave * RG + g) * 4 + i) * 64 + lane] = acc[g][tg][i];
-        __syncthreads();
+        s2_lds_barrier();
         // outputs of this token group: 16 tokens x rows_blk columns, columns fastest
         for (int o = threadIdx.x; o < 16 * rows_blk; o += 512) {
           const int tl = o / rows_blk, cl = o % rows_blk;
@@ -263,7 +283,7 @@ __global__ void __launch_bounds__(512) skinny2_kernel(const i8* __restrict__ X, 
             if constexpr (OUT == UWC_OUT_I32) {
               reinterpret_cast<i32*>(out)[oi] = v;
             } else {
-              const float y = __fmul_rn(__fmul_rn((float)v, sx[tok]), sw[col]);
+              const float y = __fmul_rn(__fmul_rn((float)v, sxl[tok]), swv);
               if constexpr (OUT == UWC_OUT_F32)
                 reinterpret_cast<float*>(out)[oi] = y;
               else
@@ -271,17 +291,22 @@ __global__ void __launch_bounds__(512) skinny2_kernel(const i8* __restrict__ X, 
             }
           }
         }
-        __syncthreads();
+        s2_lds_barrier();
       }
 #pragma unroll
       for (int g = 0; g < RG; g++)
 #pragma unroll
         for (int tg = 0; tg < MT; tg++) acc[g][tg] = v4i{0, 0, 0, 0};
     }
-#pragma unroll
-    for (int u = 0; u < U; u++)
-#pragma unroll
-      for (int g = 0; g < RG; g++) wa[u][g] = wb[u][g];
+  };
+  // two register buffers in turn: unit t + 1 loads while unit t computes, with no copies
+  v4i wb[U][RG];
+  for (int t = 0; t < T; t += 2) {
+    if (t + 1 < T) load_unit(t + 1, wb);
+    process(t, wa);
+    if (t + 1 >= T) break;
+    if (t + 2 < T) load_unit(t + 2, wa);
+    process(t + 1, wb);
   }
 }
 
@@ -357,7 +382,7 @@ int uwc_skinny_gemm(const int8_t* X, const int8_t* W, int m, int n, int k, const
   // X-stationary form when X (padded rows) and the reduction buffer fit in LDS
   const int xpitch = k + 16;
   const int RG2 = S2_RG;
-  const size_t lds2 = (((size_t)m * xpitch + 15) & ~(size_t)15) + (size_t)8 * RG2 * 1024;
+  const size_t lds2 = (((size_t)m * xpitch + 15) & ~(size_t)15) + (size_t)8 * RG2 * 1024 + (size_t)m * 4;
   if (lds2 <= S2_MAX_LDS) {
     const int cus = uwc_cu_count();
     const int per_cu = lds2 <= 80 * 1024 ? 2 : 1;
