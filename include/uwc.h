@@ -157,6 +157,12 @@ int uwc_side_project(const int8_t* A, int m, const int8_t* EA, const int8_t* SpA
  * runtime/detgpu/kernels.py:75-114. */
 int uwc_quant_act_f32(const float* x, int rows, int k, int bs, int qmax, int8_t* q, float* scale, hipStream_t stream);
 
+/* The miner's fused activation quantizer on bf16 rows (x: rows x k bf16 bit patterns, k % 8 == 0):
+ * exactly uwc_quant_act_f32 with qmax = 64 on the rows widened to fp32 (block FWHT of size bs,
+ * q = clamp(rint(y / s), -64, 64), s = max(max|y|, 1e-8) / 64, scale = s * (1 / sqrt(bs))).
+ * Replaces ops.quant_rows_had: miner/ampere/uwc_ampere/ops.py:172-181, kernels.cu:717-778. */
+int uwc_quant_rows_had(const uint16_t* x, int rows, int k, int bs, int8_t* q, float* scale, hipStream_t stream);
+
 /* y = fmul(fmul(f32(acc), sx[i]), sw[j]) for an int32 m x n accumulator.
  * Replaces the dequant of runtime/detrt/qwen3.py:125 (detgpu deq, runtime/detgpu/kernels.py:35). */
 int uwc_dequant_f32(const int32_t* acc, const float* sx, const float* sw, int m, int n, float* y, hipStream_t stream);

@@ -21,7 +21,8 @@ def test_header_declares_expected_surface():
     names = declared()
     for must in ("uwc_noisy_gemm", "uwc_igemm_i32", "uwc_igemm_dequant_f32", "uwc_b3_root_and_seed",
                  "uwc_noise_uniform", "uwc_noise_perm", "uwc_noise_rows", "uwc_quant_act_f32", "uwc_dequant_f32",
-                 "uwc_proj_matrix", "uwc_project", "uwc_noise_project", "uwc_nonce_noise", "uwc_last_error", "uwc_version"):
+                 "uwc_proj_matrix", "uwc_project", "uwc_noise_project", "uwc_nonce_noise", "uwc_last_error", "uwc_version",
+                 "uwc_quant_rows_had", "uwc_side_project"):
         assert must in names
 
 
@@ -80,6 +81,9 @@ def test_other_entry_points_reject_bad_arguments():
     assert L.uwc_quant_act_f32(fake, 4, 96, 64, 64, fake, fake, None) == -1
     assert "power of two" in L.uwc_last_error().decode()
     assert L.uwc_quant_act_f32(fake, 4, 64, 0, 200, fake, fake, None) == -1
+    assert L.uwc_quant_rows_had(fake, 4, 100, 0, fake, fake, None) == -1
+    assert "multiple of 8" in L.uwc_last_error().decode()
+    assert L.uwc_quant_rows_had(fake, 4, 96, 64, fake, fake, None) == -1
 
 
 def test_python_surface_matches_reference_names():
@@ -89,10 +93,13 @@ def test_python_surface_matches_reference_names():
                  "OUT_I32", "OUT_BF16", "CONFIGS", "DEFAULT_CFG", "words", "words_to_bytes", "LABEL_A", "LABEL_B",
                  "SALT_A", "SALT_B", "consts", "b3_root_and_seed", "noise_uniform", "noise_perm", "noise_rows", "gemm",
                  "proj_matrix", "project", "nonce_noise", "noise_project",
-                 "MinedWeight", "GraphedForward"):
+                 "MinedWeight", "GraphedForward", "quant_rows_had"):
         assert hasattr(ops, name), name
     for name in ("quant_act", "DetLinear"):
         assert hasattr(detrt, name), name
+    from uwc_amd import model
+    for name in ("QMAX", "hadamard", "rotate", "quant_rows", "MinedLinear", "convert_qwen3"):
+        assert hasattr(model, name), name
 
 
 def test_salt_constants_match_oracle():

@@ -126,6 +126,35 @@ def test_gemm_known_answer_L1():
     assert hashlib.sha256(C.tobytes()).hexdigest()[:20] == "bf9394d180bda5b0412c"
 
 
+def l2_quantizer_input() -> np.ndarray:
+    """The L2 quantizer input of miner/ampere/bench/crosscheck.py:62-91: drawn from
+    default_rng(2026) after the L1 operands, rounded to bf16 (round to nearest even, as torch's
+    fp32 -> bf16 conversion) and widened back to fp32."""
+    rng = np.random.default_rng(2026)
+    rng.integers(-64, 65, size=(1024, 4096), dtype=np.int8)
+    rng.integers(-64, 65, size=(3072, 4096), dtype=np.int8)
+    x = rng.standard_normal((1024, 4096)).astype(np.float32) * np.linspace(0.05, 6, 4096, dtype=np.float32)
+    x[:, 7] *= 40.0
+    u = x.view(np.uint32)
+    b = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint32)
+    return (b << 16).view(np.float32)
+
+
+# sha256[:20] of (int8 q, fp32 scale) of the miner's quantizer on that input: results/xc_cpu.json:5-10,
+# the same in results/xc_3080.json and results/xc_5090.json
+L2_KAT = {0: ("ce0b9f970855d5565ecc", "c15f21b56e165b4e76b7"),
+          128: ("440e431806f833e22989", "b11bb63a72dfee572c80"),
+          512: ("c51b454f3687cd02109f", "66c49428583d960017f2")}
+
+
+@pytest.mark.parametrize("bs", [0, 128, 512])
+def test_quantizer_known_answers_L2(bs):
+    """quant_rows_had (kernels.cu:717-778) = quant_act with qmax 64 on the widened bf16 rows."""
+    q, s = O.quant_act(l2_quantizer_input(), bs, 64)
+    assert hashlib.sha256(q.tobytes()).hexdigest()[:20] == L2_KAT[bs][0]
+    assert hashlib.sha256(s.tobytes()).hexdigest()[:20] == L2_KAT[bs][1]
+
+
 def test_gemm_ragged_and_extremes():
     rng = np.random.default_rng(5)
     for m, n, k in ((1, 1, 1), (3, 70, 130), (65, 1, 257)):

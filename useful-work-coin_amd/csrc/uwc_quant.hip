@@ -11,13 +11,18 @@
 // Walsh-Hadamard transform (stages h = 1, 2, 4, ... < bs; pairs (i, i+h) -> (a+b, a-b)),
 // reduced to max|y|, then q = clamp(rint(y / s), -qmax, qmax), s = max(max|y|, 1e-8) / qmax,
 // returned scale = s * (1 / sqrt(bs)) when bs > 1.
-__global__ void __launch_bounds__(256) quant_act_kernel(const float* __restrict__ x, int k, int bs, int qmax,
+// Input elements: fp32, or bf16 bit patterns widened exactly (bits << 16).
+__device__ __forceinline__ float qa_in(const float* p, long i) { return p[i]; }
+__device__ __forceinline__ float qa_in(const uint16_t* p, long i) { return __uint_as_float((u32)p[i] << 16); }
+
+template <typename T>
+__global__ void __launch_bounds__(256) quant_act_kernel(const T* __restrict__ x, int k, int bs, int qmax,
                                                         i8* __restrict__ q, float* __restrict__ scale) {
   extern __shared__ float rowf[];
   __shared__ float red[4];
   const int row = blockIdx.x, tid = threadIdx.x;
-  const float* xr = x + (u64)row * k;
-  for (int i = tid; i < k; i += 256) rowf[i] = xr[i];
+  const T* xr = x + (u64)row * k;
+  for (int i = tid; i < k; i += 256) rowf[i] = qa_in(xr, i);
   __syncthreads();
   if (bs > 1) {
     for (int lh = 0; (1 << lh) < bs; lh++) {
@@ -91,13 +96,24 @@ __device__ __forceinline__ void load8(const float* p, float v[8]) {
   v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 
-template <bool STASH>
-__global__ void __launch_bounds__(256) quant_act_wave_kernel(const float* __restrict__ x, int rows, int k, int lbs,
+// 8 bf16 values (one 16-byte load), widened exactly to fp32
+__device__ __forceinline__ void load8(const uint16_t* p, float v[8]) {
+  const uint4 a = *reinterpret_cast<const uint4*>(p);
+  const u32 w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    v[2 * j] = __uint_as_float(w[j] << 16);
+    v[2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
+  }
+}
+
+template <bool STASH, typename T>
+__global__ void __launch_bounds__(256) quant_act_wave_kernel(const T* __restrict__ x, int rows, int k, int lbs,
                                                              int qmax, i8* __restrict__ q, float* __restrict__ scale) {
   const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;  // whole waves only; no barriers below
   const int G = k >> 9;
-  const float* xr = x + (u64)row * k + lane * 8;
+  const T* xr = x + (u64)row * k + lane * 8;
   float y[STASH ? QA_GMAX : 1][8];
   float mx = 0.f;
   if constexpr (STASH) {
@@ -155,30 +171,42 @@ __global__ void dequant_kernel(const i32* __restrict__ acc, const float* __restr
   }
 }
 
-extern "C" int uwc_quant_act_f32(const float* x, int rows, int k, int bs, int qmax, int8_t* q, float* scale,
-                                 hipStream_t stream) {
-  if (!x || !q || !scale || rows < 0 || k <= 0) return uwc_fail("uwc_quant_act_f32: null or empty arguments");
-  if (bs > 1 && ((bs & (bs - 1)) || k % bs)) return uwc_fail("uwc_quant_act_f32: bs=%d must be a power of two dividing k=%d", bs, k);
-  if (qmax < 1 || qmax > 127) return uwc_fail("uwc_quant_act_f32: qmax=%d outside 1..127", qmax);
+template <typename T>
+static int quant_rows(const char* fn, const T* x, int rows, int k, int bs, int qmax, int8_t* q, float* scale,
+                      hipStream_t stream) {
+  if (!x || !q || !scale || rows < 0 || k <= 0) return uwc_fail("%s: null or empty arguments", fn);
+  if (bs > 1 && ((bs & (bs - 1)) || k % bs)) return uwc_fail("%s: bs=%d must be a power of two dividing k=%d", fn, bs, k);
+  if (qmax < 1 || qmax > 127) return uwc_fail("%s: qmax=%d outside 1..127", fn, qmax);
   if (rows == 0) return UWC_OK;
   const int bse = bs > 1 ? bs : 1;
   if (k % 512 == 0 && bse <= 512 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)q & 7) == 0) {
     const int lbs = 31 - __builtin_clz((unsigned)bse);
     const dim3 grid((unsigned)((rows + 3) / 4));
     if (k <= 512 * QA_GMAX)
-      hipLaunchKernelGGL(quant_act_wave_kernel<true>, grid, dim3(256), 0, stream, x, rows, k, lbs, qmax, q, scale);
+      hipLaunchKernelGGL((quant_act_wave_kernel<true, T>), grid, dim3(256), 0, stream, x, rows, k, lbs, qmax, q, scale);
     else
-      hipLaunchKernelGGL(quant_act_wave_kernel<false>, grid, dim3(256), 0, stream, x, rows, k, lbs, qmax, q, scale);
-    return uwc_launch_status("quant_act_wave");
+      hipLaunchKernelGGL((quant_act_wave_kernel<false, T>), grid, dim3(256), 0, stream, x, rows, k, lbs, qmax, q, scale);
+    return uwc_launch_status(fn);
   }
   const size_t smem = (size_t)k * 4;
-  if (smem > 160 * 1024) return uwc_fail("uwc_quant_act_f32: a row of k=%d floats exceeds LDS", k);
+  if (smem > 160 * 1024) return uwc_fail("%s: a row of k=%d floats exceeds LDS", fn, k);
   if (smem > 64 * 1024) {
-    hipError_t e = hipFuncSetAttribute((const void*)quant_act_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-    if (e != hipSuccess) return uwc_fail("uwc_quant_act_f32: cannot raise LDS to %zu bytes: %s", smem, hipGetErrorString(e));
+    hipError_t e = hipFuncSetAttribute((const void*)quant_act_kernel<T>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    if (e != hipSuccess) return uwc_fail("%s: cannot raise LDS to %zu bytes: %s", fn, smem, hipGetErrorString(e));
   }
-  hipLaunchKernelGGL(quant_act_kernel, dim3(rows), dim3(256), smem, stream, x, k, bs, qmax, q, scale);
-  return uwc_launch_status("quant_act");
+  hipLaunchKernelGGL(quant_act_kernel<T>, dim3(rows), dim3(256), smem, stream, x, k, bs, qmax, q, scale);
+  return uwc_launch_status(fn);
+}
+
+extern "C" int uwc_quant_act_f32(const float* x, int rows, int k, int bs, int qmax, int8_t* q, float* scale,
+                                 hipStream_t stream) {
+  return quant_rows("uwc_quant_act_f32", x, rows, k, bs, qmax, q, scale, stream);
+}
+
+extern "C" int uwc_quant_rows_had(const uint16_t* x, int rows, int k, int bs, int8_t* q, float* scale,
+                                  hipStream_t stream) {
+  if (k % 8) return uwc_fail("uwc_quant_rows_had: k=%d must be a multiple of 8", k);
+  return quant_rows("uwc_quant_rows_had", x, rows, k, bs, 64, q, scale, stream);
 }
 
 extern "C" int uwc_dequant_f32(const int32_t* acc, const float* sx, const float* sw, int m, int n, float* y,

@@ -34,6 +34,7 @@ SIGNATURES = {
     "uwc_noise_project": [vp, i32, i32, i32, vp, vp, vp, vp, vp, i32, i32, vp, i32, vp],
     "uwc_side_project": [vp, i32, vp, vp, vp, vp, vp, i32, i32, vp, i32, vp, vp, i32, i32, i32, vp, i32, vp],
     "uwc_quant_act_f32": [vp, i32, i32, i32, i32, vp, vp, vp],
+    "uwc_quant_rows_had": [vp, i32, i32, i32, vp, vp, vp],
     "uwc_dequant_f32": [vp, vp, vp, i32, i32, vp, vp],
 }
 _RESTYPE = {"uwc_last_error": ctypes.c_char_p}

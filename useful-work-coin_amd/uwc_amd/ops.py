@@ -182,6 +182,19 @@ def side_project(A, EA, SpA, ApEA, StB, corrA, Bp, StA, corrB, *, maxabs, corr_a
               _p(Bp), n, _p(StA), _p(corrB), corr_b_off, k, r, _p(maxabs), corrA.shape[0], _stream())
 
 
+# ------------------------------------------------------------------ activation quantizer
+def quant_rows_had(x: torch.Tensor, bs: int, q: torch.Tensor | None = None, scale: torch.Tensor | None = None):
+    """x: m x k bf16 (contiguous) -> (int8 q in [-64, 64], float32 per-row scale), block Hadamard of
+    size bs (ops.py:172-181). Rows of any k % 8 == 0 when k % 512 == 0 and bs <= 512; else k <= 40960."""
+    m, k = x.shape
+    _check(x.dtype == torch.bfloat16 and x.is_contiguous() and k % 8 == 0 and (bs <= 1 or k % bs == 0),
+           f"quant_rows_had: x must be contiguous bf16 with k % 8 == 0 and bs | k (k={k}, bs={bs})")
+    q = torch.empty((m, k), dtype=torch.int8, device=x.device) if q is None else q
+    scale = torch.empty(m, dtype=torch.float32, device=x.device) if scale is None else scale
+    _lib.call("uwc_quant_rows_had", _p(x), m, k, bs, _p(q), _p(scale), _stream())
+    return q, scale
+
+
 # ------------------------------------------------------------------ GEMM
 def gemm(A, B, *, r=128, flags=0, corrA=None, corrB=None, maxabs=None, key=None, target=None, wins=None,
          max_wins=0, a_scale=None, b_scale=None, out=None, out_mode=OUT_NONE, cfg=None, dump=None):
