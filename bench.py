@@ -168,9 +168,13 @@ def detrt_layer(args, torch, np):
             lays[name](xs[name])
     torch.cuda.synchronize()
     dt = (time.perf_counter() - t0) / reps
+    import oracle as O
+    ctops, ct, ran, cores = cpu_linears(torch, np, O, M, shapes, budget_s=3.0)
     out = dict(workload="Qwen3-1.7B layer linears (qkv, o, gu, down) at M=2048, quant_act + exact GEMM + dequant",
                ms_per_layer=round(dt * 1e3, 4), tops=round(2.0 * macs / dt / 1e12, 2),
-               frac_of_peak=round(2.0 * macs / dt / 1e12 / PEAK_INT8_TOPS, 4))
+               frac_of_peak=round(2.0 * macs / dt / 1e12 / PEAK_INT8_TOPS, 4),
+               cpu_baseline=dict(value=round(ctops, 4), unit="TOPS", cores=cores, kind="port",
+                                 sample=f"quant_act + fp64 matmul + dequant, {ran}, {ct:.2f} s"))
     log(f"detrt layer: {out}")
     return out
 
@@ -198,6 +202,36 @@ def _graph_time_us(torch, launches, reps=3):
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) * 1e3 / (reps * len(launches))
+
+
+def cpu_linears(torch, np, O, m, shapes, budget_s=3.0):
+    """The reference's CPU path for detrt linears, restated: quant_act (oracle) -> the fp64 matmul
+    q.double() @ Wq.double().T (runtime/detrt/qwen3.py:109-110) -> dequant (oracle), with torch using
+    every host core as runtime/bench/xdevice.py:28 does. Runs the listed linears once each
+    (after a small warm-up) unless that exceeds budget_s, then extrapolates from the linears run.
+    Returns (TOPS of the GEMMs, seconds, what was run)."""
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    rng = np.random.default_rng(11)
+    xw = torch.from_numpy(rng.integers(-64, 65, size=(8, 64)).astype(np.float64))
+    xw @ xw.T
+    ops_done, t_done, ran, ops_all = 0.0, 0.0, [], 0.0
+    for name, (n, k) in shapes.items():
+        ops_all += 2.0 * m * n * k
+        if t_done > budget_s:
+            continue
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        Wq = torch.from_numpy(rng.integers(-64, 65, size=(n, k), dtype=np.int8))
+        sw = rng.random(n, dtype=np.float32)
+        t0 = time.perf_counter()
+        q, sx = O.quant_act(x, 512 if k % 512 == 0 else 0)
+        acc = (torch.from_numpy(q).double() @ Wq.double().T).numpy().astype(np.int32)
+        O.dequant(acc, sx, sw)
+        t_done += time.perf_counter() - t0
+        ops_done += 2.0 * m * n * k
+        ran.append(name)
+    tops = ops_done / t_done / 1e12
+    return tops, t_done, ran, threads
 
 
 def skinny_linears(args, torch, np):
@@ -235,16 +269,24 @@ def skinny_linears(args, torch, np):
             torch.cuda.empty_cache()
         return total_us, total_bytes, per
 
+    import oracle as O
     out = {}
     us, byt, per = run(64, {"mlp_up": (6144, 2048)})
-    out["config1_mlp_up_64x2048x6144"] = dict(us=round(us, 2), bytes=byt, gbs=round(byt / us / 1e3, 1),
-                                              hbm_frac=round(byt / us / 1e3 / PEAK_HBM_GBS, 4))
+    ctops, ct, ran, cores = cpu_linears(torch, np, O, 64, {"mlp_up": (6144, 2048)})
+    out["config1_mlp_up_64x2048x6144"] = dict(
+        us=round(us, 2), bytes=byt, gbs=round(byt / us / 1e3, 1), hbm_frac=round(byt / us / 1e3 / PEAK_HBM_GBS, 4),
+        tops=round(2.0 * 64 * 6144 * 2048 / us / 1e6, 2),
+        cpu_baseline=dict(value=round(ctops, 4), unit="TOPS", cores=cores, kind="port",
+                          sample=f"quant_act + fp64 matmul + dequant, {ran}, {ct:.2f} s"))
     llama = {"qkv": (6144, 4096), "o": (4096, 4096), "gu": (28672, 4096), "down": (4096, 14336)}
     dec = {}
     for m in (1, 8, 32):
         us, byt, per = run(m, llama)
+        ctops, ct, ran, cores = cpu_linears(torch, np, O, m, llama, budget_s=2.0)
         dec[f"M{m}"] = dict(us_per_layer=round(us, 2), bytes_per_layer=byt, gbs=round(byt / us / 1e3, 1),
-                            hbm_frac=round(byt / us / 1e3 / PEAK_HBM_GBS, 4), per_linear=per)
+                            hbm_frac=round(byt / us / 1e3 / PEAK_HBM_GBS, 4), per_linear=per,
+                            cpu_baseline=dict(value=round(ctops, 5), unit="TOPS", cores=cores, kind="port",
+                                              sample=f"quant_act + fp64 matmul + dequant, {ran}, {ct:.2f} s"))
     out["config4_llama8b_decode"] = dec
     log(f"skinny linears: {json.dumps(out)}")
     return out
@@ -272,8 +314,13 @@ def llama_prefill(args, torch, np):
         ops += 2.0 * M * n * k
         del X, W, Y
         torch.cuda.empty_cache()
+    import oracle as O
+    ctops, ct, ran, cores = cpu_linears(torch, np, O, 2048, {"o": (4096, 4096)}, budget_s=1.0)
     out = dict(us_per_layer=round(total_us, 1), tops=round(ops / total_us / 1e6, 1),
-               frac_of_peak=round(ops / total_us / 1e6 / PEAK_INT8_TOPS, 4), per_linear=per)
+               frac_of_peak=round(ops / total_us / 1e6 / PEAK_INT8_TOPS, 4), per_linear=per,
+               cpu_baseline=dict(value=round(ctops, 4), unit="TOPS", cores=cores, kind="port",
+                                 sample=f"quant_act + fp64 matmul + dequant of the o linear at M=2048 "
+                                        f"(a quarter of the prefill rows), {ct:.2f} s"))
     log(f"llama prefill: {out}")
     return out
 
