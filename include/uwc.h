@@ -1,6 +1,7 @@
 /*
  * uwc.h - C-ABI of libuwc_hip.so, the MI355X (gfx950) int8 x int8 -> int32 GEMM hot path of
- * useful-work-coin: the cuPOW NoisyGEMM miner and the detrt deterministic integer linear.
+ * useful-work-coin: the cuPOW NoisyGEMM miner and the detrt deterministic integer linear, with
+ * the decoder-layer ops and stage commitments around detrt's GEMMs.
  *
  * Conventions (all entry points):
  *   - every pointer is device memory unless stated otherwise, allocated by the caller;
@@ -166,6 +167,100 @@ int uwc_quant_rows_had(const uint16_t* x, int rows, int k, int bs, int8_t* q, fl
 /* y = fmul(fmul(f32(acc), sx[i]), sw[j]) for an int32 m x n accumulator.
  * Replaces the dequant of runtime/detrt/qwen3.py:125 (detgpu deq, runtime/detgpu/kernels.py:35). */
 int uwc_dequant_f32(const int32_t* acc, const float* sx, const float* sw, int m, int n, float* y, hipStream_t stream);
+
+/* ======================================================================== decoder layer
+ * detrt's deterministic decoder-layer ops around the exact GEMMs (the fused GPU layer of
+ * runtime/detgpu/stages.py:154-168), bit-identical to the CPU reference runtime/detrt
+ * (core.py, stage.py:146-233). Row-major fp32 / int8 / int32 buffers; N = B * T tokens of
+ * B sequences, token n at position n % T. inv_d = float32(1 / k), eps = float32(rms_norm_eps).
+ * A row must fit in LDS (k <= 40960 floats). */
+
+/* q, scale = quant_act(det_rmsnorm(x, w, eps), bs) per row of x (rows x k).
+ * Replaces detgpu kernels.rmsnorm_quant: runtime/detgpu/kernels.py:712-728, :117-195. */
+int uwc_rmsnorm_quant_f32(const float* x, const float* w, int rows, int k, int bs, float inv_d, float eps, int8_t* q,
+                          float* scale, hipStream_t stream);
+
+/* y = det_rmsnorm(x, w, eps) per row (the final-norm hidden state, qwen3.py:300).
+ * Replaces core.det_rmsnorm: runtime/detrt/core.py:149-156. */
+int uwc_rmsnorm_f32(const float* x, const float* w, int rows, int k, float inv_d, float eps, float* y,
+                    hipStream_t stream);
+
+/* From the qkv GEMM's int32 rows (N x (H + 2 Hkv) hd): dequant with s1[n] and sw[col] (or, with
+ * s1 = sw = NULL, acc holds the already dequantized fp32 rows), per-head
+ * det_rmsnorm with qnw / knw (qknorm != 0: Qwen3; 0: Llama / Mistral), rope from the cos / sin
+ * tables (max_pos x hd, row = position), and quant_sym(127) per head: qq (N, H, hd) int8, qs
+ * (N, H), kq / vq (N, Hkv, hd), ks / vs (N, Hkv). vt (optional, NULL to skip) receives V
+ * transposed per (sequence, kv head) in the attention kernel's key order, (B, Hkv, hd,
+ * uwc_vt_tokens(T)) int8. hd in {32, 64, 128}.
+ * Replaces detgpu kernels.qkv_post: runtime/detgpu/kernels.py:788-802, :356-398. */
+int uwc_qkv_post(const void* acc, const float* s1, const float* sw, const float* qnw, const float* knw,
+                 const float* cos_tab, const float* sin_tab, int B, int T, int H, int Hkv, int hd, float eps, int qknorm,
+                 int8_t* qq, float* qs, int8_t* kq, float* ks, int8_t* vq, float* vs, int8_t* vt, hipStream_t stream);
+
+/* Padded key count of the transposed V (T rounded up to 64). Host-side, no GPU work. */
+int uwc_vt_tokens(int T);
+
+/* vt = V (N x Hkv x hd int8) in the attention kernel's transposed layout (see uwc_qkv_post). */
+int uwc_v_transpose(const int8_t* vq, int B, int T, int Hkv, int hd, int8_t* vt, hipStream_t stream);
+
+/* Exact causal attention per sequence from quantized heads (qq, qs, kq, ks as uwc_qkv_post;
+ * vt from uwc_qkv_post / uwc_v_transpose; vs (N, Hkv)): o (N, H * hd) fp32, the O rows.
+ * Scores are exact int8 dot products, softmax uses det_exp and an exact fixed-point sum, P is
+ * quantized to 14 bits and multiplied as two 7-bit limbs with an exact integer sum.
+ * T <= 131072, H % Hkv == 0, hd in {32, 64, 128}; qq, kq, vt, o 16-byte aligned.
+ * Replaces detgpu kernels.attention: runtime/detgpu/kernels.py:731-770 (stage.py:171-196). */
+int uwc_attention(const int8_t* qq, const float* qs, const int8_t* kq, const float* ks, const int8_t* vt,
+                  const float* vs, int B, int T, int H, int Hkv, int hd, float inv_sqrt_hd, float* o,
+                  hipStream_t stream);
+
+/* q, scale = quant_act(fmul(det_silu(g), u), bs) per row, g and u the dequantized halves of the
+ * gate_up GEMM's int32 row (rows x 2I; s3[row], sw[col]), or with s3 = sw = NULL its fp32 row.
+ * Replaces detgpu kernels.swiglu_quant: runtime/detgpu/kernels.py:816-826. */
+int uwc_swiglu_quant(const void* acc, const float* s3, const float* sw, int rows, int I, int bs, int8_t* q,
+                     float* scale, hipStream_t stream);
+
+/* out = fadd(x, fmul(fmul(f32(acc), s[row]), sw[col])) (rows x n): R1 and R2; with s = sw = NULL,
+ * acc holds the fp32 term and out = fadd(x, acc).
+ * Replaces detgpu kernels.dequant_residual: runtime/detgpu/kernels.py:805-813. */
+int uwc_dequant_residual(const void* acc, const float* s, const float* sw, const float* x, int rows, int n,
+                         float* out, hipStream_t stream);
+
+/* out[t] = table[ids[t]] (V x D fp32); an id outside [0, V) gives a zero row and increments *bad
+ * (optional). Replaces the embedding lookup m.embed[tokens] (stage.py:141, detgpu/stages.py:185). */
+int uwc_embed_rows(const float* table, int64_t V, int D, const int64_t* ids, int N, float* out, int* bad,
+                   hipStream_t stream);
+
+/* out[i] = op(x[i], y[i]) for one of detrt's elementwise fp32 ops exactly as the layer kernels
+ * compute it (y unused for SQRT, EXP, SILU): the per-op check that native gfx950 fp32 equals
+ * detrt's emulated fp32. Replaces runtime/tests/test_fp32_native.py's per-op GPU check
+ * (core.py:45-63 fadd/fsub/fmul/fdiv/fsqrt, :108-146 det_exp, det_silu). */
+#define UWC_OP_ADD 0
+#define UWC_OP_SUB 1
+#define UWC_OP_MUL 2
+#define UWC_OP_DIV 3
+#define UWC_OP_SQRT 4
+#define UWC_OP_EXP 5
+#define UWC_OP_SILU 6
+int uwc_det_elementwise(int op, const float* x, const float* y, float* out, int64_t n, hipStream_t stream);
+
+/* ======================================================================== stage commitments
+ * SHA-256 / RFC 6962 trees as runtime/detrt/stage.py:33-77: a row is little-endian 4-byte
+ * words cut into 1 KiB blocks, row_root = MerkleRoot(H(0x00 || block)); a tagged leaf is
+ * H(0x00 || tag || u32le index || row_root) with tag "leaf" (trace) or "sout" (stage outputs,
+ * spec/stage-program.md:82-88). Digests are 8 SHA-256 state words (big-endian bytes). */
+
+/* For nrows rows of row_words words each: row roots (optional, nrows x 8) and tagged leaves
+ * (optional, nrows x 8) with index (index_base + row) % index_mod (index_mod 0: no modulus);
+ * tag is the 4 tag bytes as a big-endian word. scratch: nrows * ceil(row_words / 256) * 8 words.
+ * Replaces detgpu sha.sout_leaves / _leaf_words: runtime/detgpu/sha.py:139-200. */
+int uwc_sha_row_leaves(const uint32_t* rows, int64_t nrows, int row_words, uint32_t* scratch, int64_t scratch_words,
+                       uint32_t tag, uint32_t index_base, uint32_t index_mod, uint32_t* row_roots, uint32_t* leaves,
+                       hipStream_t stream);
+
+/* roots[t] = MerkleRoot(leaves[t * n .. t * n + n)) for ntrees trees; scratch 2 * ntrees * n * 8 words.
+ * Replaces detgpu sha.tree_roots / stage_roots_gpu: runtime/detgpu/sha.py:117-136, :203-215. */
+int uwc_sha_merkle_roots(const uint32_t* leaves, int ntrees, int n, uint32_t* scratch, int64_t scratch_words,
+                         uint32_t* roots, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,175 @@
+"""CPU emulation of the attention kernel's data movement (useful-work-coin_amd/csrc/uwc_attn.hip,
+uwc_layer.hip's vt_pos): which key and query every lane and MFMA slot touches, and every load and
+store address against its buffer. No GPU needed.
+
+v_mfma_i32_16x16x64_i8 (gfx950): A is 16 rows x 64 k with lane l holding row l & 15 and k bytes
+16 (l >> 4) .. + 16; B likewise with column l & 15; C lane l register i is row 4 (l >> 4) + i,
+column l & 15. The kernel relies only on A and B using the same (lane group, slot) -> k map,
+so the emulation below applies the product exactly that way."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import detrt_stage as S
+
+
+def vt_pos(j: int) -> int:
+    return (j & ~63) | (((j >> 2) & 3) << 4) | (((j >> 4) & 3) << 2) | (j & 3)
+
+
+def mfma_16x16x64(a_frag, b_frag):
+    """a_frag, b_frag: (64 lanes, 16 slots) int. Returns C (64 lanes, 4 regs)."""
+    A = np.zeros((16, 64), np.int64)
+    Bm = np.zeros((64, 16), np.int64)
+    for l in range(64):
+        for s in range(16):
+            A[l & 15, 16 * (l >> 4) + s] = a_frag[l, s]
+            Bm[16 * (l >> 4) + s, l & 15] = b_frag[l, s]
+    C = A @ Bm
+    out = np.zeros((64, 4), np.int64)
+    for l in range(64):
+        for i in range(4):
+            out[l, i] = C[4 * (l >> 4) + i, l & 15]
+    return out
+
+
+def test_vt_pos_is_a_block_permutation():
+    for base in (0, 64, 128):
+        got = sorted(vt_pos(base + j) for j in range(64))
+        assert got == list(range(base, base + 64))
+    # the C register order of a 64-key tile equals the k slot order of the P x V MFMA
+    for g in range(4):
+        for s in range(16):
+            key = 16 * (s >> 2) + 4 * g + (s & 3)   # C: block b = s >> 2, register i = s & 3
+            assert vt_pos(key) == 16 * g + s        # where the A operand's lane group g reads slot s
+
+
+def emulate(qq, qs, kq, ks, vq, vs, B, T, H, Hkv, hd, inv):
+    """The kernel's index arithmetic with exact integer products; returns o (N, H * hd) and the
+    largest address touched per buffer."""
+    NC, ND = (hd + 63) // 64, hd // 16
+    Tp = -(-T // 64) * 64
+    N = B * T
+    vt = np.zeros(B * Hkv * hd * Tp, np.int64)
+    for n in range(N):  # v_transpose / qkv_post's vt store
+        bseq, pos = divmod(n, T)
+        for hk in range(Hkv):
+            for d in range(hd):
+                vt[((bseq * Hkv + hk) * hd + d) * Tp + vt_pos(pos)] = vq[n, hk, d]
+    maxaddr = dict(qq=0, kq=0, vt=0, ks=0, vs=0, o=0, qs=0)
+    o = np.zeros((N, H * hd), np.float32)
+    lanes = np.arange(64)
+    ql, g = lanes & 15, lanes >> 4
+    for bseq in range(B):
+        nb = bseq * T
+        for h in range(H):
+            hk = h // (H // Hkv)
+            for q0 in range(0, T, 16):  # one wave per 16 queries
+                qi = q0 + ql
+                qc = np.minimum(qi, T - 1)
+                maxaddr["qs"] = max(maxaddr["qs"], int(((nb + qc) * H + h).max()))
+                my_qs = qs[nb + qc, h, 0]
+                qf = np.zeros((NC, 64, 16), np.int64)
+                for c in range(NC):
+                    for l in range(64):
+                        d0 = 64 * c + 16 * g[l]
+                        if d0 < hd:
+                            addr = ((nb + qc[l]) * H + h) * hd + d0
+                            maxaddr["qq"] = max(maxaddr["qq"], addr + 15)
+                            qf[c, l] = qq[nb + qc[l], h, d0:d0 + 16]
+                kmax = min(T, q0 + 16)
+                nkt = (kmax + 63) // 64
+                tiles = []
+                for kt in range(nkt):
+                    Sv = np.full((64, 4, 4), -np.inf, np.float32)
+                    for b in range(4):
+                        kr = np.minimum(kt * 64 + 16 * b + ql, T - 1)
+                        acc = np.zeros((64, 4), np.int64)
+                        for c in range(NC):
+                            kf = np.zeros((64, 16), np.int64)
+                            for l in range(64):
+                                d0 = 64 * c + 16 * g[l]
+                                if d0 < hd:
+                                    addr = ((nb + kr[l]) * Hkv + hk) * hd + d0
+                                    maxaddr["kq"] = max(maxaddr["kq"], addr + 15)
+                                    kf[l] = kq[nb + kr[l], hk, d0:d0 + 16]
+                            acc += mfma_16x16x64(kf, qf[c])
+                        for i in range(4):
+                            j = kt * 64 + 16 * b + 4 * g + i
+                            ok = (j <= qi) & (j < T)
+                            jc = np.minimum(j, T - 1)
+                            sc = ((acc[:, i].astype(np.float32) * my_qs) * ks[nb + jc, hk, 0]) * inv
+                            Sv[:, b, i] = np.where(ok, sc, -np.inf)
+                            if ok.any():
+                                maxaddr["ks"] = max(maxaddr["ks"], int(((nb + j[ok]) * Hkv + hk).max()))
+                    tiles.append(Sv)
+                # row statistics per query (lanes with equal ql), as the oracle defines them
+                allS = np.concatenate([t.reshape(64, 16) for t in tiles], axis=1)  # (64, 16 * nkt)
+                keys = np.concatenate([[kt * 64 + 16 * (s >> 2) + 4 * g + (s & 3) for s in range(16)]
+                                       for kt in range(nkt)], axis=0).T            # (64, 16 * nkt)
+                ohi = np.zeros((ND, 64, 4), np.int64)
+                olo = np.zeros((ND, 64, 4), np.int64)
+                pis = np.zeros((64, allS.shape[1]), np.int64)
+                sps = np.zeros(64, np.float32)
+                for qv in range(16):
+                    ls = np.nonzero(ql == qv)[0]
+                    row = allS[ls].ravel()
+                    kk = keys[ls].ravel()
+                    valid = row != -np.inf
+                    if not valid.any():
+                        continue
+                    mx = row[valid].max()
+                    e = np.zeros_like(row)
+                    e[valid] = S.det_exp(row[valid] - mx)
+                    den = S.exact_rowsum(e[None, :], S.MAX_KEYS)[0]
+                    pv = np.zeros_like(row)
+                    pv[valid] = (e[valid] / den) * vs[nb + kk[valid], hk, 0]
+                    sp = np.maximum(pv.max(), np.float32(1e-30)) / np.float32(S.P_LEVELS)
+                    pi = np.where(valid, np.clip(np.rint(pv / sp), 0, S.P_LEVELS), 0).astype(np.int64)
+                    pis[ls] = pi.reshape(len(ls), -1)
+                    sps[ls] = sp
+                for kt in range(nkt):
+                    p = pis[:, 16 * kt:16 * kt + 16]
+                    bhi, blo = p >> 7, p & 127
+                    for d in range(ND):
+                        vf = np.zeros((64, 16), np.int64)
+                        for l in range(64):
+                            addr = ((bseq * Hkv + hk) * hd + 16 * d + ql[l]) * Tp + kt * 64 + 16 * g[l]
+                            maxaddr["vt"] = max(maxaddr["vt"], addr + 15)
+                            vf[l] = vt[addr:addr + 16]
+                        ohi[d] += mfma_16x16x64(vf, bhi)
+                        olo[d] += mfma_16x16x64(vf, blo)
+                for l in range(64):
+                    if qi[l] >= T:
+                        continue
+                    for d in range(ND):
+                        for i in range(4):
+                            a = (int(ohi[d, l, i]) << 7) + int(olo[d, l, i])
+                            col = 16 * d + 4 * g[l] + i
+                            addr = ((nb + qi[l]) * H + h) * hd + col
+                            maxaddr["o"] = max(maxaddr["o"], addr)
+                            o[nb + qi[l], h * hd + col] = np.float32(a) * sps[l]
+    return o, maxaddr
+
+
+@pytest.mark.parametrize("B,T,H,Hkv,hd", [(1, 12, 4, 2, 32), (2, 5, 2, 1, 64), (1, 70, 2, 2, 128), (1, 1, 1, 1, 32)])
+def test_attention_layout_matches_oracle(B, T, H, Hkv, hd):
+    rng = np.random.default_rng(T * 31 + hd)
+    N = B * T
+    qq = rng.integers(-127, 128, (N, H, hd))
+    kq = rng.integers(-127, 128, (N, Hkv, hd))
+    vq = rng.integers(-127, 128, (N, Hkv, hd))
+    qs = rng.uniform(1e-3, 1e-2, (N, H, 1)).astype(np.float32)
+    ks = rng.uniform(1e-3, 1e-2, (N, Hkv, 1)).astype(np.float32)
+    vs = rng.uniform(1e-3, 1e-2, (N, Hkv, 1)).astype(np.float32)
+    inv = S.inv_sqrt_hd(hd)
+    o, maxaddr = emulate(qq, qs, kq, ks, vq, vs, B, T, H, Hkv, hd, inv)
+    for bseq in range(B):
+        sl = slice(bseq * T, (bseq + 1) * T)
+        _, _, _, ref = S.attention(qq[sl], qs[sl], kq[sl], ks[sl], vq[sl], vs[sl], inv)
+        np.testing.assert_array_equal(o[sl].view(np.uint32), ref.transpose(1, 0, 2).reshape(T, H * hd).view(np.uint32))
+    Tp = -(-T // 64) * 64
+    assert maxaddr["qq"] < N * H * hd and maxaddr["kq"] < N * Hkv * hd
+    assert maxaddr["vt"] < B * Hkv * hd * Tp and maxaddr["o"] < N * H * hd
+    assert maxaddr["ks"] < N * Hkv and maxaddr["qs"] < N * H

@@ -7,5 +7,6 @@ cd "$(dirname "$0")"
 OUT=../uwc_amd/libuwc_hip.so
 /opt/rocm/bin/hipcc --offload-arch=gfx950 -O3 -std=c++17 -fPIC -shared -ffp-contract=off \
   -Xclang -target-feature -Xclang -packed-fp32-ops -Wno-unused-result -I../../include ${UWC_HIPCC_EXTRA} \
-  uwc_abi.hip uwc_commit.hip uwc_gemm.hip uwc_gemm256.hip uwc_noise.hip uwc_quant.hip uwc_side.hip uwc_skinny.hip -o "$OUT.tmp"
+  uwc_abi.hip uwc_commit.hip uwc_gemm.hip uwc_gemm256.hip uwc_noise.hip uwc_quant.hip uwc_side.hip uwc_skinny.hip \
+  uwc_layer.hip uwc_attn.hip uwc_sha.hip -o "$OUT.tmp"
 mv "$OUT.tmp" "$OUT"

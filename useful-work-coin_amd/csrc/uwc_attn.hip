@@ -1,0 +1,227 @@
+// detrt's exact causal attention on gfx950, bit-identical to the CPU reference
+// (runtime/detrt/stage.py:171-196, runtime/detrt/qwen3.py:255-282; CUDA twin
+// runtime/detgpu/kernels.py:196-633):
+//
+//   s_ij  = ((f32(q_i . k_j) * qs_i) * ks_j) * (1 / sqrt(hd))          exact int dot product
+//   e_ij  = det_exp(s_ij - max_j s_ij)                                  j <= i, else 0
+//   den_i = exact_rowsum(e_i)                                           int64 fixed point
+//   pv_ij = (e_ij / den_i) * vs_j,  sp_i = max(max_j pv_ij, 1e-30) / 16383
+//   p_ij  = clamp(rint(pv_ij / sp_i), 0, 16383) = 128 hi + lo
+//   o_id  = f32(sum_j p_ij v_jd) * sp_i                                 exact int64 sum
+//
+// The design is MI355X-first rather than a row-per-block port:
+//   * a wave owns 16 queries of one head; both products run on v_mfma_i32_16x16x64_i8:
+//     scores as S^T = K Q^T (A = 16 keys, B = the wave's 16 queries, held in registers), the
+//     output as O^T = V^T P^T with P's two 7-bit limbs as int8 B operands (int32 accumulators
+//     stay exact: 127 * 127 * T < 2^31 for T <= 131072);
+//   * the C registers of the four 16x16 score blocks of a 64-key tile are, lane by lane, the
+//     16 keys of one query that the P x V MFMA needs as its k slots (keys 16 b + 4 g + i for lane
+//     group g), so P never leaves registers; V^T is stored with its keys in that order
+//     (qkv_post / v_transpose write it so), one 16-byte load per lane and dim block;
+//   * the three row statistics (max, exact sum, max of the scaled probabilities) each need the
+//     previous one over the whole causal row, so the kernel sweeps the keys four times and
+//     recomputes the scores (cheap on the matrix cores) instead of storing T x T rows;
+//   * exp rows have max exactly det_exp(0) = 1 and every term below 2, so exact_rowsum's
+//     scale is the constant 2^41 (L = 20 for MAX_KEYS = 2^20): a term is rint(e * 2^41) < 2^42,
+//     converted to u64 through two exact float32 halves.
+// Row statistics are per lane partials combined across the 4 lane groups (xor 16, 32); all
+// reductions are max or exact integer sums, so the key split cannot change a bit.
+#include "uwc_rows.h"
+
+#define AT_PLEVELS 16383.0f
+
+__device__ __forceinline__ v4i at_zero4() { return v4i{0, 0, 0, 0}; }
+
+// round_half_even(e * 2^41) as u64 for 0 <= e < 2 (exact; see the file comment).
+__device__ __forceinline__ u64 at_fix41(float e) {
+  const float v = rintf(__fmul_rn(e, 0x1p41f));
+  const float hi = floorf(__fmul_rn(v, 0x1p-32f));
+  const float lo = __fsub_rn(v, __fmul_rn(hi, 0x1p32f));
+  return ((u64)(u32)hi << 32) | (u64)(u32)lo;
+}
+
+__device__ __forceinline__ float at_max_groups(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16, 64));
+  return fmaxf(v, __shfl_xor(v, 32, 64));
+}
+
+__device__ __forceinline__ u64 at_sum_groups(u64 v) {
+#pragma unroll
+  for (int s = 16; s <= 32; s <<= 1) {
+    const u32 lo = (u32)__shfl_xor((int)(u32)v, s, 64), hi = (u32)__shfl_xor((int)(u32)(v >> 32), s, 64);
+    v += ((u64)hi << 32) | lo;
+  }
+  return v;
+}
+
+template <int HD>
+__global__ void __launch_bounds__(256) attention_kernel(const i8* __restrict__ qq, const float* __restrict__ qs,
+                                                        const i8* __restrict__ kq, const float* __restrict__ ks,
+                                                        const i8* __restrict__ vt, const float* __restrict__ vs, int T,
+                                                        int Tp, int H, int Hkv, float inv_sqrt, float* __restrict__ o) {
+  constexpr int NC = (HD + 63) / 64;  // 64-dim chunks of the score product
+  constexpr int ND = HD / 16;         // 16-dim blocks of the output
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int ql = lane & 15, g = lane >> 4;
+  // longest rows first: the q tile index counts down
+  const int q0 = (gridDim.x - 1 - blockIdx.x) * 64 + wave * 16;
+  if (q0 >= T) return;  // whole waves only; the kernel has no barriers
+  const int h = blockIdx.y, bseq = blockIdx.z, hk = h / (H / Hkv);
+  const long nb = (long)bseq * T;
+  const int qi = q0 + ql, qc = min(qi, T - 1);
+  const float my_qs = qs[(nb + qc) * H + h];
+
+  v4i qf[NC];
+#pragma unroll
+  for (int c = 0; c < NC; c++) {
+    const int d0 = 64 * c + 16 * g;
+    qf[c] = d0 < HD ? *reinterpret_cast<const v4i*>(qq + ((nb + qc) * H + h) * HD + d0) : at_zero4();
+  }
+  const int kmax = min(T, q0 + 16);  // keys any query of the wave sees
+  const int nkt = (kmax + 63) / 64;
+
+  // scores of key tile kt: S[b][i] = score of key 64 kt + 16 b + 4 g + i for query qi (or -inf)
+  auto scores = [&](int kt, float S[4][4]) {
+    v4i acc[4];
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+      acc[b] = at_zero4();
+      const int kr = min(kt * 64 + 16 * b + ql, T - 1);
+      const i8* kp = kq + ((nb + kr) * Hkv + hk) * HD;
+#pragma unroll
+      for (int c = 0; c < NC; c++) {
+        const int d0 = 64 * c + 16 * g;
+        const v4i kf = d0 < HD ? *reinterpret_cast<const v4i*>(kp + d0) : at_zero4();
+        acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf, qf[c], acc[b], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < 4; b++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int j = kt * 64 + 16 * b + 4 * g + i;
+        float s = -__int_as_float(0x7f800000);
+        if (j <= qi && j < T) s = __fmul_rn(__fmul_rn(__fmul_rn((float)acc[b][i], my_qs), ks[(nb + j) * Hkv + hk]), inv_sqrt);
+        S[b][i] = s;
+      }
+  };
+
+  // sweep 1: row max
+  float mx = -__int_as_float(0x7f800000);
+  for (int kt = 0; kt < nkt; kt++) {
+    float S[4][4];
+    scores(kt, S);
+#pragma unroll
+    for (int b = 0; b < 4; b++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) mx = fmaxf(mx, S[b][i]);
+  }
+  mx = at_max_groups(mx);
+
+  // sweep 2: exact denominator (fixed point at 2^41)
+  u64 dsum = 0;
+  for (int kt = 0; kt < nkt; kt++) {
+    float S[4][4];
+    scores(kt, S);
+#pragma unroll
+    for (int b = 0; b < 4; b++)
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        if (S[b][i] != -__int_as_float(0x7f800000)) dsum += at_fix41(dx_exp(__fsub_rn(S[b][i], mx)));
+  }
+  dsum = at_sum_groups(dsum);
+  const float den = (float)ldexp((double)dsum, -41);
+
+  // sweep 3: max of the V-scaled probabilities
+  float pm = 0.f;
+  for (int kt = 0; kt < nkt; kt++) {
+    float S[4][4];
+    scores(kt, S);
+#pragma unroll
+    for (int b = 0; b < 4; b++)
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        if (S[b][i] != -__int_as_float(0x7f800000)) {
+          const int j = kt * 64 + 16 * b + 4 * g + i;
+          const float e = dx_exp(__fsub_rn(S[b][i], mx));
+          pm = fmaxf(pm, __fmul_rn(__fdiv_rn(e, den), vs[(nb + j) * Hkv + hk]));
+        }
+  }
+  pm = at_max_groups(pm);
+  const float sp = __fdiv_rn(fmaxf(pm, 1e-30f), AT_PLEVELS);
+
+  // sweep 4: 14-bit probabilities as two 7-bit limbs, O^T = V^T P^T on the matrix cores
+  v4i ohi[ND], olo[ND];
+#pragma unroll
+  for (int d = 0; d < ND; d++) ohi[d] = olo[d] = at_zero4();
+  const i8* vbase = vt + ((long)(bseq * Hkv + hk) * HD) * Tp;
+  for (int kt = 0; kt < nkt; kt++) {
+    float S[4][4];
+    scores(kt, S);
+    v4i bhi, blo;
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+      u32 ph = 0, pl = 0;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        int p = 0;
+        if (S[b][i] != -__int_as_float(0x7f800000)) {
+          const int j = kt * 64 + 16 * b + 4 * g + i;
+          const float e = dx_exp(__fsub_rn(S[b][i], mx));
+          const float pv = __fmul_rn(__fdiv_rn(e, den), vs[(nb + j) * Hkv + hk]);
+          p = (int)fminf(fmaxf(rintf(__fdiv_rn(pv, sp)), 0.0f), AT_PLEVELS);
+        }
+        ph |= (u32)(p >> 7) << (8 * i);
+        pl |= (u32)(p & 127) << (8 * i);
+      }
+      bhi[b] = (int)ph;
+      blo[b] = (int)pl;
+    }
+#pragma unroll
+    for (int d = 0; d < ND; d++) {
+      const v4i vf = *reinterpret_cast<const v4i*>(vbase + (long)(16 * d + ql) * Tp + kt * 64 + 16 * g);
+      ohi[d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(vf, bhi, ohi[d], 0, 0, 0);
+      olo[d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(vf, blo, olo[d], 0, 0, 0);
+    }
+  }
+  if (qi >= T) return;
+  // lane holds dims 16 d + 4 g + i of query qi
+  float* orow = o + ((nb + qi) * H + h) * HD;
+#pragma unroll
+  for (int d = 0; d < ND; d++) {
+    float4 r;
+    float* rr = reinterpret_cast<float*>(&r);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const long long a = ((long long)ohi[d][i] << 7) + (long long)olo[d][i];
+      rr[i] = __fmul_rn((float)a, sp);
+    }
+    *reinterpret_cast<float4*>(orow + 16 * d + 4 * g) = r;
+  }
+}
+
+extern "C" int uwc_attention(const int8_t* qq, const float* qs, const int8_t* kq, const float* ks, const int8_t* vt,
+                             const float* vs, int B, int T, int H, int Hkv, int hd, float inv_sqrt_hd, float* o,
+                             hipStream_t stream) {
+  const char* fn = "uwc_attention";
+  if (!qq || !qs || !kq || !ks || !vt || !vs || !o) return uwc_fail("%s: null arguments", fn);
+  if (B < 0 || T <= 0 || T > 131072 || H <= 0 || Hkv <= 0 || H % Hkv)
+    return uwc_fail("%s: bad B=%d T=%d H=%d Hkv=%d (T <= 131072)", fn, B, T, H, Hkv);
+  if (hd != 32 && hd != 64 && hd != 128) return uwc_fail("%s: head_dim %d not in {32, 64, 128}", fn, hd);
+  if (((uintptr_t)qq | (uintptr_t)kq | (uintptr_t)vt) & 15) return uwc_fail("%s: qq, kq, vt must be 16-byte aligned", fn);
+  if ((uintptr_t)o & 15) return uwc_fail("%s: o must be 16-byte aligned", fn);
+  if (B == 0) return UWC_OK;
+  if (B > 65535 || H > 65535) return uwc_fail("%s: B and H must be <= 65535", fn);
+  const int Tp = ((T + 63) / 64) * 64;
+  const dim3 grid((unsigned)(Tp / 64), (unsigned)H, (unsigned)B);
+  if (hd == 32)
+    hipLaunchKernelGGL(attention_kernel<32>, grid, dim3(256), 0, stream, qq, qs, kq, ks, vt, vs, T, Tp, H, Hkv,
+                       inv_sqrt_hd, o);
+  else if (hd == 64)
+    hipLaunchKernelGGL(attention_kernel<64>, grid, dim3(256), 0, stream, qq, qs, kq, ks, vt, vs, T, Tp, H, Hkv,
+                       inv_sqrt_hd, o);
+  else
+    hipLaunchKernelGGL(attention_kernel<128>, grid, dim3(256), 0, stream, qq, qs, kq, ks, vt, vs, T, Tp, H, Hkv,
+                       inv_sqrt_hd, o);
+  return uwc_launch_status(fn);
+}

@@ -15,6 +15,13 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 
 #define UWC_OK 0
 
+// Correctly rounded float32 square root. HIP's __fsqrt_rn is the native (approximate) sqrt
+// unless OCML's rounded operations are enabled, so the root is taken in float64 (correctly
+// rounded) and rounded once to float32: double rounding is innocuous for sqrt since
+// 53 >= 2 * 24 + 2. (__fdiv_rn / __fmul_rn / __fadd_rn are the plain correctly rounded ops;
+// the library builds with -ffp-contract=off so they are never fused.)
+__device__ __forceinline__ float uwc_sqrt_rn(float x) { return (float)__builtin_sqrt((double)x); }
+
 // Records a message for uwc_last_error() and returns UWC_EINVAL.
 int uwc_fail(const char* fmt, ...);
 // hipGetLastError() after a launch, converted to a status (and a message on failure).

@@ -1,0 +1,371 @@
+// detrt's decoder-layer row ops on gfx950, bit-identical to the CPU reference: the fused
+// kernels around the exact int8 GEMMs of one layer (runtime/detgpu/stages.py:154-168 calls
+// them; CUDA twins runtime/detgpu/kernels.py:117-353, CPU definitions runtime/detrt/core.py and
+// runtime/detrt/stage.py:146-233):
+//
+//   rmsnorm_quant    N1 / N2 (and the final norm before lm_head) fused with the next quant_act
+//   qkv_post         QKV dequant -> per-head RMSNorm (Qwen3) -> rope -> per-head int8 quant of
+//                    q, k and v, plus V transposed into the attention kernel's key order
+//   swiglu_quant     GU dequant -> SiLU(g) * u -> quant_act (SM, QA4)
+//   dequant_residual x + dequant(acc) (R1, R2)
+//   embed_rows       the embedding gather (EMBED)
+//   rmsnorm          det_rmsnorm alone (the final-norm hidden state)
+//
+// Row kernels keep one row in LDS (one workgroup of 256 threads per row). qkv_post gives each
+// head row to one wave (head_dim 32, 64 or 128; lane d holds elements d, d + 64, ...), so its
+// reductions are wave shuffles. Every fp32 step is one correctly rounded op in the reference's
+// order (uwc_rows.h).
+#include "uwc_rows.h"
+
+// ------------------------------------------------------------------ rmsnorm (+ quant_act)
+template <bool QUANT>
+__global__ void __launch_bounds__(256) rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w, int k,
+                                                      int bs, float inv_d, float eps, i8* __restrict__ q,
+                                                      float* __restrict__ scale, float* __restrict__ y) {
+  extern __shared__ float dx_row[];
+  __shared__ DxRed red;
+  const long r = blockIdx.x;
+  const float* xr = x + r * k;
+  for (int i = threadIdx.x; i < k; i += 256) dx_row[i] = xr[i];
+  __syncthreads();
+  dx_rmsnorm_lds(dx_row, k, w, inv_d, eps, red);
+  if constexpr (QUANT) {
+    dx_quant_lds(dx_row, k, bs, 64, q + r * k, scale + r, red);
+  } else {
+    float* yr = y + r * k;
+    for (int i = threadIdx.x; i < k; i += 256) yr[i] = dx_row[i];
+  }
+}
+
+// ------------------------------------------------------------------ swiglu + quant_act
+// acc: rows x 2I (gate | up), int32 accumulators dequantized with s3[row], sw[col], or with FP
+// already fp32; row value i = fmul(silu(g_i), u_i) (stage.py:220-221).
+template <bool FP>
+__global__ void __launch_bounds__(256) swiglu_quant_kernel(const void* __restrict__ acc, const float* __restrict__ s3,
+                                                           const float* __restrict__ sw, int I, int bs,
+                                                           i8* __restrict__ q, float* __restrict__ scale) {
+  extern __shared__ float dx_row[];
+  __shared__ DxRed red;
+  const long r = blockIdx.x;
+  for (int i = threadIdx.x; i < I; i += 256) {
+    float g, u;
+    if constexpr (FP) {
+      const float* ar = static_cast<const float*>(acc) + r * 2L * I;
+      g = ar[i];
+      u = ar[I + i];
+    } else {
+      const i32* ar = static_cast<const i32*>(acc) + r * 2L * I;
+      const float sx = s3[r];
+      g = dx_deq(ar[i], sx, sw[i]);
+      u = dx_deq(ar[I + i], sx, sw[I + i]);
+    }
+    dx_row[i] = __fmul_rn(dx_silu(g), u);
+  }
+  __syncthreads();
+  dx_quant_lds(dx_row, I, bs, 64, q + r * (long)I, scale + r, red);
+}
+
+// ------------------------------------------------------------------ residual
+// out = fadd(x, fmul(fmul(f32(acc), s[row]), sw[col])) (stage.py:217, 224); with FP acc is the
+// already dequantized fp32 term.
+template <bool FP>
+__global__ void dequant_residual_kernel(const void* __restrict__ acc, const float* __restrict__ s,
+                                        const float* __restrict__ sw, const float* __restrict__ x, int n, u64 total,
+                                        float* __restrict__ out) {
+  for (u64 i = (u64)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (u64)gridDim.x * blockDim.x) {
+    float y;
+    if constexpr (FP) {
+      y = static_cast<const float*>(acc)[i];
+    } else {
+      const u64 r = i / (u64)n;
+      const int c = (int)(i - r * n);
+      y = dx_deq(static_cast<const i32*>(acc)[i], s[r], sw[c]);
+    }
+    out[i] = __fadd_rn(x[i], y);
+  }
+}
+
+// ------------------------------------------------------------------ embedding gather
+// out[t] = table[ids[t]]; an id outside [0, V) yields a zero row and bumps *bad (never read out
+// of bounds).
+__global__ void embed_kernel(const float* __restrict__ table, long V, int D, const int64_t* __restrict__ ids, int N,
+                             float* __restrict__ out, int* __restrict__ bad) {
+  const int t = blockIdx.x;
+  if (t >= N) return;
+  const int64_t id = ids[t];
+  const bool ok = id >= 0 && id < V;
+  if (!ok && threadIdx.x == 0 && bad) atomicAdd(bad, 1);
+  const float* src = table + (ok ? id : 0) * (long)D;
+  float* dst = out + (long)t * D;
+  for (int i = threadIdx.x; i < D; i += blockDim.x) dst[i] = ok ? src[i] : 0.0f;
+}
+
+// ------------------------------------------------------------------ qkv_post
+// Position of key j inside its 64-key block in the transposed V the attention kernel reads:
+// key 16 kb + 4 kg + ki sits at 16 kg + 4 kb + ki (the order in which a 16x16 score block's
+// C registers hand keys to the P x V MFMA's k slots).
+__host__ __device__ __forceinline__ int vt_pos(int j) {
+  return (j & ~63) | (((j >> 2) & 3) << 4) | (((j >> 4) & 3) << 2) | (j & 3);
+}
+
+template <int HD, bool FP>
+__global__ void __launch_bounds__(256) qkv_post_kernel(
+    const void* __restrict__ acc, const float* __restrict__ s1, const float* __restrict__ sw,
+    const float* __restrict__ qnw, const float* __restrict__ knw, const float* __restrict__ cosb,
+    const float* __restrict__ sinb, int T, int H, int Hkv, float inv_hd, float eps, int qknorm, i8* __restrict__ qq,
+    float* __restrict__ qs, i8* __restrict__ kq, float* __restrict__ ks, i8* __restrict__ vq, float* __restrict__ vs,
+    i8* __restrict__ vt, int Tp) {
+  constexpr int NV = HD >= 64 ? HD / 64 : 1;
+  constexpr int L = HD == 32 ? 5 : HD == 64 ? 6 : 7;  // ceil(log2(HD))
+  const int n = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int pos = n % T, bseq = n / T;
+  const int NH = H + 2 * Hkv;
+  const long W = (long)NH * HD;
+  const bool act = HD >= 64 || lane < HD;
+  const float sx = FP ? 1.0f : s1[n];
+  for (int hh = wave; hh < NH; hh += 4) {
+    const int col0 = hh * HD;
+    float v[NV];
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+      const int d = lane + 64 * j;
+      if (!act) v[j] = 0.0f;
+      else if constexpr (FP) v[j] = static_cast<const float*>(acc)[n * W + col0 + d];
+      else v[j] = dx_deq(static_cast<const i32*>(acc)[n * W + col0 + d], sx, sw[col0 + d]);
+    }
+    const bool isq = hh < H, isv = hh >= H + Hkv;
+    if (!isv) {
+      if (qknorm) {  // det_rmsnorm over the head (qwen3.py:214-216)
+        const float* wn = isq ? qnw : knw;
+        float mx = 0.f;
+#pragma unroll
+        for (int j = 0; j < NV; j++) mx = fmaxf(mx, __fmul_rn(v[j], v[j]));
+        const int sh = dx_shift(wave_max(mx), L);
+        long long s = 0;
+#pragma unroll
+        for (int j = 0; j < NV; j++) s += act ? dx_fix(__fmul_rn(v[j], v[j]), sh) : 0;
+        const float ss = dx_unfix(wave_sum64(s), sh);
+        const float r = __fdiv_rn(1.0f, uwc_sqrt_rn(__fadd_rn(__fmul_rn(ss, inv_hd), eps)));
+#pragma unroll
+        for (int j = 0; j < NV; j++) v[j] = act ? __fmul_rn(__fmul_rn(v[j], r), wn[lane + 64 * j]) : 0.0f;
+      }
+      // rope: fadd(fmul(z, cos), fmul(rot(z), sin)), rot(z) = cat(-z[half:], z[:half])
+      float rot[NV];
+      if constexpr (NV >= 2) {
+#pragma unroll
+        for (int j = 0; j < NV; j++) rot[j] = j < NV / 2 ? -v[j + NV / 2] : v[j - NV / 2];
+      } else {
+        const float o = __shfl_xor(v[0], HD / 2, 64);
+        rot[0] = (lane & (HD / 2)) ? o : -o;
+      }
+      const float* cr = cosb + (long)pos * HD;
+      const float* sr = sinb + (long)pos * HD;
+#pragma unroll
+      for (int j = 0; j < NV; j++) {
+        const int d = lane + 64 * j;
+        v[j] = act ? __fadd_rn(__fmul_rn(v[j], cr[d]), __fmul_rn(rot[j], sr[d])) : 0.0f;
+      }
+    }
+    // quant_sym(qmax = 127) over the head (core.py:160-166)
+    float am = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; j++) am = fmaxf(am, fabsf(v[j]));
+    const float s = __fdiv_rn(fmaxf(wave_max(am), 1e-8f), 127.0f);
+    i8 qv[NV];
+#pragma unroll
+    for (int j = 0; j < NV; j++) qv[j] = (i8)(int)fminf(fmaxf(rintf(__fdiv_rn(v[j], s)), -127.f), 127.f);
+    i8* qo;
+    float* so;
+    if (isq) {
+      qo = qq + ((long)n * H + hh) * HD;
+      so = qs + (long)n * H + hh;
+    } else if (!isv) {
+      qo = kq + ((long)n * Hkv + (hh - H)) * HD;
+      so = ks + (long)n * Hkv + (hh - H);
+    } else {
+      qo = vq + ((long)n * Hkv + (hh - H - Hkv)) * HD;
+      so = vs + (long)n * Hkv + (hh - H - Hkv);
+    }
+    if (act) {
+#pragma unroll
+      for (int j = 0; j < NV; j++) qo[lane + 64 * j] = qv[j];
+    }
+    if (lane == 0) *so = s;
+    if (isv && vt && act) {
+      const int hk = hh - H - Hkv;
+      i8* col = vt + ((long)(bseq * Hkv + hk) * HD) * Tp + vt_pos(pos);
+#pragma unroll
+      for (int j = 0; j < NV; j++) col[(long)(lane + 64 * j) * Tp] = qv[j];
+    }
+  }
+}
+
+// V (N x Hkv x HD int8) transposed per (sequence, kv head) into the attention kernel's layout.
+__global__ void v_transpose_kernel(const i8* __restrict__ vq, int T, int Hkv, int HD, int Tp, i8* __restrict__ vt) {
+  const int n = blockIdx.x, bseq = n / T, pos = n % T;
+  for (int i = threadIdx.x; i < Hkv * HD; i += blockDim.x) {
+    const int hk = i / HD, d = i % HD;
+    vt[((long)(bseq * Hkv + hk) * HD + d) * Tp + vt_pos(pos)] = vq[(long)n * Hkv * HD + i];
+  }
+}
+
+// ------------------------------------------------------------------ per-op conformance
+// out[i] = op(x[i], y[i]) for one of detrt's elementwise fp32 ops, as the kernels above compute
+// it: the per-op check of native fp32 against detrt's emulation (runtime/tests/test_fp32_native.py).
+__global__ void det_elementwise_kernel(int op, const float* __restrict__ x, const float* __restrict__ y,
+                                       float* __restrict__ out, u64 n) {
+  for (u64 i = (u64)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (u64)gridDim.x * blockDim.x) {
+    const float a = x[i], b = y ? y[i] : 0.0f;
+    float r;
+    switch (op) {
+      case UWC_OP_ADD: r = __fadd_rn(a, b); break;
+      case UWC_OP_SUB: r = __fsub_rn(a, b); break;
+      case UWC_OP_MUL: r = __fmul_rn(a, b); break;
+      case UWC_OP_DIV: r = __fdiv_rn(a, b); break;
+      case UWC_OP_SQRT: r = uwc_sqrt_rn(a); break;
+      case UWC_OP_EXP: r = dx_exp(a); break;
+      default: r = dx_silu(a); break;
+    }
+    out[i] = r;
+  }
+}
+
+// ------------------------------------------------------------------ C-ABI
+extern "C" int uwc_det_elementwise(int op, const float* x, const float* y, float* out, int64_t n, hipStream_t stream) {
+  const char* fn = "uwc_det_elementwise";
+  if (op < UWC_OP_ADD || op > UWC_OP_SILU) return uwc_fail("%s: unknown op %d", fn, op);
+  if (!x || !out || n < 0 || (op <= UWC_OP_DIV && !y)) return uwc_fail("%s: null or empty arguments", fn);
+  if (n == 0) return UWC_OK;
+  const u64 blocks = ((u64)n + 255) / 256;
+  hipLaunchKernelGGL(det_elementwise_kernel, dim3((unsigned)(blocks < 65536 ? blocks : 65536)), dim3(256), 0, stream,
+                     op, x, y, out, (u64)n);
+  return uwc_launch_status(fn);
+}
+
+static int row_lds(const char* fn, const void* kern, int k, size_t& smem) {
+  smem = (size_t)k * 4;
+  if (smem > 160 * 1024) return uwc_fail("%s: a row of %d floats exceeds LDS", fn, k);
+  if (smem > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    if (e != hipSuccess) return uwc_fail("%s: cannot raise LDS to %zu bytes: %s", fn, smem, hipGetErrorString(e));
+  }
+  return UWC_OK;
+}
+
+static int check_bs(const char* fn, int bs, int k) {
+  if (bs > 1 && ((bs & (bs - 1)) || k % bs)) return uwc_fail("%s: bs=%d must be a power of two dividing %d", fn, bs, k);
+  return UWC_OK;
+}
+
+extern "C" int uwc_rmsnorm_quant_f32(const float* x, const float* w, int rows, int k, int bs, float inv_d, float eps,
+                                     int8_t* q, float* scale, hipStream_t stream) {
+  const char* fn = "uwc_rmsnorm_quant_f32";
+  if (!x || !w || !q || !scale || rows < 0 || k <= 0) return uwc_fail("%s: null or empty arguments", fn);
+  int st = check_bs(fn, bs, k);
+  if (st) return st;
+  if (rows == 0) return UWC_OK;
+  size_t smem;
+  if ((st = row_lds(fn, (const void*)rmsnorm_kernel<true>, k, smem))) return st;
+  hipLaunchKernelGGL(rmsnorm_kernel<true>, dim3(rows), dim3(256), smem, stream, x, w, k, bs, inv_d, eps, q, scale,
+                     (float*)nullptr);
+  return uwc_launch_status(fn);
+}
+
+extern "C" int uwc_rmsnorm_f32(const float* x, const float* w, int rows, int k, float inv_d, float eps, float* y,
+                               hipStream_t stream) {
+  const char* fn = "uwc_rmsnorm_f32";
+  if (!x || !w || !y || rows < 0 || k <= 0) return uwc_fail("%s: null or empty arguments", fn);
+  if (rows == 0) return UWC_OK;
+  size_t smem;
+  int st = row_lds(fn, (const void*)rmsnorm_kernel<false>, k, smem);
+  if (st) return st;
+  hipLaunchKernelGGL(rmsnorm_kernel<false>, dim3(rows), dim3(256), smem, stream, x, w, k, 0, inv_d, eps,
+                     (i8*)nullptr, (float*)nullptr, y);
+  return uwc_launch_status(fn);
+}
+
+extern "C" int uwc_swiglu_quant(const void* acc, const float* s3, const float* sw, int rows, int I, int bs,
+                                int8_t* q, float* scale, hipStream_t stream) {
+  const char* fn = "uwc_swiglu_quant";
+  if (!acc || !q || !scale || rows < 0 || I <= 0) return uwc_fail("%s: null or empty arguments", fn);
+  if (!s3 != !sw) return uwc_fail("%s: give both scales (int32 acc) or neither (fp32 rows)", fn);
+  int st = check_bs(fn, bs, I);
+  if (st) return st;
+  if (rows == 0) return UWC_OK;
+  size_t smem;
+  if (s3) {
+    if ((st = row_lds(fn, (const void*)swiglu_quant_kernel<false>, I, smem))) return st;
+    hipLaunchKernelGGL(swiglu_quant_kernel<false>, dim3(rows), dim3(256), smem, stream, acc, s3, sw, I, bs, q, scale);
+  } else {
+    if ((st = row_lds(fn, (const void*)swiglu_quant_kernel<true>, I, smem))) return st;
+    hipLaunchKernelGGL(swiglu_quant_kernel<true>, dim3(rows), dim3(256), smem, stream, acc, s3, sw, I, bs, q, scale);
+  }
+  return uwc_launch_status(fn);
+}
+
+extern "C" int uwc_dequant_residual(const void* acc, const float* s, const float* sw, const float* x, int rows, int n,
+                                    float* out, hipStream_t stream) {
+  const char* fn = "uwc_dequant_residual";
+  if (!acc || !x || !out || rows < 0 || n <= 0) return uwc_fail("%s: null or empty arguments", fn);
+  if (!s != !sw) return uwc_fail("%s: give both scales (int32 acc) or neither (fp32 rows)", fn);
+  const u64 total = (u64)rows * n;
+  if (total == 0) return UWC_OK;
+  const u64 blocks = (total + 255) / 256;
+  const dim3 grid((unsigned)(blocks < 65536 ? blocks : 65536));
+  if (s)
+    hipLaunchKernelGGL(dequant_residual_kernel<false>, grid, dim3(256), 0, stream, acc, s, sw, x, n, total, out);
+  else
+    hipLaunchKernelGGL(dequant_residual_kernel<true>, grid, dim3(256), 0, stream, acc, s, sw, x, n, total, out);
+  return uwc_launch_status(fn);
+}
+
+extern "C" int uwc_embed_rows(const float* table, int64_t V, int D, const int64_t* ids, int N, float* out, int* bad,
+                              hipStream_t stream) {
+  const char* fn = "uwc_embed_rows";
+  if (!table || !ids || !out || V <= 0 || D <= 0 || N < 0) return uwc_fail("%s: null or empty arguments", fn);
+  if (N == 0) return UWC_OK;
+  hipLaunchKernelGGL(embed_kernel, dim3(N), dim3(256), 0, stream, table, (long)V, D, ids, N, out, bad);
+  return uwc_launch_status(fn);
+}
+
+extern "C" int uwc_vt_tokens(int T) { return T <= 0 ? 0 : ((T + 63) / 64) * 64; }
+
+extern "C" int uwc_qkv_post(const void* acc, const float* s1, const float* sw, const float* qnw, const float* knw,
+                            const float* cosb, const float* sinb, int B, int T, int H, int Hkv, int hd, float eps,
+                            int qknorm, int8_t* qq, float* qs, int8_t* kq, float* ks, int8_t* vq, float* vs, int8_t* vt,
+                            hipStream_t stream) {
+  const char* fn = "uwc_qkv_post";
+  if (!acc || !cosb || !sinb || !qq || !qs || !kq || !ks || !vq || !vs) return uwc_fail("%s: null arguments", fn);
+  if (!s1 != !sw) return uwc_fail("%s: give both scales (int32 acc) or neither (fp32 rows)", fn);
+  if (qknorm && (!qnw || !knw)) return uwc_fail("%s: q/k norm weights are needed with qknorm", fn);
+  if (B < 0 || T <= 0 || H <= 0 || Hkv <= 0 || H % Hkv) return uwc_fail("%s: bad B=%d T=%d H=%d Hkv=%d", fn, B, T, H, Hkv);
+  if (hd != 32 && hd != 64 && hd != 128) return uwc_fail("%s: head_dim %d not in {32, 64, 128}", fn, hd);
+  const long N = (long)B * T;
+  if (N == 0) return UWC_OK;
+  if (N > 0x7fffffff) return uwc_fail("%s: too many tokens", fn);
+  const float inv_hd = (float)(1.0 / (double)hd);
+  const int Tp = uwc_vt_tokens(T);
+#define QKV_LAUNCH(HD)                                                                                               \
+  do {                                                                                                               \
+    if (s1)                                                                                                          \
+      hipLaunchKernelGGL((qkv_post_kernel<HD, false>), dim3((unsigned)N), dim3(256), 0, stream, acc, s1, sw, qnw,    \
+                         knw, cosb, sinb, T, H, Hkv, inv_hd, eps, qknorm, qq, qs, kq, ks, vq, vs, vt, Tp);            \
+    else                                                                                                             \
+      hipLaunchKernelGGL((qkv_post_kernel<HD, true>), dim3((unsigned)N), dim3(256), 0, stream, acc, s1, sw, qnw,     \
+                         knw, cosb, sinb, T, H, Hkv, inv_hd, eps, qknorm, qq, qs, kq, ks, vq, vs, vt, Tp);            \
+  } while (0)
+  if (hd == 32) QKV_LAUNCH(32);
+  else if (hd == 64) QKV_LAUNCH(64);
+  else QKV_LAUNCH(128);
+#undef QKV_LAUNCH
+  return uwc_launch_status(fn);
+}
+
+extern "C" int uwc_v_transpose(const int8_t* vq, int B, int T, int Hkv, int hd, int8_t* vt, hipStream_t stream) {
+  const char* fn = "uwc_v_transpose";
+  if (!vq || !vt || B < 0 || T <= 0 || Hkv <= 0 || hd <= 0) return uwc_fail("%s: null or empty arguments", fn);
+  const long N = (long)B * T;
+  if (N == 0) return UWC_OK;
+  hipLaunchKernelGGL(v_transpose_kernel, dim3((unsigned)N), dim3(256), 0, stream, vq, T, Hkv, hd, uwc_vt_tokens(T), vt);
+  return uwc_launch_status(fn);
+}

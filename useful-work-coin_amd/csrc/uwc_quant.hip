@@ -2,7 +2,7 @@
 // runtime/detrt/qwen3.py:125 (GPU twins: runtime/detgpu/kernels.py:35, 75-114, 346-353).
 //
 // Every floating-point step is a single correctly rounded IEEE binary32 operation in the
-// reference's order: __fadd_rn/__fsub_rn/__fmul_rn/__fdiv_rn/__fsqrt_rn are never contracted
+// reference's order: __fadd_rn/__fsub_rn/__fmul_rn/__fdiv_rn/uwc_sqrt_rn are never contracted
 // into fused multiply-adds, denormals are kept (no flush flags at build time), rintf rounds
 // half to even, and max/abs/int->float conversions are exact or correctly rounded.
 #include "uwc_common.h"
@@ -50,7 +50,7 @@ __global__ void __launch_bounds__(256) quant_act_kernel(const T* __restrict__ x,
     const float v = fminf(fmaxf(rintf(__fdiv_rn(rowf[i], s)), -fq), fq);
     qr[i] = (i8)(int)v;
   }
-  if (tid == 0) scale[row] = bs > 1 ? __fmul_rn(s, __fdiv_rn(1.0f, __fsqrt_rn((float)bs))) : s;
+  if (tid == 0) scale[row] = bs > 1 ? __fmul_rn(s, __fdiv_rn(1.0f, uwc_sqrt_rn((float)bs))) : s;
 }
 
 // The same quant_act with one wave per row and no LDS: for k % 512 == 0 and bs <= 512. A row is
@@ -158,7 +158,7 @@ __global__ void __launch_bounds__(256) quant_act_wave_kernel(const T* __restrict
       emit(y[0], g);
     }
   }
-  if (lane == 0) scale[row] = lbs > 0 ? __fmul_rn(s, __fdiv_rn(1.0f, __fsqrt_rn((float)(1 << lbs)))) : s;
+  if (lane == 0) scale[row] = lbs > 0 ? __fmul_rn(s, __fdiv_rn(1.0f, uwc_sqrt_rn((float)(1 << lbs)))) : s;
 }
 
 // y = (f32(acc) * sx[row]) * sw[col], each product rounded once (qwen3.py:125).

@@ -1,0 +1,161 @@
+// Row-wise exact fp32 helpers for the detrt decoder-layer kernels on gfx950: detrt's det_exp,
+// SiLU, the exact fixed-point row sum behind RMSNorm, the block Walsh-Hadamard + symmetric
+// quantizer, and wave / workgroup reductions (runtime/detrt/core.py:77-193; GPU twins
+// runtime/detgpu/kernels.py:17-74).
+//
+// Every fp32 step is one correctly rounded IEEE operation in the reference's order
+// (__fadd_rn/__fsub_rn/__fmul_rn/__fdiv_rn/uwc_sqrt_rn, never contracted; the library builds with
+// -ffp-contract=off and keeps denormals). Integer and fixed-point sums are exact, so their order
+// and the lane / workgroup split cannot change a bit.
+#pragma once
+#include "uwc_common.h"
+
+// detrt's float32 constants (core.py:101-105), rounded once from the float64 literals.
+#define DX_LOG2E 0x1.715476p+0f
+#define DX_E0 0x1.0p+0f
+#define DX_E1 0x1.62e43p-1f
+#define DX_E2 0x1.ebfbdp-3f
+#define DX_E3 0x1.c6b2acp-5f
+#define DX_E4 0x1.3b0872p-7f
+#define DX_E5 0x1.5fdb08p-10f
+#define DX_E6 0x1.2d0dd8p-13f
+#define DX_E7 0x1.6889f4p-16f
+
+// det_exp (core.py:108-126): 2**t with t = z log2(e) split into floor and fraction, the
+// fraction's power from a fixed degree-7 Horner polynomial (one rounding per op).
+__device__ __forceinline__ float dx_exp(float z) {
+  float t = __fmul_rn(z, DX_LOG2E);
+  const bool under = t < -126.0f, over = t >= 128.0f;
+  if (under || over || __builtin_isnan(t)) t = 0.0f;
+  const float n = floorf(t);
+  const float f = __fsub_rn(t, n);
+  float p = DX_E7;
+  p = __fadd_rn(__fmul_rn(p, f), DX_E6);
+  p = __fadd_rn(__fmul_rn(p, f), DX_E5);
+  p = __fadd_rn(__fmul_rn(p, f), DX_E4);
+  p = __fadd_rn(__fmul_rn(p, f), DX_E3);
+  p = __fadd_rn(__fmul_rn(p, f), DX_E2);
+  p = __fadd_rn(__fmul_rn(p, f), DX_E1);
+  p = __fadd_rn(__fmul_rn(p, f), DX_E0);
+  float r = __fmul_rn(p, __int_as_float(((int)n + 127) << 23));
+  if (under) r = 0.0f;
+  if (over) r = __int_as_float(0x7f800000);
+  if (__builtin_isnan(z)) r = z;
+  return r;
+}
+
+// det_silu (core.py:144-146): x / (1 + det_exp(-x)).
+__device__ __forceinline__ float dx_silu(float x) { return __fdiv_rn(x, __fadd_rn(1.0f, dx_exp(-x))); }
+
+// detrt dequant fmul(fmul(f32(acc), s_row), s_col) (qwen3.py:125).
+__device__ __forceinline__ float dx_deq(int acc, float s, float sw) { return __fmul_rn(__fmul_rn((float)acc, s), sw); }
+
+// ceil(log2(n)) for n >= 1, at least 1 (core.py:84).
+__host__ __device__ __forceinline__ int dx_log2ceil(int n) {
+  int L = 0;
+  while ((1 << L) < n) L++;
+  return L < 1 ? 1 : L;
+}
+
+// exact_rowsum's fixed-point scale (core.py:84-90): 2**(e-1) <= amax < 2**e, shift = (62 - L) - e.
+__device__ __forceinline__ int dx_shift(float amax, int L) {
+  int e;
+  frexpf(amax, &e);
+  int sh = (62 - L) - e;
+  return sh < -1000 ? -1000 : (sh > 1000 ? 1000 : sh);
+}
+
+// One term round_half_even(v * 2**sh) as int64 (exact: the scaling is a power of two).
+__device__ __forceinline__ long long dx_fix(float v, int sh) {
+  return (long long)rint(ldexp((double)v, sh));
+}
+
+// float32(float64(sum) * 2**-sh): the int64 sum rounded once to float64, scaled exactly,
+// rounded once to float32 (core.py:95-97).
+__device__ __forceinline__ float dx_unfix(long long s, int sh) { return (float)ldexp((double)s, -sh); }
+
+// ------------------------------------------------------------------ wave reductions (wave64)
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int s = 32; s > 0; s >>= 1) v = fmaxf(v, __shfl_xor(v, s, 64));
+  return v;
+}
+
+__device__ __forceinline__ long long wave_sum64(long long v) {
+#pragma unroll
+  for (int s = 32; s > 0; s >>= 1) {
+    const int lo = __shfl_xor((int)(unsigned)v, s, 64), hi = __shfl_xor((int)(v >> 32), s, 64);
+    v += (long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo);
+  }
+  return v;
+}
+
+// ------------------------------------------------------------------ workgroup (256 threads) reductions
+struct DxRed {
+  float f[4];
+  long long l[4];
+};
+
+__device__ __forceinline__ float block_max256(float v, DxRed& red) {
+  v = wave_max(v);
+  __syncthreads();  // red may still be read from a previous reduction
+  if ((threadIdx.x & 63) == 0) red.f[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(red.f[0], red.f[1]), fmaxf(red.f[2], red.f[3]));
+}
+
+__device__ __forceinline__ long long block_sum256(long long v, DxRed& red) {
+  v = wave_sum64(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red.l[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return red.l[0] + red.l[1] + red.l[2] + red.l[3];
+}
+
+// det_rmsnorm in place on an LDS row (core.py:149-156): row[i] = (row[i] * r) * w[i],
+// r = 1 / sqrt(exact_rowsum(row^2) / k + eps). 256 threads.
+__device__ __forceinline__ void dx_rmsnorm_lds(float* row, int k, const float* __restrict__ w, float inv_d, float eps,
+                                               DxRed& red) {
+  const int tid = threadIdx.x;
+  float mx = 0.f;
+  for (int i = tid; i < k; i += 256) mx = fmaxf(mx, __fmul_rn(row[i], row[i]));
+  mx = block_max256(mx, red);
+  const int sh = dx_shift(mx, dx_log2ceil(k));
+  long long acc = 0;
+  for (int i = tid; i < k; i += 256) acc += dx_fix(__fmul_rn(row[i], row[i]), sh);
+  acc = block_sum256(acc, red);
+  const float ss = dx_unfix(acc, sh);
+  const float r = __fdiv_rn(1.0f, uwc_sqrt_rn(__fadd_rn(__fmul_rn(ss, inv_d), eps)));
+  for (int i = tid; i < k; i += 256) row[i] = __fmul_rn(__fmul_rn(row[i], r), w[i]);
+  __syncthreads();
+}
+
+// quant_act on an LDS row (core.py:169-193): block FWHT of size bs (stages h = 1, 2, 4, ...,
+// pairs (i, i+h) -> (a+b, a-b)), s = max(max|y|, 1e-8) / qmax, q = clamp(rint(y / s)), scale
+// s * (1 / sqrt(bs)) when bs > 1. 256 threads; the row must be complete in LDS (barrier done).
+__device__ __forceinline__ void dx_quant_lds(float* row, int k, int bs, int qmax, i8* __restrict__ q,
+                                             float* __restrict__ scale, DxRed& red) {
+  const int tid = threadIdx.x;
+  if (bs > 1) {
+    for (int lh = 0; (1 << lh) < bs; lh++) {
+      const int h = 1 << lh;
+      for (int p = tid; p < (k >> 1); p += 256) {
+        const int i = ((p >> lh) << (lh + 1)) | (p & (h - 1)), j = i + h;
+        const float a = row[i], b = row[j];
+        row[i] = __fadd_rn(a, b);
+        row[j] = __fsub_rn(a, b);
+      }
+      __syncthreads();
+    }
+  }
+  float mx = 0.f;
+  for (int i = tid; i < k; i += 256) mx = fmaxf(mx, fabsf(row[i]));
+  mx = block_max256(mx, red);
+  const float fq = (float)qmax;
+  const float s = __fdiv_rn(fmaxf(mx, 1e-8f), fq);
+  for (int i = tid; i < k; i += 256) {
+    const float v = fminf(fmaxf(rintf(__fdiv_rn(row[i], s)), -fq), fq);
+    q[i] = (i8)(int)v;
+  }
+  if (tid == 0) *scale = bs > 1 ? __fmul_rn(s, __fdiv_rn(1.0f, uwc_sqrt_rn((float)bs))) : s;
+}

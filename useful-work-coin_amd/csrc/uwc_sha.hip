@@ -1,0 +1,255 @@
+// Stage commitments on gfx950: SHA-256 row roots, tagged leaves and Merkle roots, identical to
+// runtime/detrt/stage.py:33-77 (RFC 6962 trees: leaf = H(0x00 || x), node = H(0x01 || l || r),
+// split at the largest power of two) and the stage-output root of
+// spec/stage-program.md:82-88 (leaf H(0x00 || "sout" || u32le t || row_root)); the reference's
+// GPU twin is runtime/detgpu/sha.py:19-153.
+//
+//   row root     rows are little-endian 4-byte words cut into 1 KiB blocks; one thread hashes
+//                one block (17 compressions for a full block); the per-row tree is built
+//                bottom-up, pairing neighbours and promoting an odd last node, which equals
+//                the recursive split;
+//   tagged leaf  H(0x00 || tag || u32le index || row_root), index = (base + row) % mod;
+//   tree root    one workgroup per tree of n leaves, bottom-up through a scratch buffer.
+//
+// Every message here is a prefix byte followed by a stream of 32-bit words (row words, digest
+// words, the tag and index words). With the stream in big-endian order Z_0 .. Z_{n-1} and
+// Z_{-1} = the prefix byte, message word j is (Z_{j-1} << 24) | (Z_j >> 8): the one-byte
+// prefix shifts the stream by a byte, so no byte-wise packing is needed. SHA-256 itself is
+// restated from FIPS 180-4 (constants: fractional parts of the cube and square roots of the
+// first primes).
+#include "uwc_common.h"
+
+__device__ __constant__ u32 kSha256K[64] = {
+    0x428a2f98u, 0x71374491u, 0xb5c0fbcfu, 0xe9b5dba5u, 0x3956c25bu, 0x59f111f1u, 0x923f82a4u, 0xab1c5ed5u,
+    0xd807aa98u, 0x12835b01u, 0x243185beu, 0x550c7dc3u, 0x72be5d74u, 0x80deb1feu, 0x9bdc06a7u, 0xc19bf174u,
+    0xe49b69c1u, 0xefbe4786u, 0x0fc19dc6u, 0x240ca1ccu, 0x2de92c6fu, 0x4a7484aau, 0x5cb0a9dcu, 0x76f988dau,
+    0x983e5152u, 0xa831c66du, 0xb00327c8u, 0xbf597fc7u, 0xc6e00bf3u, 0xd5a79147u, 0x06ca6351u, 0x14292967u,
+    0x27b70a85u, 0x2e1b2138u, 0x4d2c6dfcu, 0x53380d13u, 0x650a7354u, 0x766a0abbu, 0x81c2c92eu, 0x92722c85u,
+    0xa2bfe8a1u, 0xa81a664bu, 0xc24b8b70u, 0xc76c51a3u, 0xd192e819u, 0xd6990624u, 0xf40e3585u, 0x106aa070u,
+    0x19a4c116u, 0x1e376c08u, 0x2748774cu, 0x34b0bcb5u, 0x391c0cb3u, 0x4ed8aa4au, 0x5b9cca4fu, 0x682e6ff3u,
+    0x748f82eeu, 0x78a5636fu, 0x84c87814u, 0x8cc70208u, 0x90befffau, 0xa4506cebu, 0xbef9a3f7u, 0xc67178f2u};
+
+__device__ __forceinline__ void sha_init(u32 s[8]) {
+  s[0] = 0x6a09e667u; s[1] = 0xbb67ae85u; s[2] = 0x3c6ef372u; s[3] = 0xa54ff53au;
+  s[4] = 0x510e527fu; s[5] = 0x9b05688cu; s[6] = 0x1f83d9abu; s[7] = 0x5be0cd19u;
+}
+
+__device__ __forceinline__ u32 ror(u32 x, int n) { return __builtin_amdgcn_alignbit(x, x, n); }
+
+// One compression of the 16-word block w (big-endian words) into s.
+__device__ __forceinline__ void sha_compress(u32 s[8], u32 w[16]) {
+  u32 a = s[0], b = s[1], c = s[2], d = s[3], e = s[4], f = s[5], g = s[6], h = s[7];
+#pragma unroll
+  for (int i = 0; i < 64; i++) {
+    u32 wi;
+    if (i < 16) {
+      wi = w[i];
+    } else {
+      const u32 w15 = w[(i + 1) & 15], w2 = w[(i + 14) & 15];
+      const u32 s0 = ror(w15, 7) ^ ror(w15, 18) ^ (w15 >> 3);
+      const u32 s1 = ror(w2, 17) ^ ror(w2, 19) ^ (w2 >> 10);
+      wi = w[i & 15] = w[i & 15] + s0 + w[(i + 9) & 15] + s1;
+    }
+    const u32 S1 = ror(e, 6) ^ ror(e, 11) ^ ror(e, 25);
+    const u32 ch = (e & f) ^ (~e & g);
+    const u32 t1 = h + S1 + ch + kSha256K[i] + wi;
+    const u32 S0 = ror(a, 2) ^ ror(a, 13) ^ ror(a, 22);
+    const u32 mj = (a & b) ^ (a & c) ^ (b & c);
+    h = g; g = f; f = e; e = d + t1; d = c; c = b; b = a; a = t1 + S0 + mj;
+  }
+  s[0] += a; s[1] += b; s[2] += c; s[3] += d; s[4] += e; s[5] += f; s[6] += g; s[7] += h;
+}
+
+// SHA-256 of (prefix byte || z[0..n) as big-endian words) for a short stream held in
+// registers (n <= 16, compile time).
+template <int N>
+__device__ __forceinline__ void sha_short(u32 prefix, const u32 z[N], u32 out[8]) {
+  constexpr int NB = (4 * N + 1 + 1 + 8 + 63) / 64;  // 64-byte blocks after padding
+  u32 w[NB * 16];
+#pragma unroll
+  for (int j = 0; j < NB * 16; j++) w[j] = 0;
+#pragma unroll
+  for (int j = 0; j <= N; j++) {
+    const u32 prev = j == 0 ? prefix : z[j - 1];
+    const u32 cur = j < N ? (z[j] >> 8) : 0x00800000u;
+    w[j] = (prev << 24) | cur;
+  }
+  w[NB * 16 - 1] = (u32)((4 * N + 1) * 8);
+  sha_init(out);
+#pragma unroll
+  for (int b = 0; b < NB; b++) sha_compress(out, w + 16 * b);
+}
+
+__device__ __forceinline__ void sha_node(const u32* l, const u32* r, u32 out[8]) {
+  u32 z[16];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    z[i] = l[i];
+    z[8 + i] = r[i];
+  }
+  sha_short<16>(1u, z, out);
+}
+
+// H(0x00 || block) of n little-endian data words at p (n <= 256); VEC: p is 16-byte aligned.
+template <bool VEC>
+__device__ void sha_block_leaf(const u32* __restrict__ p, int n, u32 out[8]) {
+  const int nb = (4 * n + 1 + 1 + 8 + 63) / 64;
+  sha_init(out);
+  u32 prev = 0;  // the 0x00 prefix
+  for (int b = 0; b < nb; b++) {
+    u32 w[16];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int j0 = 16 * b + 4 * q;
+      u32 d[4];
+      if (VEC && j0 + 4 <= n) {
+        const uint4 v = *reinterpret_cast<const uint4*>(p + j0);
+        d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; t++) d[t] = j0 + t < n ? p[j0 + t] : 0u;
+      }
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const int j = j0 + t;
+        u32 cur;
+        if (j < n) cur = __builtin_bswap32(d[t]) >> 8;
+        else if (j == n) cur = 0x00800000u;
+        else cur = 0;
+        w[4 * q + t] = (j <= n ? (prev << 24) : 0u) | cur;
+        prev = j < n ? __builtin_bswap32(d[t]) : 0u;
+      }
+    }
+    if (b == nb - 1) w[15] = (u32)((4 * n + 1) * 8);
+    sha_compress(out, w);
+  }
+}
+
+#define SHA_BLOCK_WORDS 256  // 1 KiB
+
+// One thread per (row, block): the block leaves of every row.
+template <bool VEC>
+__global__ void sha_block_leaves_kernel(const u32* __restrict__ rows, long nrows, int row_words, int nblk,
+                                        u32* __restrict__ leaves) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= nrows * nblk) return;
+  const long r = i / nblk;
+  const int b = (int)(i - r * nblk);
+  const int off = b * SHA_BLOCK_WORDS, n = min(SHA_BLOCK_WORDS, row_words - off);
+  u32 h[8];
+  sha_block_leaf<VEC>(rows + r * row_words + off, n, h);
+  uint4* o = reinterpret_cast<uint4*>(leaves + i * 8);
+  o[0] = make_uint4(h[0], h[1], h[2], h[3]);
+  o[1] = make_uint4(h[4], h[5], h[6], h[7]);
+}
+
+// One thread per row: the row root from its block leaves (bottom-up in place in the leaf
+// buffer), then the tagged leaf H(0x00 || tag || u32le index || root).
+__global__ void sha_row_leaf_kernel(u32* __restrict__ leaves, long nrows, int nblk, u32 tag, u32 base, u32 mod,
+                                    u32* __restrict__ roots, u32* __restrict__ out) {
+  const long r = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= nrows) return;
+  u32* lv = leaves + r * nblk * 8;
+  int n = nblk;
+  while (n > 1) {
+    const int half = n >> 1;
+    for (int i = 0; i < half; i++) {
+      u32 h[8];
+      sha_node(lv + 16 * i, lv + 16 * i + 8, h);
+#pragma unroll
+      for (int k = 0; k < 8; k++) lv[8 * i + k] = h[k];
+    }
+    if (n & 1) {
+#pragma unroll
+      for (int k = 0; k < 8; k++) lv[8 * half + k] = lv[8 * (n - 1) + k];
+    }
+    n = half + (n & 1);
+  }
+  u32 root[8];
+#pragma unroll
+  for (int k = 0; k < 8; k++) root[k] = lv[k];
+  if (roots) {
+#pragma unroll
+    for (int k = 0; k < 8; k++) roots[r * 8 + k] = root[k];
+  }
+  if (out) {
+    u32 idx = base + (u32)r;
+    if (mod) idx %= mod;
+    u32 z[10];
+    z[0] = tag;
+    z[1] = __builtin_bswap32(idx);  // u32 little-endian bytes as a big-endian word
+#pragma unroll
+    for (int k = 0; k < 8; k++) z[2 + k] = root[k];
+    u32 h[8];
+    sha_short<10>(0u, z, h);
+#pragma unroll
+    for (int k = 0; k < 8; k++) out[r * 8 + k] = h[k];
+  }
+}
+
+// One workgroup per tree of n leaves: the Merkle root, bottom-up through scratch.
+__global__ void __launch_bounds__(256) sha_tree_kernel(const u32* __restrict__ leaves, int n0, u32* __restrict__ a,
+                                                       u32* __restrict__ b, u32* __restrict__ roots) {
+  const long t0 = (long)blockIdx.x * n0 * 8;
+  const u32* src = leaves + t0;
+  u32* dst = a + t0;
+  u32* other = b + t0;
+  int n = n0;
+  if (n == 1) {
+    if (threadIdx.x < 8) roots[blockIdx.x * 8 + threadIdx.x] = src[threadIdx.x];
+    return;
+  }
+  while (n > 1) {
+    const int half = n >> 1;
+    for (int i = threadIdx.x; i < half; i += blockDim.x) {
+      u32 h[8];
+      sha_node(src + 16 * i, src + 16 * i + 8, h);
+#pragma unroll
+      for (int k = 0; k < 8; k++) dst[8 * i + k] = h[k];
+    }
+    if ((n & 1) && threadIdx.x < 8) dst[8 * half + threadIdx.x] = src[8 * (n - 1) + threadIdx.x];
+    __syncthreads();
+    src = dst;
+    u32* t = other;
+    other = dst;
+    dst = t;
+    n = half + (n & 1);
+  }
+  if (threadIdx.x < 8) roots[blockIdx.x * 8 + threadIdx.x] = src[threadIdx.x];
+}
+
+extern "C" int uwc_sha_row_leaves(const uint32_t* rows, int64_t nrows, int row_words, uint32_t* scratch,
+                                  int64_t scratch_words, uint32_t tag, uint32_t index_base, uint32_t index_mod,
+                                  uint32_t* row_roots, uint32_t* leaves_out, hipStream_t stream) {
+  const char* fn = "uwc_sha_row_leaves";
+  if ((!rows && row_words > 0) || !scratch || nrows < 0 || row_words < 0) return uwc_fail("%s: bad arguments", fn);
+  if (!row_roots && !leaves_out) return uwc_fail("%s: nothing to write", fn);
+  if (rows && ((uintptr_t)rows & 3)) return uwc_fail("%s: rows must be 4-byte aligned", fn);
+  if (nrows == 0) return UWC_OK;
+  const int nblk = row_words == 0 ? 1 : (row_words + SHA_BLOCK_WORDS - 1) / SHA_BLOCK_WORDS;
+  if (scratch_words < nrows * nblk * 8)
+    return uwc_fail("%s: scratch has %lld words, needs %lld", fn, (long long)scratch_words, (long long)(nrows * nblk * 8));
+  const long nt = nrows * nblk;
+  const dim3 grid((unsigned)((nt + 127) / 128));
+  if (row_words % 4 == 0 && ((uintptr_t)rows & 15) == 0)
+    hipLaunchKernelGGL(sha_block_leaves_kernel<true>, grid, dim3(128), 0, stream, rows, (long)nrows, row_words, nblk, scratch);
+  else
+    hipLaunchKernelGGL(sha_block_leaves_kernel<false>, grid, dim3(128), 0, stream, rows, (long)nrows, row_words, nblk, scratch);
+  int st = uwc_launch_status("sha_block_leaves");
+  if (st) return st;
+  hipLaunchKernelGGL(sha_row_leaf_kernel, dim3((unsigned)((nrows + 63) / 64)), dim3(64), 0, stream, scratch, (long)nrows,
+                     nblk, tag, index_base, index_mod, row_roots, leaves_out);
+  return uwc_launch_status("sha_row_leaf");
+}
+
+extern "C" int uwc_sha_merkle_roots(const uint32_t* leaves, int ntrees, int n, uint32_t* scratch, int64_t scratch_words,
+                                    uint32_t* roots, hipStream_t stream) {
+  const char* fn = "uwc_sha_merkle_roots";
+  if (!leaves || !scratch || !roots || ntrees < 0 || n <= 0) return uwc_fail("%s: bad arguments", fn);
+  if (ntrees == 0) return UWC_OK;
+  const long need = 2L * ntrees * n * 8;
+  if (scratch_words < need) return uwc_fail("%s: scratch has %lld words, needs %ld", fn, (long long)scratch_words, need);
+  hipLaunchKernelGGL(sha_tree_kernel, dim3((unsigned)ntrees), dim3(256), 0, stream, leaves, n, scratch,
+                     scratch + (long)ntrees * n * 8, roots);
+  return uwc_launch_status(fn);
+}

@@ -15,6 +15,8 @@ vp = ctypes.c_void_p
 i32 = ctypes.c_int
 u32 = ctypes.c_uint32
 u64 = ctypes.c_uint64
+i64 = ctypes.c_int64
+f32 = ctypes.c_float
 
 # name -> argument types (every function returns int status unless listed in _RESTYPE)
 SIGNATURES = {
@@ -36,6 +38,18 @@ SIGNATURES = {
     "uwc_quant_act_f32": [vp, i32, i32, i32, i32, vp, vp, vp],
     "uwc_quant_rows_had": [vp, i32, i32, i32, vp, vp, vp],
     "uwc_dequant_f32": [vp, vp, vp, i32, i32, vp, vp],
+    "uwc_rmsnorm_quant_f32": [vp, vp, i32, i32, i32, f32, f32, vp, vp, vp],
+    "uwc_rmsnorm_f32": [vp, vp, i32, i32, f32, f32, vp, vp],
+    "uwc_qkv_post": [vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, f32, i32, vp, vp, vp, vp, vp, vp, vp, vp],
+    "uwc_vt_tokens": [i32],
+    "uwc_v_transpose": [vp, i32, i32, i32, i32, vp, vp],
+    "uwc_attention": [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, f32, vp, vp],
+    "uwc_swiglu_quant": [vp, vp, vp, i32, i32, i32, vp, vp, vp],
+    "uwc_dequant_residual": [vp, vp, vp, vp, i32, i32, vp, vp],
+    "uwc_embed_rows": [vp, i64, i32, vp, i32, vp, vp, vp],
+    "uwc_sha_row_leaves": [vp, i64, i32, vp, i64, u32, u32, u32, vp, vp, vp],
+    "uwc_sha_merkle_roots": [vp, i32, i32, vp, i64, vp, vp],
+    "uwc_det_elementwise": [i32, vp, vp, vp, i64, vp],
 }
 _RESTYPE = {"uwc_last_error": ctypes.c_char_p}
 

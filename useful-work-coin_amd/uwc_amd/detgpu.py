@@ -1,0 +1,406 @@
+"""detrt's deterministic decoder layer and stage commitments on MI355X: the call surface of the
+reference's GPU engine runtime/detgpu (kernels.py, sha.py, stages.py), over libuwc_hip.so.
+
+Bit-identical to the CPU reference runtime/detrt: every fp32 step is one correctly rounded IEEE
+op in detrt's order, every sum is exact (int32 / int64 / fixed point), and max is exact, so no
+batching, tiling or key split changes a bit.
+
+  kernels   quant_act, rmsnorm_quant, rmsnorm, qkv_post, attention, dequant_residual,
+            swiglu_quant, embed                     (runtime/detgpu/kernels.py:699-826)
+  sha       sout_leaves, stage_roots_gpu, digest_bytes, stage_output_roots, row_roots,
+            trace_root                              (runtime/detgpu/sha.py:139-236)
+  stages    layer_fused, stage_outputs, job_outputs, final_logits
+                                                    (runtime/detgpu/stages.py:154-219)
+  DetModel  the attributes of detrt.qwen3.DetQwen3 that the stages read (qwen3.py:165-199),
+            built from quantized weight tables or from a seeded random init.
+
+Everything runs on torch's current HIP stream; buffers are torch tensors on the caller's GPU.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import _lib
+from .detrt import DetLinear, hadamard_bs
+from .detrt import quant_act as _quant_act
+
+F32 = torch.float32
+TAG_LEAF = int.from_bytes(b"leaf", "big")
+TAG_SOUT = int.from_bytes(b"sout", "big")
+BLOCK = 1024  # bytes per committed row block (runtime/detrt/stage.py:25)
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _f32(v: float) -> float:
+    """A Python float rounded once to float32 (detrt's c32)."""
+    return float(np.float32(v))
+
+
+def _inv(k: int) -> float:
+    return float(np.float32(1.0 / k))
+
+
+# ================================================================== kernels
+def quant_act(x: torch.Tensor, bs: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """detrt.core.quant_act(x, bs) for float32 x (rows, k): (int8 q, float32 scale)."""
+    return _quant_act(x, bs)
+
+
+def rmsnorm_quant(x: torch.Tensor, w: torch.Tensor, eps: float, bs: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """quant_act(det_rmsnorm(x, w, eps), bs) for float32 x (rows, k) (detgpu/kernels.py:712-728)."""
+    x = x.contiguous()
+    rows, k = x.shape
+    if x.dtype != F32 or w.dtype != F32 or (bs > 1 and k % bs):
+        raise AssertionError("rmsnorm_quant: float32 x and w, bs dividing k")
+    q = torch.empty((rows, k), dtype=torch.int8, device=x.device)
+    s = torch.empty(rows, dtype=F32, device=x.device)
+    _lib.call("uwc_rmsnorm_quant_f32", x.data_ptr(), w.contiguous().data_ptr(), rows, k, bs, _inv(k), _f32(eps),
+              q.data_ptr(), s.data_ptr(), _stream())
+    return q, s
+
+
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    """detrt.core.det_rmsnorm along the last dim of float32 x."""
+    shp = x.shape
+    x2 = x.reshape(-1, shp[-1]).contiguous()
+    rows, k = x2.shape
+    y = torch.empty_like(x2)
+    _lib.call("uwc_rmsnorm_f32", x2.data_ptr(), w.contiguous().data_ptr(), rows, k, _inv(k), _f32(eps), y.data_ptr(),
+              _stream())
+    return y.reshape(shp)
+
+
+def vt_tokens(T: int) -> int:
+    return _lib.lib().uwc_vt_tokens(T)
+
+
+def qkv_post_vt(acc, s1, sw, qnw, knw, cos, sin, T: int, H: int, Hkv: int, eps: float, qknorm: bool = True):
+    """qkv_post plus V transposed for attention(): (qq, qs, kq, ks, vq, vs, vt). acc is the int32
+    GEMM output (with s1, sw), or already dequantized float32 rows (s1 = sw = None)."""
+    acc = acc.contiguous()
+    N = acc.shape[0]
+    hd = acc.shape[1] // (H + 2 * Hkv)
+    fp = acc.dtype == F32
+    if (acc.dtype != torch.int32 and not fp) or acc.shape[1] != (H + 2 * Hkv) * hd or N % T:
+        raise AssertionError(f"qkv_post: acc must be int32 or float32 (B*T, (H + 2 Hkv) hd), got {tuple(acc.shape)}")
+    if fp != (s1 is None) or (s1 is None) != (sw is None):
+        raise AssertionError("qkv_post: int32 acc needs s1 and sw; float32 rows take neither")
+    B = N // T
+    dev = acc.device
+    e = lambda *shape, dt=torch.int8: torch.empty(shape, dtype=dt, device=dev)
+    qq, qs, kq, ks, vq, vs = e(N, H, hd), e(N, H, 1, dt=F32), e(N, Hkv, hd), e(N, Hkv, 1, dt=F32), e(N, Hkv, hd), e(N, Hkv, 1, dt=F32)
+    vt = torch.zeros((B, Hkv, hd, vt_tokens(T)), dtype=torch.int8, device=dev)
+    qn = qnw.contiguous() if qknorm else None
+    kn = knw.contiguous() if qknorm else None
+    cos, sin = cos.contiguous(), sin.contiguous()
+    if cos.shape[0] < T or cos.shape[1] != hd:
+        raise AssertionError("qkv_post: the rope tables need T rows of head_dim")
+    _lib.call("uwc_qkv_post", acc.data_ptr(), None if fp else s1.contiguous().data_ptr(),
+              None if fp else sw.contiguous().data_ptr(),
+              qn.data_ptr() if qn is not None else None, kn.data_ptr() if kn is not None else None,
+              cos.data_ptr(), sin.data_ptr(), B, T, H, Hkv, hd, _f32(eps), int(bool(qknorm)),
+              qq.data_ptr(), qs.data_ptr(), kq.data_ptr(), ks.data_ptr(), vq.data_ptr(), vs.data_ptr(), vt.data_ptr(),
+              _stream())
+    return qq, qs, kq, ks, vq, vs, vt
+
+
+def qkv_post(acc, s1, sw, qnw, knw, cos, sin, T: int, H: int, Hkv: int, eps: float, qknorm: bool = True):
+    """Quantized q, k, v from the qkv GEMM's int32 output: (qq (N,H,hd) int8, qs (N,H,1), kq, ks,
+    vq, vs) (detgpu/kernels.py:788-802). qknorm False (Llama, Mistral): no per-head RMSNorm."""
+    return qkv_post_vt(acc, s1, sw, qnw, knw, cos, sin, T, H, Hkv, eps, qknorm)[:6]
+
+
+def attention(qq, qs, kq, ks, vq, vs, B: int, T: int, H: int, Hkv: int, inv_sqrt_hd_f32: float, vt=None):
+    """detrt's attention from quantized q, k, v: qq (N, H, hd), kq and vq (N, Hkv, hd) int8, qs
+    (N, H, 1), ks and vs (N, Hkv, 1). Returns o as (N, H*hd) float32 (detgpu/kernels.py:731-770).
+    vt (from qkv_post_vt) skips the transpose of vq."""
+    N, _, hd = qq.shape
+    if N != B * T or kq.shape != (N, Hkv, hd) or vq.shape != (N, Hkv, hd):
+        raise AssertionError("attention: shapes (B*T, H, hd) / (B*T, Hkv, hd)")
+    i8 = lambda z: z.to(torch.int8).contiguous()
+    f = lambda z: z.contiguous().to(F32)
+    qq, kq, vq = i8(qq), i8(kq), i8(vq)
+    qs, ks, vs = f(qs), f(ks), f(vs)
+    if vt is None:
+        vt = torch.zeros((B, Hkv, hd, vt_tokens(T)), dtype=torch.int8, device=qq.device)
+        _lib.call("uwc_v_transpose", vq.data_ptr(), B, T, Hkv, hd, vt.data_ptr(), _stream())
+    o = torch.empty((N, H * hd), dtype=F32, device=qq.device)
+    _lib.call("uwc_attention", qq.data_ptr(), qs.data_ptr(), kq.data_ptr(), ks.data_ptr(), vt.data_ptr(), vs.data_ptr(),
+              B, T, H, Hkv, hd, float(np.float32(inv_sqrt_hd_f32)), o.data_ptr(), _stream())
+    return o
+
+
+def _scales(acc, *scales):
+    fp = acc.dtype == F32
+    if fp != all(s is None for s in scales) or any(s is None for s in scales) != fp:
+        raise AssertionError("int32 accumulators need their scales; float32 rows take none")
+    return [None if fp else s.contiguous().data_ptr() for s in scales]
+
+
+def dequant_residual(acc, s, sw, x):
+    """x + fmul(fmul(f32(acc), s), sw) (detgpu/kernels.py:805-813); x + acc for float32 acc (s = sw = None)."""
+    acc, x = acc.contiguous(), x.contiguous()
+    N, k = acc.shape
+    out = torch.empty((N, k), dtype=F32, device=acc.device)
+    ps, psw = _scales(acc, s, sw)
+    _lib.call("uwc_dequant_residual", acc.data_ptr(), ps, psw, x.data_ptr(), N, k, out.data_ptr(), _stream())
+    return out
+
+
+def swiglu_quant(acc, s3, sw, bs: int):
+    """quant_act(silu(g) * u, bs) from the gate_up GEMM's int32 rows (detgpu/kernels.py:816-826),
+    or from float32 GU rows (s3 = sw = None)."""
+    acc = acc.contiguous()
+    N, two_i = acc.shape
+    I = two_i // 2
+    if bs > 1 and I % bs:
+        raise AssertionError("swiglu_quant: bs must divide I")
+    q = torch.empty((N, I), dtype=torch.int8, device=acc.device)
+    sc = torch.empty(N, dtype=F32, device=acc.device)
+    ps3, psw = _scales(acc, s3, sw)
+    _lib.call("uwc_swiglu_quant", acc.data_ptr(), ps3, psw, N, I, bs, q.data_ptr(), sc.data_ptr(), _stream())
+    return q, sc
+
+
+def embed(table: torch.Tensor, ids: torch.Tensor) -> torch.Tensor:
+    """table[ids] for float32 table (V, D); ids outside [0, V) raise (checked on the host)."""
+    ids64 = ids.reshape(-1).to(device=table.device, dtype=torch.int64).contiguous()
+    V, D = table.shape
+    if ids64.numel() and (int(ids64.min()) < 0 or int(ids64.max()) >= V):
+        raise IndexError(f"embed: token id outside [0, {V})")
+    out = torch.empty((ids64.numel(), D), dtype=F32, device=table.device)
+    _lib.call("uwc_embed_rows", table.contiguous().data_ptr(), V, D, ids64.data_ptr(), ids64.numel(), out.data_ptr(),
+              None, _stream())
+    return out
+
+
+OPS = {"add": 0, "sub": 1, "mul": 2, "div": 3, "sqrt": 4, "exp": 5, "silu": 6}
+
+
+def elementwise(op: str, x: torch.Tensor, y: torch.Tensor | None = None) -> torch.Tensor:
+    """One of detrt's fp32 ops (fadd, fsub, fmul, fdiv, fsqrt, det_exp, det_silu) elementwise, as the
+    layer kernels compute it (the native-fp32 check of runtime/tests/test_fp32_native.py)."""
+    x = x.contiguous().to(F32)
+    y = y.contiguous().to(F32) if y is not None else None
+    out = torch.empty_like(x)
+    _lib.call("uwc_det_elementwise", OPS[op], x.data_ptr(), y.data_ptr() if y is not None else None, out.data_ptr(),
+              x.numel(), _stream())
+    return out
+
+
+# ================================================================== sha
+def _row_leaf_words(rows: torch.Tensor, tag: int, base: int, mod: int, want_roots: bool = False):
+    """(n, 8) int32 tagged leaves (and row roots) of the rows of a 2-D float32 / int32 tensor."""
+    rows = rows.contiguous()
+    n, w = rows.shape
+    nblk = max(1, -(-w // (BLOCK // 4)))
+    scratch = torch.empty(n * nblk * 8, dtype=torch.int32, device=rows.device)
+    leaves = torch.empty((n, 8), dtype=torch.int32, device=rows.device)
+    roots = torch.empty((n, 8), dtype=torch.int32, device=rows.device) if want_roots else None
+    _lib.call("uwc_sha_row_leaves", rows.data_ptr() if rows.numel() else None, n, w, scratch.data_ptr(),
+              scratch.numel(), tag, base, mod, roots.data_ptr() if roots is not None else None, leaves.data_ptr(),
+              _stream())
+    return (leaves, roots) if want_roots else leaves
+
+
+def _leaf_words(out: torch.Tensor) -> torch.Tensor:
+    """(B * T, 8) int32: the stage-output leaves H(0x00 || "sout" || u32 t || row_root) as words."""
+    B, T, D = out.shape
+    return _row_leaf_words(out.reshape(B * T, D).to(F32), TAG_SOUT, 0, T)
+
+
+def merkle_roots(words: torch.Tensor, ntrees: int) -> torch.Tensor:
+    """(ntrees, 8) roots of ntrees consecutive trees of equal size over (ntrees * n, 8) leaf words."""
+    n = words.shape[0] // ntrees
+    scratch = torch.empty(2 * words.numel(), dtype=torch.int32, device=words.device)
+    roots = torch.empty((ntrees, 8), dtype=torch.int32, device=words.device)
+    _lib.call("uwc_sha_merkle_roots", words.contiguous().data_ptr(), ntrees, n, scratch.data_ptr(), scratch.numel(),
+              roots.data_ptr(), _stream())
+    return roots
+
+
+def digest_bytes(words) -> np.ndarray:
+    """(..., 8) sha256 state words (torch or numpy) -> (..., 32) digest bytes."""
+    if isinstance(words, torch.Tensor):
+        words = words.cpu().numpy()
+    w = np.ascontiguousarray(words).view(np.uint32)
+    return w.byteswap().view(np.uint8).reshape(*w.shape[:-1], 32)
+
+
+def sout_leaves(out: torch.Tensor) -> np.ndarray:
+    """Stage-output leaves of B stages: out (B, T, D) float32 on the GPU -> (B, T, 32) uint8 on the CPU."""
+    B, T, _ = out.shape
+    return digest_bytes(_leaf_words(out)).reshape(B, T, 32)
+
+
+def stage_roots_gpu(out: torch.Tensor) -> torch.Tensor:
+    """stage_output_root of each of the B stages in out (B, T, D), on the GPU: (B, 8) int32 words."""
+    B = out.shape[0]
+    return merkle_roots(_leaf_words(out), B)
+
+
+def stage_output_roots(out: torch.Tensor) -> list[bytes]:
+    """agent.proto.stage_output_root for each of the B stages in out (B, T, D)."""
+    return [bytes(r) for r in digest_bytes(stage_roots_gpu(out))]
+
+
+def row_roots(rows: torch.Tensor) -> torch.Tensor:
+    """(n, 8) int32 row roots of the rows of a 2-D float32 / int32 tensor."""
+    return _row_leaf_words(rows, TAG_LEAF, 0, 0, want_roots=True)[1]
+
+
+def trace_root(rows: list[torch.Tensor]) -> bytes:
+    """Stage trace root over leaf rows in program order (stage.py:120-133), hashed on the GPU:
+    rows of equal length are hashed together; leaf i = H(0x00 || "leaf" || u32 i || row_root)."""
+    dev = rows[0].device
+    n = len(rows)
+    leaves = torch.empty((n, 8), dtype=torch.int32, device=dev)
+    by_len: dict = {}
+    for i, r in enumerate(rows):
+        by_len.setdefault(int(r.numel()), []).append(i)
+    for w, idx in by_len.items():
+        mat = torch.stack([rows[i].reshape(-1).view(torch.int32) for i in idx]) if w else \
+            torch.empty((len(idx), 0), dtype=torch.int32, device=dev)
+        idx_t = torch.tensor(idx, dtype=torch.int64, device=dev)
+        # one call per run of consecutive indices, so that the leaf index is base + row
+        runs, start = [], 0
+        for j in range(1, len(idx) + 1):
+            if j == len(idx) or idx[j] != idx[j - 1] + 1:
+                runs.append((start, j))
+                start = j
+        for a, b in runs:
+            leaves[idx_t[a:b]] = _row_leaf_words(mat[a:b], TAG_LEAF, idx[a], 0)
+    return bytes(digest_bytes(merkle_roots(leaves, 1))[0])
+
+
+# ================================================================== model and stages
+class DetModel:
+    """What detgpu's stages read from detrt.qwen3.DetQwen3 (qwen3.py:165-199): D, H, Hkv, hd, eps,
+    qk_norm, inv_sqrt_hd, embed, cos, sin, layers[l] = dict(in_norm, post_norm, q_norm, k_norm,
+    qkv, o, gu, down (DetLinear), dev, cos, sin), norm and lm_head. Weights are already quantized
+    (int8 rows with their fp32 scales, as committed in the weights tree, stage.py:239-264)."""
+
+    def __init__(self, cfg: dict, embed: torch.Tensor, layers: list[dict], cos: torch.Tensor, sin: torch.Tensor,
+                 norm: torch.Tensor | None = None, lm_head: DetLinear | None = None):
+        self.D, self.H, self.Hkv, self.hd = cfg["D"], cfg["H"], cfg["Hkv"], cfg["hd"]
+        self.eps = float(np.array([cfg["eps_bits"]], np.uint32).view(np.float32)[0]) if "eps_bits" in cfg \
+            else _f32(cfg["eps"])
+        self.arch = cfg.get("arch", 0)
+        self.qk_norm = self.arch == 0
+        self.hadamard_block = cfg["Bs"]
+        self.inv_sqrt_hd = float(np.float32(1.0 / np.sqrt(self.hd)))
+        self.embed, self.cos, self.sin = embed, cos, sin
+        self.device = embed.device
+        self.layers = layers
+        for L in layers:
+            L.setdefault("dev", self.device)
+            L.setdefault("cos", cos)
+            L.setdefault("sin", sin)
+        self.norm, self.lm_head = norm, lm_head
+
+    def enter(self, dev):
+        return dev
+
+    @classmethod
+    def from_tables(cls, cfg: dict, embed, norms: list[dict], lins: list[dict], cos, sin, device="cuda",
+                    norm=None, lm_head=None) -> "DetModel":
+        """From numpy tables: norms[l] = {in_norm, post_norm, q_norm, k_norm}, lins[l][name] = (Wq, sw)."""
+        t = lambda a, dt=F32: torch.as_tensor(np.ascontiguousarray(a)).to(device=device, dtype=dt)
+        layers = []
+        for nrm, ls in zip(norms, lins):
+            L = {nm: t(nrm[nm]) for nm in ("in_norm", "post_norm", "q_norm", "k_norm")}
+            for name in ("qkv", "o", "gu", "down"):
+                Wq, sw = ls[name]
+                L[name] = DetLinear.from_quantized(t(Wq, torch.int8), t(sw), hadamard_bs(cfg["Bs"], Wq.shape[1]))
+            layers.append(L)
+        lm = None
+        if lm_head is not None:
+            lm = DetLinear.from_quantized(t(lm_head[0], torch.int8), t(lm_head[1]), hadamard_bs(cfg["Bs"], lm_head[0].shape[1]))
+        return cls(cfg, t(embed), layers, t(cos), t(sin), t(norm) if norm is not None else None, lm)
+
+    @classmethod
+    def random(cls, cfg: dict, seed: int = 0, device="cuda", with_lm_head: bool = True) -> "DetModel":
+        """A model of cfg's shape with seeded random weights, quantized on the GPU as DetLinear does
+        (Wq = quant_sym(fwht(W, bs), 64) per row, N(0, 0.02) weights), N(0, 1) embedding rows,
+        norm weights near 1, and the rope table of theta 1e6 built in float64 (qwen3.py:47-66)."""
+        g = torch.Generator(device=device)
+        g.manual_seed(seed)
+        D, H, Hkv, hd, I, V = cfg["D"], cfg["H"], cfg["Hkv"], cfg["hd"], cfg["I"], cfg["V"]
+        bs = cfg["Bs"]
+
+        def lin(n, k):
+            W = torch.randn((n, k), generator=g, device=device) * 0.02
+            q, s = _quant_act(W, hadamard_bs(bs, k))
+            del W
+            return DetLinear.from_quantized(q, s, hadamard_bs(bs, k))
+
+        def nw(k):
+            return 1.0 + 0.05 * torch.randn(k, generator=g, device=device)
+        layers = []
+        for _ in range(cfg["L"]):
+            layers.append(dict(in_norm=nw(D), post_norm=nw(D), q_norm=nw(hd), k_norm=nw(hd),
+                               qkv=lin((H + 2 * Hkv) * hd, D), o=lin(D, H * hd), gu=lin(2 * I, D), down=lin(D, I)))
+        embed_t = torch.randn((V, D), generator=g, device=device)
+        inv = 1.0 / (cfg.get("theta", 1e6) ** (np.arange(0, hd, 2, dtype=np.float64) / hd))
+        ang = np.arange(cfg.get("max_pos", 8192), dtype=np.float64)[:, None] * inv[None, :]
+        emb = np.concatenate([ang, ang], axis=1)
+        cos = torch.from_numpy(np.cos(emb).astype(np.float32)).to(device)
+        sin = torch.from_numpy(np.sin(emb).astype(np.float32)).to(device)
+        lm = lin(V, D) if with_lm_head else None
+        return cls(cfg, embed_t, layers, cos, sin, nw(D), lm)
+
+
+def layer_fused(m, L, x: torch.Tensor, B: int, T: int) -> torch.Tensor:
+    """One decoder layer: x (N, D) float32 -> (N, D) float32, bit-identical to detrt
+    (detgpu/stages.py:154-168)."""
+    H, Hkv = m.H, m.Hkv
+    q1, s1 = rmsnorm_quant(x, L["in_norm"], m.eps, L["qkv"].bs)
+    qq, qs, kq, ks, vq, vs, vt = qkv_post_vt(L["qkv"].int_gemm(q1), s1, L["qkv"].sw, L["q_norm"], L["k_norm"],
+                                             L["cos"][:T], L["sin"][:T], T, H, Hkv, m.eps, m.qk_norm)
+    oc = attention(qq, qs, kq, ks, vq, vs, B, T, H, Hkv, m.inv_sqrt_hd, vt=vt)
+    q2, s2 = quant_act(oc, L["o"].bs)
+    r1 = dequant_residual(L["o"].int_gemm(q2), s2, L["o"].sw, x)
+    q3, s3 = rmsnorm_quant(r1, L["post_norm"], m.eps, L["gu"].bs)
+    q4, s4 = swiglu_quant(L["gu"].int_gemm(q3), s3, L["gu"].sw, L["down"].bs)
+    return dequant_residual(L["down"].int_gemm(q4), s4, L["down"].sw, r1)
+
+
+@torch.no_grad()
+def stage_outputs(m, tokens: torch.Tensor | None, x: torch.Tensor | None, l0: int, l1: int) -> torch.Tensor:
+    """Layers l0..l1-1 for B sequences of T tokens: tokens (B, T) int64 when l0 == 0, else x
+    (B, T, D) float32, the previous group's output. Returns (B, T, D) float32 on the GPU
+    (detgpu/stages.py:172-214)."""
+    if l0 == 0:
+        B, T = tokens.shape
+        x = embed(m.embed, tokens)
+    else:
+        B, T = x.shape[0], x.shape[1]
+        x = x.to(m.device, F32).reshape(B * T, m.D)
+    for l in range(l0, l1):
+        x = layer_fused(m, m.layers[l], x, B, T)
+    return x.reshape(B, T, m.D)
+
+
+def job_outputs(m, tokens: torch.Tensor, groups: int, upto: int | None = None) -> list[torch.Tensor]:
+    """Every group's output for a batch of sequences, kept on the GPU (detgpu/stages.py:216-225)."""
+    lpg = len(m.layers) // groups
+    upto = groups - 1 if upto is None else upto
+    outs, x = [], None
+    for g in range(upto + 1):
+        x = stage_outputs(m, tokens if g == 0 else None, x, g * lpg, (g + 1) * lpg)
+        outs.append(x)
+    return outs
+
+
+@torch.no_grad()
+def final_logits(m, x: torch.Tensor):
+    """lm_head(det_rmsnorm(x, norm)) for hidden rows x (N, D): (int32 logits accumulators, fp32
+    logits), the rows DetQwen3.logprobs starts from (qwen3.py:300-311)."""
+    q, s = rmsnorm_quant(x.reshape(-1, m.D), m.norm, m.eps, m.lm_head.bs)
+    acc = m.lm_head.int_gemm(q)
+    from .detrt import dequant
+    return acc, dequant(acc, s, m.lm_head.sw)
