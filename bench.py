@@ -18,6 +18,9 @@ miner/ampere/bench/bench_gemm.py:37-56). The line also carries:
                 linears at M = 1, 8, 32): device time from graph replays over > 1.2 GB of rotated
                 weights, algorithmic bytes / time against 8 TB/s HBM;
   llama_prefill configs[3]'s prefill shapes (M = 8192), TOPS of the four GEMMs;
+  qwen3_e2e     configs[4]: the 28-layer Qwen3-1.7B-shaped integer forward over 8192 tokens (all
+                decoder-layer ops, per-layer stage-output roots and the lm_head logits on the GPU),
+                with a T = 64 parity check against the CPU oracle and a CPU baseline;
   cpu_baseline  the CPU oracle (this repo's C restatement, OpenMP) on a bounded sample of the
                 same workload: full mined forwards of whole nonces at the same shape;
   parity        the sampled nonce's GPU output, every tile digest and the winner set compared
@@ -325,6 +328,122 @@ def llama_prefill(args, torch, np):
     return out
 
 
+QWEN3_1P7B = dict(D=2048, H=16, Hkv=8, hd=128, I=6144, L=28, V=151936, eps=1e-6, Bs=512, max_pos=8192, theta=1e6,
+                  arch=0)
+
+
+def _oracle_model(m, layers, token_rows):
+    """The oracle's Model for the first `layers` layers of a GPU DetModel, with the embedding
+    restricted to token_rows (the tokens are remapped to 0 .. len - 1)."""
+    import numpy as np
+    from oracle import detrt_stage as S
+    c = lambda t: t.detach().cpu().numpy()  # noqa: E731
+    cfg = dict(QWEN3_1P7B, eps_bits=int(np.float32(QWEN3_1P7B["eps"]).view(np.uint32)))
+    norms = [{nm: c(L[nm]) for nm in ("in_norm", "post_norm", "q_norm", "k_norm")} for L in m.layers[:layers]]
+    lins = [{nm: (c(L[nm].Wq), c(L[nm].sw)) for nm in ("qkv", "o", "gu", "down")} for L in m.layers[:layers]]
+    emb = c(m.embed[token_rows])
+    om = S.Model(cfg, emb, norms, lins, c(m.cos), c(m.sin), lm_head=(c(m.lm_head.Wq), c(m.lm_head.sw)),
+                 final_norm=c(m.norm))
+    return om
+
+
+def qwen3_e2e(args, torch, np):
+    """the deterministic Qwen3-1.7B-shaped integer forward (28 layers, vocab
+    151936, seeded random weights quantized per detrt on the GPU) over one 8192-token prompt of
+    seeded uniform ids: embedding, 28 fused decoder layers (rmsnorm_quant, qkv GEMM, qkv_post,
+    exact attention, o GEMM + residual, rmsnorm_quant, gate_up GEMM, swiglu_quant, down GEMM +
+    residual), every layer's stage-output root (SHA-256 Merkle over its 8192 output rows) on the
+    GPU, then the final norm, the lm_head GEMM (int32 logits) and a SHA-256 Merkle root of the
+    logits rows. Parity: the same model's first two layers and the lm_head at T = 64 against the
+    CPU oracle, bit for bit (outputs, stage roots, int logits)."""
+    from uwc_amd import detgpu
+    from oracle import detrt_stage as S
+    cfg = QWEN3_1P7B
+    T, NL = args.e2e_tokens, args.e2e_layers
+    cfg = dict(cfg, L=NL)
+    dev = "cuda"
+    t0 = time.perf_counter()
+    m = detgpu.DetModel.random(cfg, seed=5, device=dev)
+    torch.cuda.synchronize()
+    log(f"e2e: model of {NL} layers built in {time.perf_counter() - t0:.1f} s")
+    rng = np.random.default_rng(2026)
+    toks = rng.integers(0, cfg["V"], size=T)
+    tokens = torch.from_numpy(toks[None]).to(dev)
+
+    def forward(tok):
+        Tn = tok.shape[1]
+        x = detgpu.embed(m.embed, tok)
+        roots = []
+        for L in m.layers:
+            x = detgpu.layer_fused(m, L, x, 1, Tn)
+            roots.append(detgpu.stage_roots_gpu(x.reshape(1, Tn, cfg["D"])))
+        acc, _ = detgpu.final_logits(m, x)
+        lroot = detgpu.merkle_roots(detgpu._row_leaf_words(acc, detgpu.TAG_SOUT, 0, 0), 1)
+        return x, torch.cat(roots), acc, lroot
+
+    forward(tokens)  # warm-up
+    torch.cuda.synchronize()
+    reps = 2
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        x, roots, acc, lroot = forward(tokens)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / reps
+    D, H, Hkv, hd, I, V = cfg["D"], cfg["H"], cfg["Hkv"], cfg["hd"], cfg["I"], cfg["V"]
+    lin_macs = T * D * ((H + 2 * Hkv) * hd + H * hd + 2 * I) + T * I * D
+    gemm_ops = 2.0 * (NL * lin_macs + T * D * V)
+    attn_macs = NL * H * hd * T * (T + 1) // 2 * 2  # q.k and p.v over the causal half
+    layer_roots = detgpu.digest_bytes(roots)
+    import hashlib
+    out = dict(workload=f"Qwen3-1.7B-shaped deterministic integer forward, {NL} layers, vocab {V}, {T} tokens, "
+                        "random-init weights quantized per detrt; per-layer stage-output roots and the int32 "
+                        "logits' Merkle root on the GPU",
+               ms_per_forward=round(dt * 1e3, 2), tokens_per_s=round(T / dt, 1),
+               gemm_tops=round(gemm_ops / dt / 1e12, 1),
+               attention_gmac=round(attn_macs / 1e9, 1),
+               layer_roots_sha256=hashlib.sha256(b"".join(bytes(r) for r in layer_roots)).hexdigest()[:20],
+               first_layer_root=bytes(layer_roots[0]).hex()[:20],
+               logits_root=bytes(detgpu.digest_bytes(lroot)[0]).hex()[:20])
+    log(f"e2e: {out}")
+    del x, roots, acc, lroot
+    torch.cuda.empty_cache()
+    # parity at T = 64: two layers + lm_head vs the oracle
+    Tp = 64
+    sub = toks[:Tp]
+    uniq, inv = np.unique(sub, return_inverse=True)
+    om = _oracle_model(m, 2, torch.from_numpy(uniq).to(dev))
+    tk = torch.from_numpy(sub[None]).to(dev)
+    xg = detgpu.embed(m.embed, tk)
+    xo = om.embed[inv]
+    ok_rows, ok_roots = True, True
+    for l in range(2):
+        xg = detgpu.layer_fused(m, m.layers[l], xg, 1, Tp)
+        xo = S.layer(om, l, xo)
+        ok_rows &= bool(np.array_equal(xg.cpu().numpy().view(np.uint32), xo.view(np.uint32)))
+        ok_roots &= detgpu.stage_output_roots(xg.reshape(1, Tp, D))[0] == S.stage_output_root(xo)
+    acc_g, _ = detgpu.final_logits(m, xg)
+    acc_o, _ = S.final_logits(om, xo)
+    out["parity"] = dict(tokens=Tp, layers=2, outputs_equal=ok_rows, stage_roots_equal=ok_roots,
+                         int_logits_equal=bool(np.array_equal(acc_g.cpu().numpy(), acc_o)))
+    # CPU baseline: the oracle's layer at Tc tokens (float64 BLAS GEMMs as the reference's CPU path)
+    Tc = args.e2e_cpu_tokens
+    subc = toks[:Tc]
+    uc, ic = np.unique(subc, return_inverse=True)
+    omc = _oracle_model(m, 1, torch.from_numpy(uc).to(dev))
+    threads = os.cpu_count() or 1
+    t0 = time.perf_counter()
+    S.layer(omc, 0, omc.embed[ic])
+    ct = time.perf_counter() - t0
+    cl_ops = 2.0 * Tc * D * ((H + 2 * Hkv) * hd + H * hd + 2 * I) + 2.0 * Tc * I * D
+    out["cpu_baseline"] = dict(value=round(cl_ops / ct / 1e12, 5), unit="TOPS (linear ops / whole-layer time)",
+                               cores=threads, kind="port",
+                               sample=f"one decoder layer at T={Tc} through oracle/detrt_stage.py (numpy fp32 "
+                                      f"ops, float64 BLAS GEMMs), {ct:.2f} s")
+    out["gemm_tops_unit"] = "TOPS (linear + lm_head ops / whole-forward time)"
+    log(f"e2e parity / cpu: {out['parity']} {out['cpu_baseline']}")
+    return out
+
+
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "noisy_gemm256_mining_4096_traffic.txt")
 COPY_BYTES = 256 << 20  # the calibration copy: reads and writes exactly this many bytes
 
@@ -420,6 +539,11 @@ def main():
     ap.add_argument("--cpu-max-nonces", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-detrt", action="store_true")
+    ap.add_argument("--no-e2e", action="store_true", help="skip configs[4] (the 28-layer forward)")
+    ap.add_argument("--e2e-only", action="store_true", help="run only configs[4]")
+    ap.add_argument("--e2e-tokens", type=int, default=8192)
+    ap.add_argument("--e2e-layers", type=int, default=28)
+    ap.add_argument("--e2e-cpu-tokens", type=int, default=256)
     ap.add_argument("--traffic-probe", action="store_true", help="the workload of the FETCH_SIZE / WRITE_SIZE passes")
     ap.add_argument("--summarize-pmc", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "CMD"),
                     help="write the traffic summary under profiles/ from two counter_collection.csv files")
@@ -446,11 +570,15 @@ def main():
     if args.traffic_probe:
         traffic_probe(args, torch, ops, O, np)
         return
+    if args.e2e_only:
+        print(json.dumps(qwen3_e2e(args, torch, np)))
+        return
     res = mining(args, torch, np, ops, O)
     parity, cpu = (None, None) if args.no_cpu else parity_and_cpu(args, res, torch, np, ops, O)
     det = None if args.no_detrt else detrt_layer(args, torch, np)
     skinny = None if args.no_detrt else skinny_linears(args, torch, np)
     prefill = None if args.no_detrt else llama_prefill(args, torch, np)
+    e2e = None if (args.no_detrt or args.no_e2e) else qwen3_e2e(args, torch, np)
     m, n, k, r = res["m"], res["n"], res["k"], res["r"]
     line = {
         "metric": METRIC,
@@ -478,6 +606,7 @@ def main():
         "detrt_layer": det,
         "detrt_skinny": skinny,
         "llama_prefill": prefill,
+        "qwen3_e2e": e2e,
     }
     print(json.dumps(line), flush=True)
 

@@ -142,8 +142,10 @@ def lin_bs(hadamard_block: int, k: int) -> int:
 
 
 def int_gemm(q: np.ndarray, Wq: np.ndarray) -> np.ndarray:
-    """Exact q @ Wq^T (qwen3.py:106-110, fp64 on the CPU: exact at these ranges)."""
-    return q.astype(I64) @ Wq.astype(I64).T
+    """Exact q @ Wq^T as the reference's CPU path computes it, a float64 GEMM (qwen3.py:106-110):
+    every product is an integer below 2**14 and every partial sum below 2**53 for k < 2**39, so
+    any summation order is exact."""
+    return (np.asarray(q, F64) @ np.asarray(Wq, F64).T).astype(I64)
 
 
 def dequant(acc: np.ndarray, s: np.ndarray, sw: np.ndarray) -> np.ndarray:
@@ -179,11 +181,12 @@ def attention(qq, qs, kq, ks, vq, vs, inv_sqrt: np.float32):
     T, H, hd = qq.shape
     Hkv = kq.shape[1]
     rep = H // Hkv
-    K = np.repeat(kq.transpose(1, 0, 2), rep, axis=0).astype(I64)   # (H, T, hd)
+    # float64 products are exact here: |q . k| < 2**24 and |sum p v| < 16383 * 127 * T < 2**53
+    K = np.repeat(kq.transpose(1, 0, 2), rep, axis=0).astype(F64)   # (H, T, hd)
     SK = np.repeat(ks.transpose(1, 0, 2), rep, axis=0)               # (H, T, 1)
-    V = np.repeat(vq.transpose(1, 0, 2), rep, axis=0).astype(I64)
+    V = np.repeat(vq.transpose(1, 0, 2), rep, axis=0).astype(F64)
     SV = np.repeat(vs.transpose(1, 0, 2), rep, axis=0)
-    Q, QS = qq.transpose(1, 0, 2).astype(I64), qs.transpose(1, 0, 2)
+    Q, QS = qq.transpose(1, 0, 2).astype(F64), qs.transpose(1, 0, 2)
     sc_int = (Q @ K.transpose(0, 2, 1)).astype(F32)                 # exact: |s| < 2**24
     sc = ((sc_int * QS) * SK.transpose(0, 2, 1)) * inv_sqrt
     mask = np.arange(T)[None, :] <= np.arange(T)[:, None]
@@ -197,7 +200,7 @@ def attention(qq, qs, kq, ks, vq, vs, inv_sqrt: np.float32):
     pmax = Pv.max(axis=-1, keepdims=True)
     sp = np.maximum(pmax, c32(1e-30)) / c32(float(P_LEVELS))
     pi = np.clip(np.rint(Pv / sp), 0, P_LEVELS).astype(np.int32)
-    acc = pi.astype(I64) @ V                                          # = sum over key chunks of (hi << 7) + lo
+    acc = (pi.astype(F64) @ V).astype(I64)                            # = sum over key chunks of (hi << 7) + lo
     o = acc.astype(F32) * sp
     return sc, pi, sp, o
 
@@ -300,6 +303,15 @@ def layer(m: Model, l: int, x: np.ndarray, put=None) -> np.ndarray:
                 put("VT", l, d, hh, np.ascontiguousarray(vq[:, hh, d]).astype(np.int32))
             put("VS", l, -1, hh, vs[:, hh, 0])
     return r2.astype(F32)
+
+
+def final_logits(m: Model, x: np.ndarray):
+    """lm_head(det_rmsnorm(x, norm)) (qwen3.py:300, :306): (int32 accumulators, fp32 logits)."""
+    h = det_rmsnorm(x, m.final_norm, m.eps32)
+    Wq, sw = m.lm_head
+    q, s = quant_act(h, m.bs(h.shape[1]))
+    acc = int_gemm(q, Wq)
+    return acc.astype(np.int32), dequant(acc, s, sw)
 
 
 def run_stage(m: Model, tokens, x_in, l0: int, l1: int, keep_rows: bool = True):
