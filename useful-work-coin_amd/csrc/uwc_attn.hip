@@ -22,23 +22,49 @@
 //     previous one over the whole causal row, so the kernel sweeps the keys four times and
 //     recomputes the scores (cheap on the matrix cores) instead of storing T x T rows;
 //   * exp rows have max exactly det_exp(0) = 1 and every term below 2, so exact_rowsum's
-//     scale is the constant 2^41 (L = 20 for MAX_KEYS = 2^20): a term is rint(e * 2^41) < 2^42,
-//     converted to u64 through two exact float32 halves.
+//     scale is the constant 2^41 (L = 20 for MAX_KEYS = 2^20): a term is rint(e * 2^41) < 2^42;
+//   * the divisions by the row constants den and sp are products with their float64
+//     reciprocals (exact after rounding to float32, see at_div).
 // Row statistics are per lane partials combined across the 4 lane groups (xor 16, 32); all
 // reductions are max or exact integer sums, so the key split cannot change a bit.
+#include <type_traits>
+
 #include "uwc_rows.h"
 
 #define AT_PLEVELS 16383.0f
 
 __device__ __forceinline__ v4i at_zero4() { return v4i{0, 0, 0, 0}; }
 
-// round_half_even(e * 2^41) as u64 for 0 <= e < 2 (exact; see the file comment).
-__device__ __forceinline__ u64 at_fix41(float e) {
-  const float v = rintf(__fmul_rn(e, 0x1p41f));
-  const float hi = floorf(__fmul_rn(v, 0x1p-32f));
-  const float lo = __fsub_rn(v, __fmul_rn(hi, 0x1p32f));
-  return ((u64)(u32)hi << 32) | (u64)(u32)lo;
+// round_half_even(e * 2^41) for 0 <= e < 2, as a float64 integer (exact: e * 2^41 is a float32
+// scaled by a power of two, its rounding to an integer is a float32 integer below 2^42).
+__device__ __forceinline__ double at_fix41(float e) { return (double)rintf(__fmul_rn(e, 0x1p41f)); }
+
+// det_exp(z) for z <= 0 or z = -inf (the attention's s - max): the overflow and NaN branches of
+// dx_exp cannot trigger, the rest is dx_exp's op sequence.
+__device__ __forceinline__ float at_exp(float z) {
+  float t = __fmul_rn(z, DX_LOG2E);
+  const bool under = t < -126.0f;
+  if (under) t = 0.0f;
+  const float n = floorf(t);
+  const float f = __fsub_rn(t, n);
+  float p = DX_E7;
+  p = __fadd_rn(__fmul_rn(p, f), DX_E6);
+  p = __fadd_rn(__fmul_rn(p, f), DX_E5);
+  p = __fadd_rn(__fmul_rn(p, f), DX_E4);
+  p = __fadd_rn(__fmul_rn(p, f), DX_E3);
+  p = __fadd_rn(__fmul_rn(p, f), DX_E2);
+  p = __fadd_rn(__fmul_rn(p, f), DX_E1);
+  p = __fadd_rn(__fmul_rn(p, f), DX_E0);
+  const float r = __fmul_rn(p, __int_as_float(((int)n + 127) << 23));
+  return under ? 0.0f : r;
 }
+
+// x / d correctly rounded to float32, for float32 x and a per-row divisor given as
+// rd = 1.0 / (double)d (correctly rounded in float64): the float64 product is within 2^-52
+// (relative) of x / d, while a float32 quotient of two float32 values is never a rounding tie and
+// lies more than 2^-49 (relative) from every float32 midpoint, so rounding the product to float32
+// gives the correctly rounded quotient.
+__device__ __forceinline__ float at_div(float x, double rd) { return (float)((double)x * rd); }
 
 __device__ __forceinline__ float at_max_groups(float v) {
   v = fmaxf(v, __shfl_xor(v, 16, 64));
@@ -54,40 +80,63 @@ __device__ __forceinline__ u64 at_sum_groups(u64 v) {
   return v;
 }
 
+// The scales of one 64-key tile (keys kt*64 .. +63, clamped to T - 1) staged through the wave's
+// own LDS slot; lane group g then reads keys 16 b + 4 g .. + 3 of block b as one float4. LDS
+// operations of a wave complete in order, so no barrier is involved.
+__device__ __forceinline__ void at_stage_scales(const float* __restrict__ sc, u32 base, int stride, int k0, int T,
+                                                float* slot, int lane, float4 out[4]) {
+  const int j = min(k0 + lane, T - 1);
+  slot[lane] = sc[base + (u32)j * (u32)stride];
+  __builtin_amdgcn_wave_barrier();
+  const int g = lane >> 4;
+#pragma unroll
+  for (int b = 0; b < 4; b++) out[b] = *reinterpret_cast<const float4*>(slot + 16 * b + 4 * g);
+  __builtin_amdgcn_wave_barrier();
+}
+
+__device__ __forceinline__ float at_get(const float4& v, int i) {
+  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
 template <int HD>
-__global__ void __launch_bounds__(256) attention_kernel(const i8* __restrict__ qq, const float* __restrict__ qs,
+__global__ void __launch_bounds__(256, 3) attention_kernel(const i8* __restrict__ qq, const float* __restrict__ qs,
                                                         const i8* __restrict__ kq, const float* __restrict__ ks,
                                                         const i8* __restrict__ vt, const float* __restrict__ vs, int T,
                                                         int Tp, int H, int Hkv, float inv_sqrt, float* __restrict__ o) {
   constexpr int NC = (HD + 63) / 64;  // 64-dim chunks of the score product
   constexpr int ND = HD / 16;         // 16-dim blocks of the output
+  __shared__ __attribute__((aligned(16))) float at_slot[4][2][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int ql = lane & 15, g = lane >> 4;
   // longest rows first: the q tile index counts down
   const int q0 = (gridDim.x - 1 - blockIdx.x) * 64 + wave * 16;
-  if (q0 >= T) return;  // whole waves only; the kernel has no barriers
+  if (q0 >= T) return;  // whole waves only; the kernel has no workgroup barriers
   const int h = blockIdx.y, bseq = blockIdx.z, hk = h / (H / Hkv);
-  const long nb = (long)bseq * T;
+  // 32-bit offsets: the host checks B * T * max(H, Hkv) * HD < 2^31
+  const u32 nb = (u32)(bseq * T);
   const int qi = q0 + ql, qc = min(qi, T - 1);
-  const float my_qs = qs[(nb + qc) * H + h];
+  const float my_qs = qs[(nb + qc) * (u32)H + h];
+  float* sk_slot = at_slot[wave][0];
+  float* sv_slot = at_slot[wave][1];
+  const u32 sc_base = nb * (u32)Hkv + hk;  // ks / vs index of key j: sc_base + j * Hkv
 
   v4i qf[NC];
 #pragma unroll
   for (int c = 0; c < NC; c++) {
     const int d0 = 64 * c + 16 * g;
-    qf[c] = d0 < HD ? *reinterpret_cast<const v4i*>(qq + ((nb + qc) * H + h) * HD + d0) : at_zero4();
+    qf[c] = d0 < HD ? *reinterpret_cast<const v4i*>(qq + ((nb + qc) * (u32)H + h) * HD + d0) : at_zero4();
   }
   const int kmax = min(T, q0 + 16);  // keys any query of the wave sees
   const int nkt = (kmax + 63) / 64;
+  const i8* kbase = kq + (size_t)hk * HD;
 
-  // scores of key tile kt: S[b][i] = score of key 64 kt + 16 b + 4 g + i for query qi (or -inf)
-  auto scores = [&](int kt, float S[4][4]) {
-    v4i acc[4];
+  // integer scores of key tile kt: acc[b][i] = q_qi . k_j, j = 64 kt + 16 b + 4 g + i
+  auto iscores = [&](int kt, v4i acc[4]) {
 #pragma unroll
     for (int b = 0; b < 4; b++) {
       acc[b] = at_zero4();
       const int kr = min(kt * 64 + 16 * b + ql, T - 1);
-      const i8* kp = kq + ((nb + kr) * Hkv + hk) * HD;
+      const i8* kp = kbase + (nb + kr) * (u32)(Hkv * HD);
 #pragma unroll
       for (int c = 0; c < NC; c++) {
         const int d0 = 64 * c + 16 * g;
@@ -95,82 +144,103 @@ __global__ void __launch_bounds__(256) attention_kernel(const i8* __restrict__ q
         acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf, qf[c], acc[b], 0, 0, 0);
       }
     }
+  };
+  // scores as floats. Tiles below nfull hold only keys <= q0 (the wave's first query) and < T and
+  // need no mask; in the others masked entries are -inf. MASK is a compile-time flag: the sweeps
+  // run the full tiles, then the one diagonal tile.
+  const int nfull = (q0 + 1) / 64;
+  auto scores = [&](int kt, float S[4][4], float4 skv[4], auto mask) {
+    constexpr bool MASK = decltype(mask)::value;
+    v4i acc[4];
+    iscores(kt, acc);
+    at_stage_scales(ks, sc_base, Hkv, kt * 64, T, sk_slot, lane, skv);
 #pragma unroll
     for (int b = 0; b < 4; b++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const int j = kt * 64 + 16 * b + 4 * g + i;
-        float s = -__int_as_float(0x7f800000);
-        if (j <= qi && j < T) s = __fmul_rn(__fmul_rn(__fmul_rn((float)acc[b][i], my_qs), ks[(nb + j) * Hkv + hk]), inv_sqrt);
-        S[b][i] = s;
+        const float s = __fmul_rn(__fmul_rn(__fmul_rn((float)acc[b][i], my_qs), at_get(skv[b], i)), inv_sqrt);
+        if constexpr (MASK) {
+          const int j = kt * 64 + 16 * b + 4 * g + i;
+          S[b][i] = (j <= qi && j < T) ? s : -__int_as_float(0x7f800000);
+        } else {
+          S[b][i] = s;
+        }
       }
+  };
+  auto sweep = [&](auto body) {
+    for (int kt = 0; kt < nfull; kt++) body(kt, std::false_type{});
+    for (int kt = nfull; kt < nkt; kt++) body(kt, std::true_type{});
   };
 
   // sweep 1: row max
   float mx = -__int_as_float(0x7f800000);
-  for (int kt = 0; kt < nkt; kt++) {
+  sweep([&](int kt, auto mask) {
     float S[4][4];
-    scores(kt, S);
+    float4 skv[4];
+    scores(kt, S, skv, mask);
 #pragma unroll
     for (int b = 0; b < 4; b++)
 #pragma unroll
       for (int i = 0; i < 4; i++) mx = fmaxf(mx, S[b][i]);
-  }
+  });
   mx = at_max_groups(mx);
 
-  // sweep 2: exact denominator (fixed point at 2^41)
+  // sweep 2: exact denominator (fixed point at 2^41); masked entries give det_exp(-inf) = 0.
+  // A tile's 16 terms per lane sum exactly in float64 (< 2^46), then join a u64 total.
   u64 dsum = 0;
-  for (int kt = 0; kt < nkt; kt++) {
+  sweep([&](int kt, auto mask) {
     float S[4][4];
-    scores(kt, S);
+    float4 skv[4];
+    scores(kt, S, skv, mask);
+    double part = 0.0;
 #pragma unroll
     for (int b = 0; b < 4; b++)
 #pragma unroll
-      for (int i = 0; i < 4; i++)
-        if (S[b][i] != -__int_as_float(0x7f800000)) dsum += at_fix41(dx_exp(__fsub_rn(S[b][i], mx)));
-  }
+      for (int i = 0; i < 4; i++) part += at_fix41(at_exp(__fsub_rn(S[b][i], mx)));
+    dsum += (u64)part;
+  });
   dsum = at_sum_groups(dsum);
   const float den = (float)ldexp((double)dsum, -41);
+  const double rden = 1.0 / (double)den;
 
   // sweep 3: max of the V-scaled probabilities
   float pm = 0.f;
-  for (int kt = 0; kt < nkt; kt++) {
+  sweep([&](int kt, auto mask) {
     float S[4][4];
-    scores(kt, S);
+    float4 skv[4], svv[4];
+    scores(kt, S, skv, mask);
+    at_stage_scales(vs, sc_base, Hkv, kt * 64, T, sv_slot, lane, svv);
 #pragma unroll
     for (int b = 0; b < 4; b++)
 #pragma unroll
-      for (int i = 0; i < 4; i++)
-        if (S[b][i] != -__int_as_float(0x7f800000)) {
-          const int j = kt * 64 + 16 * b + 4 * g + i;
-          const float e = dx_exp(__fsub_rn(S[b][i], mx));
-          pm = fmaxf(pm, __fmul_rn(__fdiv_rn(e, den), vs[(nb + j) * Hkv + hk]));
-        }
-  }
+      for (int i = 0; i < 4; i++) {
+        const float e = at_exp(__fsub_rn(S[b][i], mx));
+        pm = fmaxf(pm, __fmul_rn(at_div(e, rden), at_get(svv[b], i)));
+      }
+  });
   pm = at_max_groups(pm);
   const float sp = __fdiv_rn(fmaxf(pm, 1e-30f), AT_PLEVELS);
+  const double rsp = 1.0 / (double)sp;
 
   // sweep 4: 14-bit probabilities as two 7-bit limbs, O^T = V^T P^T on the matrix cores
   v4i ohi[ND], olo[ND];
 #pragma unroll
   for (int d = 0; d < ND; d++) ohi[d] = olo[d] = at_zero4();
-  const i8* vbase = vt + ((long)(bseq * Hkv + hk) * HD) * Tp;
-  for (int kt = 0; kt < nkt; kt++) {
+  const i8* vbase = vt + (size_t)(bseq * Hkv + hk) * HD * Tp;
+  sweep([&](int kt, auto mask) {
     float S[4][4];
-    scores(kt, S);
+    float4 skv[4], svv[4];
+    scores(kt, S, skv, mask);
+    at_stage_scales(vs, sc_base, Hkv, kt * 64, T, sv_slot, lane, svv);
     v4i bhi, blo;
 #pragma unroll
     for (int b = 0; b < 4; b++) {
       u32 ph = 0, pl = 0;
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        int p = 0;
-        if (S[b][i] != -__int_as_float(0x7f800000)) {
-          const int j = kt * 64 + 16 * b + 4 * g + i;
-          const float e = dx_exp(__fsub_rn(S[b][i], mx));
-          const float pv = __fmul_rn(__fdiv_rn(e, den), vs[(nb + j) * Hkv + hk]);
-          p = (int)fminf(fmaxf(rintf(__fdiv_rn(pv, sp)), 0.0f), AT_PLEVELS);
-        }
+        const float e = at_exp(__fsub_rn(S[b][i], mx));
+        const float pv = __fmul_rn(at_div(e, rden), at_get(svv[b], i));
+        const int p = (int)fminf(fmaxf(rintf(at_div(pv, rsp)), 0.0f), AT_PLEVELS);
         ph |= (u32)(p >> 7) << (8 * i);
         pl |= (u32)(p & 127) << (8 * i);
       }
@@ -179,14 +249,14 @@ __global__ void __launch_bounds__(256) attention_kernel(const i8* __restrict__ q
     }
 #pragma unroll
     for (int d = 0; d < ND; d++) {
-      const v4i vf = *reinterpret_cast<const v4i*>(vbase + (long)(16 * d + ql) * Tp + kt * 64 + 16 * g);
+      const v4i vf = *reinterpret_cast<const v4i*>(vbase + (u32)(16 * d + ql) * (u32)Tp + kt * 64 + 16 * g);
       ohi[d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(vf, bhi, ohi[d], 0, 0, 0);
       olo[d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(vf, blo, olo[d], 0, 0, 0);
     }
-  }
+  });
   if (qi >= T) return;
   // lane holds dims 16 d + 4 g + i of query qi
-  float* orow = o + ((nb + qi) * H + h) * HD;
+  float* orow = o + ((nb + qi) * (u32)H + h) * HD;
 #pragma unroll
   for (int d = 0; d < ND; d++) {
     float4 r;
@@ -212,6 +282,8 @@ extern "C" int uwc_attention(const int8_t* qq, const float* qs, const int8_t* kq
   if ((uintptr_t)o & 15) return uwc_fail("%s: o must be 16-byte aligned", fn);
   if (B == 0) return UWC_OK;
   if (B > 65535 || H > 65535) return uwc_fail("%s: B and H must be <= 65535", fn);
+  if ((int64_t)B * T * (H > Hkv ? H : Hkv) * hd >= (1LL << 31))
+    return uwc_fail("%s: B * T * H * hd must be below 2^31 (32-bit offsets)", fn);
   const int Tp = ((T + 63) / 64) * 64;
   const dim3 grid((unsigned)(Tp / 64), (unsigned)H, (unsigned)B);
   if (hd == 32)
