@@ -119,3 +119,25 @@ def test_det_linear_call_matches_oracle(dev):
     y = lay(torch.from_numpy(x).to(dev))
     _, _, _, want = O.det_linear(x, Wq, sw, bs)
     assert np.array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("m,n,k", [(4096, 4096 + 128, 1024), (4096, 4096 + 384, 256)])
+def test_column_split_gemm_all_out_modes(dev, m, n, k):
+    """n not a multiple of 256 with enough 256 x 256 tiles to fill the CUs (a vocabulary-sized
+    lm_head): the column split (256 x 256 tiles, then a 128 x 128 tail writing into the same rows)
+    gives the exact product and the exact fused epilogues."""
+    ops, _ = _mods()
+    from uwc_amd import _lib
+    rng = np.random.default_rng(n + k)
+    A = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, size=(n, k), dtype=np.int8)
+    At, Bt = torch.from_numpy(A).to(dev), torch.from_numpy(B).to(dev)
+    ref = O.igemm(A, B)
+    assert np.array_equal(ops.igemm_i32(At, Bt).cpu().numpy(), ref)
+    sx = rng.uniform(1e-3, 1.0, m).astype(np.float32)
+    sw = rng.uniform(1e-3, 1.0, n).astype(np.float32)
+    Y = torch.empty((m, n), dtype=torch.float32, device=dev)
+    sxt, swt = torch.from_numpy(sx).to(dev), torch.from_numpy(sw).to(dev)  # held until the launch has run
+    _lib.call("uwc_igemm_dequant_f32", At.data_ptr(), Bt.data_ptr(), m, n, k, sxt.data_ptr(), swt.data_ptr(),
+              Y.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    assert np.array_equal(Y.cpu().numpy().view(np.uint32), O.dequant(ref, sx, sw).view(np.uint32))

@@ -306,7 +306,7 @@ def test_sha_row_roots_and_trace_roots(dev):
         for i in range(5):
             assert bytes(got[i]) == S.row_root(rows[i]), (w, i)
     # stage-output roots for several tree sizes
-    for T in (1, 2, 3, 5, 8, 12, 33):
+    for T in (1, 2, 3, 5, 8, 12, 33, 512, 513, 700, 1100, 2048):  # > 512: the two-phase tree
         out = rng.standard_normal((2, T, 40)).astype(np.float32)
         roots = detgpu.stage_output_roots(_t(out, dev))
         assert roots == [S.stage_output_root(out[b]) for b in range(2)], T

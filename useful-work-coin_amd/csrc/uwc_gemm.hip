@@ -57,6 +57,7 @@ struct GemmParams {
   const float* b_scale;
   void* out;
   u32* dump;
+  int ldc;  // output row stride in elements (n unless the GEMM writes a column slice)
 };
 
 // Global -> register prefetch of one 128 x 64 operand tile: 512 16-byte pieces, 2 per thread.
@@ -296,7 +297,7 @@ __global__ void __launch_bounds__(G_THREADS) noisy_gemm_kernel(GemmParams p) {
         for (int e = 0; e < 16; e++) {
           const int row = bm0 + wm * 64 + mb * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
           if (row >= p.m) continue;
-          const long o = (long)row * p.n + col;
+          const long o = (long)row * p.ldc + col;
           const int v = acc[mb][nb][e];
           if constexpr (OUT == OUT_I32) {
             reinterpret_cast<i32*>(p.out)[o] = v;
@@ -316,7 +317,7 @@ __global__ void __launch_bounds__(G_THREADS) noisy_gemm_kernel(GemmParams p) {
 int uwc_noisy_gemm256(const int8_t* A, const int8_t* B, int m, int n, int k, int r, const int8_t* corrA,
                       const int8_t* corrB, const int32_t* maxabs, int lmax, const uint32_t* key,
                       const uint32_t* target, uint32_t* wins, int max_wins, const float* a_scale, const float* b_scale,
-                      void* out, int out_mode, int flags, uint32_t* tile_dump, hipStream_t stream);
+                      void* out, int out_mode, int flags, uint32_t* tile_dump, int ldc, hipStream_t stream);
 
 int uwc_skinny_gemm(const int8_t* X, const int8_t* W, int m, int n, int k, const float* sx, const float* sw,
                     void* out, int out_mode, hipStream_t stream);
@@ -368,9 +369,25 @@ extern "C" int uwc_noisy_gemm(const int8_t* A, const int8_t* B, int m, int n, in
   const bool fills = (long)(m / 256) * (n / 256) >= 256;
   if (m % 256 == 0 && n % 256 == 0 && k % 128 == 0 && !(flags & FLAG_TILE128) && (!plain || fills))
     return uwc_noisy_gemm256(A, B, m, n, k, r, corrA, corrB, maxabs, lmax, key, target, wins, max_wins, a_scale,
-                             b_scale, out, out_mode, flags & ~FLAG_TILE128, tile_dump, stream);
+                             b_scale, out, out_mode, flags & ~FLAG_TILE128, tile_dump, n, stream);
+  // A plain GEMM whose n is not a multiple of 256 (e.g. a vocabulary of 151936) but whose 256 x 256
+  // tiles would fill the CUs: columns [0, n256) on 256 x 256 tiles, the last n - n256 on 128 x 128
+  // tiles writing into the same rows (integer sums: the split cannot change a value).
+  const int n256 = n / 256 * 256;
+  if (plain && m % 256 == 0 && k % 128 == 0 && n256 > 0 && n256 < n && !(flags & FLAG_TILE128) &&
+      (long)(m / 256) * (n256 / 256) >= 256) {
+    const int st = uwc_noisy_gemm256(A, B, m, n256, k, 0, nullptr, nullptr, nullptr, 0, nullptr, nullptr, nullptr, 0,
+                                     a_scale, b_scale, out, out_mode, 0, nullptr, n, stream);
+    if (st || out_mode == OUT_NONE) return st;
+    const size_t es = out_mode == OUT_BF16 ? 2 : 4;
+    GemmParams q{A, B + (long)n256 * k, m, n - n256, k, 0, nullptr, nullptr, nullptr, 0, nullptr, nullptr, nullptr, 0,
+                 a_scale, b_scale ? b_scale + n256 : nullptr, static_cast<char*>(out) + n256 * es, nullptr, n};
+    const dim3 g2(((m + G_BM - 1) / G_BM) * ((n - n256 + G_BN - 1) / G_BN));
+    launch_out<false, false>(out_mode, g2, stream, q);
+    return uwc_launch_status("noisy_gemm (column tail)");
+  }
   GemmParams p{A, B, m, n, k, r, corrA, corrB, maxabs, lmax, key, target, wins, max_wins, a_scale, b_scale, out,
-               hash ? tile_dump : nullptr};
+               hash ? tile_dump : nullptr, n};
   const dim3 grid(((m + G_BM - 1) / G_BM) * ((n + G_BN - 1) / G_BN));
   if (hash && denoise) launch_out<true, true>(out_mode, grid, stream, p);
   else if (hash) launch_out<true, false>(out_mode, grid, stream, p);

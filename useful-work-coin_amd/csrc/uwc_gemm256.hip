@@ -72,6 +72,7 @@ struct Gemm256Params {
   const float* b_scale;
   void* out;
   u32* dump;
+  int ldc;  // output row stride in elements
 };
 
 typedef const void __attribute__((address_space(1)))* gptr_t;
@@ -495,13 +496,13 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
       // wave-uniform base per e plus one 32-bit lane offset (scalar-base addressing)
       const int row0 = bm0 + wm * 128 + mb * 32, col0 = bn0 + wn * 64 + nb * 32;
       const int lr = 4 * (lane >> 5), lc = lane & 31;
-      const u32 loff = (u32)(lr * p.n + lc) * ES;
+      const u32 loff = (u32)(lr * p.ldc + lc) * ES;
       float bsc = 0.f;
       if constexpr (OUT == OUT_BF16 || OUT == OUT_F32) bsc = p.b_scale[col0 + lc];
 #pragma unroll
       for (int e = 0; e < 16; e++) {
         const int re = row0 + 8 * (e >> 2) + (e & 3);
-        u8* base = reinterpret_cast<u8*>(p.out) + ((long)re * p.n + col0) * ES;
+        u8* base = reinterpret_cast<u8*>(p.out) + ((long)re * p.ldc + col0) * ES;
         if constexpr (OUT == OUT_I32) {
           *reinterpret_cast<i32*>(base + loff) = v[e];
         } else {
@@ -612,14 +613,15 @@ static void out256(int out_mode, dim3 grid, hipStream_t s, const Gemm256Params& 
   }
 }
 
-// Called by uwc_noisy_gemm after argument checks when m % 256 == 0 and n % 256 == 0.
+// Called by uwc_noisy_gemm after argument checks when m % 256 == 0 and n % 256 == 0; ldc is the
+// output row stride (n, or wider when this GEMM writes the first n columns of a wider output).
 int uwc_noisy_gemm256(const int8_t* A, const int8_t* B, int m, int n, int k, int r, const int8_t* corrA,
                       const int8_t* corrB, const int32_t* maxabs, int lmax, const uint32_t* key,
                       const uint32_t* target, uint32_t* wins, int max_wins, const float* a_scale, const float* b_scale,
-                      void* out, int out_mode, int flags, uint32_t* tile_dump, hipStream_t stream) {
+                      void* out, int out_mode, int flags, uint32_t* tile_dump, int ldc, hipStream_t stream) {
   const bool hash = flags & FLAG_HASH, denoise = flags & FLAG_DENOISE;
   Gemm256Params p{A, B, m, n, k, r, corrA, corrB, maxabs, lmax, key, target, wins, max_wins, a_scale, b_scale, out,
-                  hash ? tile_dump : nullptr};
+                  hash ? tile_dump : nullptr, ldc};
   const dim3 grid((m / W_BM) * (n / W_BN));
   if (hash && denoise) out256<true, true>(out_mode, grid, stream, p);
   else if (hash) out256<true, false>(out_mode, grid, stream, p);

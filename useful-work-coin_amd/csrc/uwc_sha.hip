@@ -218,6 +218,36 @@ __global__ void __launch_bounds__(256) sha_tree_kernel(const u32* __restrict__ l
   if (threadIdx.x < 8) roots[blockIdx.x * 8 + threadIdx.x] = src[threadIdx.x];
 }
 
+// One workgroup per aligned group of up to SHA_GROUP leaves of a tree: the group's bottom-up root
+// (8 pairing levels). Pairs never cross an aligned power-of-two boundary and a trailing partial
+// group is the tail of every level, so the tree of the group roots, built the same way, has the
+// same root as the whole tree.
+#define SHA_GROUP 256
+__global__ void __launch_bounds__(256) sha_group_kernel(const u32* __restrict__ leaves, int n0, int groups,
+                                                        u32* __restrict__ out) {
+  __shared__ u32 lv[SHA_GROUP * 8];
+  const int t = blockIdx.x / groups, gi = blockIdx.x % groups;
+  const int base = gi * SHA_GROUP, cnt = min(SHA_GROUP, n0 - base);
+  const u32* src = leaves + ((long)t * n0 + base) * 8;
+  for (int i = threadIdx.x; i < cnt * 8; i += blockDim.x) lv[i] = src[i];
+  __syncthreads();
+  int n = cnt;
+  while (n > 1) {
+    const int half = n >> 1;
+    u32 h[8];
+    if (threadIdx.x < half) sha_node(lv + 16 * threadIdx.x, lv + 16 * threadIdx.x + 8, h);
+    __syncthreads();
+    if (threadIdx.x < half) {
+#pragma unroll
+      for (int k = 0; k < 8; k++) lv[8 * threadIdx.x + k] = h[k];
+    }
+    if ((n & 1) && threadIdx.x < 8) lv[8 * half + threadIdx.x] = lv[8 * (n - 1) + threadIdx.x];
+    __syncthreads();
+    n = half + (n & 1);
+  }
+  if (threadIdx.x < 8) out[((long)t * groups + gi) * 8 + threadIdx.x] = lv[threadIdx.x];
+}
+
 extern "C" int uwc_sha_row_leaves(const uint32_t* rows, int64_t nrows, int row_words, uint32_t* scratch,
                                   int64_t scratch_words, uint32_t tag, uint32_t index_base, uint32_t index_mod,
                                   uint32_t* row_roots, uint32_t* leaves_out, hipStream_t stream) {
@@ -249,6 +279,16 @@ extern "C" int uwc_sha_merkle_roots(const uint32_t* leaves, int ntrees, int n, u
   if (ntrees == 0) return UWC_OK;
   const long need = 2L * ntrees * n * 8;
   if (scratch_words < need) return uwc_fail("%s: scratch has %lld words, needs %ld", fn, (long long)scratch_words, need);
+  if (n > 2 * SHA_GROUP) {  // group roots first, in parallel, into the second half of scratch
+    const int groups = (n + SHA_GROUP - 1) / SHA_GROUP;
+    u32* gr = scratch + (long)ntrees * n * 8;
+    hipLaunchKernelGGL(sha_group_kernel, dim3((unsigned)(ntrees * groups)), dim3(256), 0, stream, leaves, n, groups, gr);
+    int st = uwc_launch_status("sha_group");
+    if (st) return st;
+    hipLaunchKernelGGL(sha_tree_kernel, dim3((unsigned)ntrees), dim3(256), 0, stream, gr, groups, scratch,
+                       scratch + (long)ntrees * groups * 8, roots);
+    return uwc_launch_status(fn);
+  }
   hipLaunchKernelGGL(sha_tree_kernel, dim3((unsigned)ntrees), dim3(256), 0, stream, leaves, n, scratch,
                      scratch + (long)ntrees * n * 8, roots);
   return uwc_launch_status(fn);
