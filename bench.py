@@ -516,6 +516,28 @@ def summarize_trace(stats_csv, out_path, cmd, nonces):
     print(open(out_path).read())
 
 
+def summarize_e2e_trace(stats_csv, out_path, cmd):
+    """The kernel-trace --stats table of a `bench.py --e2e-only` run as text: per kernel
+    calls, average and share, plus per-forward totals (3 forwards: one warm-up, two timed)."""
+    import csv
+    import re
+    rows = list(csv.DictReader(open(stats_csv)))
+    with open(out_path, "w") as f:
+        f.write("rocprofv3 kernel trace, configs[4]: 28-layer Qwen3-1.7B-shaped integer forward over 8192 tokens "
+                "(bench.py --e2e-only: 3 forwards + the T=64 parity run and the CPU-baseline weight copies)\n")
+        f.write(f"command: {cmd}\n\n")
+        f.write(f"{'kernel':58s} {'calls':>6s} {'avg_us':>9s} {'ms/fwd':>8s} {'share':>6s}\n")
+        for r in rows:
+            name = re.sub(r"\(.*", "", r["Name"])[:58]
+            f.write(f"{name:58s} {int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:9.2f} "
+                    f"{float(r['TotalDurationNs']) / 3e6:8.2f} {float(r['Percentage']):5.1f}%\n")
+        f.write("\nPer forward: 28 x (rmsnorm_kernel<true> x 2, noisy_gemm256_kernel<false, false, 1> x 4 (qkv, o, gu, "
+                "down), qkv_post_kernel, attention_kernel<128>, quant_act_wave_kernel, dequant_residual x 2, "
+                "swiglu_quant, sha_* for the layer's stage-output root), then rmsnorm_quant + the lm_head GEMM "
+                "(256x256 tiles + a 128-wide column tail) + the logits' Merkle root; ms/fwd = total / 3.\n")
+    print(open(out_path).read())
+
+
 def read_traffic():
     """traffic_bytes_per_launch from the committed summary, or None."""
     try:
@@ -547,11 +569,16 @@ def main():
     ap.add_argument("--traffic-probe", action="store_true", help="the workload of the FETCH_SIZE / WRITE_SIZE passes")
     ap.add_argument("--summarize-pmc", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "CMD"),
                     help="write the traffic summary under profiles/ from two counter_collection.csv files")
+    ap.add_argument("--summarize-e2e-trace", nargs=3, metavar=("STATS_CSV", "OUT", "CMD"),
+                    help="write a configs[4] kernel-trace summary under profiles/")
     ap.add_argument("--summarize-trace", nargs=4, metavar=("STATS_CSV", "OUT", "CMD", "NONCES"),
                     help="write a kernel-trace summary under profiles/ from a kernel_stats.csv")
     args = ap.parse_args()
     if args.summarize_trace:
         summarize_trace(*args.summarize_trace)
+        return
+    if args.summarize_e2e_trace:
+        summarize_e2e_trace(*args.summarize_e2e_trace)
         return
     if args.summarize_pmc:
         summarize_pmc(*args.summarize_pmc)
