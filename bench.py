@@ -48,6 +48,33 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def mfma_ceiling(torch):
+    """Sustained int8 MFMA rate of the part (uwc_mfma_rate_probe: a register-only MFMA loop on every
+    SIMD), with constant and with random operands, in TOP/s. The random-operand rate is the
+    power-limited ceiling for a GEMM on real data."""
+    from uwc_amd import _lib
+    L = _lib.lib()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    sink = torch.empty(cus * 512, dtype=torch.int32, device="cuda")
+    iters = 20000
+    ops_per_launch = cus * 8.0 * iters * 8 * 65536
+    out = {}
+    for name, rnd in (("constant_operands", 0), ("random_operands", 1)):
+        f = lambda: L.uwc_mfma_rate_probe(iters, rnd, sink.data_ptr(), sink.numel(),  # noqa: E731
+                                          torch.cuda.current_stream().cuda_stream)
+        assert f() == 0
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(3):
+            f()
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = round(ops_per_launch * 3 / (e0.elapsed_time(e1) * 1e-3) / 1e12, 1)
+    log(f"mfma ceiling: {out}")
+    return out
+
+
 def mining(args, torch, np, ops, O):
     dev = "cuda"
     m = n = k = args.size
@@ -600,6 +627,7 @@ def main():
     if args.e2e_only:
         print(json.dumps(qwen3_e2e(args, torch, np)))
         return
+    ceiling = mfma_ceiling(torch)
     res = mining(args, torch, np, ops, O)
     parity, cpu = (None, None) if args.no_cpu else parity_and_cpu(args, res, torch, np, ops, O)
     det = None if args.no_detrt else detrt_layer(args, torch, np)
@@ -624,6 +652,7 @@ def main():
         "config": {"workload": f"cuPOW NoisyGEMM mined forward (commit + noise + hashed GEMM + exact denoise, int32 out), "
                                f"{m}x{n}x{k}, r={r}, one nonce per step, {args.steps}-nonce sweep",
                    "m": m, "n": n, "k": k, "r": r, "noise": "reference rules (E in [-32,31], +-1 pairs)"},
+        "mfma_sustained_tops": ceiling,
         "roofline": {"bound": "mfma", "achieved": round(res["kern_tops"], 2), "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
                      "frac": round(res["kern_tops"] / PEAK_INT8_TOPS, 4), "traffic": read_traffic(),
                      "kernel": "noisy_gemm256_kernel<HASH=true, DENOISE=true, OUT_I32>", "avg_us": round(res["kern_ms"] * 1e3, 2),

@@ -262,6 +262,13 @@ int uwc_sha_row_leaves(const uint32_t* rows, int64_t nrows, int row_words, uint3
 int uwc_sha_merkle_roots(const uint32_t* leaves, int ntrees, int n, uint32_t* scratch, int64_t scratch_words,
                          uint32_t* roots, hipStream_t stream);
 
+/* Measurement aid (no reference counterpart): iters x 8 v_mfma_i32_32x32x32_i8 per wave in a
+ * register-only loop, 8 waves on every CU, with constant (random_operands = 0) or seeded random
+ * operands; each MFMA is 65,536 int8 ops. Timing it gives the part's sustained int8 MFMA rate,
+ * which is lower with switching operands (power-limited clock): the practical ceiling of an int8
+ * GEMM on real data. sink: uwc CU count x 512 words. */
+int uwc_mfma_rate_probe(int iters, int random_operands, uint32_t* sink, int64_t sink_words, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

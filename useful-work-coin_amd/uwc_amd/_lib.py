@@ -50,6 +50,7 @@ SIGNATURES = {
     "uwc_sha_row_leaves": [vp, i64, i32, vp, i64, u32, u32, u32, vp, vp, vp],
     "uwc_sha_merkle_roots": [vp, i32, i32, vp, i64, vp, vp],
     "uwc_det_elementwise": [i32, vp, vp, vp, i64, vp],
+    "uwc_mfma_rate_probe": [i32, i32, vp, i64, vp],
 }
 _RESTYPE = {"uwc_last_error": ctypes.c_char_p}
 
