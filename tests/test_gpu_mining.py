@@ -351,3 +351,34 @@ def test_large_tile_plain_gemm(dev, m, n, k):
     B = rng.integers(-128, 128, size=(n, k), dtype=np.int8)
     C = ops.igemm_i32(torch.from_numpy(A).to(dev), torch.from_numpy(B).to(dev))
     assert np.array_equal(C.cpu().numpy(), O.igemm(A, B))
+
+
+def test_forward_many_pipelined_equals_forward(dev):
+    """forward_many (the commitment of nonce i + 1 beside the rest of nonce i, two workspaces, two
+    streams) gives every nonce's output and winner set exactly as a sequential forward does."""
+    ops = _ops()
+    rng = np.random.default_rng(77)
+    m, n, k, r = 256, 256, 1024, 64
+    Bt = torch.from_numpy(rng.integers(-64, 65, size=(n, k), dtype=np.int8)).to(dev)
+    job_key = rng.bytes(32)
+    target = O.bound_for_wins(m, n, 8)
+    w = ops.MinedWeight(Bt=Bt, b_scale=torch.ones(n, device=dev), r=r, max_wins=4096)
+    w.setup_block(job_key, target)
+    As = [torch.from_numpy(rng.integers(-64, 65, size=(m, k), dtype=np.int8)).to(dev) for _ in range(5)]
+    ones = torch.ones(m, device=dev)
+    ref = []
+    for A in As:
+        out = w.forward(A, ones, out_mode=ops.OUT_I32)
+        torch.cuda.synchronize()
+        ref.append((out.clone(), set(w.winners(m))))
+    wins = [torch.zeros(1 + w.max_wins * ops.WIN_WORDS, dtype=torch.int32, device=dev) for _ in As]
+    outs = w.forward_many(As, ones, out_mode=ops.OUT_I32, wins=wins)
+    torch.cuda.synchronize()
+    for i, (o, wb) in enumerate(zip(outs, wins)):
+        assert torch.equal(o, ref[i][0]), i
+        words = wb.cpu().numpy().view(np.uint32)
+        cnt = min(int(words[0]), w.max_wins)
+        recs = words[1:1 + cnt * ops.WIN_WORDS].reshape(cnt, ops.WIN_WORDS)
+        got = {(int(x[0]), int(x[1]), x[2:].astype("<u4").tobytes()) for x in recs}
+        assert got == ref[i][1], i
+    assert any(len(x[1]) for x in ref)

@@ -227,6 +227,16 @@ def igemm_i32(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None)
 
 # ------------------------------------------------------------------ one mined linear layer
 _WORKSPACE: dict = {}
+_STREAMS: dict = {}
+
+
+def _streams(device) -> tuple:
+    """The two side streams forward_many pipelines over (default priority), per device."""
+    key = str(device)
+    st = _STREAMS.get(key)
+    if st is None:
+        st = _STREAMS[key] = (torch.cuda.Stream(device=device), torch.cuda.Stream(device=device))
+    return st
 
 
 @dataclass
@@ -287,11 +297,12 @@ class MinedWeight:
         self.SBt = proj_matrix(self.PB, k, r)
         del Bt
 
-    def _buf(self, m: int):
+    def _buf(self, m: int, slot: int = 0, wins: torch.Tensor | None = None):
         """Per-call buffers. The large ones are a workspace shared by every weight with the same
-        (m, k, r): layers run one after another on one stream. Win records are per weight."""
+        (m, k, r): layers run one after another on one stream; forward_many alternates two slots.
+        Win records are per weight (or the caller's buffer)."""
         dev, k, r = self.device, self.k, self.r
-        key = (str(dev), m, k, r)
+        key = (str(dev), m, k, r, slot)
         ws = _WORKSPACE.get(key)
         if ws is None:
             ws = _WORKSPACE[key] = dict(
@@ -305,9 +316,10 @@ class MinedWeight:
                 maxabs=torch.zeros(2, dtype=torch.int32, device=dev),
                 scratch=torch.empty(max(8, b3_scratch_words(m * k)), dtype=torch.int32, device=dev),
             )
-        wins = self._bufs.get(m)
         if wins is None:
-            wins = self._bufs[m] = torch.zeros(1 + self.max_wins * WIN_WORDS, dtype=torch.int32, device=dev)
+            wins = self._bufs.get(m)
+            if wins is None:
+                wins = self._bufs[m] = torch.zeros(1 + self.max_wins * WIN_WORDS, dtype=torch.int32, device=dev)
         return {**ws, "wins": wins}
 
     def forward(self, A: torch.Tensor, a_scale: torch.Tensor, out: torch.Tensor | None = None,
@@ -315,20 +327,21 @@ class MinedWeight:
         """A: m x k int8 (values in [-64, 64]). Returns A @ Bt^T scaled (bf16/f32) or exact int32."""
         return self._forward(A, a_scale, out, out_mode, hash_tiles)
 
-    def _forward(self, A, a_scale, out, out_mode, hash_tiles, cfg=None, proj=True, dump=None):
+    def _check_a(self, A):
         m, k = A.shape
-        n, r = self.n, self.r
         _check(k == self.k and m % BM == 0, f"MinedWeight.forward: A is {tuple(A.shape)}, need m % {BM} == 0, k == {self.k}")
         _check(A.is_contiguous() and A.dtype == torch.int8, "MinedWeight.forward: A must be contiguous int8")
-        dev = A.device
-        b = self._buf(m)
-        c = consts(dev)
-        if out is None and out_mode != OUT_NONE:
-            dt = {OUT_BF16: torch.bfloat16, OUT_I32: torch.int32, OUT_F32: torch.float32}[out_mode]
-            out = torch.empty((m, n), dtype=dt, device=dev)
-        # 1. commit to A, derive a_seed = H(b_seed || bind_a(root_A, m))
-        b3_root_and_seed(A.view(-1), self.job_key, prefix=self.b_seed, salt=c["SALT_A"], dim=m,
+
+    def _commit(self, A, b):
+        """1. commit to A, derive a_seed = H(b_seed || bind_a(root_A, m)) (ops.py:322-324)."""
+        c = consts(A.device)
+        b3_root_and_seed(A.view(-1), self.job_key, prefix=self.b_seed, salt=c["SALT_A"], dim=A.shape[0],
                          seed_out=b["a_seed"], scratch=b["scratch"])
+
+    def _after_commit(self, A, b, a_scale, out, out_mode, hash_tiles, cfg=None, proj=True, dump=None):
+        m, k = A.shape
+        n, r = self.n, self.r
+        c = consts(A.device)
         # 2. A-side noise E_AL, P_A (and its selection matrix); the same launch zeroes maxabs and
         #    the win counter
         # 3. ApEA = A + EAL*P_A ; X = A * P_B^T (limbs) ; EAL copy
@@ -357,6 +370,67 @@ class MinedWeight:
              wins=b["wins"], max_wins=self.max_wins, a_scale=a_scale, b_scale=self.b_scale, out=out, out_mode=out_mode,
              cfg=cfg, dump=dump)
         return out
+
+    def _out(self, m, out, out_mode):
+        if out is None and out_mode != OUT_NONE:
+            dt = {OUT_BF16: torch.bfloat16, OUT_I32: torch.int32, OUT_F32: torch.float32}[out_mode]
+            out = torch.empty((m, self.n), dtype=dt, device=self.device)
+        return out
+
+    def _forward(self, A, a_scale, out, out_mode, hash_tiles, cfg=None, proj=True, dump=None):
+        self._check_a(A)
+        b = self._buf(A.shape[0])
+        out = self._out(A.shape[0], out, out_mode)
+        self._commit(A, b)
+        return self._after_commit(A, b, a_scale, out, out_mode, hash_tiles, cfg=cfg, proj=proj, dump=dump)
+
+    def forward_many(self, As, a_scale: torch.Tensor, outs=None, out_mode: int = OUT_BF16, hash_tiles: bool = True,
+                     wins=None):
+        """Mined forwards of a sequence of activations (the nonces of a sweep), each equal to
+        forward(As[i]) bit for bit, pipelined over two streams: the commitment of As[i + 1] (a
+        latency-bound BLAKE3 tree) runs beside the noising and projections of As[i], in a second
+        workspace. outs / wins: optional per-item output tensors and win buffers (1 + max_wins *
+        WIN_WORDS int32 each; without them every item shares the weight's win buffer and winners()
+        reports the last item). Returns the outputs; work is queued behind the current stream and the
+        current stream waits for all of it."""
+        n_items = len(As)
+        if n_items == 0:
+            return []
+        m = As[0].shape[0]
+        for A in As:
+            self._check_a(A)
+            _check(A.shape[0] == m, "MinedWeight.forward_many: every A needs the same shape")
+        outs = [self._out(m, outs[i] if outs is not None else None, out_mode) for i in range(n_items)]
+        cur = torch.cuda.current_stream(self.device)
+        sc, sm = _streams(self.device)
+        sc.wait_stream(cur)
+        sm.wait_stream(cur)
+        bufs = [self._buf(m, 0), self._buf(m, 1)]
+        committed = [torch.cuda.Event() for _ in range(2)]
+        consumed = [torch.cuda.Event() for _ in range(2)]
+
+        def commit(i):
+            b = bufs[i % 2]
+            with torch.cuda.stream(sc):
+                if i >= 2:
+                    sc.wait_event(consumed[i % 2])  # item i - 2 is done with this workspace
+                self._commit(As[i], b)
+                committed[i % 2].record(sc)
+
+        commit(0)
+        for i in range(n_items):
+            if i + 1 < n_items:
+                commit(i + 1)
+            b = dict(bufs[i % 2])
+            if wins is not None:
+                b["wins"] = wins[i]
+            with torch.cuda.stream(sm):
+                sm.wait_event(committed[i % 2])
+                self._after_commit(As[i], b, a_scale, outs[i], out_mode, hash_tiles)
+                consumed[i % 2].record(sm)
+        cur.wait_stream(sm)
+        cur.wait_stream(sc)
+        return outs
 
     def noise_mine(self, A: torch.Tensor, dump=None):
         """What a pure noise miner runs per attempt batch: commit A, noise it, hashed GEMM, no output.
