@@ -75,14 +75,14 @@ def mfma_ceiling(torch):
     return out
 
 
-def mining(args, torch, np, ops, O):
+def mining(args, torch, np, ops):
     dev = "cuda"
     m = n = k = args.size
     r = args.rank
     rng = np.random.default_rng(2026)
     Bt = torch.from_numpy(rng.integers(-64, 64, size=(n, k), dtype=np.int8)).to(dev)
     job_key = rng.bytes(32)
-    target = O.bound_for_wins(m, n, 12)
+    target = ops.bound_words(((1 << 256) - 1) * 12 // ((m // 8) * (n // 16)))  # about 12 winning 8 x 16 tiles
     w = ops.MinedWeight(Bt=Bt, b_scale=torch.ones(n, device=dev), r=r, max_wins=4096)
     w.setup_block(job_key, target)
     nA = args.steps + args.warmup
@@ -126,7 +126,7 @@ def mining(args, torch, np, ops, O):
     kern_ms = sum(s.elapsed_time(e) for s, e in ev) / len(ev)
     b = w._buf(m)
     mx = int(b["maxabs"].max().item())
-    L = O.limbs_needed(mx)
+    L = ops.limbs_for_max(mx)
     ops_main = 2.0 * m * n * k
     ops_kernel = ops_main + 2.0 * m * n * 2 * r * L
     tops = ops_main * args.steps / dt / 1e12
@@ -482,7 +482,7 @@ def traffic_probe(args, torch, ops, O, np):
     forwards at the bench shape, then a plain device copy of COPY_BYTES three times, whose
     counter readings calibrate the KiB units of both counters."""
     args.steps, args.warmup = 4, 2
-    mining(args, torch, np, ops, O)
+    mining(args, torch, np, ops)
     x = torch.empty(COPY_BYTES, dtype=torch.int8, device="cuda").fill_(1)
     y = torch.empty_like(x)
     for _ in range(3):
@@ -630,7 +630,7 @@ def main():
         print(json.dumps(qwen3_e2e(args, torch, np)))
         return
     ceiling = mfma_ceiling(torch)
-    res = mining(args, torch, np, ops, O)
+    res = mining(args, torch, np, ops)
     parity, cpu = (None, None) if args.no_cpu else parity_and_cpu(args, res, torch, np, ops, O)
     det = None if args.no_detrt else detrt_layer(args, torch, np)
     skinny = None if args.no_detrt else skinny_linears(args, torch, np)

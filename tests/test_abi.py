@@ -117,3 +117,16 @@ def test_product_does_not_import_oracle():
             if f.endswith((".py", ".hip", ".h", ".cpp")):
                 src = open(os.path.join(dirpath, f)).read()
                 assert "oracle" not in re.sub(r"#.*|//.*", "", src).lower(), f
+
+
+def test_host_limb_rule_and_bound_words_match_oracle():
+    """The host-side limb rule and difficulty-bound packing the bench uses agree with the oracle's
+    (kernels.cu:602-607, pearl_glue.py:65-66), at every limb boundary."""
+    import oracle as O
+    from uwc_amd import ops
+    for mx in (0, 63, 64, 8127, 8128, 1040319, 1040320, 1 << 30):
+        assert ops.limbs_for_max(mx) == O.limbs_needed(mx), mx
+    for m, n, w in ((4096, 4096, 12), (256, 512, 20), (128, 128, 1)):
+        want = O.bound_for_wins(m, n, w)
+        got = ops.bound_words(((1 << 256) - 1) * w // ((m // 8) * (n // 16)))
+        assert got.dtype == want.dtype and (got == want).all()

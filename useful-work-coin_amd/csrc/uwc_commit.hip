@@ -45,13 +45,16 @@ __device__ __forceinline__ QuadMsgOffsets quad_offsets(int q) {
   return t;
 }
 
-// One compression by a quad. msg: the 16-word message in LDS. (ca, cb): this lane's chaining
-// value words cv[q], cv[4+q]. Returns this lane's output words out[q] = a ^ c, out[4+q] = b ^ d.
-__device__ __forceinline__ void quad_compress(const u8* msg, const QuadMsgOffsets& off, int q, u32 ca, u32 cb,
-                                              u64 counter, u32 blen, u32 flags, u32& lo, u32& hi) {
-  u32 m[28];
+// The 28 message words lane q of a quad consumes, read from a 16-word message in LDS.
+__device__ __forceinline__ void quad_msg(const u8* msg, const QuadMsgOffsets& off, u32 m[28]) {
 #pragma unroll
   for (int j = 0; j < 28; j++) m[j] = *reinterpret_cast<const u32*>(msg + off.o[j]);
+}
+
+// One compression by a quad on message words m (quad_msg). (ca, cb): this lane's chaining
+// value words cv[q], cv[4+q]. Returns this lane's output words out[q] = a ^ c, out[4+q] = b ^ d.
+__device__ __forceinline__ void quad_compress_m(const u32 m[28], int q, u32 ca, u32 cb, u64 counter, u32 blen,
+                                                u32 flags, u32& lo, u32& hi) {
   u32 a = ca, b = cb, c = b3_iv(0), d = (u32)counter;
   // c = IV[q], d = (counter lo, counter hi, blen, flags)[q]
   if (q == 1) { c = b3_iv(1); d = (u32)(counter >> 32); }
@@ -66,6 +69,14 @@ __device__ __forceinline__ void quad_compress(const u8* msg, const QuadMsgOffset
   }
   lo = a ^ c;
   hi = b ^ d;
+}
+
+// quad_compress_m on a message in LDS.
+__device__ __forceinline__ void quad_compress(const u8* msg, const QuadMsgOffsets& off, int q, u32 ca, u32 cb,
+                                              u64 counter, u32 blen, u32 flags, u32& lo, u32& hi) {
+  u32 m[28];
+  quad_msg(msg, off, m);
+  quad_compress_m(m, q, ca, cb, counter, blen, flags, lo, hi);
 }
 
 // Level-wise pairwise reduction, by quads, of `count` chaining values in LDS (8 words each):
@@ -100,12 +111,15 @@ __device__ void quad_level_reduce(u32* cvs, int count, u32 k_lo, u32 k_hi, u32 k
 #define B3_CHUNKS_PER_WG 64
 #define B3_QSTRIDE 80  // LDS bytes per quad's message block (64 + 16 pad: fewer bank conflicts)
 
-// 64 chunks per workgroup (256 threads, one quad per chunk). Each lane fetches 16 bytes of
-// its chunk's next block from HBM while the quad compresses the current one; the block goes
-// through the quad's own LDS slot, so only wave-local ordering is needed there.
+// 64 chunks per workgroup (256 threads, one quad per chunk). A chunk is a chain of 16 dependent
+// compressions, so its loads are issued all at once up front (lane q holds bytes [16 q, 16 q + 16)
+// of every 64-byte block: 64 VGPRs) and the chain waits for HBM once, not once per block. Blocks
+// reach the quad's message words through two LDS slots per quad: block b + 1 is written and its
+// words read while block b compresses (a wave's LDS accesses complete in order, and a quad only
+// touches its own slots).
 __global__ void __launch_bounds__(256) b3_chunks_kernel(const u8* __restrict__ data, u64 nchunks,
                                                         const u32* __restrict__ key, u32* __restrict__ wg_cvs) {
-  __shared__ __attribute__((aligned(16))) u8 blk[B3_CHUNKS_PER_WG * B3_QSTRIDE];
+  __shared__ __attribute__((aligned(16))) u8 blk[2][B3_CHUNKS_PER_WG * B3_QSTRIDE];
   __shared__ u32 cvs[B3_CHUNKS_PER_WG * 8];
   const int tid = threadIdx.x, q = tid & 3, c = tid >> 2;
   const u64 base = (u64)blockIdx.x * B3_CHUNKS_PER_WG;
@@ -114,17 +128,25 @@ __global__ void __launch_bounds__(256) b3_chunks_kernel(const u8* __restrict__ d
   const u32 k_lo = key[q], k_hi = key[4 + q];
   const bool active = c < count;
   const v4i* src = reinterpret_cast<const v4i*>(data + (base + (active ? c : 0)) * 1024ull) + q;
-  u8* my = blk + c * B3_QSTRIDE;
-  v4i nxt = active ? src[0] : v4i{0, 0, 0, 0};
+  v4i d[16];
+#pragma unroll
+  for (int b = 0; b < 16; b++) d[b] = active ? src[b * 4] : v4i{0, 0, 0, 0};
+  u8* slot[2] = {blk[0] + c * B3_QSTRIDE, blk[1] + c * B3_QSTRIDE};
+  u32 m[2][28];
+  *reinterpret_cast<v4i*>(slot[0] + q * 16) = d[0];
+  __builtin_amdgcn_wave_barrier();
+  quad_msg(slot[0], off, m[0]);
   u32 lo = k_lo, hi = k_hi;
+#pragma unroll
   for (int b = 0; b < 16; b++) {
-    *reinterpret_cast<v4i*>(my + q * 16) = nxt;
-    __builtin_amdgcn_wave_barrier();
-    if (b + 1 < 16 && active) nxt = src[(b + 1) * 4];
+    if (b + 1 < 16) {
+      *reinterpret_cast<v4i*>(slot[(b + 1) & 1] + q * 16) = d[b + 1];
+      __builtin_amdgcn_wave_barrier();
+      quad_msg(slot[(b + 1) & 1], off, m[(b + 1) & 1]);
+    }
     const u32 flags = B3_KEYED | (b == 0 ? B3_CHUNK_START : 0u) | (b == 15 ? B3_CHUNK_END : 0u) |
                       ((b == 15 && nchunks == 1) ? B3_ROOT : 0u);
-    quad_compress(my, off, q, lo, hi, base + c, 64, flags, lo, hi);
-    __builtin_amdgcn_wave_barrier();
+    quad_compress_m(m[b & 1], q, lo, hi, base + c, 64, flags, lo, hi);
   }
   if (active) { cvs[c * 8 + q] = lo; cvs[c * 8 + 4 + q] = hi; }
   __syncthreads();

@@ -336,7 +336,7 @@ static void np_go(size_t smem, dim3 grid, hipStream_t stream, const int8_t* src,
                   const int8_t* E, const uint32_t* Pn, int8_t* dst, const int8_t* St, int8_t* corr, int corr_off,
                   int ecopy_off, int32_t* maxabs, int lmax) {
   auto kern = noise_project_kernel<NOISE, PROJ, NB, NPF>;
-  if (smem > 64 * 1024) hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+  if (smem > 64 * 1024) (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   hipLaunchKernelGGL(kern, grid, dim3(NP_THREADS), smem, stream, src, rows, k, r, E, Pn, dst, St, corr, corr_off,
                      ecopy_off, maxabs, lmax);
 }

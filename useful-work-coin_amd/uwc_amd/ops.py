@@ -28,6 +28,16 @@ def limbs_for(k: int) -> int:
     return L
 
 
+def limbs_for_max(mx: int) -> int:
+    """Limbs the denoise pass uses for a runtime max |projection| mx (kernels.cu:602-607)."""
+    return 1 if mx <= 63 else 2 if mx <= 8127 else 3 if mx <= 1040319 else 4
+
+
+def bound_words(bound: int) -> np.ndarray:
+    """A 256-bit difficulty bound as eight little-endian uint32 words (pearl_glue.py:65-66)."""
+    return np.array([(bound >> (32 * i)) & 0xFFFFFFFF for i in range(8)], dtype=np.uint32)
+
+
 WIN_WORDS = 10
 DUMP_WORDS = 24
 CHUNKS_PER_CTA = 64
