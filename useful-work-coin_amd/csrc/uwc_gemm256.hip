@@ -6,7 +6,12 @@
 //     128 x 64 = two consensus 64 x 64 hash blocks, as 4 x 2 v_mfma_i32_32x32x32_i8 blocks
 //     (128 int32 accumulators per lane, in VGPRs so the fold reads them directly).
 //   * Operand tiles go HBM -> LDS with global_load_lds_dwordx4 (no VGPR staging) into a ring of
-//     W_STAGES k steps (128 KiB); one barrier per k step.
+//     W_STAGES k steps (128 KiB): the ring's A tiles, then its B tiles, so that every fragment
+//     read is a per-lane base register plus an immediate offset. One barrier per k step. The
+//     main-loop DMA uses the scalar-base form: the tile window's address stays in SGPRs and each
+//     lane adds a fixed 32-bit offset, so a k step costs no vector address arithmetic. A step's
+//     refill goes out in three parts (W_DMA_SPREAD) so that the waves' MFMA issue is not stuck
+//     behind a burst of DMA instructions.
 //   * Software pipeline at k32-pass granularity: the six LDS fragments of pass p + 1 are read
 //     while the eight MFMAs of pass p run (two fragment sets in registers). The step barrier and
 //     the next DMA issue sit before the MFMAs of a step's last pass, whose fragments are already
@@ -38,11 +43,17 @@
 #define W_KP (W_BK / 32)                    // k32 MFMA passes per k step
 #define W_THREADS 512
 #define W_TILE (W_BM * W_BK)                 // bytes of one operand tile
-#define W_STAGE (2 * W_TILE)                 // A + B
-#define W_LDS (W_STAGES * W_STAGE)           // at most 160 KiB (gfx950 LDS per workgroup)
+#define W_BOFF (W_STAGES * W_TILE)           // LDS byte offset of the ring's B tiles
+#define W_LDS (2 * W_STAGES * W_TILE)        // at most 160 KiB (gfx950 LDS per workgroup)
 static_assert(W_LDS <= 160 * 1024, "LDS ring exceeds 160 KiB");
 #define W_WAVES (W_THREADS / 64)
 #define W_SEGS_PER_WAVE (W_TILE / 1024 / W_WAVES)  // 1 KiB DMA segments per wave per operand per k step
+#ifndef W_DMA_SPREAD
+// Issue a k step's refill in three parts (after the barrier, before pass 0 and before pass 1 of
+// the next step) instead of one burst: 64 DMA instructions per CU in one burst keep every wave
+// blocked on the address unit, and its MFMAs queued behind them, for ~1600 cycles
+#define W_DMA_SPREAD 1
+#endif
 #ifndef W_DB_HASH
 #define W_DB_HASH 0  // double-buffered fragments in the hashing kernels too
 #endif
@@ -117,17 +128,52 @@ __device__ __forceinline__ void dma16(const void* g, u32 lds) {
 
 __device__ __forceinline__ u32 lds_addr(const u8* p) { return (u32)(uintptr_t)(lptr_t)p; }
 
-// Issue this wave's DMA segments of one k step (segments wave * SPW .. of A and of B).
-__device__ __forceinline__ void dma_step(u8* stage, const DmaLane& d, long lda, long ldb, long k0, int wave) {
-  const u32 base = __builtin_amdgcn_readfirstlane(lds_addr(stage));
+// Issue this wave's DMA segments of one k step (segments wave * SPW .. of A and of B) into the
+// LDS tiles at byte addresses lds_a, lds_b (wave-uniform).
+__device__ __forceinline__ void dma_step(u32 lds_a, u32 lds_b, const DmaLane& d, long lda, long ldb, long k0, int wave) {
 #pragma unroll
   for (int t = 0; t < W_SEGS_PER_WAVE; t++) {
     const int s = W_SEGS_PER_WAVE * wave + t;
     const int c = d.phys ^ swz(W_RPS * s + d.rin);
     const long off = (long)W_RPS * s;
-    const u32 ls = __builtin_amdgcn_readfirstlane(base + s * 1024);
-    dma16(d.a + off * lda + k0 + c * 16, ls);
-    dma16(d.b + off * ldb + k0 + c * 16, ls + W_TILE);
+    dma16(d.a + off * lda + k0 + c * 16, __builtin_amdgcn_readfirstlane(lds_a + s * 1024));
+    dma16(d.b + off * ldb + k0 + c * 16, __builtin_amdgcn_readfirstlane(lds_b + s * 1024));
+  }
+}
+
+// dma16 with a wave-uniform 64-bit base in SGPRs plus a 32-bit lane offset.
+__device__ __forceinline__ void dma16s(u32 voff, const void* sbase, u32 lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds) : "memory", "m0");
+}
+
+// Lane byte offsets of the main loop's DMA segments within a 256-row window of a k-contiguous
+// operand with row stride k (the same for A and B): segment s = SPW wave + t, tile row
+// RPS s + i / W_CH, physical chunk i % W_CH = logical chunk (i % W_CH) ^ swz(row).
+struct DmaOff {
+  u32 v[W_SEGS_PER_WAVE];
+};
+
+__device__ __forceinline__ DmaOff dma_offsets(long k, int wave, int lane) {
+  DmaOff d;
+  const int rin = lane / W_CH, phys = lane % W_CH;
+#pragma unroll
+  for (int t = 0; t < W_SEGS_PER_WAVE; t++) {
+    const int row = W_RPS * (W_SEGS_PER_WAVE * wave + t) + rin;
+    d.v[t] = (u32)((long)row * k + ((phys ^ swz(row)) << 4));
+  }
+  return d;
+}
+
+// Segments [T0, T1) of one k step of the main loop's DMA: a_win = A + bm0 k + k0 and
+// b_win = B + bn0 k + k0 are wave-uniform (SGPRs).
+template <int T0 = 0, int T1 = W_SEGS_PER_WAVE>
+__device__ __forceinline__ void dma_step_s(u32 lds_a, u32 lds_b, const DmaOff& d, const i8* a_win, const i8* b_win,
+                                           int wave) {
+#pragma unroll
+  for (int t = T0; t < T1; t++) {
+    const u32 so = (u32)(W_SEGS_PER_WAVE * wave + t) * 1024u;
+    dma16s(d.v[t], a_win, lds_a + so);
+    dma16s(d.v[t], b_win, lds_b + so);
   }
 }
 
@@ -153,21 +199,28 @@ __device__ __forceinline__ int frag_off(int lane, int kp, int par) {
   return r * W_BK + ((c ^ swz(r + 32 * par)) << 4);
 }
 
-// Offsets of one lane's fragment reads for the k32 passes of a step, for even 32-row blocks;
-// odd blocks (row bit 5 set) read o[kp ^ 2] with 128-byte rows (swz then flips chunk bit 2)
-// and o[kp] with 64-byte rows (swz does not see row bit 5).
-struct FragOff {
-  int o[W_KP];
-  __device__ __forceinline__ int at(int kp, int par) const {
-    if constexpr (W_BK == 128) return o[par ? kp ^ 2 : kp];
-    else return o[kp];
-  }
+// One lane's LDS byte addresses of its fragment reads for the k32 passes of a step, in stage 0,
+// for the wave's first 32-row (A) and 32-column (B) block. Stage st and block j add the
+// immediate st W_TILE + 32 j W_BK. Even blocks use entry kp; odd blocks (row bit 5 set) use
+// kp ^ 2 with 128-byte rows (swz then flips chunk bit 2) and kp with 64-byte rows (swz does not
+// see row bit 5).
+struct FragBase {
+  u32 a[W_KP], b[W_KP];
 };
 
-__device__ __forceinline__ FragOff frag_offsets(int lane) {
-  FragOff f;
+__device__ __forceinline__ int par_kp(int kp, int par) {
+  if constexpr (W_BK == 128) return par ? kp ^ 2 : kp;
+  else return kp;
+}
+
+__device__ __forceinline__ FragBase frag_bases(u32 wsm_lds, int wm, int wn, int lane) {
+  FragBase f;
 #pragma unroll
-  for (int kp = 0; kp < W_KP; kp++) f.o[kp] = frag_off(lane, kp, 0);
+  for (int kp = 0; kp < W_KP; kp++) {
+    const u32 o = (u32)frag_off(lane, kp, 0);
+    f.a[kp] = wsm_lds + (u32)(wm * 128 * W_BK) + o;
+    f.b[kp] = wsm_lds + (u32)(W_BOFF + wn * 64 * W_BK) + o;
+  }
   return f;
 }
 
@@ -176,18 +229,21 @@ struct Frag {
   v4i a[4], b[2];
 };
 
-__device__ __forceinline__ v4i frag_a(const u8* stage, int wm, const FragOff& fo, int kp, int mb) {
-  return lds16(stage + (wm * 128 + mb * 32) * W_BK + fo.at(kp, mb & 1));
+typedef const v4i __attribute__((address_space(3)))* lds_v4i_t;
+__device__ __forceinline__ v4i lds_at(u32 a) { return *(lds_v4i_t)(uintptr_t)a; }
+
+__device__ __forceinline__ v4i frag_a(const FragBase& fb, int st, int kp, int mb) {
+  return lds_at(fb.a[par_kp(kp, mb & 1)] + (u32)(st * W_TILE + mb * 32 * W_BK));
 }
-__device__ __forceinline__ v4i frag_b(const u8* stage, int wn, const FragOff& fo, int kp, int nb) {
-  return lds16(stage + W_TILE + (wn * 64 + nb * 32) * W_BK + fo.at(kp, nb & 1));
+__device__ __forceinline__ v4i frag_b(const FragBase& fb, int st, int kp, int nb) {
+  return lds_at(fb.b[par_kp(kp, nb & 1)] + (u32)(st * W_TILE + nb * 32 * W_BK));
 }
 
-__device__ __forceinline__ void frag_read(Frag& f, const u8* stage, int wm, int wn, const FragOff& fo, int kp) {
+__device__ __forceinline__ void frag_read(Frag& f, const FragBase& fb, int st, int kp) {
 #pragma unroll
-  for (int nb = 0; nb < 2; nb++) f.b[nb] = frag_b(stage, wn, fo, kp, nb);
+  for (int nb = 0; nb < 2; nb++) f.b[nb] = frag_b(fb, st, kp, nb);
 #pragma unroll
-  for (int mb = 0; mb < 4; mb++) f.a[mb] = frag_a(stage, wm, fo, kp, mb);
+  for (int mb = 0; mb < 4; mb++) f.a[mb] = frag_a(fb, st, kp, mb);
 }
 
 __device__ __forceinline__ u32 xor3(u32 a, u32 b, u32 c) { return __builtin_amdgcn_bitop3_b32(a, b, c, 0x96); }
@@ -209,21 +265,20 @@ __device__ __forceinline__ void fold_block(const v16i& v, u32* x, bool first) {
 // half-0 MFMAs, a[mb] after MFMA (mb, 1), b[1] last; one fragment set stays in registers and
 // each read still has several MFMAs to land before its first use in the next pass.
 template <bool FOLD, bool READ>
-__device__ __forceinline__ void pass_mma(v16i acc[4][2], Frag& f, u32 x[8], const u8* nst, int wm, int wn,
-                                         const FragOff& fo, int nkp) {
+__device__ __forceinline__ void pass_mma(v16i acc[4][2], Frag& f, u32 x[8], const FragBase& fb, int nst, int nkp) {
 #pragma unroll
   for (int mb = 0; mb < 4; mb++) {
     if constexpr (FOLD) fold_block(acc[mb][0], x + (mb >> 1) * 4, (mb & 1) == 0);
     acc[mb][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[mb], f.b[0], acc[mb][0], 0, 0, 0);
   }
-  if constexpr (READ) f.b[0] = frag_b(nst, wn, fo, nkp, 0);
+  if constexpr (READ) f.b[0] = frag_b(fb, nst, nkp, 0);
 #pragma unroll
   for (int mb = 0; mb < 4; mb++) {
     if constexpr (FOLD) fold_block(acc[mb][1], x + (mb >> 1) * 4, false);
     acc[mb][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[mb], f.b[1], acc[mb][1], 0, 0, 0);
-    if constexpr (READ) f.a[mb] = frag_a(nst, wm, fo, nkp, mb);
+    if constexpr (READ) f.a[mb] = frag_a(fb, nst, nkp, mb);
   }
-  if constexpr (READ) f.b[1] = frag_b(nst, wn, fo, nkp, 1);
+  if constexpr (READ) f.b[1] = frag_b(fb, nst, nkp, 1);
   // pin the interleave: [fold VALU,] MFMA ... with the reads after the MFMAs that free them
 #pragma unroll
   for (int i = 0; i < 4; i++) {
@@ -244,9 +299,9 @@ __device__ __forceinline__ void pass_mma(v16i acc[4][2], Frag& f, u32 x[8], cons
 // before the MFMAs on cur, so they have the whole pass to land. Costs a second fragment set
 // (24 VGPRs); used where registers allow.
 template <bool FOLD, bool READ>
-__device__ __forceinline__ void pass_mma_db(v16i acc[4][2], const Frag& cur, Frag& nxt, u32 x[8], const u8* nst,
-                                            int wm, int wn, const FragOff& fo, int nkp) {
-  if constexpr (READ) frag_read(nxt, nst, wm, wn, fo, nkp);
+__device__ __forceinline__ void pass_mma_db(v16i acc[4][2], const Frag& cur, Frag& nxt, u32 x[8], const FragBase& fb,
+                                            int nst, int nkp) {
+  if constexpr (READ) frag_read(nxt, fb, nst, nkp);
 #pragma unroll
   for (int mb = 0; mb < 4; mb++)
 #pragma unroll
@@ -265,16 +320,15 @@ __device__ __forceinline__ void pass_mma_db(v16i acc[4][2], const Frag& cur, Fra
 // Denoise k step for one quarter of the wave's block: M blocks 2h, 2h+1 of column half nb.
 // The fragments of two passes are requested before their MFMAs, so each MFMA waits only for
 // its own reads and the second pass's reads overlap the first pass's MFMAs.
-__device__ __forceinline__ void step_mma_quarter(v16i tmp[2], const u8* stage, int wm, int wn, int h, int nb,
-                                                 const FragOff& fo) {
+__device__ __forceinline__ void step_mma_quarter(v16i tmp[2], const FragBase& fb, int st, int h, int nb) {
 #pragma unroll
   for (int k2 = 0; k2 < W_KP; k2 += 2) {
     v4i a0[2], a1[2], b[2];
 #pragma unroll
     for (int j = 0; j < 2; j++) {
-      b[j] = frag_b(stage, wn, fo, k2 + j, nb);
-      a0[j] = frag_a(stage, wm, fo, k2 + j, 2 * h);
-      a1[j] = frag_a(stage, wm, fo, k2 + j, 2 * h + 1);
+      b[j] = frag_b(fb, st, k2 + j, nb);
+      a0[j] = frag_a(fb, st, k2 + j, 2 * h);
+      a1[j] = frag_a(fb, st, k2 + j, 2 * h + 1);
     }
 #pragma unroll
     for (int j = 0; j < 2; j++) {
@@ -362,7 +416,9 @@ __device__ __forceinline__ void static_for(F&& f) {
 template <bool HASH, bool DENOISE, int OUT>
 __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params p) {
   extern __shared__ __attribute__((aligned(1024))) u8 wsm[];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave >> 2, wn = wave & 3;
+  // the wave index is uniform: readfirstlane keeps everything derived from it scalar
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 2, wn = wave & 3;
   int bm0, bn0;
   tile256(p.m, p.n, bm0, bn0);
   const long k = p.k;
@@ -374,46 +430,74 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
 #pragma unroll
     for (int j = 0; j < 2; j++) acc[i][j] = v16i{};
 
-  const FragOff fo = frag_offsets(lane);
-  const DmaLane dl = dma_lane(p.A, k, p.B, k, bm0, bn0, lane);
+  const u32 wsm_l = __builtin_amdgcn_readfirstlane(lds_addr(wsm));
+  auto lds_a = [&](int st) { return wsm_l + (u32)(st * W_TILE); };           // stage st's A tile
+  auto lds_b = [&](int st) { return wsm_l + (u32)(W_BOFF + st * W_TILE); };  // and its B tile
+  const FragBase fbase = frag_bases(wsm_l, wm, wn, lane);
+  const DmaOff doff = dma_offsets(k, wave, lane);
+  const i8* a_win = p.A + (long)bm0 * k;  // + k0: this workgroup's operand windows
+  const i8* b_win = p.B + (long)bn0 * k;
   // prologue: every stage of the ring loading, then step 0 resident and its first pass read
 #pragma unroll
   for (int s = 0; s < W_STAGES; s++)
-    if (s < KT) dma_step(wsm + s * W_STAGE, dl, k, k, (long)s * W_BK, wave);
+    if (s < KT) dma_step_s(lds_a(s), lds_b(s), doff, a_win + s * W_BK, b_win + s * W_BK, wave);
   wait_step(min(KT - 1, W_STAGES - 1));
   // fragment sets: single set streamed (pass_mma) or two alternating sets (pass_mma_db)
   constexpr bool DB = !HASH || W_DB_HASH;
   Frag fb[DB ? 2 : 1];
-  frag_read(fb[0], wsm, wm, wn, fo, 0);
+  frag_read(fb[0], fbase, 0, 0);
 
   // One k step. Pass kp runs its MFMAs on the fragments in `cur` while reading those of pass
   // kp + 1. Before the last pass the wave waits for step kt + 1 (vmcnt + barrier: every wave is
   // then done reading step kt's stage) and refills that stage with step kt + W_STAGES; the last
   // pass reads the next step's first fragments (on the final step that read of a resident stage
   // is unused, which keeps the MFMA code free of branches). Bit kp of FM: pass kp first folds
-  // the chunk that ended with the previous pass into m0 (kp == 0) or m1 (kp > 0).
-  auto step = [&](auto fm, int kt, u32& m0, u32& m1) {
-    constexpr int FM = decltype(fm)::value;
-    const u8* st = wsm + (kt % W_STAGES) * W_STAGE;
+  // the chunk that ended with the previous pass into m0 (kp == 0) or m1 (kp > 0). The stage
+  // index ST == kt % W_STAGES is a compile-time constant, so every LDS address of the step is a
+  // base register plus an immediate.
+  auto step = [&](auto fm, auto stc, int kt, u32& m0, u32& m1) {
+    constexpr int FM = decltype(fm)::value, ST = decltype(stc)::value;
     static_for<W_KP>([&](auto kpc) {
       constexpr int kp = decltype(kpc)::value;
       constexpr bool fold = ((FM >> kp) & 1) != 0;
       u32 x[8];
-      const u8* nst = st;
-      int nkp = kp + 1;
+      constexpr int nst = kp + 1 == W_KP ? (ST + 1) % W_STAGES : ST;
+      constexpr int nkp = kp + 1 == W_KP ? 0 : kp + 1;
+#if W_DMA_SPREAD
+      // the refill of the previous step's stage, continued: segment 2 before pass 0, segment 3
+      // before pass 1 (the first half went out after the previous step's barrier)
+      if constexpr (kp < 2 && W_SEGS_PER_WAVE == 4) {
+        if (kt >= 1 && kt - 1 + W_STAGES < KT) {
+          constexpr int PST = (ST + W_STAGES - 1) % W_STAGES;
+          const long k0 = (long)(kt - 1 + W_STAGES) * W_BK;
+          dma_step_s<2 + kp, 3 + kp>(lds_a(PST), lds_b(PST), doff, a_win + k0, b_win + k0, wave);
+        }
+      }
+#endif
       if constexpr (kp + 1 == W_KP) {
         if (kt + 1 < KT) {
           asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this stage's reads are complete
           wait_step(min(KT - 2 - kt, W_STAGES - 2));
-          if (kt + W_STAGES < KT)
-            dma_step(wsm + (kt % W_STAGES) * W_STAGE, dl, k, k, (long)(kt + W_STAGES) * W_BK, wave);
+          if (kt + W_STAGES < KT) {
+            const long k0 = (long)(kt + W_STAGES) * W_BK;
+#if W_DMA_SPREAD
+            if constexpr (W_SEGS_PER_WAVE == 4)
+              dma_step_s<0, 2>(lds_a(ST), lds_b(ST), doff, a_win + k0, b_win + k0, wave);
+            else
+#endif
+            dma_step_s(lds_a(ST), lds_b(ST), doff, a_win + k0, b_win + k0, wave);
+          }
         }
-        nst = wsm + ((kt + 1) % W_STAGES) * W_STAGE;
-        nkp = 0;
       }
-      if constexpr (DB) pass_mma_db<fold, true>(acc, fb[kp & 1], fb[(kp + 1) & 1], x, nst, wm, wn, fo, nkp);
-      else pass_mma<fold, true>(acc, fb[0], x, nst, wm, wn, fo, nkp);
+      if constexpr (DB) pass_mma_db<fold, true>(acc, fb[kp & 1], fb[(kp + 1) & 1], x, fbase, nst, nkp);
+      else pass_mma<fold, true>(acc, fb[0], x, fbase, nst, nkp);
       if constexpr (fold) fold_into(kp == 0 ? m0 : m1, x, lane);
+    });
+  };
+  // step() for a k step whose stage is known only at run time
+  auto step_rt = [&](auto fm, int kt, u32& m0, u32& m1) {
+    static_for<W_STAGES>([&](auto stc) {
+      if (kt % W_STAGES == decltype(stc)::value) step(fm, stc, kt, m0, m1);
     });
   };
   using NoFold = std::integral_constant<int, 0>;
@@ -428,24 +512,40 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
     // The fold of chunk c runs in the first pass of chunk c + 1 (slot (c - 1) mod 16 for the
     // chunk starting at slot c). For chunk 0 that folds the all-zero accumulators into the
     // all-zero slot 15, which leaves it zero.
-    if (p.r >= W_BK) {
+    if (p.r == W_BK) {
+      // one k step per chunk: an outer iteration is 16 k steps, so k step c0 + s sits in stage
+      // s % W_STAGES
+      static_assert(16 % W_STAGES == 0, "stage of an unrolled k step");
+      for (int c0 = 0; c0 < nchunks; c0 += 16) {
+        static_for<16>([&](auto sc) {
+          constexpr int s = decltype(sc)::value;
+          if (c0 + s < nchunks)
+            step(std::integral_constant<int, 1>{}, std::integral_constant<int, s % W_STAGES>{}, c0 + s,
+                 msg[(s + 15) & 15], unused);
+        });
+      }
+    } else if (p.r > W_BK) {
       const int tpc = p.r / W_BK;
       for (int c0 = 0; c0 < nchunks; c0 += 16) {
 #pragma unroll
         for (int s = 0; s < 16; s++) {
           if (c0 + s < nchunks) {
-            step(std::integral_constant<int, 1>{}, kt++, msg[(s + 15) & 15], unused);
-            for (int i = 1; i < tpc; i++) step(NoFold{}, kt++, unused, unused);
+            step_rt(std::integral_constant<int, 1>{}, kt++, msg[(s + 15) & 15], unused);
+            for (int i = 1; i < tpc; i++) step_rt(NoFold{}, kt++, unused, unused);
           }
         }
       }
     } else if constexpr (W_KP == 4) {
-      // r = 64 = W_BK / 2: k step j holds chunks 2j (passes 0, 1) and 2j + 1 (passes 2, 3)
+      // r = 64 = W_BK / 2: k step j holds chunks 2j (passes 0, 1) and 2j + 1 (passes 2, 3); an
+      // outer iteration is 8 k steps, so k step c0 / 2 + s / 2 sits in stage (s / 2) % W_STAGES
+      static_assert(8 % W_STAGES == 0, "stage of an unrolled k step");
       for (int c0 = 0; c0 < nchunks; c0 += 16) {
-#pragma unroll
-        for (int s = 0; s < 16; s += 2) {
-          if (c0 + s < nchunks) step(std::integral_constant<int, 0b0101>{}, kt++, msg[(s + 15) & 15], msg[s]);
-        }
+        static_for<8>([&](auto jc) {
+          constexpr int j = decltype(jc)::value, s = 2 * j;
+          if (c0 + s < nchunks)
+            step(std::integral_constant<int, 0b0101>{}, std::integral_constant<int, j % W_STAGES>{}, c0 / 2 + j,
+                 msg[(s + 15) & 15], msg[s]);
+        });
       }
     }
     {  // the last chunk
@@ -484,7 +584,10 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
     }
   } else {
     u32 unused = 0;
-    for (int kt = 0; kt < KT; kt++) step(NoFold{}, kt, unused, unused);
+    int kt = 0;
+    for (; kt + W_STAGES <= KT; kt += W_STAGES)
+      static_for<W_STAGES>([&](auto stc) { step(NoFold{}, stc, kt + decltype(stc)::value, unused, unused); });
+    for (; kt < KT; kt++) step_rt(NoFold{}, kt, unused, unused);
   }
 
   // epilogue of one 32 x 32 MFMA block: lane holds col (lane & 31) of rows
@@ -535,7 +638,7 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
     int ig = 0, li = L - 1, kc = 0;
     auto cissue = [&]() {
       const DmaLane cl = dma_lane(p.corrA + (long)li * p.m * R2, R2, p.corrB + (long)li * p.n * R2, R2, bm0, bn0, lane);
-      dma_step(wsm + (ig % W_STAGES) * W_STAGE, cl, R2, R2, (long)kc * W_BK, wave);
+      dma_step(lds_a(ig % W_STAGES), lds_b(ig % W_STAGES), cl, R2, R2, (long)kc * W_BK, wave);
       ig++;
       if (++kc == CPL) {
         kc = 0;
@@ -556,7 +659,7 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
             tmp[1] = tmp[1] << 7;
           }
           if (++c == CPL) c = 0;
-          step_mma_quarter(tmp, wsm + t * W_STAGE, wm, wn, h, nb, fo);
+          step_mma_quarter(tmp, fbase, t, h, nb);
         }
         store_block(2 * h, nb, acc[2 * h][nb] - tmp[0]);
         store_block(2 * h + 1, nb, acc[2 * h + 1][nb] - tmp[1]);
@@ -579,7 +682,7 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
           tmp[1] = tmp[1] << 7;
         }
         if (++c == CPL) c = 0;
-        step_mma_quarter(tmp, wsm + (g % W_STAGES) * W_STAGE, wm, wn, h, nb, fo);
+        step_mma_quarter(tmp, fbase, g % W_STAGES, h, nb);
       }
       store_block(2 * h, nb, acc[2 * h][nb] - tmp[0]);
       store_block(2 * h + 1, nb, acc[2 * h + 1][nb] - tmp[1]);
