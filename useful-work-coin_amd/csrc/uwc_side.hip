@@ -7,9 +7,12 @@
 // with S^T given as the r x k selection matrix St[j][l] = [P0[l] == j] - [P1[l] == j], and the
 // A-side noise EAL[:, P0] - EAL[:, P1] = (SpA EAL^T)^T with SpA = S_A as k rows of 64 bytes.
 //
-// Workgroup = 32 rows of the A side or of the B side over the full k, 8 wave64s. k goes in
-// chunks of 256 columns through an LDS ring (global_load_lds, 1 KiB contiguous segments): the
-// chunk's 32 source rows, its r rows of St and (A side) its 256 rows of SpA. Wave w computes
+// Workgroup = 32 rows of the A side or of the B side over the full k: 8 compute wave64s and
+// SP_PROD producer wave64s. k goes in chunks of 256 columns through an LDS ring (global_load_lds,
+// 1 KiB contiguous segments): the chunk's 32 source rows, its r rows of St and (A side) its 256
+// rows of SpA. Only the producer waves issue these loads: a chunk is 24-40 DMA instructions per
+// CU, which keep the issuing waves blocked on the texture address unit for ~1000 cycles, and in
+// the compute waves that would hold up the chunk's MFMAs behind them. Compute wave w computes
 // the 16-row tile w & 1 on the 64-column step w >> 1 of every chunk, so each byte crosses the
 // texture address unit once per workgroup (per-wave fragment loads from global memory made
 // that unit the bottleneck). Everything runs on v_mfma_i32_16x16x64_i8: the projection
@@ -25,8 +28,9 @@
 #include "uwc_common.h"
 
 #define SP_ROWS 32
-#define SP_THREADS 512
-#define SP_WAVES (SP_THREADS / 64)
+#define SP_WAVES 8                       // compute waves
+#define SP_PROD 4                        // producer (DMA) waves
+#define SP_THREADS (64 * (SP_WAVES + SP_PROD))
 #define SP_MAXR 64
 #define SP_CH 256  // columns per chunk
 
@@ -53,9 +57,8 @@ __device__ __forceinline__ void side_dma16(const void* g, u32 lds) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
 }
 
-// Wait until at most `younger` chunks (SPW DMA instructions each) of this wave are still in
-// flight, then barrier. Loads retire in issue order; stores issued after those DMAs can only
-// make this wait longer.
+// A producer wave's wait until at most `younger` chunks (SPW DMA instructions each) of its own
+// are still in flight (loads retire in issue order).
 template <int SPW>
 __device__ __forceinline__ void side_wait(int younger) {
   static_assert(3 * SPW < 64, "vmcnt is 6 bits");
@@ -63,7 +66,6 @@ __device__ __forceinline__ void side_wait(int younger) {
   else if (younger == 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * SPW) : "memory");
   else if (younger == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(SPW) : "memory");
   else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
 }
 
 template <int NB, bool ASIDE>
@@ -74,7 +76,7 @@ struct SideGeom {
   static constexpr int SPT = ASIDE ? SP_CH * 64 : 0;  // SpA rows of a chunk
   static constexpr int STAGE = SRC + STB + SPT;
   static constexpr int NSEG = STAGE / 1024;     // 1 KiB DMA segments per chunk
-  static constexpr int SPW = (NSEG + SP_WAVES - 1) / SP_WAVES;  // per wave (the last repeats)
+  static constexpr int SPW = (NSEG + SP_PROD - 1) / SP_PROD;  // per producer wave (the last repeats)
   static constexpr int NS = ASIDE ? 3 : 5;      // ring stages (NS - 1 chunks in flight)
   static constexpr int LDS = NS * STAGE;
 };
@@ -90,15 +92,17 @@ __device__ __forceinline__ u32 add_bytes(u32 a, u32 c) {
 }
 
 // The chunk loop of one side: projections into acc (C layout of the 16x16x64 MFMA); on the A
-// side also the noised source bytes into dst.
+// side also the noised source bytes into dst. Producer waves (wave >= SP_WAVES) only load; one
+// barrier per chunk: before it the producers wait for chunk c, after it they refill the stage
+// every compute wave finished with (chunk c - 1's) while the compute waves work on chunk c.
 template <int NB, bool ASIDE>
 __device__ __forceinline__ void side_chunks(v4i acc[NB], u8* ring, const i8* src, const i8* St, const i8* SpA,
                                             const i8* EA, i8* dst, int row0, int k, int wave, int lane) {
   using G = SideGeom<NB, ASIDE>;
   const int NC = k / SP_CH;
   const u32 ring_base = __builtin_amdgcn_readfirstlane((u32)(uintptr_t)(side_lptr_t)ring);
-  // DMA of chunk c into stage c % NS: segment g (wave w issues g = t * 8 + w, the last segment
-  // repeating to keep the count per wave uniform) holds 4 rows of 256 bytes (source rows, then
+  // DMA of chunk c into stage c % NS: segment g (producer pw issues g = t * SP_PROD + pw, the
+  // last segment repeating to keep the count per wave uniform) holds 4 rows of 256 bytes (source rows, then
   // St rows) or 16 SpA rows of 64 bytes. 256-byte rows: lane i -> row 4 g' + (i >> 4), physical
   // chunk i & 15 = logical chunk (i & 15) ^ (row & 15). SpA rows: lane i -> row 16 g'' + (i >> 2),
   // physical chunk i & 3 = logical chunk (i & 3) ^ (g'' & 3).
@@ -107,7 +111,7 @@ __device__ __forceinline__ void side_chunks(v4i acc[NB], u8* ring, const i8* src
     const int col0 = c * SP_CH;
 #pragma unroll
     for (int t = 0; t < G::SPW; t++) {
-      const int g = min(t * SP_WAVES + wave, G::NSEG - 1);
+      const int g = min(t * SP_PROD + (wave - SP_WAVES), G::NSEG - 1);
       const u32 lds = __builtin_amdgcn_readfirstlane(stage + (u32)g * 1024u);
       const void* gp;
       if (g < (G::SRC + G::STB) / 1024) {
@@ -123,6 +127,20 @@ __device__ __forceinline__ void side_chunks(v4i acc[NB], u8* ring, const i8* src
     }
   };
 
+  const bool prod = wave >= SP_WAVES;
+  if (prod) {
+#pragma unroll
+    for (int c = 0; c < G::NS - 1; c++)
+      if (c < NC) issue(c);
+    for (int c = 0; c < NC; c++) {
+      // chunk c has landed once every producer has waited for its own DMAs and the barrier
+      // passed; every compute wave is then also done with chunk c - 1, whose stage is refilled
+      side_wait<G::SPW>(min(NC - 1 - c, G::NS - 2));
+      __builtin_amdgcn_s_barrier();
+      if (c + G::NS - 1 < NC) issue(c + G::NS - 1);
+    }
+    return;
+  }
   const int rt = wave & 1, si = wave >> 1, rr = lane & 15, q = lane >> 4;
   const int lrow = rt * 16 + rr;
   const int phys = ((si * 4 + q) ^ rr) << 4;  // fragment byte offset in a 256-byte row
@@ -131,14 +149,8 @@ __device__ __forceinline__ void side_chunks(v4i acc[NB], u8* ring, const i8* src
     if (16 * q < G::r) ef = *reinterpret_cast<const v4i*>(EA + (u64)(row0 + lrow) * G::r + 16 * q);
   i8* drow = ASIDE ? dst + (u64)(row0 + lrow) * k + si * 64 + q * 16 : nullptr;
 
-#pragma unroll
-  for (int c = 0; c < G::NS - 1; c++)
-    if (c < NC) issue(c);
   for (int c = 0; c < NC; c++) {
-    // chunk c has landed (each wave waited for its own DMAs, then the barrier), and every wave
-    // is done with chunk c - 1, whose stage the next issue refills
-    side_wait<G::SPW>(min(NC - 1 - c, G::NS - 2));
-    if (c + G::NS - 1 < NC) issue(c + G::NS - 1);
+    __builtin_amdgcn_s_barrier();
     const u8* st = ring + (c % G::NS) * G::STAGE;
     const v4i a = *reinterpret_cast<const v4i*>(st + lrow * SP_CH + phys);
 #pragma unroll
@@ -170,7 +182,7 @@ __global__ void __launch_bounds__(SP_THREADS) side_kernel(SideParams p) {
   extern __shared__ __attribute__((aligned(1024))) u8 ring[];
   __shared__ __attribute__((aligned(16))) i8 Es[SP_ROWS * SP_MAXR];
   __shared__ i32 Xs[SP_ROWS * SP_MAXR];
-  __shared__ int wmax[SP_WAVES];
+  __shared__ int wmax[SP_WAVES + SP_PROD];
   constexpr int r = NB * 16;
   // the wave index is uniform: readfirstlane keeps everything derived from it scalar
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -192,10 +204,11 @@ __global__ void __launch_bounds__(SP_THREADS) side_kernel(SideParams p) {
 
   // C layout of the 16x16x64 MFMA: lane holds rows 4 (lane >> 4) + e, column lane & 15
   const int rt = wave & 1, rr = lane & 15, q = lane >> 4;
+  if (wave < SP_WAVES)
 #pragma unroll
-  for (int b = 0; b < NB; b++)
+    for (int b = 0; b < NB; b++)
 #pragma unroll
-    for (int e = 0; e < 4; e++) atomicAdd(&Xs[(rt * 16 + 4 * q + e) * r + b * 16 + rr], acc[b][e]);
+      for (int e = 0; e < 4; e++) atomicAdd(&Xs[(rt * 16 + 4 * q + e) * r + b * 16 + rr], acc[b][e]);
   __syncthreads();
 
   // limbs (+ the EAL copy on the A side) and the workgroup max
@@ -226,7 +239,7 @@ __global__ void __launch_bounds__(SP_THREADS) side_kernel(SideParams p) {
     if (tid == 0) {
       int mx = 0;
 #pragma unroll
-      for (int w = 0; w < SP_WAVES; w++) mx = max(mx, wmax[w]);
+      for (int w = 0; w < SP_WAVES + SP_PROD; w++) mx = max(mx, wmax[w]);
       atomicMax(p.maxabs + (aside ? 0 : 1), mx);
     }
   }
