@@ -538,10 +538,11 @@ def summarize_trace(stats_csv, out_path, cmd, nonces):
             name = re.sub(r"\(.*", "", r["Name"])[:58]
             f.write(f"{name:58s} {int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:9.2f} {float(r['MinNs']) / 1e3:9.2f} "
                     f"{float(r['MaxNs']) / 1e3:9.2f} {float(r['Percentage']):5.1f}%\n")
-        f.write("\nPer nonce: b3_chunks + b3_reduce (commitment of A), nonce_noise (E_A, P_A, selection matrices),\n"
-                "side_kernel (noised A, both projections in limbs), noisy_gemm256_kernel<true, true, 1> (hashed GEMM,\n"
-                "exact denoise, int32 out). at::native random kernels = the bench's setup of its distinct A inputs,\n"
-                "outside the timed region; the rest = setup_block and the warm-up.\n")
+        f.write("\nPer nonce: b3_chunks + b3_reduce (commitment of A, on a second stream beside the previous nonce's\n"
+                "work), nonce_noise (E_A, P_A, selection matrices), side_kernel (noised A, both projections in limbs),\n"
+                "noisy_gemm256_kernel<true, true, 1> (hashed GEMM, exact denoise, int32 out). at::native random\n"
+                "kernels = the bench's setup of its distinct A inputs, outside the timed region; mfma_rate_kernel =\n"
+                "the sustained MFMA-rate probe run before the sweep; the rest = setup_block and the warm-up.\n")
     print(open(out_path).read())
 
 
