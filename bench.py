@@ -97,34 +97,40 @@ def mining(args, torch, np, ops):
     torch.cuda.synchronize()
     log(f"mining: {m}x{n}x{k} r={r}, {nbuf} distinct A resident, warmup {args.warmup}, steps {args.steps}")
 
-    # the per-nonce path, with HIP events around the noisy GEMM launch on its stream
-    orig_gemm = ops.gemm
-    ev = []
-
-    def timed_gemm(*a, **kw):
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record()
-        orig_gemm(*a, **kw)
-        e.record()
-        ev.append((s, e))
-
-    # the sweep runs through MinedWeight.forward_many: the commitment of nonce i + 1 overlaps the
-    # noising, projections and hashed GEMM of nonce i (two workspaces, two streams)
-    w.forward_many([As[i % nbuf] for i in range(args.warmup)], ones, outs=[out] * args.warmup, out_mode=ops.OUT_I32)
+    # the sweep runs through MinedWeight.forward_many: one batched commitment and one noise launch
+    # per group of nonces, then each nonce's projections and hashed GEMM
+    w.forward_many([As[i % nbuf] for i in range(args.warmup)], ones, outs=[out] * args.warmup, out_mode=ops.OUT_I32,
+                   group=args.group)
     torch.cuda.synchronize()
-    ops.gemm = timed_gemm
+    sweep = [As[(args.warmup + i) % nbuf] for i in range(args.steps)]
+    t0 = time.perf_counter()
+    w.forward_many(sweep, ones, outs=[out] * args.steps, out_mode=ops.OUT_I32, group=args.group)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+
+    # the noisy GEMM alone: HIP events on its stream around back-to-back launches of the sweep's
+    # last GEMM call (same operands, corrections, seed and target). No events sit inside the sweep:
+    # recording one costs the host ~0.2 ms, more than a nonce's GPU time.
+    orig_gemm = ops.gemm
+    calls = []
+    ops.gemm = lambda *a, **kw: (calls.append((a, kw)), orig_gemm(*a, **kw))[1]
     try:
-        sweep = [As[(args.warmup + i) % nbuf] for i in range(args.steps)]
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        w.forward_many(sweep, ones, outs=[out] * args.steps, out_mode=ops.OUT_I32)
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
+        w.forward_many(sweep[-1:], ones, outs=[out], out_mode=ops.OUT_I32)
     finally:
         ops.gemm = orig_gemm
+    a, kw = calls[-1]
+    reps = gemm_reps(args.steps)
+    for _ in range(2):
+        orig_gemm(*a, **kw)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        orig_gemm(*a, **kw)
+    e1.record()
+    torch.cuda.synchronize()
     dt = t1 - t0
-    kern_ms = sum(s.elapsed_time(e) for s, e in ev) / len(ev)
-    b = w._buf(m)
+    kern_ms = e0.elapsed_time(e1) / reps
+    b = w._buf(m, slot=1)  # forward_many's first slot: an item of the last group
     mx = int(b["maxabs"].max().item())
     L = ops.limbs_for_max(mx)
     ops_main = 2.0 * m * n * k
@@ -525,24 +531,43 @@ def summarize_pmc(fetch_csv, write_csv, cmd):
     print(open(TRAFFIC_FILE).read())
 
 
-def summarize_trace(stats_csv, out_path, cmd, nonces):
-    """A kernel-trace --stats table (per kernel: calls, average, share) as text, per nonce."""
+def gemm_reps(steps: int) -> int:
+    """Back-to-back launches of the noisy GEMM that time it after the sweep."""
+    return max(8, min(steps, 64))
+
+
+def summarize_trace(trace_csv, out_path, cmd, steps, warmup):
+    """A kernel trace (run_kernel_trace.csv) of `bench.py --no-cpu --no-detrt --no-e2e --steps S
+    --warmup W` as text: per kernel of the timed sweep (from the end of the warm-up's last GEMM to
+    the end of the sweep's last GEMM) calls, average and time per nonce, and the average of the
+    back-to-back GEMM launches that give the bench's roofline figure."""
     import csv
     import re
-    rows = list(csv.DictReader(open(stats_csv)))
+    steps, warmup = int(steps), int(warmup)
+    rows = sorted(csv.DictReader(open(trace_csv)), key=lambda r: int(r["Start_Timestamp"]))
+    name = lambda r: re.sub(r"\(.*", "", r["Kernel_Name"])  # noqa: E731
+    dur = lambda r: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3  # noqa: E731
+    g = [i for i, r in enumerate(rows) if "noisy_gemm256_kernel<true, true, 1>" in r["Kernel_Name"]]
+    t0, t1 = int(rows[g[warmup - 1]]["End_Timestamp"]), int(rows[g[warmup + steps - 1]]["End_Timestamp"])
+    per = {}
+    for r in rows:
+        if t0 < int(r["Start_Timestamp"]) and int(r["End_Timestamp"]) <= t1:
+            per.setdefault(name(r), []).append(dur(r))
+    b2b = [dur(rows[i]) for i in g[warmup + steps + 3:warmup + steps + 3 + gemm_reps(steps)]]
     with open(out_path, "w") as f:
-        f.write(f"rocprofv3 kernel trace, mined forward 4096x4096x4096 r=64 (bench.py workload), {nonces} timed nonces\n")
+        f.write(f"rocprofv3 kernel trace, mined forward 4096x4096x4096 r=64 (bench.py workload), sweep of {steps} "
+                f"nonces after {warmup} warm-up nonces\n")
         f.write(f"command: {cmd}\n\n")
-        f.write(f"{'kernel':58s} {'calls':>6s} {'avg_us':>9s} {'min_us':>9s} {'max_us':>9s} {'share':>6s}\n")
-        for r in rows:
-            name = re.sub(r"\(.*", "", r["Name"])[:58]
-            f.write(f"{name:58s} {int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:9.2f} {float(r['MinNs']) / 1e3:9.2f} "
-                    f"{float(r['MaxNs']) / 1e3:9.2f} {float(r['Percentage']):5.1f}%\n")
-        f.write("\nPer nonce: b3_chunks + b3_reduce (commitment of A, on a second stream beside the previous nonce's\n"
-                "work), nonce_noise (E_A, P_A, selection matrices), side_kernel (noised A, both projections in limbs),\n"
-                "noisy_gemm256_kernel<true, true, 1> (hashed GEMM, exact denoise, int32 out). at::native random\n"
-                "kernels = the bench's setup of its distinct A inputs, outside the timed region; mfma_rate_kernel =\n"
-                "the sustained MFMA-rate probe run before the sweep; the rest = setup_block and the warm-up.\n")
+        f.write(f"timed sweep: {(t1 - t0) / 1e3 / steps:.2f} us per nonce (kernel trace clock)\n")
+        f.write(f"{'kernel':58s} {'calls':>6s} {'avg_us':>9s} {'min_us':>9s} {'max_us':>9s} {'us/nonce':>9s}\n")
+        for k_, xs in sorted(per.items(), key=lambda kv: -sum(kv[1])):
+            f.write(f"{k_[:58]:58s} {len(xs):6d} {sum(xs) / len(xs):9.2f} {min(xs):9.2f} {max(xs):9.2f} "
+                    f"{sum(xs) / steps:9.2f}\n")
+        f.write(f"\nback-to-back noisy_gemm256_kernel<true, true, 1> (the bench's roofline figure): {len(b2b)} calls, "
+                f"avg {sum(b2b) / len(b2b):.2f} us, min {min(b2b):.2f}, max {max(b2b):.2f}\n")
+        f.write("\nPer group of 8 nonces: b3_chunks + b3_reduce (one batched commitment of the group's A), one\n"
+                "nonce_noise (E_A, P_A, selection matrices of all 8); per nonce: side_kernel (noised A, both\n"
+                "projections in limbs), noisy_gemm256_kernel<true, true, 1> (hashed GEMM, exact denoise, int32 out).\n")
     print(open(out_path).read())
 
 
@@ -587,6 +612,7 @@ def main():
     ap.add_argument("--size", type=int, default=4096)
     ap.add_argument("--rank", type=int, default=64)
     ap.add_argument("--distinct", type=int, default=64, help="distinct resident A matrices cycled over")
+    ap.add_argument("--group", type=int, default=8, help="nonces per batched commitment / noise launch")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--cpu-max-nonces", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true")
@@ -601,8 +627,8 @@ def main():
                     help="write the traffic summary under profiles/ from two counter_collection.csv files")
     ap.add_argument("--summarize-e2e-trace", nargs=3, metavar=("STATS_CSV", "OUT", "CMD"),
                     help="write a configs[4] kernel-trace summary under profiles/")
-    ap.add_argument("--summarize-trace", nargs=4, metavar=("STATS_CSV", "OUT", "CMD", "NONCES"),
-                    help="write a kernel-trace summary under profiles/ from a kernel_stats.csv")
+    ap.add_argument("--summarize-trace", nargs=5, metavar=("TRACE_CSV", "OUT", "CMD", "STEPS", "WARMUP"),
+                    help="write a kernel-trace summary under profiles/ from a run_kernel_trace.csv")
     args = ap.parse_args()
     if args.summarize_trace:
         summarize_trace(*args.summarize_trace)

@@ -86,6 +86,18 @@ int uwc_b3_root_and_seed(const uint8_t* data, uint64_t nbytes, const uint32_t* k
                          const uint32_t* salt, uint32_t dim, uint32_t* root_out, uint32_t* seed_out,
                          uint32_t* scratch, uint64_t scratch_words, hipStream_t stream);
 
+/* uwc_b3_root_and_seed over `count` (1..16) inputs of nbytes each, in one set of launches:
+ * data, root_out and seed_out are HOST arrays of `count` device pointers (root_out / seed_out
+ * may be NULL arrays; their entries may not be NULL). Item i uses scratch words
+ * [i * s, (i + 1) * s) with s = uwc_b3_scratch_words(nbytes). Results equal `count` separate
+ * calls. The reference commits one operand per call (ops.py:99-118 from MinedWeight._forward,
+ * ops.py:322-324); this form serves a sweep of nonces whose activations are all known up front,
+ * where one commitment alone leaves the latency-bound chunk chains at one wave per SIMD. */
+int uwc_b3_root_and_seed_many(const uint8_t* const* data, int count, uint64_t nbytes, const uint32_t* key,
+                              const uint32_t* prefix, const uint32_t* salt, uint32_t dim, uint32_t* const* root_out,
+                              uint32_t* const* seed_out, uint32_t* scratch, uint64_t scratch_words,
+                              hipStream_t stream);
+
 /* out (nblocks x 32 int8) = (bytes of keyed_BLAKE3(key, msg(index, label)) & 63) - 32; also
  * zeroes zero_me[0..zero_n) (may be NULL with zero_n = 0).
  * Replaces ops.noise_uniform: ops.py:122-125, kernels.cu:259-282. */
@@ -105,6 +117,14 @@ int uwc_noise_perm(uint32_t* out, uint32_t k, uint32_t r, const uint32_t* label,
  * (ops.py:328-336). */
 int uwc_nonce_noise(int8_t* E, int rows, int r, uint32_t* P, int k, int8_t* St, int8_t* SpT, const uint32_t* label,
                     const uint32_t* key, int32_t* zero0, int n0, int32_t* zero1, int n1, hipStream_t stream);
+
+/* uwc_nonce_noise for `count` (1..16) nonces in one launch: E, P, St, SpT, key, zero0, zero1 are
+ * HOST arrays of `count` device pointers (St, SpT, zero0, zero1 may be NULL arrays; entries of a
+ * given array may not be NULL). Same label for every item. Results equal `count` separate calls.
+ * Batches the per-nonce noise of ops.py:328-336 over a sweep of nonces. */
+int uwc_nonce_noise_many(int count, int8_t* const* E, int rows, int r, uint32_t* const* P, int k, int8_t* const* St,
+                         int8_t* const* SpT, const uint32_t* label, const uint32_t* const* key, int32_t* const* zero0,
+                         int n0, int32_t* const* zero1, int n1, hipStream_t stream);
 
 /* For rows (multiple of 8) x k (multiple of 4) int8 src, each part optional (NULL = skip):
  *   dst = int8(src + E[row][Pn.first] - E[row][Pn.second]);

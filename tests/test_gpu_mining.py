@@ -48,6 +48,59 @@ def test_seed_derivation_matches_oracle(dev):
     assert ops.words_to_bytes(as_) == a_seed
 
 
+@pytest.mark.parametrize("count,nchunks", [(1, 65), (3, 1), (5, 130), (16, 64), (4, 4097), (2, 65537)])
+def test_batched_commitment_matches_oracle(dev, count, nchunks):
+    """b3_root_and_seed_many: every item's root and salted seed equal the oracle's (and the
+    single-input entry point's), whatever the batch size and tree shape."""
+    ops = _ops()
+    rng = np.random.default_rng(count * 1000 + nchunks)
+    datas = [rng.integers(0, 256, size=nchunks * 1024, dtype=np.uint8) for _ in range(count)]
+    key, prefix = rng.bytes(32), rng.bytes(32)
+    salt = ops.SALT_A.to(dev)
+    roots = [torch.zeros(8, dtype=torch.int32, device=dev) for _ in range(count)]
+    seeds = [torch.zeros(8, dtype=torch.int32, device=dev) for _ in range(count)]
+    ops.b3_root_and_seed_many([torch.from_numpy(d).to(dev) for d in datas], ops.words(key), prefix=ops.words(prefix),
+                              salt=salt, dim=nchunks, root_outs=roots, seed_outs=seeds)
+    for d, root, seed in zip(datas, roots, seeds):
+        want = O.b3(d.tobytes(), key)
+        assert ops.words_to_bytes(root) == want
+        one = torch.zeros(8, dtype=torch.int32, device=dev)
+        ops.b3_root_and_seed(torch.from_numpy(d).to(dev), ops.words(key), prefix=ops.words(prefix), salt=salt,
+                             dim=nchunks, seed_out=one)
+        assert ops.words_to_bytes(seed) == ops.words_to_bytes(one)
+    # the seed itself against the oracle's derivation: BLAKE3(prefix || keyed(salt, root || dim || 0^28))
+    assert ops.words_to_bytes(seeds[-1]) == O.b3(prefix + O.bind_root(want, nchunks, O.SEED_SALT_A))
+
+
+@pytest.mark.parametrize("count,rows,k,r", [(4, 256, 4096, 64), (3, 128, 1000, 128), (16, 32, 8, 64)])
+def test_batched_nonce_noise_matches_single(dev, count, rows, k, r):
+    """nonce_noise_many: item i equals nonce_noise with key i (E, P, St, SpT, zeroed counters)."""
+    ops = _ops()
+    rng = np.random.default_rng(count + rows + k + r)
+    keys = [ops.words(rng.bytes(32)) for _ in range(count)]
+    lab = ops.LABEL_A.to(dev)
+
+    def bufs():
+        return dict(E=torch.empty((rows, r), dtype=torch.int8, device=dev), P=torch.empty(k, dtype=torch.int32, device=dev),
+                    St=torch.full((r, k), 5, dtype=torch.int8, device=dev),
+                    SpT=torch.full((k, 64), 5, dtype=torch.int8, device=dev) if r <= 64 else None,
+                    z0=torch.full((2,), 9, dtype=torch.int32, device=dev),
+                    z1=torch.full((3,), 9, dtype=torch.int32, device=dev))
+    many = [bufs() for _ in range(count)]
+    ops.nonce_noise_many([b["E"] for b in many], [b["P"] for b in many], k, r, lab, keys, Sts=[b["St"] for b in many],
+                         zero0s=[b["z0"] for b in many], zero1s=[b["z1"][:1] for b in many],
+                         SpTs=[b["SpT"] for b in many] if r <= 64 else None)
+    for key, b in zip(keys, many):
+        one = bufs()
+        ops.nonce_noise(one["E"], one["P"], k, r, lab, key, St=one["St"], zero0=one["z0"], zero1=one["z1"][:1],
+                        SpT=one["SpT"])
+        for name in ("E", "P", "St", "SpT", "z0", "z1"):
+            if one[name] is not None:
+                assert torch.equal(b[name], one[name]), name
+        assert b["z0"].cpu().tolist() == [0, 0] and b["z1"].cpu().tolist() == [0, 9, 9]
+    assert np.array_equal(many[0]["E"].cpu().numpy(), O.uniform_matrix(O.SEED_LABEL_A, ops.words_to_bytes(keys[0]), rows, r))
+
+
 @pytest.mark.parametrize("r", [64, 128])
 def test_noise_generation_matches_oracle(dev, r):
     ops = _ops()
@@ -353,18 +406,20 @@ def test_large_tile_plain_gemm(dev, m, n, k):
     assert np.array_equal(C.cpu().numpy(), O.igemm(A, B))
 
 
-def test_forward_many_pipelined_equals_forward(dev):
-    """forward_many (the commitment of nonce i + 1 beside the rest of nonce i, two workspaces, two
-    streams) gives every nonce's output and winner set exactly as a sequential forward does."""
+@pytest.mark.parametrize("group,n_items", [(8, 5), (2, 5), (1, 3), (16, 17)])
+def test_forward_many_grouped_equals_forward(dev, group, n_items):
+    """forward_many (batched commitments and noise per group of nonces, then each nonce's
+    projections and hashed GEMM) gives every nonce's output and winner set exactly as a
+    sequential forward does; without per-item win buffers winners() reports the last item."""
     ops = _ops()
-    rng = np.random.default_rng(77)
+    rng = np.random.default_rng(77 + group)
     m, n, k, r = 256, 256, 1024, 64
     Bt = torch.from_numpy(rng.integers(-64, 65, size=(n, k), dtype=np.int8)).to(dev)
     job_key = rng.bytes(32)
     target = O.bound_for_wins(m, n, 8)
     w = ops.MinedWeight(Bt=Bt, b_scale=torch.ones(n, device=dev), r=r, max_wins=4096)
     w.setup_block(job_key, target)
-    As = [torch.from_numpy(rng.integers(-64, 65, size=(m, k), dtype=np.int8)).to(dev) for _ in range(5)]
+    As = [torch.from_numpy(rng.integers(-64, 65, size=(m, k), dtype=np.int8)).to(dev) for _ in range(n_items)]
     ones = torch.ones(m, device=dev)
     ref = []
     for A in As:
@@ -372,7 +427,7 @@ def test_forward_many_pipelined_equals_forward(dev):
         torch.cuda.synchronize()
         ref.append((out.clone(), set(w.winners(m))))
     wins = [torch.zeros(1 + w.max_wins * ops.WIN_WORDS, dtype=torch.int32, device=dev) for _ in As]
-    outs = w.forward_many(As, ones, out_mode=ops.OUT_I32, wins=wins)
+    outs = w.forward_many(As, ones, out_mode=ops.OUT_I32, wins=wins, group=group)
     torch.cuda.synchronize()
     for i, (o, wb) in enumerate(zip(outs, wins)):
         assert torch.equal(o, ref[i][0]), i
@@ -382,3 +437,7 @@ def test_forward_many_pipelined_equals_forward(dev):
         got = {(int(x[0]), int(x[1]), x[2:].astype("<u4").tobytes()) for x in recs}
         assert got == ref[i][1], i
     assert any(len(x[1]) for x in ref)
+    outs = w.forward_many(As, ones, out_mode=ops.OUT_I32, group=group)
+    torch.cuda.synchronize()
+    assert all(torch.equal(o, x[0]) for o, x in zip(outs, ref))
+    assert set(w.winners(m)) == ref[-1][1]

@@ -117,10 +117,25 @@ __device__ void quad_level_reduce(u32* cvs, int count, u32 k_lo, u32 k_hi, u32 k
 // reach the quad's message words through two LDS slots per quad: block b + 1 is written and its
 // words read while block b compresses (a wave's LDS accesses complete in order, and a quad only
 // touches its own slots).
-__global__ void __launch_bounds__(256) b3_chunks_kernel(const u8* __restrict__ data, u64 nchunks,
-                                                        const u32* __restrict__ key, u32* __restrict__ wg_cvs) {
+// Inputs of a batch of equal-size commitments (blockIdx.y = item): one launch commits several
+// operands at once, which gives a latency-bound chain kernel several waves per SIMD to switch
+// between.
+#define B3_MAXB 16
+struct B3In {
+  const u8* data[B3_MAXB];
+};
+struct B3Out {
+  u32* root[B3_MAXB];
+  u32* seed[B3_MAXB];
+};
+
+// Item blockIdx.y hashes bt.data[item] into wg_cvs + item * stride (stride in words).
+__global__ void __launch_bounds__(256) b3_chunks_kernel(B3In bt, u64 nchunks, const u32* __restrict__ key,
+                                                        u32* __restrict__ wg_cvs, u64 stride) {
   __shared__ __attribute__((aligned(16))) u8 blk[2][B3_CHUNKS_PER_WG * B3_QSTRIDE];
   __shared__ u32 cvs[B3_CHUNKS_PER_WG * 8];
+  const u8* __restrict__ data = bt.data[blockIdx.y];
+  wg_cvs += blockIdx.y * stride;
   const int tid = threadIdx.x, q = tid & 3, c = tid >> 2;
   const u64 base = (u64)blockIdx.x * B3_CHUNKS_PER_WG;
   const int count = (int)min((u64)B3_CHUNKS_PER_WG, nchunks - base);
@@ -159,12 +174,17 @@ __global__ void __launch_bounds__(256) b3_chunks_kernel(const u8* __restrict__ d
 // group (final), the last merge carries ROOT and the salted seed may follow:
 //   seed = BLAKE3(prefix || keyed_BLAKE3(salt, root || dim_le32 || 0^28))
 // (Pearl's v3 derivation: b_seed with prefix = job_key, a_seed with prefix = b_seed).
+// Item blockIdx.y of a batch reads in_cvs + item * stride and writes out_cvs + item * stride (or,
+// in the final launch, outs.root[item] and outs.seed[item], either may be NULL).
 __global__ void __launch_bounds__(256) b3_reduce_kernel(const u32* __restrict__ in_cvs, int count,
                                                         const u32* __restrict__ key, u32* __restrict__ out_cvs,
-                                                        int final_level, const u32* __restrict__ prefix,
-                                                        const u32* __restrict__ salt, u32 dim,
-                                                        u32* __restrict__ root_out, u32* __restrict__ seed_out) {
+                                                        u64 stride, int final_level, const u32* __restrict__ prefix,
+                                                        const u32* __restrict__ salt, u32 dim, B3Out outs) {
   __shared__ __attribute__((aligned(16))) u32 cvs[B3_GROUP * 8];
+  in_cvs += blockIdx.y * stride;
+  if (out_cvs) out_cvs += blockIdx.y * stride;
+  u32* __restrict__ root_out = outs.root[blockIdx.y];
+  u32* __restrict__ seed_out = outs.seed[blockIdx.y];
   const int tid = threadIdx.x, q = tid & 3;
   const int base = blockIdx.x * B3_GROUP, cnt = min(B3_GROUP, count - base);
   for (int i = tid; i < cnt * 8; i += blockDim.x) cvs[i] = in_cvs[(u64)base * 8 + i];
@@ -241,35 +261,79 @@ extern "C" int uwc_b3_scratch_words(uint64_t nbytes) {
   return words > 0x7fffffff ? -1 : (int)words;
 }
 
-extern "C" int uwc_b3_root_and_seed(const uint8_t* data, uint64_t nbytes, const uint32_t* key, const uint32_t* prefix,
-                                    const uint32_t* salt, uint32_t dim, uint32_t* root_out, uint32_t* seed_out,
-                                    uint32_t* scratch, uint64_t scratch_words, hipStream_t stream) {
-  if (!data || !key || !scratch) return uwc_fail("uwc_b3_root_and_seed: null data, key or scratch");
-  if (nbytes == 0 || nbytes % 1024) return uwc_fail("uwc_b3_root_and_seed: nbytes=%llu must be a positive multiple of 1024",
-                                                    (unsigned long long)nbytes);
-  if (((uintptr_t)data & 15u) != 0) return uwc_fail("uwc_b3_root_and_seed: data must be 16-byte aligned");
-  if (seed_out && (!prefix || !salt)) return uwc_fail("uwc_b3_root_and_seed: a seed needs prefix and salt");
-  const int need = uwc_b3_scratch_words(nbytes);
-  if (need < 0 || scratch_words < (u64)need)
-    return uwc_fail("uwc_b3_root_and_seed: scratch has %llu words, needs %d", (unsigned long long)scratch_words, need);
+// Commitments (and seeds) of `count` equal-size inputs; item i uses scratch words
+// [i * stride, (i + 1) * stride).
+static int b3_launch(const B3In& in, int count, u64 nbytes, const u32* key, const u32* prefix, const u32* salt, u32 dim,
+                     const B3Out& outs, u32* scratch, u64 stride, hipStream_t stream) {
   const u64 nch = nbytes / 1024;
   int cnt = (int)((nch + B3_CHUNKS_PER_WG - 1) / B3_CHUNKS_PER_WG);
-  hipLaunchKernelGGL(b3_chunks_kernel, dim3(cnt), dim3(256), 0, stream, data, nch, key, scratch);
+  hipLaunchKernelGGL(b3_chunks_kernel, dim3(cnt, count), dim3(256), 0, stream, in, nch, key, scratch, stride);
   int st = uwc_launch_status("b3_chunks");
   if (st) return st;
   u32* cur = scratch;
   while (cnt > B3_GROUP) {
     const int groups = (cnt + B3_GROUP - 1) / B3_GROUP;
     u32* nxt = cur + (u64)cnt * 8;
-    hipLaunchKernelGGL(b3_reduce_kernel, dim3(groups), dim3(256), 0, stream, cur, cnt, key, nxt, 0, nullptr, nullptr,
-                       0u, nullptr, nullptr);
+    hipLaunchKernelGGL(b3_reduce_kernel, dim3(groups, count), dim3(256), 0, stream, cur, cnt, key, nxt, stride, 0,
+                       nullptr, nullptr, 0u, B3Out{});
     if ((st = uwc_launch_status("b3_reduce"))) return st;
     cur = nxt;
     cnt = groups;
   }
-  hipLaunchKernelGGL(b3_reduce_kernel, dim3(1), dim3(256), 0, stream, cur, cnt, key, nullptr, 1, prefix, salt, dim,
-                     root_out, seed_out);
+  hipLaunchKernelGGL(b3_reduce_kernel, dim3(1, count), dim3(256), 0, stream, cur, cnt, key, nullptr, stride, 1, prefix,
+                     salt, dim, outs);
   return uwc_launch_status("b3_reduce_final");
+}
+
+static int b3_check(u64 nbytes, const u32* key, const u32* prefix, const u32* salt, bool seeds, const char* fn) {
+  if (!key) return uwc_fail("%s: null key", fn);
+  if (nbytes == 0 || nbytes % 1024)
+    return uwc_fail("%s: nbytes=%llu must be a positive multiple of 1024", fn, (unsigned long long)nbytes);
+  if (seeds && (!prefix || !salt)) return uwc_fail("%s: a seed needs prefix and salt", fn);
+  if (uwc_b3_scratch_words(nbytes) < 0) return uwc_fail("%s: input too large", fn);
+  return 0;
+}
+
+extern "C" int uwc_b3_root_and_seed(const uint8_t* data, uint64_t nbytes, const uint32_t* key, const uint32_t* prefix,
+                                    const uint32_t* salt, uint32_t dim, uint32_t* root_out, uint32_t* seed_out,
+                                    uint32_t* scratch, uint64_t scratch_words, hipStream_t stream) {
+  if (!data || !scratch) return uwc_fail("uwc_b3_root_and_seed: null data or scratch");
+  if (int st = b3_check(nbytes, key, prefix, salt, seed_out != nullptr, "uwc_b3_root_and_seed")) return st;
+  if (((uintptr_t)data & 15u) != 0) return uwc_fail("uwc_b3_root_and_seed: data must be 16-byte aligned");
+  const int need = uwc_b3_scratch_words(nbytes);
+  if (scratch_words < (u64)need)
+    return uwc_fail("uwc_b3_root_and_seed: scratch has %llu words, needs %d", (unsigned long long)scratch_words, need);
+  B3In in{};
+  B3Out outs{};
+  in.data[0] = data;
+  outs.root[0] = root_out;
+  outs.seed[0] = seed_out;
+  return b3_launch(in, 1, nbytes, key, prefix, salt, dim, outs, scratch, (u64)need, stream);
+}
+
+extern "C" int uwc_b3_root_and_seed_many(const uint8_t* const* data, int count, uint64_t nbytes, const uint32_t* key,
+                                         const uint32_t* prefix, const uint32_t* salt, uint32_t dim,
+                                         uint32_t* const* root_out, uint32_t* const* seed_out, uint32_t* scratch,
+                                         uint64_t scratch_words, hipStream_t stream) {
+  if (!data || !scratch) return uwc_fail("uwc_b3_root_and_seed_many: null data array or scratch");
+  if (count < 1 || count > B3_MAXB) return uwc_fail("uwc_b3_root_and_seed_many: count=%d must be 1..%d", count, B3_MAXB);
+  if (int st = b3_check(nbytes, key, prefix, salt, seed_out != nullptr, "uwc_b3_root_and_seed_many")) return st;
+  const int need = uwc_b3_scratch_words(nbytes);
+  if (scratch_words < (u64)need * count)
+    return uwc_fail("uwc_b3_root_and_seed_many: scratch has %llu words, needs %llu", (unsigned long long)scratch_words,
+                    (unsigned long long)need * count);
+  B3In in{};
+  B3Out outs{};
+  for (int i = 0; i < count; i++) {
+    if (!data[i] || ((uintptr_t)data[i] & 15u))
+      return uwc_fail("uwc_b3_root_and_seed_many: data[%d] is null or not 16-byte aligned", i);
+    if ((root_out && !root_out[i]) || (seed_out && !seed_out[i]))
+      return uwc_fail("uwc_b3_root_and_seed_many: root_out[%d] / seed_out[%d] is null", i, i);
+    in.data[i] = data[i];
+    outs.root[i] = root_out ? root_out[i] : nullptr;
+    outs.seed[i] = seed_out ? seed_out[i] : nullptr;
+  }
+  return b3_launch(in, count, nbytes, key, prefix, salt, dim, outs, scratch, (u64)need, stream);
 }
 
 // ------------------------------------------------------------------ per-nonce noise in one launch
@@ -288,13 +352,30 @@ __device__ __forceinline__ void pair_of(u32 u, u32 r, u32& first, u32& second) {
   second = first ^ (1u + __umulhi(r - 1, u));
 }
 
-__global__ void __launch_bounds__(256) nonce_noise_kernel(i8* __restrict__ E, u32 eblocks, u32 nE, u32* __restrict__ P,
-                                                          u32 k, u32 r, i8* __restrict__ St, i8* __restrict__ SpT,
-                                                          const u32* __restrict__ label,
-                                                          const u32* __restrict__ key, i32* __restrict__ z0, int n0,
-                                                          i32* __restrict__ z1, int n1) {
+// Per-item outputs of a batch of nonces (blockIdx.y = item); St, SpT, z0, z1 entries are all NULL
+// or all set.
+struct NNBatch {
+  i8* E[B3_MAXB];
+  u32* P[B3_MAXB];
+  i8* St[B3_MAXB];
+  i8* SpT[B3_MAXB];
+  const u32* key[B3_MAXB];
+  i32* z0[B3_MAXB];
+  i32* z1[B3_MAXB];
+};
+
+__global__ void __launch_bounds__(256) nonce_noise_kernel(NNBatch nb, u32 eblocks, u32 nE, u32 k, u32 r,
+                                                          const u32* __restrict__ label, int n0, int n1) {
   __shared__ __attribute__((aligned(16))) u8 msgs[64 * B3_QSTRIDE];
   extern __shared__ __attribute__((aligned(16))) u8 nn_blk[];  // per P wave: St [r][128], SpT [128][64]
+  const int item = blockIdx.y;
+  i8* __restrict__ E = nb.E[item];
+  u32* __restrict__ P = nb.P[item];
+  i8* __restrict__ St = nb.St[item];
+  i8* __restrict__ SpT = nb.SpT[item];
+  const u32* __restrict__ key = nb.key[item];
+  i32* __restrict__ z0 = nb.z0[item];
+  i32* __restrict__ z1 = nb.z1[item];
   const int tid = threadIdx.x, q = tid & 3, lq = tid >> 2, lane = tid & 63, wave = tid >> 6;
   if (blockIdx.x == 0) {
     if (z0 && tid < n0) z0[tid] = 0;
@@ -383,27 +464,65 @@ __global__ void __launch_bounds__(256) nonce_noise_kernel(i8* __restrict__ E, u3
     }
 }
 
-extern "C" int uwc_nonce_noise(int8_t* E, int rows, int r, uint32_t* P, int k, int8_t* St, int8_t* SpT,
-                               const uint32_t* label, const uint32_t* key, int32_t* zero0, int n0, int32_t* zero1, int n1,
-                               hipStream_t stream) {
-  if (!E || !P || !label || !key || rows < 0 || k < 0) return uwc_fail("uwc_nonce_noise: null or negative arguments");
-  if (SpT && (r > 64 || ((uintptr_t)SpT & 15u))) return uwc_fail("uwc_nonce_noise: SpT needs r <= 64 and 16-byte alignment");
-  if (r < 2 || r > 65536 || (r & (r - 1))) return uwc_fail("uwc_nonce_noise: r=%d must be a power of two", r);
-  if (((u64)rows * r) % 32) return uwc_fail("uwc_nonce_noise: rows * r must be a multiple of 32");
-  if (((uintptr_t)E & 3u)) return uwc_fail("uwc_nonce_noise: E must be 4-byte aligned");
-  if (n0 < 0 || n1 < 0 || n0 > 256 || n1 > 256 || (n0 && !zero0) || (n1 && !zero1))
-    return uwc_fail("uwc_nonce_noise: zero ranges must be 0..256 words with pointers");
+static int nn_launch(const NNBatch& nb, int count, int rows, int r, int k, bool st, bool spt, const uint32_t* label,
+                     int n0, int n1, hipStream_t stream, const char* fn) {
+  if (!label || rows < 0 || k < 0) return uwc_fail("%s: null label or negative sizes", fn);
+  if (spt && r > 64) return uwc_fail("%s: SpT needs r <= 64", fn);
+  if (r < 2 || r > 65536 || (r & (r - 1))) return uwc_fail("%s: r=%d must be a power of two", fn, r);
+  if (((u64)rows * r) % 32) return uwc_fail("%s: rows * r must be a multiple of 32", fn);
+  if (n0 < 0 || n1 < 0 || n0 > 256 || n1 > 256) return uwc_fail("%s: zero ranges must be 0..256 words", fn);
+  for (int i = 0; i < count; i++) {
+    if (!nb.E[i] || !nb.P[i] || !nb.key[i]) return uwc_fail("%s: item %d has a null E, P or key", fn, i);
+    if ((uintptr_t)nb.E[i] & 3u) return uwc_fail("%s: E must be 4-byte aligned", fn);
+    if (spt && (!nb.SpT[i] || ((uintptr_t)nb.SpT[i] & 15u)))
+      return uwc_fail("%s: SpT[%d] is null or not 16-byte aligned", fn, i);
+    if (st && !nb.St[i]) return uwc_fail("%s: St[%d] is null", fn, i);
+    if ((n0 && !nb.z0[i]) || (n1 && !nb.z1[i])) return uwc_fail("%s: zero range of item %d without a pointer", fn, i);
+  }
   const u64 eblocks = (u64)rows * r / 32, nE = (eblocks + 63) / 64, nP = (((u64)k + 7) / 8 + 63) / 64;
   const u64 blocks = nE + nP > 0 ? nE + nP : 1;
-  if (blocks > 0x7fffffff) return uwc_fail("uwc_nonce_noise: too large");
-  const size_t smem = r <= 128 ? (size_t)4 * ((St ? (size_t)r * NN_COLS : 0) + (SpT ? NN_COLS * 64 : 0)) : 0;
+  if (blocks > 0x7fffffff) return uwc_fail("%s: too large", fn);
+  const size_t smem = r <= 128 ? (size_t)4 * ((st ? (size_t)r * NN_COLS : 0) + (spt ? NN_COLS * 64 : 0)) : 0;
   static bool attr = false;  // one attribute call (96 KiB at r = 128 with SpT absent, 64 KiB + 32 KiB max)
   if (!attr) {
     (void)hipFuncSetAttribute((const void*)nonce_noise_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                               4 * (128 * NN_COLS + NN_COLS * 64));
     attr = true;
   }
-  hipLaunchKernelGGL(nonce_noise_kernel, dim3((unsigned)blocks), dim3(256), smem, stream, E, (u32)eblocks, (u32)nE, P,
-                     (u32)k, (u32)r, St, SpT, label, key, zero0, n0, zero1, n1);
+  hipLaunchKernelGGL(nonce_noise_kernel, dim3((unsigned)blocks, count), dim3(256), smem, stream, nb, (u32)eblocks,
+                     (u32)nE, (u32)k, (u32)r, label, n0, n1);
   return uwc_launch_status("nonce_noise");
+}
+
+extern "C" int uwc_nonce_noise(int8_t* E, int rows, int r, uint32_t* P, int k, int8_t* St, int8_t* SpT,
+                               const uint32_t* label, const uint32_t* key, int32_t* zero0, int n0, int32_t* zero1, int n1,
+                               hipStream_t stream) {
+  NNBatch nb{};
+  nb.E[0] = E;
+  nb.P[0] = P;
+  nb.St[0] = St;
+  nb.SpT[0] = SpT;
+  nb.key[0] = key;
+  nb.z0[0] = zero0;
+  nb.z1[0] = zero1;
+  return nn_launch(nb, 1, rows, r, k, St != nullptr, SpT != nullptr, label, n0, n1, stream, "uwc_nonce_noise");
+}
+
+extern "C" int uwc_nonce_noise_many(int count, int8_t* const* E, int rows, int r, uint32_t* const* P, int k,
+                                    int8_t* const* St, int8_t* const* SpT, const uint32_t* label,
+                                    const uint32_t* const* key, int32_t* const* zero0, int n0, int32_t* const* zero1,
+                                    int n1, hipStream_t stream) {
+  if (!E || !P || !key) return uwc_fail("uwc_nonce_noise_many: null E, P or key array");
+  if (count < 1 || count > B3_MAXB) return uwc_fail("uwc_nonce_noise_many: count=%d must be 1..%d", count, B3_MAXB);
+  NNBatch nb{};
+  for (int i = 0; i < count; i++) {
+    nb.E[i] = E[i];
+    nb.P[i] = P[i];
+    nb.St[i] = St ? St[i] : nullptr;
+    nb.SpT[i] = SpT ? SpT[i] : nullptr;
+    nb.key[i] = key[i];
+    nb.z0[i] = zero0 ? zero0[i] : nullptr;
+    nb.z1[i] = zero1 ? zero1[i] : nullptr;
+  }
+  return nn_launch(nb, count, rows, r, k, St != nullptr, SpT != nullptr, label, n0, n1, stream, "uwc_nonce_noise_many");
 }

@@ -27,10 +27,12 @@ SIGNATURES = {
     "uwc_igemm_dequant_f32": [vp, vp, i32, i32, i32, vp, vp, vp, vp],
     "uwc_b3_scratch_words": [u64],
     "uwc_b3_root_and_seed": [vp, u64, vp, vp, vp, u32, vp, vp, vp, u64, vp],
+    "uwc_b3_root_and_seed_many": [vp, i32, u64, vp, vp, vp, u32, vp, vp, vp, u64, vp],
     "uwc_noise_uniform": [vp, u32, vp, vp, vp, i32, vp],
     "uwc_noise_perm": [vp, u32, u32, vp, vp, vp],
     "uwc_noise_rows": [vp, i32, i32, i32, vp, vp, vp, vp, vp, i32, i32, vp, i32, vp],
     "uwc_nonce_noise": [vp, i32, i32, vp, i32, vp, vp, vp, vp, vp, i32, vp, i32, vp],
+    "uwc_nonce_noise_many": [i32, vp, i32, i32, vp, i32, vp, vp, vp, vp, vp, i32, vp, i32, vp],
     "uwc_proj_matrix": [vp, i32, i32, vp, vp],
     "uwc_project": [vp, i32, i32, i32, vp, vp, i32, vp, i32, vp],
     "uwc_noise_project": [vp, i32, i32, i32, vp, vp, vp, vp, vp, i32, i32, vp, i32, vp],

@@ -9,6 +9,7 @@ gemm() can also dump every tile's message and digest (`dump`). OUT_F32 is an ext
 """
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -115,6 +116,43 @@ def b3_root_and_seed(data: torch.Tensor, key: torch.Tensor, *, prefix=None, salt
     return scratch
 
 
+def _ptrs(ts) -> "ctypes.Array | None":
+    """A host array of device pointers (None stays None: the C-ABI's absent array)."""
+    if ts is None:
+        return None
+    return (ctypes.c_void_p * len(ts))(*[t.data_ptr() for t in ts])
+
+
+MAX_BATCH = 16  # items per batched commitment / noise launch (the C-ABI's limit)
+
+
+def b3_root_and_seed_many(datas, key: torch.Tensor, *, prefix=None, salt=None, dim: int = 0, root_outs=None,
+                          seed_outs=None, scratch=None):
+    """b3_root_and_seed of several equal-size inputs in one set of launches; item i's result equals
+    b3_root_and_seed(datas[i], ...). Returns the scratch buffer (item i uses words
+    [i * s, (i + 1) * s), s = b3_scratch_words(nbytes))."""
+    count = len(datas)
+    _check(1 <= count <= MAX_BATCH, f"b3_root_and_seed_many: {count} inputs, need 1..{MAX_BATCH}")
+    nbytes = datas[0].numel() * datas[0].element_size()
+    _check(nbytes % 1024 == 0 and nbytes > 0, f"b3_root_and_seed_many: {nbytes} bytes is not a positive multiple of 1024")
+    for d in datas:
+        _check(d.is_contiguous() and d.numel() * d.element_size() == nbytes,
+               "b3_root_and_seed_many: inputs must be contiguous and of equal size")
+    for outs in (root_outs, seed_outs):
+        _check(outs is None or len(outs) == count, "b3_root_and_seed_many: one root / seed output per input")
+    need = b3_scratch_words(nbytes) * count
+    if scratch is None or scratch.numel() < need:
+        scratch = torch.empty(need, dtype=torch.int32, device=datas[0].device)
+    _lib.call("uwc_b3_root_and_seed_many", ctypes.cast(_ptrs(datas), ctypes.c_void_p), count, nbytes, _p(key),
+              _p(prefix), _p(salt), dim, _arr(root_outs), _arr(seed_outs), _p(scratch), scratch.numel(), _stream())
+    return scratch
+
+
+def _arr(ts):
+    a = _ptrs(ts)
+    return None if a is None else ctypes.cast(a, ctypes.c_void_p)
+
+
 # ------------------------------------------------------------------ noise
 def noise_uniform(out: torch.Tensor, label: torch.Tensor, key: torch.Tensor, zero_me=None, zero_n: int = 0):
     _check(out.numel() % 32 == 0, "noise_uniform: out size must be a multiple of 32")
@@ -136,6 +174,25 @@ def nonce_noise(E: torch.Tensor, P: torch.Tensor, k: int, r: int, label: torch.T
     n1 = zero1.numel() if zero1 is not None else 0
     _lib.call("uwc_nonce_noise", _p(E), rows, r, _p(P), k, _p(St), _p(SpT), _p(label), _p(key), _p(zero0), n0,
               _p(zero1), n1, _stream())
+
+
+def nonce_noise_many(Es, Ps, k: int, r: int, label: torch.Tensor, keys, Sts=None, zero0s=None, zero1s=None,
+                     SpTs=None):
+    """nonce_noise for several nonces in one launch (item i as nonce_noise(Es[i], Ps[i], k, r,
+    label, keys[i], ...)). Every list has one entry per item or is None."""
+    count = len(Es)
+    _check(1 <= count <= MAX_BATCH, f"nonce_noise_many: {count} items, need 1..{MAX_BATCH}")
+    rows = Es[0].shape[0]
+    for E, P in zip(Es, Ps):
+        _check(tuple(E.shape) == (rows, r) and P.numel() >= k, "nonce_noise_many: E must be rows x r and P hold k words")
+    for xs in (Ps, keys, Sts, zero0s, zero1s, SpTs):
+        _check(xs is None or len(xs) == count, "nonce_noise_many: one entry per item")
+    n0 = zero0s[0].numel() if zero0s is not None else 0
+    n1 = zero1s[0].numel() if zero1s is not None else 0
+    for zs, nz in ((zero0s, n0), (zero1s, n1)):
+        _check(zs is None or all(z.numel() == nz for z in zs), "nonce_noise_many: zero ranges must be of equal size")
+    _lib.call("uwc_nonce_noise_many", count, _arr(Es), rows, r, _arr(Ps), k, _arr(Sts), _arr(SpTs), _p(label),
+              _arr(keys), _arr(zero0s), n0, _arr(zero1s), n1, _stream())
 
 
 def noise_rows(src, rows, k, r, *, E=None, Pn=None, dst=None, Pp=None, corr=None, corr_off=-1, ecopy_off=-1,
@@ -237,16 +294,7 @@ def igemm_i32(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None)
 
 # ------------------------------------------------------------------ one mined linear layer
 _WORKSPACE: dict = {}
-_STREAMS: dict = {}
-
-
-def _streams(device) -> tuple:
-    """The two side streams forward_many pipelines over (default priority), per device."""
-    key = str(device)
-    st = _STREAMS.get(key)
-    if st is None:
-        st = _STREAMS[key] = (torch.cuda.Stream(device=device), torch.cuda.Stream(device=device))
-    return st
+SWEEP_GROUP = 8  # nonces per batched commitment / noise launch in MinedWeight.forward_many
 
 
 @dataclass
@@ -308,10 +356,19 @@ class MinedWeight:
         del Bt
 
     def _buf(self, m: int, slot: int = 0, wins: torch.Tensor | None = None):
-        """Per-call buffers. The large ones are a workspace shared by every weight with the same
-        (m, k, r): layers run one after another on one stream; forward_many alternates two slots.
-        Win records are per weight (or the caller's buffer)."""
+        """Per-call buffers, a workspace shared by every weight with the same (m, k, r): layers run
+        one after another on one stream. The noised operand and the corrections (ApEA, corrA) live
+        only from the projections to the GEMM of one call and are shared by all slots; the
+        per-nonce noise (a_seed, E, P, selection matrices, maxabs, commitment scratch) has one
+        copy per slot, so forward_many can draw a group of nonces' noise before their GEMMs.
+        Win records are per weight (or the caller's buffer); slots > 0 carry their own."""
         dev, k, r = self.device, self.k, self.r
+        big = _WORKSPACE.get((str(dev), m, k, r))
+        if big is None:
+            big = _WORKSPACE[(str(dev), m, k, r)] = dict(
+                ApEA=torch.empty((m, k), dtype=torch.int8, device=dev),
+                corrA=torch.zeros((limbs_for(k), m, 2 * r), dtype=torch.int8, device=dev),
+            )
         key = (str(dev), m, k, r, slot)
         ws = _WORKSPACE.get(key)
         if ws is None:
@@ -319,18 +376,17 @@ class MinedWeight:
                 a_seed=torch.empty(8, dtype=torch.int32, device=dev),
                 EAL=torch.empty((m, r), dtype=torch.int8, device=dev),
                 PA=torch.empty(k, dtype=torch.int32, device=dev),
-                ApEA=torch.empty((m, k), dtype=torch.int8, device=dev),
                 SA=torch.empty((r, k), dtype=torch.int8, device=dev),
                 SpA=torch.empty((k, 64), dtype=torch.int8, device=dev) if r <= 64 else None,
-                corrA=torch.zeros((limbs_for(k), m, 2 * r), dtype=torch.int8, device=dev),
                 maxabs=torch.zeros(2, dtype=torch.int32, device=dev),
                 scratch=torch.empty(max(8, b3_scratch_words(m * k)), dtype=torch.int32, device=dev),
             )
         if wins is None:
-            wins = self._bufs.get(m)
+            wkey = (m, slot)
+            wins = self._bufs.get(wkey)
             if wins is None:
-                wins = self._bufs[m] = torch.zeros(1 + self.max_wins * WIN_WORDS, dtype=torch.int32, device=dev)
-        return {**ws, "wins": wins}
+                wins = self._bufs[wkey] = torch.zeros(1 + self.max_wins * WIN_WORDS, dtype=torch.int32, device=dev)
+        return {**big, **ws, "wins": wins}
 
     def forward(self, A: torch.Tensor, a_scale: torch.Tensor, out: torch.Tensor | None = None,
                 out_mode: int = OUT_BF16, hash_tiles: bool = True) -> torch.Tensor:
@@ -352,34 +408,53 @@ class MinedWeight:
         m, k = A.shape
         n, r = self.n, self.r
         c = consts(A.device)
-        # 2. A-side noise E_AL, P_A (and its selection matrix); the same launch zeroes maxabs and
-        #    the win counter
-        # 3. ApEA = A + EAL*P_A ; X = A * P_B^T (limbs) ; EAL copy
-        # 4. Y = BpEBt * P_A^T (limbs)
         if proj:  # projections on the matrix cores (the reference's PROJ_GEMM path)
             side = side_ok(m, n, k, r)
+            # 2. A-side noise E_AL, P_A (and its selection matrices); the same launch zeroes maxabs
+            #    and the win counter
             nonce_noise(b["EAL"], b["PA"], k, r, c["LABEL_A"], b["a_seed"], St=b["SA"], zero0=b["maxabs"],
                         zero1=b["wins"][:1], SpT=b["SpA"] if side else None)
-            if side:
-                side_project(A, b["EAL"], b["SpA"], b["ApEA"], self.SBt, b["corrA"], self.BpEBt, b["SA"], self.corrB,
-                             maxabs=b["maxabs"], corr_a_off=0, ecopy_off=r, corr_b_off=r)
-            else:
-                noise_project(A, m, k, r, E=b["EAL"], Pn=b["PA"], dst=b["ApEA"], St=self.SBt, corr=b["corrA"],
-                              corr_off=0, ecopy_off=r, maxabs=b["maxabs"][0:1])
-                project(self.BpEBt, b["SA"], self.corrB, r, b["maxabs"][1:2])
-        else:     # projections by LDS atomics (noise_rows with Pp)
-            noise_uniform(b["EAL"], c["LABEL_A"], b["a_seed"], zero_me=b["maxabs"], zero_n=2)
-            b["wins"][:1].zero_()
-            noise_perm(b["PA"], k, r, c["LABEL_A"], b["a_seed"])
-            noise_rows(A, m, k, r, E=b["EAL"], Pn=b["PA"], dst=b["ApEA"], Pp=self.PB, corr=b["corrA"], corr_off=0,
-                       ecopy_off=r, maxabs=b["maxabs"][0:1])
-            noise_rows(self.BpEBt, n, k, r, Pp=b["PA"], corr=self.corrB, corr_off=r, maxabs=b["maxabs"][1:2])
+            return self._mine(A, b, a_scale, out, out_mode, hash_tiles, side, cfg=cfg, dump=dump)
+        # projections by LDS atomics (noise_rows with Pp)
+        noise_uniform(b["EAL"], c["LABEL_A"], b["a_seed"], zero_me=b["maxabs"], zero_n=2)
+        b["wins"][:1].zero_()
+        noise_perm(b["PA"], k, r, c["LABEL_A"], b["a_seed"])
+        noise_rows(A, m, k, r, E=b["EAL"], Pn=b["PA"], dst=b["ApEA"], Pp=self.PB, corr=b["corrA"], corr_off=0,
+                   ecopy_off=r, maxabs=b["maxabs"][0:1])
+        noise_rows(self.BpEBt, n, k, r, Pp=b["PA"], corr=self.corrB, corr_off=r, maxabs=b["maxabs"][1:2])
+        return self._gemm(b, a_scale, out, out_mode, hash_tiles, cfg=cfg, dump=dump)
+
+    def _mine(self, A, b, a_scale, out, out_mode, hash_tiles, side, cfg=None, dump=None):
+        """Steps 3-5 of a mined forward once the nonce's noise is drawn (ops.py:331-347)."""
+        m, k = A.shape
+        r = self.r
+        # 3. ApEA = A + EAL*P_A ; X = A * P_B^T (limbs) ; EAL copy
+        # 4. Y = BpEBt * P_A^T (limbs)
+        if side:
+            side_project(A, b["EAL"], b["SpA"], b["ApEA"], self.SBt, b["corrA"], self.BpEBt, b["SA"], self.corrB,
+                         maxabs=b["maxabs"], corr_a_off=0, ecopy_off=r, corr_b_off=r)
+        else:
+            noise_project(A, m, k, r, E=b["EAL"], Pn=b["PA"], dst=b["ApEA"], St=self.SBt, corr=b["corrA"],
+                          corr_off=0, ecopy_off=r, maxabs=b["maxabs"][0:1])
+            project(self.BpEBt, b["SA"], self.corrB, r, b["maxabs"][1:2])
+        return self._gemm(b, a_scale, out, out_mode, hash_tiles, cfg=cfg, dump=dump)
+
+    def _gemm(self, b, a_scale, out, out_mode, hash_tiles, cfg=None, dump=None):
         # 5. noisy GEMM: hash every tile, denoise exactly, scale
-        gemm(b["ApEA"], self.BpEBt, r=r, flags=(FLAG_HASH if hash_tiles else 0) | FLAG_DENOISE,
+        gemm(b["ApEA"], self.BpEBt, r=self.r, flags=(FLAG_HASH if hash_tiles else 0) | FLAG_DENOISE,
              corrA=b["corrA"], corrB=self.corrB, maxabs=b["maxabs"], key=b["a_seed"], target=self.target,
              wins=b["wins"], max_wins=self.max_wins, a_scale=a_scale, b_scale=self.b_scale, out=out, out_mode=out_mode,
              cfg=cfg, dump=dump)
         return out
+
+    def _sweep_scratch(self, m: int, count: int) -> torch.Tensor:
+        """Commitment scratch for `count` operands of m x k in one batched launch."""
+        need = b3_scratch_words(m * self.k) * count
+        key = (str(self.device), m, self.k, "sweep")
+        t = _WORKSPACE.get(key)
+        if t is None or t.numel() < need:
+            t = _WORKSPACE[key] = torch.empty(need, dtype=torch.int32, device=self.device)
+        return t
 
     def _out(self, m, out, out_mode):
         if out is None and out_mode != OUT_NONE:
@@ -395,51 +470,45 @@ class MinedWeight:
         return self._after_commit(A, b, a_scale, out, out_mode, hash_tiles, cfg=cfg, proj=proj, dump=dump)
 
     def forward_many(self, As, a_scale: torch.Tensor, outs=None, out_mode: int = OUT_BF16, hash_tiles: bool = True,
-                     wins=None):
+                     wins=None, group: int = SWEEP_GROUP):
         """Mined forwards of a sequence of activations (the nonces of a sweep), each equal to
-        forward(As[i]) bit for bit, pipelined over two streams: the commitment of As[i + 1] (a
-        latency-bound BLAKE3 tree) runs beside the noising and projections of As[i], in a second
-        workspace. outs / wins: optional per-item output tensors and win buffers (1 + max_wins *
-        WIN_WORDS int32 each; without them every item shares the weight's win buffer and winners()
-        reports the last item). Returns the outputs; work is queued behind the current stream and the
-        current stream waits for all of it."""
+        forward(As[i]) bit for bit. The nonces go in groups of `group` (1..MAX_BATCH): one set of
+        launches commits the whole group (BLAKE3 trees and salted seeds) and one launch draws all
+        of its noise, so those latency-bound chains run several waves per SIMD instead of one;
+        then every nonce of the group runs its projections and hashed GEMM. Everything is queued
+        in order on the current stream. outs / wins: optional per-item output tensors and win
+        buffers (1 + max_wins * WIN_WORDS int32 each); without wins, winners() reports the last
+        item (the others' records go to per-slot buffers). Returns the outputs."""
         n_items = len(As)
         if n_items == 0:
             return []
-        m = As[0].shape[0]
+        _check(1 <= group <= MAX_BATCH, f"MinedWeight.forward_many: group={group}, need 1..{MAX_BATCH}")
+        m, k, r = As[0].shape[0], self.k, self.r
         for A in As:
             self._check_a(A)
             _check(A.shape[0] == m, "MinedWeight.forward_many: every A needs the same shape")
         outs = [self._out(m, outs[i] if outs is not None else None, out_mode) for i in range(n_items)]
-        cur = torch.cuda.current_stream(self.device)
-        sc, sm = _streams(self.device)
-        sc.wait_stream(cur)
-        sm.wait_stream(cur)
-        bufs = [self._buf(m, 0), self._buf(m, 1)]
-        committed = [torch.cuda.Event() for _ in range(2)]
-        consumed = [torch.cuda.Event() for _ in range(2)]
-
-        def commit(i):
-            b = bufs[i % 2]
-            with torch.cuda.stream(sc):
-                if i >= 2:
-                    sc.wait_event(consumed[i % 2])  # item i - 2 is done with this workspace
-                self._commit(As[i], b)
-                committed[i % 2].record(sc)
-
-        commit(0)
-        for i in range(n_items):
-            if i + 1 < n_items:
-                commit(i + 1)
-            b = dict(bufs[i % 2])
-            if wins is not None:
-                b["wins"] = wins[i]
-            with torch.cuda.stream(sm):
-                sm.wait_event(committed[i % 2])
-                self._after_commit(As[i], b, a_scale, outs[i], out_mode, hash_tiles)
-                consumed[i % 2].record(sm)
-        cur.wait_stream(sm)
-        cur.wait_stream(sc)
+        c = consts(As[0].device)
+        side = side_ok(m, self.n, k, r)
+        for g0 in range(0, n_items, group):
+            items = list(range(g0, min(g0 + group, n_items)))
+            bufs = []
+            for j, i in enumerate(items):
+                # the sweep's last item reports through the weight's own win buffer (slot 0's)
+                wb = wins[i] if wins is not None else (self._buf(m)["wins"] if i == n_items - 1 else None)
+                bufs.append(self._buf(m, slot=j + 1, wins=wb))
+            # 1. commit to every A of the group, a_seed_i = H(b_seed || bind_a(root_Ai, m))
+            #    (ops.py:322-324)
+            b3_root_and_seed_many([As[i].view(-1) for i in items], self.job_key, prefix=self.b_seed, salt=c["SALT_A"],
+                                  dim=m, seed_outs=[b["a_seed"] for b in bufs], scratch=self._sweep_scratch(m, len(items)))
+            # 2. every nonce's noise E_A, P_A and selection matrices; zeroes its maxabs and win count
+            nonce_noise_many([b["EAL"] for b in bufs], [b["PA"] for b in bufs], k, r, c["LABEL_A"],
+                             [b["a_seed"] for b in bufs], Sts=[b["SA"] for b in bufs],
+                             zero0s=[b["maxabs"] for b in bufs], zero1s=[b["wins"][:1] for b in bufs],
+                             SpTs=[b["SpA"] for b in bufs] if side else None)
+            # 3.-5. per nonce: projections, hashed GEMM, exact denoise
+            for b, i in zip(bufs, items):
+                self._mine(As[i], b, a_scale, outs[i], out_mode, hash_tiles, side)
         return outs
 
     def noise_mine(self, A: torch.Tensor, dump=None):
