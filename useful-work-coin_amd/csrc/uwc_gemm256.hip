@@ -31,6 +31,9 @@
 //     accumulator), streaming [X_li | EAL] and [EBRt | Y_li] through the same ring.
 #include "uwc_common.h"
 
+// lambdas are always inlined: an out-of-line call would take the accumulator arrays' addresses
+// (private memory) and load captured uniform values per lane
+#define UWC_AI __attribute__((always_inline))
 #define W_BM 256
 #define W_BN 256
 #ifndef W_BK
@@ -48,14 +51,14 @@
 static_assert(W_LDS <= 160 * 1024, "LDS ring exceeds 160 KiB");
 #define W_WAVES (W_THREADS / 64)
 #define W_SEGS_PER_WAVE (W_TILE / 1024 / W_WAVES)  // 1 KiB DMA segments per wave per operand per k step
+#ifndef W_DB_PLAIN
+#define W_DB_PLAIN 1  // two alternating fragment sets in the kernels without a transcript
+#endif
 #ifndef W_DMA_SPREAD
 // Issue a k step's refill in three parts (after the barrier, before pass 0 and before pass 1 of
 // the next step) instead of one burst: 64 DMA instructions per CU in one burst keep every wave
 // blocked on the address unit, and its MFMAs queued behind them, for ~1600 cycles
 #define W_DMA_SPREAD 1
-#endif
-#ifndef W_DB_HASH
-#define W_DB_HASH 0  // double-buffered fragments in the hashing kernels too
 #endif
 
 #define FLAG_HASH 1
@@ -85,6 +88,19 @@ struct Gemm256Params {
   u32* dump;
   int ldc;  // output row stride in elements
 };
+
+// f(std::integral_constant<int, i>) for i = 0 .. N - 1, each i a compile-time constant.
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for_(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for_<I + 1, N>(f);
+  }
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_<0, N>(f);
+}
 
 typedef const void __attribute__((address_space(1)))* gptr_t;
 typedef void __attribute__((address_space(3)))* lptr_t;
@@ -258,63 +274,68 @@ __device__ __forceinline__ void fold_block(const v16i& v, u32* x, bool first) {
   }
 }
 
-// The eight MFMAs of one pass, column half 0 first. With FOLD, each block's accumulators are
-// first XORed into the fold partials x[8] (the cumulative sums of the chunk that ended with the
-// previous pass), so the fold's VALU work interleaves with the MFMAs. With READ, f is refilled
-// with the fragments of pass nkp of stage nst as the current ones retire: b[0] after the four
-// half-0 MFMAs, a[mb] after MFMA (mb, 1), b[1] last; one fragment set stays in registers and
-// each read still has several MFMAs to land before its first use in the next pass.
-template <bool FOLD, bool READ>
+// The eight MFMAs of one pass, column half 0 first: block position pos = 4 nb + mb. With READ,
+// f is refilled with the fragments of pass nkp of stage nst as the current ones retire: b[0]
+// after the four half-0 MFMAs, a[mb] after MFMA (mb, 1), b[1] last; one fragment set stays in
+// registers and each read still has several MFMAs to land before its first use in the next pass.
+//
+// The transcript fold of a chunk is spread over two passes so that neither carries all of its
+// VALU work: in the chunk's last pass (TAIL) block pos - FOLD_LAG is XORed into the partials x
+// right after MFMA pos (its accumulators became final FOLD_LAG MFMAs earlier), which covers
+// blocks 0 .. 7 - FOLD_LAG; in the next chunk's first pass (HEAD) blocks 8 - FOLD_LAG .. 7 are
+// XORed right before their first MFMA of the new chunk. Partials group 0 collects mb 0, 1 and
+// group 1 mb 2, 3; blocks 0 and 2 (the first of each group in TAIL order) initialise them.
+#define FOLD_LAG 3
+template <bool HEAD, bool TAIL, bool READ>
 __device__ __forceinline__ void pass_mma(v16i acc[4][2], Frag& f, u32 x[8], const FragBase& fb, int nst, int nkp) {
 #pragma unroll
-  for (int mb = 0; mb < 4; mb++) {
-    if constexpr (FOLD) fold_block(acc[mb][0], x + (mb >> 1) * 4, (mb & 1) == 0);
-    acc[mb][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[mb], f.b[0], acc[mb][0], 0, 0, 0);
-  }
-  if constexpr (READ) f.b[0] = frag_b(fb, nst, nkp, 0);
-#pragma unroll
-  for (int mb = 0; mb < 4; mb++) {
-    if constexpr (FOLD) fold_block(acc[mb][1], x + (mb >> 1) * 4, false);
-    acc[mb][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[mb], f.b[1], acc[mb][1], 0, 0, 0);
-    if constexpr (READ) f.a[mb] = frag_a(fb, nst, nkp, mb);
+  for (int pos = 0; pos < 8; pos++) {
+    const int mb = pos & 3, nb = pos >> 2;
+    if (HEAD && pos >= 8 - FOLD_LAG) fold_block(acc[mb][nb], x + (mb >> 1) * 4, false);
+    acc[mb][nb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[mb], f.b[nb], acc[mb][nb], 0, 0, 0);
+    if (TAIL && pos >= FOLD_LAG) {
+      const int q = pos - FOLD_LAG, qm = q & 3, qn = q >> 2;
+      fold_block(acc[qm][qn], x + (qm >> 1) * 4, q == 0 || q == 2);
+    }
+    if (READ && pos == 3) f.b[0] = frag_b(fb, nst, nkp, 0);
+    if (READ && pos >= 4) f.a[pos - 4] = frag_a(fb, nst, nkp, pos - 4);
   }
   if constexpr (READ) f.b[1] = frag_b(fb, nst, nkp, 1);
-  // pin the interleave: [fold VALU,] MFMA ... with the reads after the MFMAs that free them
+  // pin the interleave: [fold VALU,] MFMA [, fold VALU] [, read] per block position
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    if constexpr (FOLD) __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+  for (int pos = 0; pos < 8; pos++) {
+    if (HEAD && pos >= 8 - FOLD_LAG) __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-  }
-  if constexpr (READ) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    if constexpr (FOLD) __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    if constexpr (READ) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    if (TAIL && pos >= FOLD_LAG) __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+    if (READ && pos >= 3) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
   }
   if constexpr (READ) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
 }
 
-// Double-buffered form of pass_mma: with READ, the six fragments of pass nkp go into nxt
-// before the MFMAs on cur, so they have the whole pass to land. Costs a second fragment set
-// (24 VGPRs); used where registers allow.
-template <bool FOLD, bool READ>
-__device__ __forceinline__ void pass_mma_db(v16i acc[4][2], const Frag& cur, Frag& nxt, u32 x[8], const FragBase& fb,
-                                            int nst, int nkp) {
+// The HEAD part of the fold without MFMAs: blocks 8 - FOLD_LAG .. 7 into x (after the k loop,
+// for the last chunk, whose TAIL pass already folded the other blocks).
+__device__ __forceinline__ void fold_head(const v16i acc[4][2], u32 x[8]) {
+  static_for<FOLD_LAG>([&](auto ic) UWC_AI {
+    constexpr int pos = 8 - FOLD_LAG + decltype(ic)::value, mb = pos & 3, nb = pos >> 2;
+    fold_block(acc[mb][nb], x + (mb >> 1) * 4, false);
+  });
+}
+
+// Double-buffered form of pass_mma for the kernels without a transcript: with READ, the six
+// fragments of pass nkp go into nxt before the MFMAs on cur, so they have the whole pass to
+// land. Costs a second fragment set (24 VGPRs).
+template <bool READ>
+__device__ __forceinline__ void pass_mma_db(v16i acc[4][2], const Frag& cur, Frag& nxt, const FragBase& fb, int nst,
+                                            int nkp) {
   if constexpr (READ) frag_read(nxt, fb, nst, nkp);
 #pragma unroll
   for (int mb = 0; mb < 4; mb++)
 #pragma unroll
-    for (int nb = 0; nb < 2; nb++) {
-      if constexpr (FOLD) fold_block(acc[mb][nb], x + (mb >> 1) * 4, (mb & 1) == 0 && nb == 0);
+    for (int nb = 0; nb < 2; nb++)
       acc[mb][nb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.a[mb], cur.b[nb], acc[mb][nb], 0, 0, 0);
-    }
   if constexpr (READ) __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
-    if constexpr (FOLD) __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-  }
+  for (int i = 0; i < 8; i++) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
 }
 
 // Denoise k step for one quarter of the wave's block: M blocks 2h, 2h+1 of column half nb.
@@ -374,14 +395,6 @@ __device__ __forceinline__ void fold_into(u32& msg, const u32 x[8], int lane) {
   msg = xor3(rotl13(msg), keep, other);
 }
 
-// Tile XOR partials of the current accumulators (no MFMA interleave).
-__device__ __forceinline__ void fold_partials(const v16i acc[4][2], u32 x[8]) {
-#pragma unroll
-  for (int mb = 0; mb < 4; mb++)
-#pragma unroll
-    for (int nb = 0; nb < 2; nb++) fold_block(acc[mb][nb], x + (mb >> 1) * 4, (mb & 1) == 0 && nb == 0);
-}
-
 __device__ __forceinline__ u32 bf16_rne(float f) {
   const u32 u = __float_as_uint(f);
   return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
@@ -398,19 +411,6 @@ __device__ __forceinline__ void tile256(int m, int n, int& bm0, int& bn0) {
   const int gsz = min(npm - first, GROUP_M), in = pid - gid * grp;
   bm0 = (first + in % gsz) * W_BM;
   bn0 = (in / gsz) * W_BN;
-}
-
-// f(std::integral_constant<int, i>) for i = 0 .. N - 1, each i a compile-time constant.
-template <int I, int N, class F>
-__device__ __forceinline__ void static_for_(F&& f) {
-  if constexpr (I < N) {
-    f(std::integral_constant<int, I>{});
-    static_for_<I + 1, N>(f);
-  }
-}
-template <int N, class F>
-__device__ __forceinline__ void static_for(F&& f) {
-  static_for_<0, N>(f);
 }
 
 template <bool HASH, bool DENOISE, int OUT>
@@ -431,8 +431,8 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
     for (int j = 0; j < 2; j++) acc[i][j] = v16i{};
 
   const u32 wsm_l = __builtin_amdgcn_readfirstlane(lds_addr(wsm));
-  auto lds_a = [&](int st) { return wsm_l + (u32)(st * W_TILE); };           // stage st's A tile
-  auto lds_b = [&](int st) { return wsm_l + (u32)(W_BOFF + st * W_TILE); };  // and its B tile
+  auto lds_a = [&](int st) UWC_AI { return wsm_l + (u32)(st * W_TILE); };           // stage st's A tile
+  auto lds_b = [&](int st) UWC_AI { return wsm_l + (u32)(W_BOFF + st * W_TILE); };  // and its B tile
   const FragBase fbase = frag_bases(wsm_l, wm, wn, lane);
   const DmaOff doff = dma_offsets(k, wave, lane);
   const i8* a_win = p.A + (long)bm0 * k;  // + k0: this workgroup's operand windows
@@ -443,7 +443,12 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
     if (s < KT) dma_step_s(lds_a(s), lds_b(s), doff, a_win + s * W_BK, b_win + s * W_BK, wave);
   wait_step(min(KT - 1, W_STAGES - 1));
   // fragment sets: single set streamed (pass_mma) or two alternating sets (pass_mma_db)
-  constexpr bool DB = !HASH || W_DB_HASH;
+  constexpr bool DB = !HASH && W_DB_PLAIN;
+  // transcript fold partials, carried from a chunk's TAIL pass to the next chunk's HEAD pass;
+  // zero before chunk 0, so the HEAD pass of the first k step folds nothing into slot 15
+  u32 fx[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) fx[i] = 0;
   Frag fb[DB ? 2 : 1];
   frag_read(fb[0], fbase, 0, 0);
 
@@ -451,16 +456,16 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
   // kp + 1. Before the last pass the wave waits for step kt + 1 (vmcnt + barrier: every wave is
   // then done reading step kt's stage) and refills that stage with step kt + W_STAGES; the last
   // pass reads the next step's first fragments (on the final step that read of a resident stage
-  // is unused, which keeps the MFMA code free of branches). Bit kp of FM: pass kp first folds
-  // the chunk that ended with the previous pass into m0 (kp == 0) or m1 (kp > 0). The stage
+  // is unused, which keeps the MFMA code free of branches). FM bit kp: pass kp is the HEAD pass
+  // of a chunk (it finishes the fold of the chunk that ended with the previous pass and folds it
+  // into m0 for kp == 0, else m1); FM bit 4 + kp: pass kp is the TAIL pass of a chunk. The stage
   // index ST == kt % W_STAGES is a compile-time constant, so every LDS address of the step is a
   // base register plus an immediate.
-  auto step = [&](auto fm, auto stc, int kt, u32& m0, u32& m1) {
+  auto step = [&](auto fm, auto stc, int kt, u32& m0, u32& m1) UWC_AI {
     constexpr int FM = decltype(fm)::value, ST = decltype(stc)::value;
-    static_for<W_KP>([&](auto kpc) {
+    static_for<W_KP>([&](auto kpc) UWC_AI {
       constexpr int kp = decltype(kpc)::value;
-      constexpr bool fold = ((FM >> kp) & 1) != 0;
-      u32 x[8];
+      constexpr bool head = ((FM >> kp) & 1) != 0, tail = ((FM >> (4 + kp)) & 1) != 0;
       constexpr int nst = kp + 1 == W_KP ? (ST + 1) % W_STAGES : ST;
       constexpr int nkp = kp + 1 == W_KP ? 0 : kp + 1;
 #if W_DMA_SPREAD
@@ -489,18 +494,45 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
           }
         }
       }
-      if constexpr (DB) pass_mma_db<fold, true>(acc, fb[kp & 1], fb[(kp + 1) & 1], x, fbase, nst, nkp);
-      else pass_mma<fold, true>(acc, fb[0], x, fbase, nst, nkp);
-      if constexpr (fold) fold_into(kp == 0 ? m0 : m1, x, lane);
+      if constexpr (DB) {
+        static_assert(FM == 0, "the double-buffered passes carry no transcript fold");
+        pass_mma_db<true>(acc, fb[kp & 1], fb[(kp + 1) & 1], fbase, nst, nkp);
+      } else {
+        pass_mma<head, tail, true>(acc, fb[0], fx, fbase, nst, nkp);
+      }
+      if constexpr (head) fold_into(kp == 0 ? m0 : m1, fx, lane);
     });
   };
   // step() for a k step whose stage is known only at run time
-  auto step_rt = [&](auto fm, int kt, u32& m0, u32& m1) {
-    static_for<W_STAGES>([&](auto stc) {
+  auto step_rt = [&](auto fm, int kt, u32& m0, u32& m1) UWC_AI {
+    static_for<W_STAGES>([&](auto stc) UWC_AI {
       if (kt % W_STAGES == decltype(stc)::value) step(fm, stc, kt, m0, m1);
     });
   };
   using NoFold = std::integral_constant<int, 0>;
+
+  // Denoise setup (kernels.cu:598-673): acc -= sum_li 128^li [X_li | EAL] [EBRt | Y_li]^T, the
+  // corr k steps running limb L-1 down to 0, each limb 2r / W_BK steps. CT steps in all.
+  int L = 1, CPL = 1, CT = 1;
+  long R2 = 0;
+  if constexpr (DENOISE) {
+    const int mx = max(p.maxabs[0], p.maxabs[1]);
+    L = min(mx > 1040319 ? 4 : mx > 8127 ? 3 : mx > 63 ? 2 : 1, p.lmax);
+    R2 = 2L * p.r;
+    CPL = (int)(R2 / W_BK);
+    CT = L * CPL;
+  }
+  // next corr step to issue: global index ig, limb li, chunk kc
+  int ig = 0, li = L - 1, kc = 0;
+  auto cissue = [&]() UWC_AI {
+    const DmaLane cl = dma_lane(p.corrA + (long)li * p.m * R2, R2, p.corrB + (long)li * p.n * R2, R2, bm0, bn0, lane);
+    dma_step(lds_a(ig % W_STAGES), lds_b(ig % W_STAGES), cl, R2, R2, (long)kc * W_BK, wave);
+    ig++;
+    if (++kc == CPL) {
+      kc = 0;
+      li = li == 0 ? L - 1 : li - 1;
+    }
+  };
 
   if constexpr (HASH) {
     u32 msg[16];
@@ -509,18 +541,20 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
     const int nchunks = p.k / p.r;
     int kt = 0;
     u32 unused = 0;
-    // The fold of chunk c runs in the first pass of chunk c + 1 (slot (c - 1) mod 16 for the
-    // chunk starting at slot c). For chunk 0 that folds the all-zero accumulators into the
-    // all-zero slot 15, which leaves it zero.
+    // The fold of chunk c ends in the first pass of chunk c + 1 (slot (c - 1) mod 16 for the
+    // chunk starting at slot c). For chunk 0 that folds the all-zero partials into the all-zero
+    // slot 15, which leaves it zero.
+    using Head = std::integral_constant<int, 0x01>;
+    using Tail = std::integral_constant<int, 0x80>;
     if (p.r == W_BK) {
       // one k step per chunk: an outer iteration is 16 k steps, so k step c0 + s sits in stage
       // s % W_STAGES
       static_assert(16 % W_STAGES == 0, "stage of an unrolled k step");
       for (int c0 = 0; c0 < nchunks; c0 += 16) {
-        static_for<16>([&](auto sc) {
+        static_for<16>([&](auto sc) UWC_AI {
           constexpr int s = decltype(sc)::value;
           if (c0 + s < nchunks)
-            step(std::integral_constant<int, 1>{}, std::integral_constant<int, s % W_STAGES>{}, c0 + s,
+            step(std::integral_constant<int, 0x81>{}, std::integral_constant<int, s % W_STAGES>{}, c0 + s,
                  msg[(s + 15) & 15], unused);
         });
       }
@@ -530,8 +564,9 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
 #pragma unroll
         for (int s = 0; s < 16; s++) {
           if (c0 + s < nchunks) {
-            step_rt(std::integral_constant<int, 1>{}, kt++, msg[(s + 15) & 15], unused);
-            for (int i = 1; i < tpc; i++) step_rt(NoFold{}, kt++, unused, unused);
+            step_rt(Head{}, kt++, msg[(s + 15) & 15], unused);
+            for (int i = 1; i + 1 < tpc; i++) step_rt(NoFold{}, kt++, unused, unused);
+            step_rt(Tail{}, kt++, unused, unused);
           }
         }
       }
@@ -540,18 +575,26 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
       // outer iteration is 8 k steps, so k step c0 / 2 + s / 2 sits in stage (s / 2) % W_STAGES
       static_assert(8 % W_STAGES == 0, "stage of an unrolled k step");
       for (int c0 = 0; c0 < nchunks; c0 += 16) {
-        static_for<8>([&](auto jc) {
+        static_for<8>([&](auto jc) UWC_AI {
           constexpr int j = decltype(jc)::value, s = 2 * j;
           if (c0 + s < nchunks)
-            step(std::integral_constant<int, 0b0101>{}, std::integral_constant<int, j % W_STAGES>{}, c0 / 2 + j,
+            step(std::integral_constant<int, 0xA5>{}, std::integral_constant<int, j % W_STAGES>{}, c0 / 2 + j,
                  msg[(s + 15) & 15], msg[s]);
         });
       }
     }
-    {  // the last chunk
-      u32 x[8], keep, other;
-      fold_partials(acc, x);
-      fold_scatter(x, lane, keep, other);
+    // The ring is idle now: when every corr step fits it, start loading them so that their
+    // latency hides behind the digest (every wave has finished its LDS reads at the barrier; the
+    // k loop's last wait left no DMA in flight).
+    if (DENOISE && CT <= W_STAGES) {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      for (int t = 0; t < CT; t++) cissue();  // corr step t -> stage t
+    }
+    {  // the last chunk: its TAIL pass was the k loop's last pass
+      u32 keep, other;
+      fold_head(acc, fx);
+      fold_scatter(fx, lane, keep, other);
       const int last = (nchunks - 1) & 15;
 #pragma unroll
       for (int s = 0; s < 16; s++)
@@ -586,13 +629,13 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
     u32 unused = 0;
     int kt = 0;
     for (; kt + W_STAGES <= KT; kt += W_STAGES)
-      static_for<W_STAGES>([&](auto stc) { step(NoFold{}, stc, kt + decltype(stc)::value, unused, unused); });
+      static_for<W_STAGES>([&](auto stc) UWC_AI { step(NoFold{}, stc, kt + decltype(stc)::value, unused, unused); });
     for (; kt < KT; kt++) step_rt(NoFold{}, kt, unused, unused);
   }
 
   // epilogue of one 32 x 32 MFMA block: lane holds col (lane & 31) of rows
   // 8 (e >> 2) + 4 (lane >> 5) + (e & 3)
-  auto store_block = [&](int mb, int nb, const v16i& v) {
+  auto store_block = [&](int mb, int nb, const v16i& v) UWC_AI {
     if constexpr (OUT != OUT_NONE) {
       constexpr int ES = OUT == OUT_BF16 ? 2 : 4;  // output element bytes
       // element e of the block is row row0 + 8 (e >> 2) + (e & 3) + lr, column col0 + lc: a
@@ -620,34 +663,20 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
   };
 
   if constexpr (DENOISE) {
-    // acc -= sum_li 128^li [X_li | EAL] [EBRt | Y_li]^T, exact mod 2^32, Horner over limbs
-    // (kernels.cu:598-673). Four passes over quarters of the wave's block keep the Horner
-    // accumulator at 32 registers; each quarter is stored as soon as it is final. The corr k
-    // steps run limb L-1 down to 0, each limb 2r / W_BK steps. When all CT of them fit in the
-    // ring (L * 2r <= W_STAGES * W_BK: the mining shapes) they are loaded once in one burst and
-    // the four passes read them without further barriers; otherwise they stream through the ring
-    // continuously across the passes (global step g is corr step g mod CT).
-    const int mx = max(p.maxabs[0], p.maxabs[1]);
-    int L = mx > 1040319 ? 4 : mx > 8127 ? 3 : mx > 63 ? 2 : 1;
-    L = min(L, p.lmax);
-    const long R2 = 2L * p.r;
-    const int CPL = (int)(R2 / W_BK), CT = L * CPL, GT = 4 * CT;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // gfx9 counts stores in vmcnt: drain the hash phase
-    __syncthreads();
-    // next corr step to issue: global index ig, limb li, chunk kc
-    int ig = 0, li = L - 1, kc = 0;
-    auto cissue = [&]() {
-      const DmaLane cl = dma_lane(p.corrA + (long)li * p.m * R2, R2, p.corrB + (long)li * p.n * R2, R2, bm0, bn0, lane);
-      dma_step(lds_a(ig % W_STAGES), lds_b(ig % W_STAGES), cl, R2, R2, (long)kc * W_BK, wave);
-      ig++;
-      if (++kc == CPL) {
-        kc = 0;
-        li = li == 0 ? L - 1 : li - 1;
-      }
-    };
+    // Four passes over quarters of the wave's block keep the Horner accumulator at 32 registers;
+    // each quarter is stored as soon as it is final. When all CT corr steps fit in the ring
+    // (L * 2r <= W_STAGES * W_BK: the mining shapes) they are loaded once (the hashing kernels
+    // issued them before the digest) and the four passes read them without further barriers;
+    // otherwise they stream through the ring continuously across the passes (global step g is
+    // corr step g mod CT).
+    const int GT = 4 * CT;
     if (CT <= W_STAGES) {
-      for (int t = 0; t < CT; t++) cissue();  // corr step t -> stage t
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      if constexpr (!HASH) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the k loop's last fragment reads
+        __builtin_amdgcn_s_barrier();
+        for (int t = 0; t < CT; t++) cissue();  // corr step t -> stage t
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // also drains the hash phase's stores
       __builtin_amdgcn_s_barrier();
 #pragma unroll
       for (int q = 0; q < 4; q++) {
@@ -666,6 +695,8 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
       }
       return;
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // gfx9 counts stores in vmcnt: drain the hash phase
+    __syncthreads();                                   // and every wave is done reading the ring
 #pragma unroll
     for (int g = 0; g < W_STAGES - 1; g++)
       if (g < GT) cissue();
