@@ -368,14 +368,16 @@ extern "C" int uwc_noisy_gemm(const int8_t* A, const int8_t* B, int m, int n, in
   // a plain GEMM with fewer 256 x 256 tiles than CUs runs faster on 128 x 128 tiles.
   const bool fills = (long)(m / 256) * (n / 256) >= 256;
   const bool k256 = k % 128 == 0 && k <= (1 << 24);  // the 256 x 256 DMA adds 32-bit lane offsets (255 k + 112)
-  if (m % 256 == 0 && n % 256 == 0 && k256 && !(flags & FLAG_TILE128) && (!plain || fills))
+  // the 256 x 256 epilogue writes 16-byte (8-byte for bf16) row segments: rows must start aligned
+  const bool vec_out = out_mode == OUT_NONE || (aligned16(out) && n % 4 == 0);
+  if (m % 256 == 0 && n % 256 == 0 && k256 && vec_out && !(flags & FLAG_TILE128) && (!plain || fills))
     return uwc_noisy_gemm256(A, B, m, n, k, r, corrA, corrB, maxabs, lmax, key, target, wins, max_wins, a_scale,
                              b_scale, out, out_mode, flags & ~FLAG_TILE128, tile_dump, n, stream);
   // A plain GEMM whose n is not a multiple of 256 (e.g. a vocabulary of 151936) but whose 256 x 256
   // tiles would fill the CUs: columns [0, n256) on 256 x 256 tiles, the last n - n256 on 128 x 128
   // tiles writing into the same rows (integer sums: the split cannot change a value).
   const int n256 = n / 256 * 256;
-  if (plain && m % 256 == 0 && k256 && n256 > 0 && n256 < n && !(flags & FLAG_TILE128) &&
+  if (plain && m % 256 == 0 && k256 && vec_out && n256 > 0 && n256 < n && !(flags & FLAG_TILE128) &&
       (long)(m / 256) * (n256 / 256) >= 256) {
     const int st = uwc_noisy_gemm256(A, B, m, n256, k, 0, nullptr, nullptr, nullptr, 0, nullptr, nullptr, nullptr, 0,
                                      a_scale, b_scale, out, out_mode, 0, nullptr, n, stream);

@@ -264,13 +264,16 @@ __device__ __forceinline__ void frag_read(Frag& f, const FragBase& fb, int st, i
 
 __device__ __forceinline__ u32 xor3(u32 a, u32 b, u32 c) { return __builtin_amdgcn_bitop3_b32(a, b, c, 0x96); }
 
-// XOR one 32 x 32 block's 16 accumulators into the lane's 4 partials of its hash block:
-// x[p] collects elements e with e % 4 == p (rows g + 8 i of one tile).
+// XOR one 32 x 32 block's 16 accumulators into the lane's 2 partials of its hash block (the
+// transposed C layout: lane l holds row l & 31 and, in register e, column 8 (e >> 2) + 4 (l >> 5)
+// + (e & 3), so bit 1 of e is bit 0 of the tile index t): x[0] collects e & 2 == 0, x[1] the rest.
 __device__ __forceinline__ void fold_block(const v16i& v, u32* x, bool first) {
-#pragma unroll
-  for (int p = 0; p < 4; p++) {
-    if (first) x[p] = xor3(v[p], v[4 + p], v[8 + p]) ^ (u32)v[12 + p];
-    else x[p] = xor3(xor3(x[p], v[p], v[4 + p]), v[8 + p], v[12 + p]);
+  if (first) {
+    x[0] = xor3(xor3(xor3(v[0], v[1], v[4]), v[5], v[8]), v[9], v[12]) ^ (u32)v[13];
+    x[1] = xor3(xor3(xor3(v[2], v[3], v[6]), v[7], v[10]), v[11], v[14]) ^ (u32)v[15];
+  } else {
+    x[0] = xor3(xor3(xor3(xor3(x[0], v[0], v[1]), v[4], v[5]), v[8], v[9]), v[12], v[13]);
+    x[1] = xor3(xor3(xor3(xor3(x[1], v[2], v[3]), v[6], v[7]), v[10], v[11]), v[14], v[15]);
   }
 }
 
@@ -283,19 +286,19 @@ __device__ __forceinline__ void fold_block(const v16i& v, u32* x, bool first) {
 // VALU work: in the chunk's last pass (TAIL) block pos - FOLD_LAG is XORed into the partials x
 // right after MFMA pos (its accumulators became final FOLD_LAG MFMAs earlier), which covers
 // blocks 0 .. 7 - FOLD_LAG; in the next chunk's first pass (HEAD) blocks 8 - FOLD_LAG .. 7 are
-// XORed right before their first MFMA of the new chunk. Partials group 0 collects mb 0, 1 and
-// group 1 mb 2, 3; blocks 0 and 2 (the first of each group in TAIL order) initialise them.
+// XORed right before their first MFMA of the new chunk. Partials x[0..1] collect mb 0, 1 (hash
+// block 0) and x[2..3] mb 2, 3; blocks 0 and 2 (the first of each in TAIL order) initialise them.
 #define FOLD_LAG 3
 template <bool HEAD, bool TAIL, bool READ>
-__device__ __forceinline__ void pass_mma(v16i acc[4][2], Frag& f, u32 x[8], const FragBase& fb, int nst, int nkp) {
+__device__ __forceinline__ void pass_mma(v16i acc[4][2], Frag& f, u32 x[4], const FragBase& fb, int nst, int nkp) {
 #pragma unroll
   for (int pos = 0; pos < 8; pos++) {
     const int mb = pos & 3, nb = pos >> 2;
-    if (HEAD && pos >= 8 - FOLD_LAG) fold_block(acc[mb][nb], x + (mb >> 1) * 4, false);
-    acc[mb][nb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[mb], f.b[nb], acc[mb][nb], 0, 0, 0);
+    if (HEAD && pos >= 8 - FOLD_LAG) fold_block(acc[mb][nb], x + (mb >> 1) * 2, false);
+    acc[mb][nb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.b[nb], f.a[mb], acc[mb][nb], 0, 0, 0);
     if (TAIL && pos >= FOLD_LAG) {
       const int q = pos - FOLD_LAG, qm = q & 3, qn = q >> 2;
-      fold_block(acc[qm][qn], x + (qm >> 1) * 4, q == 0 || q == 2);
+      fold_block(acc[qm][qn], x + (qm >> 1) * 2, q == 0 || q == 2);
     }
     if (READ && pos == 3) f.b[0] = frag_b(fb, nst, nkp, 0);
     if (READ && pos >= 4) f.a[pos - 4] = frag_a(fb, nst, nkp, pos - 4);
@@ -314,10 +317,10 @@ __device__ __forceinline__ void pass_mma(v16i acc[4][2], Frag& f, u32 x[8], cons
 
 // The HEAD part of the fold without MFMAs: blocks 8 - FOLD_LAG .. 7 into x (after the k loop,
 // for the last chunk, whose TAIL pass already folded the other blocks).
-__device__ __forceinline__ void fold_head(const v16i acc[4][2], u32 x[8]) {
+__device__ __forceinline__ void fold_head(const v16i acc[4][2], u32 x[4]) {
   static_for<FOLD_LAG>([&](auto ic) UWC_AI {
     constexpr int pos = 8 - FOLD_LAG + decltype(ic)::value, mb = pos & 3, nb = pos >> 2;
-    fold_block(acc[mb][nb], x + (mb >> 1) * 4, false);
+    fold_block(acc[mb][nb], x + (mb >> 1) * 2, false);
   });
 }
 
@@ -332,7 +335,7 @@ __device__ __forceinline__ void pass_mma_db(v16i acc[4][2], const Frag& cur, Fra
   for (int mb = 0; mb < 4; mb++)
 #pragma unroll
     for (int nb = 0; nb < 2; nb++)
-      acc[mb][nb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.a[mb], cur.b[nb], acc[mb][nb], 0, 0, 0);
+      acc[mb][nb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.b[nb], cur.a[mb], acc[mb][nb], 0, 0, 0);
   if constexpr (READ) __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
 #pragma unroll
   for (int i = 0; i < 8; i++) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -353,8 +356,8 @@ __device__ __forceinline__ void step_mma_quarter(v16i tmp[2], const FragBase& fb
     }
 #pragma unroll
     for (int j = 0; j < 2; j++) {
-      tmp[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0[j], b[j], tmp[0], 0, 0, 0);
-      tmp[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1[j], b[j], tmp[1], 0, 0, 0);
+      tmp[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b[j], a0[j], tmp[0], 0, 0, 0);
+      tmp[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b[j], a1[j], tmp[1], 0, 0, 0);
     }
   }
 }
@@ -369,27 +372,27 @@ __device__ __forceinline__ u32 dpp(u32 x) {
   return (u32)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xF, 0xF, true);
 }
 
-// Reduce-scatter of the 8 fold partials over lane bits 0, 3, 4: afterwards the tile XOR of the
-// one tile this lane owns is keep ^ other.
-__device__ __forceinline__ void fold_scatter(const u32 x[8], int lane, u32& keep, u32& other) {
-  const bool b0 = lane & 1, b3 = (lane >> 3) & 1, b4 = (lane >> 4) & 1;
-  u32 y[4], z[2];
+// Reduce-scatter of the 4 fold partials x[2 hm + tb] over lane bits 3, 4 (the lanes holding
+// rows g + 8 i of one tile differ only there): afterwards the XOR of the one tile this lane owns,
+// hash block hm = lane bit 3 and t bit 0 = lane bit 4, is keep ^ other.
+__device__ __forceinline__ void fold_scatter(const u32 x[4], int lane, u32& keep, u32& other) {
+  const bool b3 = (lane >> 3) & 1;
+  u32 y[2];
 #pragma unroll
-  for (int i = 0; i < 4; i++) {  // lane bit 0: keep hash block b0
-    const u32 kp = b0 ? x[4 + i] : x[i], send = b0 ? x[i] : x[4 + i];
-    y[i] = kp ^ dpp<0xB1>(send);  // quad_perm [1,0,3,2]: partner lane ^ 1
+  for (int tb = 0; tb < 2; tb++) {  // lane bit 3: keep hash block b3
+    const u32 kp = b3 ? x[2 + tb] : x[tb], send = b3 ? x[tb] : x[2 + tb];
+    y[tb] = kp ^ dpp<0x128>(send);  // row_ror:8 within a 16-lane row: partner lane ^ 8
   }
-#pragma unroll
-  for (int j = 0; j < 2; j++) {  // lane bit 3: keep g & 3 in {2 b3, 2 b3 + 1}
-    const u32 kp = b3 ? y[2 + j] : y[j], send = b3 ? y[j] : y[2 + j];
-    z[j] = kp ^ dpp<0x128>(send);  // row_ror:8 within a 16-lane row: partner lane ^ 8
-  }
-  keep = b4 ? z[1] : z[0];
-  other = (u32)__builtin_amdgcn_ds_swizzle((int)(b4 ? z[0] : z[1]), 0x401F);  // partner lane ^ 16
+  // lane bit 4: v_permlane16_swap exchanges y[0] of the odd 16-lane rows with y[1] of the even
+  // rows, so a lane of an even row ends with both partners' y[0] and one of an odd row with both
+  // partners' y[1]
+  const auto sw = __builtin_amdgcn_permlane16_swap(y[0], y[1], false, false);
+  keep = sw[0];
+  other = sw[1];
 }
 
 // msg = rotl13(msg) ^ (tile XOR), from the partials.
-__device__ __forceinline__ void fold_into(u32& msg, const u32 x[8], int lane) {
+__device__ __forceinline__ void fold_into(u32& msg, const u32 x[4], int lane) {
   u32 keep, other;
   fold_scatter(x, lane, keep, other);
   msg = xor3(rotl13(msg), keep, other);
@@ -446,9 +449,9 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
   constexpr bool DB = !HASH && W_DB_PLAIN;
   // transcript fold partials, carried from a chunk's TAIL pass to the next chunk's HEAD pass;
   // zero before chunk 0, so the HEAD pass of the first k step folds nothing into slot 15
-  u32 fx[8];
+  u32 fx[4];
 #pragma unroll
-  for (int i = 0; i < 8; i++) fx[i] = 0;
+  for (int i = 0; i < 4; i++) fx[i] = 0;
   Frag fb[DB ? 2 : 1];
   frag_read(fb[0], fbase, 0, 0);
 
@@ -600,8 +603,9 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
       for (int s = 0; s < 16; s++)
         if (s == last) msg[s] = xor3(rotl13(msg[s]), keep, other);
     }
-    // every lane digests the tile it owns: hash block b0, g = 4 (lane >> 5) + 2 b3 + b4, t
-    const int hb = lane & 1, g = 4 * (lane >> 5) + 2 * ((lane >> 3) & 1) + ((lane >> 4) & 1), t = (lane >> 1) & 3;
+    // every lane digests the tile it owns: hash block hb = lane bit 3, g = lane & 7,
+    // t = 2 (lane >> 5) + lane bit 4
+    const int hb = (lane >> 3) & 1, g = lane & 7, t = 2 * (lane >> 5) + ((lane >> 4) & 1);
     u32 key[8], h[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) key[i] = p.key[i];
@@ -633,30 +637,35 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
     for (; kt < KT; kt++) step_rt(NoFold{}, kt, unused, unused);
   }
 
-  // epilogue of one 32 x 32 MFMA block: lane holds col (lane & 31) of rows
-  // 8 (e >> 2) + 4 (lane >> 5) + (e & 3)
+  // epilogue of one 32 x 32 MFMA block: lane holds row (lane & 31) and, in registers 4 j ..
+  // 4 j + 3, columns 8 j + 4 (lane >> 5) .. + 3: one 16-byte (I32, F32) or 8-byte (BF16) store
+  // per j at a wave-uniform base plus a 32-bit lane offset. The host routes outputs whose rows
+  // are not 16-byte aligned (ldc % 4 != 0) to the 128 x 128 kernel.
   auto store_block = [&](int mb, int nb, const v16i& v) UWC_AI {
     if constexpr (OUT != OUT_NONE) {
       constexpr int ES = OUT == OUT_BF16 ? 2 : 4;  // output element bytes
-      // element e of the block is row row0 + 8 (e >> 2) + (e & 3) + lr, column col0 + lc: a
-      // wave-uniform base per e plus one 32-bit lane offset (scalar-base addressing)
       const int row0 = bm0 + wm * 128 + mb * 32, col0 = bn0 + wn * 64 + nb * 32;
-      const int lr = 4 * (lane >> 5), lc = lane & 31;
+      const int lr = lane & 31, lc = 4 * (lane >> 5);
+      u8* base = reinterpret_cast<u8*>(p.out) + ((long)row0 * p.ldc + col0) * ES;
       const u32 loff = (u32)(lr * p.ldc + lc) * ES;
-      float bsc = 0.f;
-      if constexpr (OUT == OUT_BF16 || OUT == OUT_F32) bsc = p.b_scale[col0 + lc];
+      float asc = 0.f;
+      if constexpr (OUT == OUT_BF16 || OUT == OUT_F32) asc = p.a_scale[row0 + lr];
 #pragma unroll
-      for (int e = 0; e < 16; e++) {
-        const int re = row0 + 8 * (e >> 2) + (e & 3);
-        u8* base = reinterpret_cast<u8*>(p.out) + ((long)re * p.ldc + col0) * ES;
+      for (int j = 0; j < 4; j++) {
+        u8* dst = base + loff + 8 * j * ES;
         if constexpr (OUT == OUT_I32) {
-          *reinterpret_cast<i32*>(base + loff) = v[e];
+          *reinterpret_cast<v4i*>(dst) = v4i{v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]};
         } else {
-          const float y = __fmul_rn(__fmul_rn((float)v[e], p.a_scale[re + lr]), bsc);
-          if constexpr (OUT == OUT_F32)
-            *reinterpret_cast<float*>(base + loff) = y;
-          else
-            *reinterpret_cast<uint16_t*>(base + loff) = (uint16_t)bf16_rne(y);
+          float y[4];
+#pragma unroll
+          for (int i = 0; i < 4; i++)
+            y[i] = __fmul_rn(__fmul_rn((float)v[4 * j + i], asc), p.b_scale[col0 + 8 * j + lc + i]);
+          if constexpr (OUT == OUT_F32) {
+            *reinterpret_cast<float4*>(dst) = float4{y[0], y[1], y[2], y[3]};
+          } else {
+            const uint2 w{bf16_rne(y[0]) | (bf16_rne(y[1]) << 16), bf16_rne(y[2]) | (bf16_rne(y[3]) << 16)};
+            *reinterpret_cast<uint2*>(dst) = w;
+          }
         }
       }
     }
