@@ -29,6 +29,7 @@ miner/ampere/bench/bench_gemm.py:37-56). The line also carries:
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import sys
@@ -100,36 +101,45 @@ def mining(args, torch, np, ops):
     # the sweep runs through MinedWeight.forward_many: one batched commitment and one noise launch
     # per group of nonces, then each nonce's projections and hashed GEMM
     w.forward_many([As[i % nbuf] for i in range(args.warmup)], ones, outs=[out] * args.warmup, out_mode=ops.OUT_I32,
-                   group=args.group)
+                   group=args.group, gemm_group=args.gemm_group)
     torch.cuda.synchronize()
     sweep = [As[(args.warmup + i) % nbuf] for i in range(args.steps)]
     t0 = time.perf_counter()
-    w.forward_many(sweep, ones, outs=[out] * args.steps, out_mode=ops.OUT_I32, group=args.group)
+    w.forward_many(sweep, ones, outs=[out] * args.steps, out_mode=ops.OUT_I32, group=args.group,
+                   gemm_group=args.gemm_group)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
 
     # the noisy GEMM alone: HIP events on its stream around back-to-back launches of the sweep's
-    # last GEMM call (same operands, corrections, seed and target). No events sit inside the sweep:
-    # recording one costs the host ~0.2 ms, more than a nonce's GPU time.
-    orig_gemm = ops.gemm
+    # last batched GEMM call (one launch = one group of nonces: same operands, corrections, seeds
+    # and target). No events sit inside the sweep: recording one costs the host ~0.2 ms, more than
+    # a nonce's GPU time.
+    orig_gemm_many = ops.gemm_many
     calls = []
-    ops.gemm = lambda *a, **kw: (calls.append((a, kw)), orig_gemm(*a, **kw))[1]
+    ops.gemm_many = lambda *a, **kw: (calls.append((a, kw)), orig_gemm_many(*a, **kw))[1]
     try:
-        w.forward_many(sweep[-1:], ones, outs=[out], out_mode=ops.OUT_I32)
+        w.forward_many(sweep[-args.group:], ones, outs=[out] * args.group, out_mode=ops.OUT_I32, group=args.group,
+                       gemm_group=args.gemm_group)
     finally:
-        ops.gemm = orig_gemm
+        ops.gemm_many = orig_gemm_many
     a, kw = calls[-1]
+    per_launch = len(a[0])
     reps = gemm_reps(args.steps)
     for _ in range(2):
-        orig_gemm(*a, **kw)
+        orig_gemm_many(*a, **kw)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
-        orig_gemm(*a, **kw)
-    e1.record()
-    torch.cuda.synchronize()
+    gc.disable()  # as forward_many does: no collection pause may starve the GPU between launches
+    try:
+        e0.record()
+        for _ in range(reps):
+            orig_gemm_many(*a, **kw)
+        e1.record()
+        torch.cuda.synchronize()
+    finally:
+        gc.enable()
     dt = t1 - t0
-    kern_ms = e0.elapsed_time(e1) / reps
+    launch_ms = e0.elapsed_time(e1) / reps
+    kern_ms = launch_ms / per_launch  # per nonce
     b = w._buf(m, slot=1)  # forward_many's first slot: an item of the last group
     mx = int(b["maxabs"].max().item())
     L = ops.limbs_for_max(mx)
@@ -137,9 +147,10 @@ def mining(args, torch, np, ops):
     ops_kernel = ops_main + 2.0 * m * n * 2 * r * L
     tops = ops_main * args.steps / dt / 1e12
     kern_tops = ops_kernel / (kern_ms * 1e-3) / 1e12
-    log(f"mining: {dt * 1e3 / args.steps:.3f} ms/nonce, {tops:.1f} TOPS whole path; noisy_gemm {kern_ms * 1e3:.1f} us "
-        f"= {kern_tops:.1f} TOP/s (L={L})")
+    log(f"mining: {dt * 1e3 / args.steps:.3f} ms/nonce, {tops:.1f} TOPS whole path; noisy_gemm {launch_ms * 1e3:.1f} us "
+        f"per launch of {per_launch} nonces = {kern_ms * 1e3:.1f} us per nonce = {kern_tops:.1f} TOP/s (L={L})")
     res = dict(m=m, n=n, k=k, r=r, dt=dt, tops=tops, kern_ms=kern_ms, kern_tops=kern_tops, L=L, w=w, As=As,
+               launch_ms=launch_ms, per_launch=per_launch,
                job_key=job_key, target=target, Bt=Bt)
     return res
 
@@ -613,6 +624,7 @@ def main():
     ap.add_argument("--rank", type=int, default=64)
     ap.add_argument("--distinct", type=int, default=64, help="distinct resident A matrices cycled over")
     ap.add_argument("--group", type=int, default=8, help="nonces per batched commitment / noise launch")
+    ap.add_argument("--gemm-group", type=int, default=8, help="nonces per batched GEMM launch")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--cpu-max-nonces", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true")
@@ -684,8 +696,9 @@ def main():
         "mfma_sustained_tops": ceiling,
         "roofline": {"bound": "mfma", "achieved": round(res["kern_tops"], 2), "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
                      "frac": round(res["kern_tops"] / PEAK_INT8_TOPS, 4), "traffic": read_traffic(),
-                     "kernel": "noisy_gemm256_kernel<HASH=true, DENOISE=true, OUT_I32>", "avg_us": round(res["kern_ms"] * 1e3, 2),
-                     "ops_per_launch": 2 * m * n * k + 2 * m * n * 2 * r * res["L"]},
+                     "kernel": "noisy_gemm256_kernel<HASH=true, DENOISE=true, OUT_I32, SPLIT=true>",
+                     "avg_us": round(res["launch_ms"] * 1e3, 2), "nonces_per_launch": res["per_launch"],
+                     "ops_per_launch": res["per_launch"] * (2 * m * n * k + 2 * m * n * 2 * r * res["L"])},
         "cpu_baseline": cpu,
         "parity": parity,
         "detrt_layer": det,

@@ -441,3 +441,49 @@ def test_forward_many_grouped_equals_forward(dev, group, n_items):
     torch.cuda.synchronize()
     assert all(torch.equal(o, x[0]) for o, x in zip(outs, ref))
     assert set(w.winners(m)) == ref[-1][1]
+
+
+@pytest.mark.parametrize("count,m,n,k,out_mode", [(3, 512, 512, 1024, 1), (17, 256, 512, 512, 1), (2, 256, 256, 1024, 2)])
+def test_gemm_many_equals_single_calls(dev, count, m, n, k, out_mode):
+    """gemm_many (hashed, denoised GEMMs sharing B: the split-role batched kernel for int32 outputs,
+    one launch per item otherwise) gives every item's output and winner set exactly as its own
+    gemm() call does, including batches longer than one launch."""
+    ops = _ops()
+    rng = np.random.default_rng(count * 7 + m + out_mode)
+    r, L = 64, 2
+    B = torch.from_numpy(rng.integers(-64, 65, size=(n, k), dtype=np.int8)).to(dev)
+    As = [torch.from_numpy(rng.integers(-64, 65, size=(m, k), dtype=np.int8)).to(dev) for _ in range(count)]
+    cAs = [torch.from_numpy(rng.integers(-64, 64, size=(L, m, 2 * r), dtype=np.int8)).to(dev) for _ in range(count)]
+    cBs = [torch.from_numpy(rng.integers(-64, 64, size=(L, n, 2 * r), dtype=np.int8)).to(dev) for _ in range(count)]
+    mxs = [torch.tensor([100 + i, 50], dtype=torch.int32, device=dev) for i in range(count)]
+    keys = [ops.words(rng.bytes(32)) for _ in range(count)]
+    target = torch.from_numpy(O.bound_for_wins(m, n, 6).astype(np.uint32).view(np.int32).copy()).to(dev)
+    a_scale = torch.from_numpy(rng.random(m, dtype=np.float32)).to(dev)
+    b_scale = torch.from_numpy(rng.random(n, dtype=np.float32)).to(dev)
+    dt = {1: torch.int32, 2: torch.bfloat16}[out_mode]
+    flags = ops.FLAG_HASH | ops.FLAG_DENOISE
+    nw = 1 + 256 * ops.WIN_WORDS
+
+    def winset(w):
+        words = w.cpu().numpy().view(np.uint32)
+        c = min(int(words[0]), 256)
+        recs = words[1:1 + c * ops.WIN_WORDS].reshape(c, ops.WIN_WORDS)
+        return {(int(x[0]), int(x[1]), x[2:].astype("<u4").tobytes()) for x in recs}
+
+    outs = [torch.empty((m, n), dtype=dt, device=dev) for _ in range(count)]
+    wins = [torch.zeros(nw, dtype=torch.int32, device=dev) for _ in range(count)]
+    ops.gemm_many(As, B, r=r, flags=flags, corrAs=cAs, corrBs=cBs, maxabss=mxs, keys=keys, target=target, winss=wins,
+                  max_wins=256, a_scale=a_scale, b_scale=b_scale, outs=outs, out_mode=out_mode)
+    torch.cuda.synchronize()
+    any_win = False
+    for i in range(count):
+        one = torch.empty((m, n), dtype=dt, device=dev)
+        w1 = torch.zeros(nw, dtype=torch.int32, device=dev)
+        ops.gemm(As[i], B, r=r, flags=flags, corrA=cAs[i], corrB=cBs[i], maxabs=mxs[i], key=keys[i], target=target,
+                 wins=w1, max_wins=256, a_scale=a_scale, b_scale=b_scale, out=one, out_mode=out_mode)
+        torch.cuda.synchronize()
+        assert torch.equal(outs[i].view(torch.int16) if out_mode == 2 else outs[i],
+                           one.view(torch.int16) if out_mode == 2 else one), i
+        assert winset(wins[i]) == winset(w1), i
+        any_win = any_win or bool(winset(w1))
+    assert any_win

@@ -334,11 +334,11 @@ static void launch_out(int out_mode, dim3 grid, hipStream_t s, const GemmParams&
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-extern "C" int uwc_noisy_gemm(const int8_t* A, const int8_t* B, int m, int n, int k, int r, const int8_t* corrA,
-                              const int8_t* corrB, const int32_t* maxabs, int lmax, const uint32_t* key,
-                              const uint32_t* target, uint32_t* wins, int max_wins, const float* a_scale,
-                              const float* b_scale, void* out, int out_mode, int flags, uint32_t* tile_dump,
-                              hipStream_t stream) {
+// The argument checks of uwc_noisy_gemm (status 0 or UWC_EINVAL with the message set).
+static int gemm_check(const int8_t* A, const int8_t* B, int m, int n, int k, int r, const int8_t* corrA,
+                      const int8_t* corrB, const int32_t* maxabs, int lmax, const uint32_t* key, const uint32_t* target,
+                      uint32_t* wins, int max_wins, const float* a_scale, const float* b_scale, void* out, int out_mode,
+                      int flags) {
   const bool hash = flags & FLAG_HASH, denoise = flags & FLAG_DENOISE;
   if (flags & ~(FLAG_HASH | FLAG_DENOISE | FLAG_TILE128)) return uwc_fail("uwc_noisy_gemm: unknown flags %d", flags);
   if (!A || !B || m <= 0 || n <= 0 || k <= 0) return uwc_fail("uwc_noisy_gemm: empty or null operands (m=%d n=%d k=%d)", m, n, k);
@@ -361,6 +361,18 @@ extern "C" int uwc_noisy_gemm(const int8_t* A, const int8_t* B, int m, int n, in
     if (lmax < 1 || lmax > 4) return uwc_fail("uwc_noisy_gemm: lmax=%d outside 1..4", lmax);
     if (!aligned16(corrA) || !aligned16(corrB)) return uwc_fail("uwc_noisy_gemm: corrA/corrB must be 16-byte aligned");
   }
+  return 0;
+}
+
+extern "C" int uwc_noisy_gemm(const int8_t* A, const int8_t* B, int m, int n, int k, int r, const int8_t* corrA,
+                              const int8_t* corrB, const int32_t* maxabs, int lmax, const uint32_t* key,
+                              const uint32_t* target, uint32_t* wins, int max_wins, const float* a_scale,
+                              const float* b_scale, void* out, int out_mode, int flags, uint32_t* tile_dump,
+                              hipStream_t stream) {
+  if (int st = gemm_check(A, B, m, n, k, r, corrA, corrB, maxabs, lmax, key, target, wins, max_wins, a_scale, b_scale,
+                          out, out_mode, flags))
+    return st;
+  const bool hash = flags & FLAG_HASH, denoise = flags & FLAG_DENOISE;
   const bool plain = !hash && !denoise;
   if (plain && m <= 64 && out_mode != OUT_NONE && !(flags & FLAG_TILE128))
     return uwc_skinny_gemm(A, B, m, n, k, a_scale, b_scale, out, out_mode, stream);
@@ -408,4 +420,49 @@ extern "C" int uwc_igemm_dequant_f32(const int8_t* A, const int8_t* B, int m, in
                                      const float* sw, float* Y, hipStream_t stream) {
   return uwc_noisy_gemm(A, B, m, n, k, 0, nullptr, nullptr, nullptr, 0, nullptr, nullptr, nullptr, 0, sx, sw, Y,
                         OUT_F32, 0, nullptr, stream);
+}
+
+int uwc_noisy_gemm256_many(int count, const int8_t* const* A, const int8_t* B, int m, int n, int k, int r,
+                           const int8_t* const* corrA, const int8_t* const* corrB, const int32_t* const* maxabs,
+                           int lmax, const uint32_t* const* key, const uint32_t* target, uint32_t* const* wins,
+                           int max_wins, void* const* out, hipStream_t stream);
+
+#define GEMM_MANY_MAX 16  // items per split launch (the kernel's item table)
+
+extern "C" int uwc_noisy_gemm_many(int count, const int8_t* const* A, const int8_t* B, int m, int n, int k, int r,
+                                   const int8_t* const* corrA, const int8_t* const* corrB,
+                                   const int32_t* const* maxabs, int lmax, const uint32_t* const* key,
+                                   const uint32_t* target, uint32_t* const* wins, int max_wins, const float* a_scale,
+                                   const float* b_scale, void* const* out, int out_mode, int flags,
+                                   hipStream_t stream) {
+  if (count < 0 || (count > 0 && (!A || !out))) return uwc_fail("uwc_noisy_gemm_many: count=%d or null A / out arrays", count);
+  const bool hash = flags & FLAG_HASH, denoise = flags & FLAG_DENOISE;
+  if ((hash && !key) || (denoise && (!corrA || !corrB || !maxabs)))
+    return uwc_fail("uwc_noisy_gemm_many: the flags need key / corrA, corrB, maxabs arrays");
+  bool split = count >= 2 && hash && denoise && out_mode == OUT_I32 && !(flags & FLAG_TILE128) && m % 256 == 0 &&
+               n % 256 == 0 && k % 128 == 0 && k <= (1 << 24);
+  for (int i = 0; i < count; i++) {
+    if (int st = gemm_check(A[i], B, m, n, k, r, denoise ? corrA[i] : nullptr, denoise ? corrB[i] : nullptr,
+                            denoise ? maxabs[i] : nullptr, lmax, hash ? key[i] : nullptr, target,
+                            wins ? wins[i] : nullptr, max_wins, a_scale, b_scale, out[i], out_mode, flags))
+      return st;
+    split = split && aligned16(out[i]);
+  }
+  if (!split) {  // one launch per item
+    for (int i = 0; i < count; i++)
+      if (int st = uwc_noisy_gemm(A[i], B, m, n, k, r, denoise ? corrA[i] : nullptr, denoise ? corrB[i] : nullptr,
+                                  denoise ? maxabs[i] : nullptr, lmax, hash ? key[i] : nullptr, target,
+                                  wins ? wins[i] : nullptr, max_wins, a_scale, b_scale, out[i], out_mode, flags,
+                                  nullptr, stream))
+        return st;
+    return 0;
+  }
+  uint32_t* no_wins[GEMM_MANY_MAX] = {};
+  for (int i0 = 0; i0 < count; i0 += GEMM_MANY_MAX) {
+    const int c = count - i0 < GEMM_MANY_MAX ? count - i0 : GEMM_MANY_MAX;
+    if (int st = uwc_noisy_gemm256_many(c, A + i0, B, m, n, k, r, corrA + i0, corrB + i0, maxabs + i0, lmax, key + i0,
+                                        target, wins ? wins + i0 : no_wins, max_wins, out + i0, stream))
+      return st;
+  }
+  return 0;
 }

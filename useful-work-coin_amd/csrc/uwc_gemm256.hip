@@ -47,8 +47,9 @@
 #define W_THREADS 512
 #define W_TILE (W_BM * W_BK)                 // bytes of one operand tile
 #define W_BOFF (W_STAGES * W_TILE)           // LDS byte offset of the ring's B tiles
-#define W_LDS (2 * W_STAGES * W_TILE)        // at most 160 KiB (gfx950 LDS per workgroup)
-static_assert(W_LDS <= 160 * 1024, "LDS ring exceeds 160 KiB");
+#define W_LDS (2 * W_STAGES * W_TILE)        // the ring
+#define W_LDS_HANDOFF (W_THREADS / 128 * 8192)  // the split kernels' hand-off slots (a quarter per loader)
+static_assert(W_LDS + W_LDS_HANDOFF <= 160 * 1024, "LDS exceeds 160 KiB (gfx950 LDS per workgroup)");
 #define W_WAVES (W_THREADS / 64)
 #define W_SEGS_PER_WAVE (W_TILE / 1024 / W_WAVES)  // 1 KiB DMA segments per wave per operand per k step
 #ifndef W_DB_PLAIN
@@ -70,23 +71,32 @@ static_assert(W_LDS <= 160 * 1024, "LDS ring exceeds 160 KiB");
 #define WIN_WORDS 10
 #define DUMP_WORDS 24
 
-struct Gemm256Params {
+// One item of a launch: a nonce's operand, corrections, seed, win records and output. Every item
+// shares B, the shape, the target and the scales; a launch runs its items one after another on
+// the same tiles.
+#define G256_MAXB 16
+struct Gemm256Item {
   const i8* A;
-  const i8* B;
-  int m, n, k, r;
   const i8* corrA;
   const i8* corrB;
   const i32* maxabs;
-  int lmax;
   const u32* key;
-  const u32* target;
   u32* wins;
+  void* out;
+};
+
+struct Gemm256Params {
+  const i8* B;
+  int m, n, k, r;
+  int lmax;
+  const u32* target;
   int max_wins;
   const float* a_scale;
   const float* b_scale;
-  void* out;
   u32* dump;
   int ldc;  // output row stride in elements
+  int count;
+  Gemm256Item it[G256_MAXB];
 };
 
 // f(std::integral_constant<int, i>) for i = 0 .. N - 1, each i a compile-time constant.
@@ -100,6 +110,15 @@ __device__ __forceinline__ void static_for_(F&& f) {
 template <int N, class F>
 __device__ __forceinline__ void static_for(F&& f) {
   static_for_<0, N>(f);
+}
+
+// A word the launch only reads, written by an earlier launch (seeds, targets, maxabs), loaded
+// through the constant address space: a scalar load, counted in lgkmcnt. A vector load would
+// make the compiler wait on vmcnt, which in a split kernel's storer wave also counts the output
+// stores still draining.
+template <class T>
+__device__ __forceinline__ T ld_uniform(const T* ptr, int i) {
+  return ((const __attribute__((address_space(4))) T*)(uintptr_t)ptr)[i];
 }
 
 typedef const void __attribute__((address_space(1)))* gptr_t;
@@ -144,12 +163,13 @@ __device__ __forceinline__ void dma16(const void* g, u32 lds) {
 
 __device__ __forceinline__ u32 lds_addr(const u8* p) { return (u32)(uintptr_t)(lptr_t)p; }
 
-// Issue this wave's DMA segments of one k step (segments wave * SPW .. of A and of B) into the
-// LDS tiles at byte addresses lds_a, lds_b (wave-uniform).
+// Issue this wave's DMA segments of one k step (segments SPL wave .. SPL wave + SPL - 1 of A and
+// of B) into the LDS tiles at byte addresses lds_a, lds_b (wave-uniform).
+template <int SPL>
 __device__ __forceinline__ void dma_step(u32 lds_a, u32 lds_b, const DmaLane& d, long lda, long ldb, long k0, int wave) {
 #pragma unroll
-  for (int t = 0; t < W_SEGS_PER_WAVE; t++) {
-    const int s = W_SEGS_PER_WAVE * wave + t;
+  for (int t = 0; t < SPL; t++) {
+    const int s = SPL * wave + t;
     const int c = d.phys ^ swz(W_RPS * s + d.rin);
     const long off = (long)W_RPS * s;
     dma16(d.a + off * lda + k0 + c * 16, __builtin_amdgcn_readfirstlane(lds_a + s * 1024));
@@ -163,18 +183,22 @@ __device__ __forceinline__ void dma16s(u32 voff, const void* sbase, u32 lds) {
 }
 
 // Lane byte offsets of the main loop's DMA segments within a 256-row window of a k-contiguous
-// operand with row stride k (the same for A and B): segment s = SPW wave + t, tile row
-// RPS s + i / W_CH, physical chunk i % W_CH = logical chunk (i % W_CH) ^ swz(row).
+// operand with row stride k (the same for A and B): segment s = SPL wave + t, tile row
+// RPS s + i / W_CH, physical chunk i % W_CH = logical chunk (i % W_CH) ^ swz(row). SPL is the
+// number of 1 KiB segments per loading wave per operand and k step: W_SEGS_PER_WAVE when every
+// wave loads, twice that when only half of them do.
+template <int SPL>
 struct DmaOff {
-  u32 v[W_SEGS_PER_WAVE];
+  u32 v[SPL];
 };
 
-__device__ __forceinline__ DmaOff dma_offsets(long k, int wave, int lane) {
-  DmaOff d;
+template <int SPL>
+__device__ __forceinline__ DmaOff<SPL> dma_offsets(long k, int wave, int lane) {
+  DmaOff<SPL> d;
   const int rin = lane / W_CH, phys = lane % W_CH;
 #pragma unroll
-  for (int t = 0; t < W_SEGS_PER_WAVE; t++) {
-    const int row = W_RPS * (W_SEGS_PER_WAVE * wave + t) + rin;
+  for (int t = 0; t < SPL; t++) {
+    const int row = W_RPS * (SPL * wave + t) + rin;
     d.v[t] = (u32)((long)row * k + ((phys ^ swz(row)) << 4));
   }
   return d;
@@ -182,26 +206,30 @@ __device__ __forceinline__ DmaOff dma_offsets(long k, int wave, int lane) {
 
 // Segments [T0, T1) of one k step of the main loop's DMA: a_win = A + bm0 k + k0 and
 // b_win = B + bn0 k + k0 are wave-uniform (SGPRs).
-template <int T0 = 0, int T1 = W_SEGS_PER_WAVE>
-__device__ __forceinline__ void dma_step_s(u32 lds_a, u32 lds_b, const DmaOff& d, const i8* a_win, const i8* b_win,
+template <int SPL, int T0, int T1>
+__device__ __forceinline__ void dma_step_s(u32 lds_a, u32 lds_b, const DmaOff<SPL>& d, const i8* a_win, const i8* b_win,
                                            int wave) {
 #pragma unroll
   for (int t = T0; t < T1; t++) {
-    const u32 so = (u32)(W_SEGS_PER_WAVE * wave + t) * 1024u;
+    const u32 so = (u32)(SPL * wave + t) * 1024u;
     dma16s(d.v[t], a_win, lds_a + so);
     dma16s(d.v[t], b_win, lds_b + so);
   }
 }
 
-// Wait until at most `younger` of this wave's k steps are still loading, then barrier.
-__device__ __forceinline__ void wait_step(int younger) {
-  constexpr int per = 2 * W_SEGS_PER_WAVE;  // DMA instructions per wave per k step
+// Wait until at most `younger` of this wave's k steps are still loading (a loading wave, vm), then
+// barrier. A wave that issues no DMA only takes the barrier: its vmcnt counts nothing but its
+// own output stores, which it never needs to wait for.
+template <int SPL>
+__device__ __forceinline__ void wait_step(int younger, bool vm) {
+  constexpr int per = 2 * SPL;  // DMA instructions per loading wave per k step
   static_assert((W_STAGES - 1) * per < 64, "vmcnt is 6 bits");
-  if (younger >= 4) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * per) : "memory");
-  else if (younger == 3) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * per) : "memory");
-  else if (younger == 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * per) : "memory");
-  else if (younger == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(per) : "memory");
-  else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if (vm) {
+    if (younger >= 3) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * per) : "memory");
+    else if (younger == 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * per) : "memory");
+    else if (younger == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(per) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
   __builtin_amdgcn_s_barrier();
 }
 
@@ -416,237 +444,43 @@ __device__ __forceinline__ void tile256(int m, int n, int& bm0, int& bn0) {
   bn0 = (in / gsz) * W_BN;
 }
 
-template <bool HASH, bool DENOISE, int OUT>
+// SPLIT: the launch's items follow each other on the same tiles, and the output stores of item
+// i drain while item i + 1 computes. On gfx9 a wave's vmcnt counts its stores as well as its
+// loads, so a wave that waits on vmcnt for its LDS DMA cannot leave stores in flight. Waves
+// 0 .. 3 (loaders, one per SIMD) therefore issue all the DMA and never store an output; waves
+// 4 .. 7 (storers) issue no DMA, never wait on vmcnt, and store their own results and, through
+// the idle ring, those of loader wave - 4 (64 sixteen-byte stores per lane and item).
+template <bool HASH, bool DENOISE, int OUT, bool SPLIT = false>
 __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params p) {
   extern __shared__ __attribute__((aligned(1024))) u8 wsm[];
   // the wave index is uniform: readfirstlane keeps everything derived from it scalar
-  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tid = threadIdx.x, lane0 = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 2, wn = wave & 3;
+  constexpr int SPL = SPLIT ? 2 * W_SEGS_PER_WAVE : W_SEGS_PER_WAVE;  // DMA segments per loading wave
+  static_assert(SPL >= 4 && SPL % 4 == 0, "the refill spread takes halves and quarters of a wave's segments");
+  const bool is_loader = !SPLIT || wave < W_WAVES / 2;
   int bm0, bn0;
   tile256(p.m, p.n, bm0, bn0);
   const long k = p.k;
   const int KT = p.k / W_BK;
-
-  v16i acc[4][2];
-#pragma unroll
-  for (int i = 0; i < 4; i++)
-#pragma unroll
-    for (int j = 0; j < 2; j++) acc[i][j] = v16i{};
-
   const u32 wsm_l = __builtin_amdgcn_readfirstlane(lds_addr(wsm));
   auto lds_a = [&](int st) UWC_AI { return wsm_l + (u32)(st * W_TILE); };           // stage st's A tile
   auto lds_b = [&](int st) UWC_AI { return wsm_l + (u32)(W_BOFF + st * W_TILE); };  // and its B tile
-  const FragBase fbase = frag_bases(wsm_l, wm, wn, lane);
-  const DmaOff doff = dma_offsets(k, wave, lane);
-  const i8* a_win = p.A + (long)bm0 * k;  // + k0: this workgroup's operand windows
   const i8* b_win = p.B + (long)bn0 * k;
-  // prologue: every stage of the ring loading, then step 0 resident and its first pass read
-#pragma unroll
-  for (int s = 0; s < W_STAGES; s++)
-    if (s < KT) dma_step_s(lds_a(s), lds_b(s), doff, a_win + s * W_BK, b_win + s * W_BK, wave);
-  wait_step(min(KT - 1, W_STAGES - 1));
   // fragment sets: single set streamed (pass_mma) or two alternating sets (pass_mma_db)
   constexpr bool DB = !HASH && W_DB_PLAIN;
-  // transcript fold partials, carried from a chunk's TAIL pass to the next chunk's HEAD pass;
-  // zero before chunk 0, so the HEAD pass of the first k step folds nothing into slot 15
-  u32 fx[4];
-#pragma unroll
-  for (int i = 0; i < 4; i++) fx[i] = 0;
-  Frag fb[DB ? 2 : 1];
-  frag_read(fb[0], fbase, 0, 0);
-
-  // One k step. Pass kp runs its MFMAs on the fragments in `cur` while reading those of pass
-  // kp + 1. Before the last pass the wave waits for step kt + 1 (vmcnt + barrier: every wave is
-  // then done reading step kt's stage) and refills that stage with step kt + W_STAGES; the last
-  // pass reads the next step's first fragments (on the final step that read of a resident stage
-  // is unused, which keeps the MFMA code free of branches). FM bit kp: pass kp is the HEAD pass
-  // of a chunk (it finishes the fold of the chunk that ended with the previous pass and folds it
-  // into m0 for kp == 0, else m1); FM bit 4 + kp: pass kp is the TAIL pass of a chunk. The stage
-  // index ST == kt % W_STAGES is a compile-time constant, so every LDS address of the step is a
-  // base register plus an immediate.
-  auto step = [&](auto fm, auto stc, int kt, u32& m0, u32& m1) UWC_AI {
-    constexpr int FM = decltype(fm)::value, ST = decltype(stc)::value;
-    static_for<W_KP>([&](auto kpc) UWC_AI {
-      constexpr int kp = decltype(kpc)::value;
-      constexpr bool head = ((FM >> kp) & 1) != 0, tail = ((FM >> (4 + kp)) & 1) != 0;
-      constexpr int nst = kp + 1 == W_KP ? (ST + 1) % W_STAGES : ST;
-      constexpr int nkp = kp + 1 == W_KP ? 0 : kp + 1;
-#if W_DMA_SPREAD
-      // the refill of the previous step's stage, continued: segment 2 before pass 0, segment 3
-      // before pass 1 (the first half went out after the previous step's barrier)
-      if constexpr (kp < 2 && W_SEGS_PER_WAVE == 4) {
-        if (kt >= 1 && kt - 1 + W_STAGES < KT) {
-          constexpr int PST = (ST + W_STAGES - 1) % W_STAGES;
-          const long k0 = (long)(kt - 1 + W_STAGES) * W_BK;
-          dma_step_s<2 + kp, 3 + kp>(lds_a(PST), lds_b(PST), doff, a_win + k0, b_win + k0, wave);
-        }
-      }
-#endif
-      if constexpr (kp + 1 == W_KP) {
-        if (kt + 1 < KT) {
-          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this stage's reads are complete
-          wait_step(min(KT - 2 - kt, W_STAGES - 2));
-          if (kt + W_STAGES < KT) {
-            const long k0 = (long)(kt + W_STAGES) * W_BK;
-#if W_DMA_SPREAD
-            if constexpr (W_SEGS_PER_WAVE == 4)
-              dma_step_s<0, 2>(lds_a(ST), lds_b(ST), doff, a_win + k0, b_win + k0, wave);
-            else
-#endif
-            dma_step_s(lds_a(ST), lds_b(ST), doff, a_win + k0, b_win + k0, wave);
-          }
-        }
-      }
-      if constexpr (DB) {
-        static_assert(FM == 0, "the double-buffered passes carry no transcript fold");
-        pass_mma_db<true>(acc, fb[kp & 1], fb[(kp + 1) & 1], fbase, nst, nkp);
-      } else {
-        pass_mma<head, tail, true>(acc, fb[0], fx, fbase, nst, nkp);
-      }
-      if constexpr (head) fold_into(kp == 0 ? m0 : m1, fx, lane);
-    });
-  };
-  // step() for a k step whose stage is known only at run time
-  auto step_rt = [&](auto fm, int kt, u32& m0, u32& m1) UWC_AI {
-    static_for<W_STAGES>([&](auto stc) UWC_AI {
-      if (kt % W_STAGES == decltype(stc)::value) step(fm, stc, kt, m0, m1);
-    });
-  };
   using NoFold = std::integral_constant<int, 0>;
 
-  // Denoise setup (kernels.cu:598-673): acc -= sum_li 128^li [X_li | EAL] [EBRt | Y_li]^T, the
-  // corr k steps running limb L-1 down to 0, each limb 2r / W_BK steps. CT steps in all.
-  int L = 1, CPL = 1, CT = 1;
-  long R2 = 0;
-  if constexpr (DENOISE) {
-    const int mx = max(p.maxabs[0], p.maxabs[1]);
-    L = min(mx > 1040319 ? 4 : mx > 8127 ? 3 : mx > 63 ? 2 : 1, p.lmax);
-    R2 = 2L * p.r;
-    CPL = (int)(R2 / W_BK);
-    CT = L * CPL;
-  }
-  // next corr step to issue: global index ig, limb li, chunk kc
-  int ig = 0, li = L - 1, kc = 0;
-  auto cissue = [&]() UWC_AI {
-    const DmaLane cl = dma_lane(p.corrA + (long)li * p.m * R2, R2, p.corrB + (long)li * p.n * R2, R2, bm0, bn0, lane);
-    dma_step(lds_a(ig % W_STAGES), lds_b(ig % W_STAGES), cl, R2, R2, (long)kc * W_BK, wave);
-    ig++;
-    if (++kc == CPL) {
-      kc = 0;
-      li = li == 0 ? L - 1 : li - 1;
-    }
-  };
-
-  if constexpr (HASH) {
-    u32 msg[16];
-#pragma unroll
-    for (int w = 0; w < 16; w++) msg[w] = 0;
-    const int nchunks = p.k / p.r;
-    int kt = 0;
-    u32 unused = 0;
-    // The fold of chunk c ends in the first pass of chunk c + 1 (slot (c - 1) mod 16 for the
-    // chunk starting at slot c). For chunk 0 that folds the all-zero partials into the all-zero
-    // slot 15, which leaves it zero.
-    using Head = std::integral_constant<int, 0x01>;
-    using Tail = std::integral_constant<int, 0x80>;
-    if (p.r == W_BK) {
-      // one k step per chunk: an outer iteration is 16 k steps, so k step c0 + s sits in stage
-      // s % W_STAGES
-      static_assert(16 % W_STAGES == 0, "stage of an unrolled k step");
-      for (int c0 = 0; c0 < nchunks; c0 += 16) {
-        static_for<16>([&](auto sc) UWC_AI {
-          constexpr int s = decltype(sc)::value;
-          if (c0 + s < nchunks)
-            step(std::integral_constant<int, 0x81>{}, std::integral_constant<int, s % W_STAGES>{}, c0 + s,
-                 msg[(s + 15) & 15], unused);
-        });
-      }
-    } else if (p.r > W_BK) {
-      const int tpc = p.r / W_BK;
-      for (int c0 = 0; c0 < nchunks; c0 += 16) {
-#pragma unroll
-        for (int s = 0; s < 16; s++) {
-          if (c0 + s < nchunks) {
-            step_rt(Head{}, kt++, msg[(s + 15) & 15], unused);
-            for (int i = 1; i + 1 < tpc; i++) step_rt(NoFold{}, kt++, unused, unused);
-            step_rt(Tail{}, kt++, unused, unused);
-          }
-        }
-      }
-    } else if constexpr (W_KP == 4) {
-      // r = 64 = W_BK / 2: k step j holds chunks 2j (passes 0, 1) and 2j + 1 (passes 2, 3); an
-      // outer iteration is 8 k steps, so k step c0 / 2 + s / 2 sits in stage (s / 2) % W_STAGES
-      static_assert(8 % W_STAGES == 0, "stage of an unrolled k step");
-      for (int c0 = 0; c0 < nchunks; c0 += 16) {
-        static_for<8>([&](auto jc) UWC_AI {
-          constexpr int j = decltype(jc)::value, s = 2 * j;
-          if (c0 + s < nchunks)
-            step(std::integral_constant<int, 0xA5>{}, std::integral_constant<int, j % W_STAGES>{}, c0 / 2 + j,
-                 msg[(s + 15) & 15], msg[s]);
-        });
-      }
-    }
-    // The ring is idle now: when every corr step fits it, start loading them so that their
-    // latency hides behind the digest (every wave has finished its LDS reads at the barrier; the
-    // k loop's last wait left no DMA in flight).
-    if (DENOISE && CT <= W_STAGES) {
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      __builtin_amdgcn_s_barrier();
-      for (int t = 0; t < CT; t++) cissue();  // corr step t -> stage t
-    }
-    {  // the last chunk: its TAIL pass was the k loop's last pass
-      u32 keep, other;
-      fold_head(acc, fx);
-      fold_scatter(fx, lane, keep, other);
-      const int last = (nchunks - 1) & 15;
-#pragma unroll
-      for (int s = 0; s < 16; s++)
-        if (s == last) msg[s] = xor3(rotl13(msg[s]), keep, other);
-    }
-    // every lane digests the tile it owns: hash block hb = lane bit 3, g = lane & 7,
-    // t = 2 (lane >> 5) + lane bit 4
-    const int hb = (lane >> 3) & 1, g = lane & 7, t = 2 * (lane >> 5) + ((lane >> 4) & 1);
-    u32 key[8], h[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) key[i] = p.key[i];
-    b3_keyed64(key, msg, h);
-    const int row = bm0 + wm * 128 + hb * 64 + g, col = bn0 + wn * 64 + 2 * t;
-    if (p.dump) {
-      const long NB = p.n / 64;
-      u32* d = p.dump + ((((long)(row >> 6) * 8 + g) * NB + (col >> 6)) * 4 + t) * DUMP_WORDS;
-#pragma unroll
-      for (int w = 0; w < 16; w++) d[w] = msg[w];
-#pragma unroll
-      for (int w = 0; w < 8; w++) d[16 + w] = h[w];
-    }
-    if (p.wins && u256_le(h, p.target)) {
-      const u32 slot = atomicAdd(p.wins, 1u);
-      if (slot < (u32)p.max_wins) {
-        u32* rec = p.wins + 1 + slot * WIN_WORDS;
-        rec[0] = row;
-        rec[1] = col;
-#pragma unroll
-        for (int i = 0; i < 8; i++) rec[2 + i] = h[i];
-      }
-    }
-  } else {
-    u32 unused = 0;
-    int kt = 0;
-    for (; kt + W_STAGES <= KT; kt += W_STAGES)
-      static_for<W_STAGES>([&](auto stc) UWC_AI { step(NoFold{}, stc, kt + decltype(stc)::value, unused, unused); });
-    for (; kt < KT; kt++) step_rt(NoFold{}, kt, unused, unused);
-  }
-
-  // epilogue of one 32 x 32 MFMA block: lane holds row (lane & 31) and, in registers 4 j ..
-  // 4 j + 3, columns 8 j + 4 (lane >> 5) .. + 3: one 16-byte (I32, F32) or 8-byte (BF16) store
-  // per j at a wave-uniform base plus a 32-bit lane offset. The host routes outputs whose rows
-  // are not 16-byte aligned (ldc % 4 != 0) to the 128 x 128 kernel.
-  auto store_block = [&](int mb, int nb, const v16i& v) UWC_AI {
+  // epilogue of one 32 x 32 MFMA block of wave (swm, swn): lane holds row (lane & 31) and, in
+  // registers 4 j .. 4 j + 3, columns 8 j + 4 (lane >> 5) .. + 3: one 16-byte (I32, F32) or
+  // 8-byte (BF16) store per j at a wave-uniform base plus a 32-bit lane offset. The host routes
+  // outputs whose rows are not 16-byte aligned (ldc % 4 != 0) to the 128 x 128 kernel.
+  auto store_block = [&](int lane, void* out, int swm, int swn, int mb, int nb, const v16i& v) UWC_AI {
     if constexpr (OUT != OUT_NONE) {
       constexpr int ES = OUT == OUT_BF16 ? 2 : 4;  // output element bytes
-      const int row0 = bm0 + wm * 128 + mb * 32, col0 = bn0 + wn * 64 + nb * 32;
+      const int row0 = bm0 + swm * 128 + mb * 32, col0 = bn0 + swn * 64 + nb * 32;
       const int lr = lane & 31, lc = 4 * (lane >> 5);
-      u8* base = reinterpret_cast<u8*>(p.out) + ((long)row0 * p.ldc + col0) * ES;
+      u8* base = reinterpret_cast<u8*>(out) + ((long)row0 * p.ldc + col0) * ES;
       const u32 loff = (u32)(lr * p.ldc + lc) * ES;
       float asc = 0.f;
       if constexpr (OUT == OUT_BF16 || OUT == OUT_F32) asc = p.a_scale[row0 + lr];
@@ -671,79 +505,360 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
     }
   };
 
-  if constexpr (DENOISE) {
-    // Four passes over quarters of the wave's block keep the Horner accumulator at 32 registers;
-    // each quarter is stored as soon as it is final. When all CT corr steps fit in the ring
-    // (L * 2r <= W_STAGES * W_BK: the mining shapes) they are loaded once (the hashing kernels
-    // issued them before the digest) and the four passes read them without further barriers;
-    // otherwise they stream through the ring continuously across the passes (global step g is
-    // corr step g mod CT).
-    const int GT = 4 * CT;
-    if (CT <= W_STAGES) {
-      if constexpr (!HASH) {
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the k loop's last fragment reads
+  const int count = SPLIT ? p.count : 1;  // the single-item kernels compile without the item loop
+  // One item, for a wave of role LOADER (a compile-time constant, so that neither role's code
+  // carries the other's branches or registers; both take the same barriers in the same order).
+  auto run_item = [&](int item, auto role) UWC_AI {
+    constexpr bool loader = decltype(role)::value;
+    const Gemm256Item& I = p.it[item];
+    // The lane index through an opaque zero: everything derived from it is recomputed per item
+    // instead of being hoisted out of the item loop and kept live across it.
+    int z;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+    const int lane = lane0 + z;
+    const FragBase fbase = frag_bases(wsm_l, wm, wn, lane);
+    const DmaOff<SPL> doff = dma_offsets<SPL>(k, wave, lane);
+    v16i acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < 2; j++) acc[i][j] = v16i{};
+    const i8* a_win = I.A + (long)bm0 * k;  // + k0: this workgroup's operand windows
+    // prologue: every stage of the ring loading, then step 0 resident and its first pass read
+    if constexpr (loader) {
+#pragma unroll
+      for (int s = 0; s < W_STAGES; s++)
+        if (s < KT) dma_step_s<SPL, 0, SPL>(lds_a(s), lds_b(s), doff, a_win + s * W_BK, b_win + s * W_BK, wave);
+    }
+    wait_step<SPL>(min(KT - 1, W_STAGES - 1), loader);
+    // transcript fold partials, carried from a chunk's TAIL pass to the next chunk's HEAD pass;
+    // zero before chunk 0, so the HEAD pass of the first k step folds nothing into slot 15
+    u32 fx[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) fx[i] = 0;
+    Frag fb[DB ? 2 : 1];
+    frag_read(fb[0], fbase, 0, 0);
+
+    // One k step. Pass kp runs its MFMAs on the fragments in `cur` while reading those of pass
+    // kp + 1. Before the last pass the wave waits for step kt + 1 (vmcnt + barrier: every wave
+    // is then done reading step kt's stage) and the loaders refill that stage with step
+    // kt + W_STAGES; the last pass reads the next step's first fragments (on the final step that
+    // read of a resident stage is unused, which keeps the MFMA code free of branches). FM bit
+    // kp: pass kp is the HEAD pass of a chunk (it finishes the fold of the chunk that ended with
+    // the previous pass and folds it into m0 for kp == 0, else m1); FM bit 4 + kp: pass kp is the
+    // TAIL pass of a chunk. The stage index ST == kt % W_STAGES is a compile-time constant, so
+    // every LDS address of the step is a base register plus an immediate.
+    auto step = [&](auto fm, auto stc, int kt, u32& m0, u32& m1) UWC_AI {
+      constexpr int FM = decltype(fm)::value, ST = decltype(stc)::value;
+      constexpr int H = SPL / 2, Q = SPL / 4;
+      static_for<W_KP>([&](auto kpc) UWC_AI {
+        constexpr int kp = decltype(kpc)::value;
+        constexpr bool head = ((FM >> kp) & 1) != 0, tail = ((FM >> (4 + kp)) & 1) != 0;
+        constexpr int nst = kp + 1 == W_KP ? (ST + 1) % W_STAGES : ST;
+        constexpr int nkp = kp + 1 == W_KP ? 0 : kp + 1;
+#if W_DMA_SPREAD
+        // the refill of the previous step's stage, continued: the third quarter of the segments
+        // before pass 0, the last quarter before pass 1 (the first half went out after the
+        // previous step's barrier)
+        if constexpr (kp < 2) {
+          if (loader && kt >= 1 && kt - 1 + W_STAGES < KT) {
+            constexpr int PST = (ST + W_STAGES - 1) % W_STAGES;
+            const long k0 = (long)(kt - 1 + W_STAGES) * W_BK;
+            dma_step_s<SPL, H + kp * Q, H + (kp + 1) * Q>(lds_a(PST), lds_b(PST), doff, a_win + k0, b_win + k0, wave);
+          }
+        }
+#endif
+        if constexpr (kp + 1 == W_KP) {
+          if (kt + 1 < KT) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this stage's reads are complete
+            wait_step<SPL>(min(KT - 2 - kt, W_STAGES - 2), loader);
+            if (loader && kt + W_STAGES < KT) {
+              const long k0 = (long)(kt + W_STAGES) * W_BK;
+#if W_DMA_SPREAD
+              dma_step_s<SPL, 0, H>(lds_a(ST), lds_b(ST), doff, a_win + k0, b_win + k0, wave);
+#else
+              dma_step_s<SPL, 0, SPL>(lds_a(ST), lds_b(ST), doff, a_win + k0, b_win + k0, wave);
+#endif
+            }
+          }
+        }
+        if constexpr (DB) {
+          static_assert(FM == 0, "the double-buffered passes carry no transcript fold");
+          pass_mma_db<true>(acc, fb[kp & 1], fb[(kp + 1) & 1], fbase, nst, nkp);
+        } else {
+          pass_mma<head, tail, true>(acc, fb[0], fx, fbase, nst, nkp);
+        }
+        if constexpr (head) fold_into(kp == 0 ? m0 : m1, fx, lane);
+      });
+    };
+    // step() for a k step whose stage is known only at run time
+    auto step_rt = [&](auto fm, int kt, u32& m0, u32& m1) UWC_AI {
+      static_for<W_STAGES>([&](auto stc) UWC_AI {
+        if (kt % W_STAGES == decltype(stc)::value) step(fm, stc, kt, m0, m1);
+      });
+    };
+
+    // Denoise setup (kernels.cu:598-673): acc -= sum_li 128^li [X_li | EAL] [EBRt | Y_li]^T, the
+    // corr k steps running limb L-1 down to 0, each limb 2r / W_BK steps. CT steps in all.
+    int L = 1, CPL = 1, CT = 1;
+    long R2 = 0;
+    if constexpr (DENOISE) {
+      const int mx = max(ld_uniform(I.maxabs, 0), ld_uniform(I.maxabs, 1));
+      L = min(mx > 1040319 ? 4 : mx > 8127 ? 3 : mx > 63 ? 2 : 1, p.lmax);
+      R2 = 2L * p.r;
+      CPL = (int)(R2 / W_BK);
+      CT = L * CPL;
+    }
+    // next corr step to issue: global index ig, limb li, chunk kc
+    int ig = 0, li = L - 1, kc = 0;
+    auto cissue = [&]() UWC_AI {
+      if constexpr (loader) {
+        const DmaLane cl =
+            dma_lane(I.corrA + (long)li * p.m * R2, R2, I.corrB + (long)li * p.n * R2, R2, bm0, bn0, lane);
+        dma_step<SPL>(lds_a(ig % W_STAGES), lds_b(ig % W_STAGES), cl, R2, R2, (long)kc * W_BK, wave);
+      }
+      ig++;
+      if (++kc == CPL) {
+        kc = 0;
+        li = li == 0 ? L - 1 : li - 1;
+      }
+    };
+
+    u32 msg[16];
+#pragma unroll
+    for (int w = 0; w < 16; w++) msg[w] = 0;
+    const int nchunks = p.k / p.r;
+    if constexpr (HASH) {
+      int kt = 0;
+      u32 unused = 0;
+      // The fold of chunk c ends in the first pass of chunk c + 1 (slot (c - 1) mod 16 for the
+      // chunk starting at slot c). For chunk 0 that folds the all-zero partials into the
+      // all-zero slot 15, which leaves it zero.
+      using Head = std::integral_constant<int, 0x01>;
+      using Tail = std::integral_constant<int, 0x80>;
+      if (p.r == W_BK) {
+        // one k step per chunk: an outer iteration is 16 k steps, so k step c0 + s sits in stage
+        // s % W_STAGES
+        static_assert(16 % W_STAGES == 0, "stage of an unrolled k step");
+        for (int c0 = 0; c0 < nchunks; c0 += 16) {
+          static_for<16>([&](auto sc) UWC_AI {
+            constexpr int s = decltype(sc)::value;
+            if (c0 + s < nchunks)
+              step(std::integral_constant<int, 0x81>{}, std::integral_constant<int, s % W_STAGES>{}, c0 + s,
+                   msg[(s + 15) & 15], unused);
+          });
+        }
+      } else if (p.r > W_BK) {
+        const int tpc = p.r / W_BK;
+        for (int c0 = 0; c0 < nchunks; c0 += 16) {
+#pragma unroll
+          for (int s = 0; s < 16; s++) {
+            if (c0 + s < nchunks) {
+              step_rt(Head{}, kt++, msg[(s + 15) & 15], unused);
+              for (int i = 1; i + 1 < tpc; i++) step_rt(NoFold{}, kt++, unused, unused);
+              step_rt(Tail{}, kt++, unused, unused);
+            }
+          }
+        }
+      } else if constexpr (W_KP == 4) {
+        // r = 64 = W_BK / 2: k step j holds chunks 2j (passes 0, 1) and 2j + 1 (passes 2, 3);
+        // an outer iteration is 8 k steps, so k step c0 / 2 + s / 2 sits in stage
+        // (s / 2) % W_STAGES
+        static_assert(8 % W_STAGES == 0, "stage of an unrolled k step");
+        for (int c0 = 0; c0 < nchunks; c0 += 16) {
+          static_for<8>([&](auto jc) UWC_AI {
+            constexpr int j = decltype(jc)::value, s = 2 * j;
+            if (c0 + s < nchunks)
+              step(std::integral_constant<int, 0xA5>{}, std::integral_constant<int, j % W_STAGES>{}, c0 / 2 + j,
+                   msg[(s + 15) & 15], msg[s]);
+          });
+        }
+      }
+      // The ring is idle now: when every corr step fits it, start loading them so that their
+      // latency hides behind the digest (every wave has finished its LDS reads at the barrier;
+      // the k loop's last wait left no DMA in flight).
+      if (DENOISE && CT <= W_STAGES) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
         for (int t = 0; t < CT; t++) cissue();  // corr step t -> stage t
       }
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // also drains the hash phase's stores
-      __builtin_amdgcn_s_barrier();
+      {  // the last chunk: its TAIL pass was the k loop's last pass
+        u32 keep, other;
+        fold_head(acc, fx);
+        fold_scatter(fx, lane, keep, other);
+        const int last = (nchunks - 1) & 15;
 #pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const int h = q >> 1, nb = q & 1;
-        v16i tmp[2] = {v16i{}, v16i{}};
-        for (int t = 0, c = 0; t < CT; t++) {
-          if (c == 0) {
-            tmp[0] = tmp[0] << 7;
-            tmp[1] = tmp[1] << 7;
+        for (int s = 0; s < 16; s++)
+          if (s == last) msg[s] = xor3(rotl13(msg[s]), keep, other);
+      }
+      // Digests and wins before the outputs: a winning lane's atomic waits for its wave's
+      // outstanding memory operations, which in a storer wave are then only the previous item's
+      // output stores (drained during this item's k loop), not this item's.
+      // every lane digests the tile it owns: hash block hb = lane bit 3, g = lane & 7,
+      // t = 2 (lane >> 5) + lane bit 4
+      const int hb = (lane >> 3) & 1, g = lane & 7, t = 2 * (lane >> 5) + ((lane >> 4) & 1);
+      u32 key[8], h[8];
+#pragma unroll
+      for (int i = 0; i < 8; i++) key[i] = ld_uniform(I.key, i);
+      b3_keyed64(key, msg, h);
+      const int row = bm0 + wm * 128 + hb * 64 + g, col = bn0 + wn * 64 + 2 * t;
+      if (p.dump) {
+        const long NB = p.n / 64;
+        u32* d = p.dump + ((((long)(row >> 6) * 8 + g) * NB + (col >> 6)) * 4 + t) * DUMP_WORDS;
+#pragma unroll
+        for (int w = 0; w < 16; w++) d[w] = msg[w];
+#pragma unroll
+        for (int w = 0; w < 8; w++) d[16 + w] = h[w];
+      }
+      u32 target[8];
+#pragma unroll
+      for (int i = 0; i < 8; i++) target[i] = ld_uniform(p.target, i);
+      if (I.wins && u256_le(h, target)) {
+        const u32 slot = atomicAdd(I.wins, 1u);
+        if (slot < (u32)p.max_wins) {
+          u32* rec = I.wins + 1 + slot * WIN_WORDS;
+          rec[0] = row;
+          rec[1] = col;
+#pragma unroll
+          for (int i = 0; i < 8; i++) rec[2 + i] = h[i];
+        }
+      }
+
+    } else {
+      u32 unused = 0;
+      int kt = 0;
+      for (; kt + W_STAGES <= KT; kt += W_STAGES)
+        static_for<W_STAGES>([&](auto stc) UWC_AI { step(NoFold{}, stc, kt + decltype(stc)::value, unused, unused); });
+      for (; kt < KT; kt++) step_rt(NoFold{}, kt, unused, unused);
+    }
+
+    // A finished quarter (blocks (2h, nb), (2h + 1, nb)): stored at once, or, in the split
+    // kernel, stored by the storers, the loaders' through a hand-off slot past the ring: loader w
+    // writes its quarter to slot w (block i, register group j, lane l at 16 ((4 i + j) 64 + l)),
+    // storer w + 4 reads it and stores it as wave (0, w). Two barriers per quarter: the slot is
+    // written, the slot is read. The loaders never store an output.
+    auto quarter_done = [&](int h, int nb, const v16i& v0, const v16i& v1) UWC_AI {
+      if constexpr (!SPLIT) {
+        store_block(lane, I.out, wm, wn, 2 * h, nb, v0);
+        store_block(lane, I.out, wm, wn, 2 * h + 1, nb, v1);
+      } else {
+        u8* slot = wsm + W_LDS + (wave & 3) * 8192;
+        if constexpr (loader) {
+#pragma unroll
+          for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+              const v16i& v = i ? v1 : v0;
+              *reinterpret_cast<v4i*>(slot + ((4 * i + j) * 64 + lane) * 16) =
+                  v4i{v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]};
+            }
+        } else {
+          store_block(lane, I.out, wm, wn, 2 * h, nb, v0);
+          store_block(lane, I.out, wm, wn, 2 * h + 1, nb, v1);
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        if constexpr (!loader) {
+#pragma unroll
+          for (int i = 0; i < 2; i++) {
+            v16i v;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+              const v4i x = *reinterpret_cast<const v4i*>(slot + ((4 * i + j) * 64 + lane) * 16);
+              v[4 * j] = x[0], v[4 * j + 1] = x[1], v[4 * j + 2] = x[2], v[4 * j + 3] = x[3];
+            }
+            store_block(lane, I.out, wm - 1, wn, 2 * h + i, nb, v);
           }
-          if (++c == CPL) c = 0;
-          step_mma_quarter(tmp, fbase, t, h, nb);
         }
-        store_block(2 * h, nb, acc[2 * h][nb] - tmp[0]);
-        store_block(2 * h + 1, nb, acc[2 * h + 1][nb] - tmp[1]);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
       }
-      return;
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // gfx9 counts stores in vmcnt: drain the hash phase
-    __syncthreads();                                   // and every wave is done reading the ring
-#pragma unroll
-    for (int g = 0; g < W_STAGES - 1; g++)
-      if (g < GT) cissue();
-    int g = 0;
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-      const int h = q >> 1, nb = q & 1;
-      v16i tmp[2] = {v16i{}, v16i{}};
-      for (int t = 0, c = 0; t < CT; t++, g++) {
-        wait_step(min(GT - 1 - g, W_STAGES - 2));
-        if (ig < GT) cissue();
-        if (c == 0) {
-          tmp[0] = tmp[0] << 7;
-          tmp[1] = tmp[1] << 7;
+    };
+
+    if constexpr (DENOISE) {
+      // Four passes over quarters of the wave's block keep the Horner accumulator at 32
+      // registers; each quarter is final as soon as its pass ends. When all CT corr steps fit in
+      // the ring (L * 2r <= W_STAGES * W_BK: the mining shapes) they are loaded once (the hashing
+      // kernels issued them before the digest) and the four passes read them without further
+      // barriers; otherwise they stream through the ring continuously across the passes (global
+      // step g is corr step g mod CT).
+      const int GT = 4 * CT;
+      if (CT <= W_STAGES) {
+        if constexpr (!HASH) {
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the k loop's last fragment reads
+          __builtin_amdgcn_s_barrier();
+          for (int t = 0; t < CT; t++) cissue();  // corr step t -> stage t
         }
-        if (++c == CPL) c = 0;
-        step_mma_quarter(tmp, fbase, g % W_STAGES, h, nb);
+        if constexpr (loader) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // also drains the hash phase's stores
+        __builtin_amdgcn_s_barrier();
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const int h = q >> 1, nb = q & 1;
+          v16i tmp[2] = {v16i{}, v16i{}};
+          for (int t = 0, c = 0; t < CT; t++) {
+            if (c == 0) {
+              tmp[0] = tmp[0] << 7;
+              tmp[1] = tmp[1] << 7;
+            }
+            if (++c == CPL) c = 0;
+            step_mma_quarter(tmp, fbase, t, h, nb);
+          }
+          quarter_done(h, nb, acc[2 * h][nb] - tmp[0], acc[2 * h + 1][nb] - tmp[1]);
+        }
+      } else {
+        if constexpr (loader) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // gfx9 counts stores in vmcnt
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();  // every wave is done reading the ring
+#pragma unroll
+        for (int g = 0; g < W_STAGES - 1; g++)
+          if (g < GT) cissue();
+        int g = 0;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const int h = q >> 1, nb = q & 1;
+          v16i tmp[2] = {v16i{}, v16i{}};
+          for (int t = 0, c = 0; t < CT; t++, g++) {
+            wait_step<SPL>(min(GT - 1 - g, W_STAGES - 2), loader);
+            if (ig < GT) cissue();
+            if (c == 0) {
+              tmp[0] = tmp[0] << 7;
+              tmp[1] = tmp[1] << 7;
+            }
+            if (++c == CPL) c = 0;
+            step_mma_quarter(tmp, fbase, g % W_STAGES, h, nb);
+          }
+          quarter_done(h, nb, acc[2 * h][nb] - tmp[0], acc[2 * h + 1][nb] - tmp[1]);
+        }
       }
-      store_block(2 * h, nb, acc[2 * h][nb] - tmp[0]);
-      store_block(2 * h + 1, nb, acc[2 * h + 1][nb] - tmp[1]);
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; q++) quarter_done(q >> 1, q & 1, acc[2 * (q >> 1)][q & 1], acc[2 * (q >> 1) + 1][q & 1]);
     }
-  } else {
-#pragma unroll
-    for (int mb = 0; mb < 4; mb++)
-#pragma unroll
-      for (int nb = 0; nb < 2; nb++) store_block(mb, nb, acc[mb][nb]);
+
+    if constexpr (!SPLIT) {
+      if (item + 1 < count) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the next prologue refills the ring
+        __builtin_amdgcn_s_barrier();
+      }
+    }
+
+  };
+  for (int item = 0; item < count; item++) {
+    if (!SPLIT || is_loader) run_item(item, std::true_type{});
+    else run_item(item, std::false_type{});
   }
 }
 
-template <bool H, bool D, int OUT>
+template <bool H, bool D, int OUT, bool SPLIT = false>
 static void go256(dim3 grid, hipStream_t s, const Gemm256Params& p) {
-  auto kern = noisy_gemm256_kernel<H, D, OUT>;
+  auto kern = noisy_gemm256_kernel<H, D, OUT, SPLIT>;
+  constexpr int lds = W_LDS + (SPLIT ? W_LDS_HANDOFF : 0);
   static bool attr = false;  // one attribute call per instantiation (the library is process-wide)
   if (!attr) {
-    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, W_LDS);
+    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     attr = true;
   }
-  hipLaunchKernelGGL(kern, grid, dim3(W_THREADS), W_LDS, s, p);
+  hipLaunchKernelGGL(kern, grid, dim3(W_THREADS), lds, s, p);
 }
 
 template <bool H, bool D>
@@ -763,12 +878,43 @@ int uwc_noisy_gemm256(const int8_t* A, const int8_t* B, int m, int n, int k, int
                       const uint32_t* target, uint32_t* wins, int max_wins, const float* a_scale, const float* b_scale,
                       void* out, int out_mode, int flags, uint32_t* tile_dump, int ldc, hipStream_t stream) {
   const bool hash = flags & FLAG_HASH, denoise = flags & FLAG_DENOISE;
-  Gemm256Params p{A, B, m, n, k, r, corrA, corrB, maxabs, lmax, key, target, wins, max_wins, a_scale, b_scale, out,
-                  hash ? tile_dump : nullptr, ldc};
+  Gemm256Params p{};
+  p.B = B;
+  p.m = m, p.n = n, p.k = k, p.r = r;
+  p.lmax = lmax;
+  p.target = target;
+  p.max_wins = max_wins;
+  p.a_scale = a_scale;
+  p.b_scale = b_scale;
+  p.dump = hash ? tile_dump : nullptr;
+  p.ldc = ldc;
+  p.count = 1;
+  p.it[0] = Gemm256Item{A, corrA, corrB, maxabs, key, wins, out};
   const dim3 grid((m / W_BM) * (n / W_BN));
   if (hash && denoise) out256<true, true>(out_mode, grid, stream, p);
   else if (hash) out256<true, false>(out_mode, grid, stream, p);
   else if (denoise) out256<false, true>(out_mode, grid, stream, p);
   else out256<false, false>(out_mode, grid, stream, p);
   return uwc_launch_status("noisy_gemm256");
+}
+
+// `count` (1 .. G256_MAXB) hashed, denoised GEMMs with int32 outputs sharing B in one launch, each
+// equal to its own uwc_noisy_gemm256 call: the split-role kernel, whose output stores of one item
+// drain while the next computes. Called by uwc_noisy_gemm_many after argument checks.
+int uwc_noisy_gemm256_many(int count, const int8_t* const* A, const int8_t* B, int m, int n, int k, int r,
+                           const int8_t* const* corrA, const int8_t* const* corrB, const int32_t* const* maxabs,
+                           int lmax, const uint32_t* const* key, const uint32_t* target, uint32_t* const* wins,
+                           int max_wins, void* const* out, hipStream_t stream) {
+  if (count < 1 || count > G256_MAXB) return uwc_fail("uwc_noisy_gemm256_many: count=%d outside 1..%d", count, G256_MAXB);
+  Gemm256Params p{};
+  p.B = B;
+  p.m = m, p.n = n, p.k = k, p.r = r;
+  p.lmax = lmax;
+  p.target = target;
+  p.max_wins = max_wins;
+  p.ldc = n;
+  p.count = count;
+  for (int i = 0; i < count; i++) p.it[i] = Gemm256Item{A[i], corrA[i], corrB[i], maxabs[i], key[i], wins[i], out[i]};
+  go256<true, true, OUT_I32, true>(dim3((m / W_BM) * (n / W_BN)), stream, p);
+  return uwc_launch_status("noisy_gemm256 (split, batched)");
 }

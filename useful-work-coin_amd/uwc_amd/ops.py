@@ -10,6 +10,7 @@ gemm() can also dump every tile's message and digest (`dump`). OUT_F32 is an ext
 from __future__ import annotations
 
 import ctypes
+import gc
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -281,6 +282,33 @@ def gemm(A, B, *, r=128, flags=0, corrA=None, corrB=None, maxabs=None, key=None,
               _p(b_scale), _p(out), out_mode, flags | (FLAG_TILE128 if cfg == "128x128" else 0), _p(dump), _stream())
 
 
+def gemm_many(As, B, *, r=128, flags=0, corrAs=None, corrBs=None, maxabss=None, keys=None, target=None, winss=None,
+              max_wins=0, a_scale=None, b_scale=None, outs=None, out_mode=OUT_NONE):
+    """gemm() of several operands As[i] against one B, item i with its own corrections, maxabs,
+    seed, win buffer and output. With FLAG_HASH | FLAG_DENOISE, OUT_I32 and m, n % 256 == 0 the
+    items share launches (up to 16 per launch, output stores overlapping the next item);
+    otherwise one launch per item. Results equal separate gemm() calls."""
+    count = len(As)
+    if count == 0:
+        return
+    m, k = As[0].shape
+    n = B.shape[0]
+    if flags:
+        _check(m % BM == 0 and n % BN == 0 and k % BK == 0 and r % BK == 0 and k % r == 0, (m, n, k, r))
+    for A in As:
+        _check(tuple(A.shape) == (m, k) and A.dtype == torch.int8 and A.is_contiguous(),
+               "gemm_many: every A must be a contiguous int8 m x k")
+    _check(B.dtype == torch.int8 and B.is_contiguous(), "gemm_many: B must be contiguous int8")
+    for xs in (corrAs, corrBs, maxabss, keys, winss, outs):
+        _check(xs is None or len(xs) == count, "gemm_many: one entry per item")
+    _check(outs is not None or out_mode == OUT_NONE, "gemm_many: outputs needed for this out_mode")
+    lmax = corrAs[0].shape[0] if corrAs is not None else 0
+    out_arr = _arr(outs) if outs is not None else ctypes.cast((ctypes.c_void_p * count)(), ctypes.c_void_p)
+    _lib.call("uwc_noisy_gemm_many", count, _arr(As), _p(B), m, n, k, r, _arr(corrAs), _arr(corrBs), _arr(maxabss),
+              lmax, _arr(keys), _p(target), _arr(winss), max_wins, _p(a_scale), _p(b_scale), out_arr, out_mode, flags,
+              _stream())
+
+
 def igemm_i32(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """Exact int32 A @ B^T for any m, n (k % 64 == 0)."""
     m, k = A.shape
@@ -295,6 +323,7 @@ def igemm_i32(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None)
 # ------------------------------------------------------------------ one mined linear layer
 _WORKSPACE: dict = {}
 SWEEP_GROUP = 8  # nonces per batched commitment / noise launch in MinedWeight.forward_many
+GEMM_GROUP = 8   # nonces per batched GEMM launch in MinedWeight.forward_many
 
 
 @dataclass
@@ -357,18 +386,11 @@ class MinedWeight:
 
     def _buf(self, m: int, slot: int = 0, wins: torch.Tensor | None = None):
         """Per-call buffers, a workspace shared by every weight with the same (m, k, r): layers run
-        one after another on one stream. The noised operand and the corrections (ApEA, corrA) live
-        only from the projections to the GEMM of one call and are shared by all slots; the
-        per-nonce noise (a_seed, E, P, selection matrices, maxabs, commitment scratch) has one
-        copy per slot, so forward_many can draw a group of nonces' noise before their GEMMs.
-        Win records are per weight (or the caller's buffer); slots > 0 carry their own."""
+        one after another on one stream (slot 0). forward_many gives each nonce of a group its own
+        slot (1, 2, ...): noise, noised operand, corrections and commitment scratch, so that a
+        group's projections all run before its GEMMs. Win records are per weight (or the caller's
+        buffer); slots > 0 carry their own."""
         dev, k, r = self.device, self.k, self.r
-        big = _WORKSPACE.get((str(dev), m, k, r))
-        if big is None:
-            big = _WORKSPACE[(str(dev), m, k, r)] = dict(
-                ApEA=torch.empty((m, k), dtype=torch.int8, device=dev),
-                corrA=torch.zeros((limbs_for(k), m, 2 * r), dtype=torch.int8, device=dev),
-            )
         key = (str(dev), m, k, r, slot)
         ws = _WORKSPACE.get(key)
         if ws is None:
@@ -376,8 +398,10 @@ class MinedWeight:
                 a_seed=torch.empty(8, dtype=torch.int32, device=dev),
                 EAL=torch.empty((m, r), dtype=torch.int8, device=dev),
                 PA=torch.empty(k, dtype=torch.int32, device=dev),
+                ApEA=torch.empty((m, k), dtype=torch.int8, device=dev),
                 SA=torch.empty((r, k), dtype=torch.int8, device=dev),
                 SpA=torch.empty((k, 64), dtype=torch.int8, device=dev) if r <= 64 else None,
+                corrA=torch.zeros((limbs_for(k), m, 2 * r), dtype=torch.int8, device=dev),
                 maxabs=torch.zeros(2, dtype=torch.int32, device=dev),
                 scratch=torch.empty(max(8, b3_scratch_words(m * k)), dtype=torch.int32, device=dev),
             )
@@ -386,7 +410,16 @@ class MinedWeight:
             wins = self._bufs.get(wkey)
             if wins is None:
                 wins = self._bufs[wkey] = torch.zeros(1 + self.max_wins * WIN_WORDS, dtype=torch.int32, device=dev)
-        return {**big, **ws, "wins": wins}
+        return {**ws, "wins": wins}
+
+    def _slot_corrB(self, slot: int) -> torch.Tensor:
+        """A per-slot copy of corrB for forward_many: the E copy setup_block wrote, and room for
+        the slot's nonce's Y limbs (the reference's single corrB serves one call at a time)."""
+        cb = self._bufs.get(("corrB", slot))
+        if cb is None or cb.shape != self.corrB.shape or self._bufs.get(("corrB_src", slot)) is not self.corrB:
+            cb = self._bufs[("corrB", slot)] = self.corrB.clone()
+            self._bufs[("corrB_src", slot)] = self.corrB
+        return cb
 
     def forward(self, A: torch.Tensor, a_scale: torch.Tensor, out: torch.Tensor | None = None,
                 out_mode: int = OUT_BF16, hash_tiles: bool = True) -> torch.Tensor:
@@ -426,18 +459,21 @@ class MinedWeight:
 
     def _mine(self, A, b, a_scale, out, out_mode, hash_tiles, side, cfg=None, dump=None):
         """Steps 3-5 of a mined forward once the nonce's noise is drawn (ops.py:331-347)."""
+        self._project(A, b, side, self.corrB)
+        return self._gemm(b, a_scale, out, out_mode, hash_tiles, cfg=cfg, dump=dump)
+
+    def _project(self, A, b, side, corrB):
+        """3. ApEA = A + EAL*P_A ; X = A * P_B^T (limbs) ; EAL copy; 4. Y = BpEBt * P_A^T (limbs)
+        into corrB."""
         m, k = A.shape
         r = self.r
-        # 3. ApEA = A + EAL*P_A ; X = A * P_B^T (limbs) ; EAL copy
-        # 4. Y = BpEBt * P_A^T (limbs)
         if side:
-            side_project(A, b["EAL"], b["SpA"], b["ApEA"], self.SBt, b["corrA"], self.BpEBt, b["SA"], self.corrB,
+            side_project(A, b["EAL"], b["SpA"], b["ApEA"], self.SBt, b["corrA"], self.BpEBt, b["SA"], corrB,
                          maxabs=b["maxabs"], corr_a_off=0, ecopy_off=r, corr_b_off=r)
         else:
             noise_project(A, m, k, r, E=b["EAL"], Pn=b["PA"], dst=b["ApEA"], St=self.SBt, corr=b["corrA"],
                           corr_off=0, ecopy_off=r, maxabs=b["maxabs"][0:1])
-            project(self.BpEBt, b["SA"], self.corrB, r, b["maxabs"][1:2])
-        return self._gemm(b, a_scale, out, out_mode, hash_tiles, cfg=cfg, dump=dump)
+            project(self.BpEBt, b["SA"], corrB, r, b["maxabs"][1:2])
 
     def _gemm(self, b, a_scale, out, out_mode, hash_tiles, cfg=None, dump=None):
         # 5. noisy GEMM: hash every tile, denoise exactly, scale
@@ -470,19 +506,25 @@ class MinedWeight:
         return self._after_commit(A, b, a_scale, out, out_mode, hash_tiles, cfg=cfg, proj=proj, dump=dump)
 
     def forward_many(self, As, a_scale: torch.Tensor, outs=None, out_mode: int = OUT_BF16, hash_tiles: bool = True,
-                     wins=None, group: int = SWEEP_GROUP):
+                     wins=None, group: int = SWEEP_GROUP, gemm_group: int = GEMM_GROUP):
         """Mined forwards of a sequence of activations (the nonces of a sweep), each equal to
         forward(As[i]) bit for bit. The nonces go in groups of `group` (1..MAX_BATCH): one set of
         launches commits the whole group (BLAKE3 trees and salted seeds) and one launch draws all
         of its noise, so those latency-bound chains run several waves per SIMD instead of one;
-        then every nonce of the group runs its projections and hashed GEMM. Everything is queued
-        in order on the current stream. outs / wins: optional per-item output tensors and win
-        buffers (1 + max_wins * WIN_WORDS int32 each); without wins, winners() reports the last
-        item (the others' records go to per-slot buffers). Returns the outputs."""
+        then the group's nonces run their projections and hashed GEMMs, `gemm_group` nonces per
+        batched GEMM call (whose output stores overlap the next nonce's tiles; a smaller batch
+        keeps the noised operands it reads in the Infinity Cache). Everything is queued in order
+        on the current stream; Python's cyclic garbage collector is paused while the launches are
+        queued (a full collection can stall the host for tens of milliseconds, longer than the
+        GPU work already queued), and its previous state restored. outs / wins: optional per-item
+        output tensors and win buffers (1 + max_wins * WIN_WORDS int32 each); without wins,
+        winners() reports the last item (the others' records go to per-slot buffers). Returns the
+        outputs."""
         n_items = len(As)
         if n_items == 0:
             return []
         _check(1 <= group <= MAX_BATCH, f"MinedWeight.forward_many: group={group}, need 1..{MAX_BATCH}")
+        _check(gemm_group >= 1, f"MinedWeight.forward_many: gemm_group={gemm_group}")
         m, k, r = As[0].shape[0], self.k, self.r
         for A in As:
             self._check_a(A)
@@ -490,6 +532,17 @@ class MinedWeight:
         outs = [self._out(m, outs[i] if outs is not None else None, out_mode) for i in range(n_items)]
         c = consts(As[0].device)
         side = side_ok(m, self.n, k, r)
+        gc_on = gc.isenabled()
+        gc.disable()
+        try:
+            self._sweep(As, a_scale, outs, out_mode, hash_tiles, wins, group, gemm_group, m, k, r, c, side)
+        finally:
+            if gc_on:
+                gc.enable()
+        return outs
+
+    def _sweep(self, As, a_scale, outs, out_mode, hash_tiles, wins, group, gemm_group, m, k, r, c, side):
+        n_items = len(As)
         for g0 in range(0, n_items, group):
             items = list(range(g0, min(g0 + group, n_items)))
             bufs = []
@@ -506,10 +559,20 @@ class MinedWeight:
                              [b["a_seed"] for b in bufs], Sts=[b["SA"] for b in bufs],
                              zero0s=[b["maxabs"] for b in bufs], zero1s=[b["wins"][:1] for b in bufs],
                              SpTs=[b["SpA"] for b in bufs] if side else None)
-            # 3.-5. per nonce: projections, hashed GEMM, exact denoise
-            for b, i in zip(bufs, items):
-                self._mine(As[i], b, a_scale, outs[i], out_mode, hash_tiles, side)
-        return outs
+            corrBs = [self._slot_corrB(j + 1) for j in range(len(items))]
+            for s0 in range(0, len(items), gemm_group):
+                sub = range(s0, min(s0 + gemm_group, len(items)))
+                # 3.-4. the nonces' noised operands and projections (own slot and corrB copy)
+                for j in sub:
+                    self._project(As[items[j]], bufs[j], side, corrBs[j])
+                # 5. their hashed GEMMs with exact denoise: one batched call
+                gemm_many([bufs[j]["ApEA"] for j in sub], self.BpEBt, r=r,
+                          flags=(FLAG_HASH if hash_tiles else 0) | FLAG_DENOISE,
+                          corrAs=[bufs[j]["corrA"] for j in sub], corrBs=[corrBs[j] for j in sub],
+                          maxabss=[bufs[j]["maxabs"] for j in sub], keys=[bufs[j]["a_seed"] for j in sub],
+                          target=self.target, winss=[bufs[j]["wins"] for j in sub], max_wins=self.max_wins,
+                          a_scale=a_scale, b_scale=self.b_scale,
+                          outs=[outs[items[j]] for j in sub] if out_mode != OUT_NONE else None, out_mode=out_mode)
 
     def noise_mine(self, A: torch.Tensor, dump=None):
         """What a pure noise miner runs per attempt batch: commit A, noise it, hashed GEMM, no output.
