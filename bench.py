@@ -496,9 +496,10 @@ COPY_BYTES = 256 << 20  # the calibration copy: reads and writes exactly this ma
 
 def traffic_probe(args, torch, ops, O, np):
     """What the two rocprofv3 --pmc passes (FETCH_SIZE, then WRITE_SIZE) profile: a few mined
-    forwards at the bench shape, then a plain device copy of COPY_BYTES three times, whose
-    counter readings calibrate the KiB units of both counters."""
-    args.steps, args.warmup = 4, 2
+    forwards at the bench shape (one group: batched GEMM launches of args.gemm_group nonces),
+    then a plain device copy of COPY_BYTES three times, whose counter readings calibrate the KiB
+    units of both counters."""
+    args.steps, args.warmup = args.gemm_group, args.gemm_group
     mining(args, torch, np, ops)
     x = torch.empty(COPY_BYTES, dtype=torch.int8, device="cuda").fill_(1)
     y = torch.empty_like(x)
@@ -508,7 +509,7 @@ def traffic_probe(args, torch, ops, O, np):
     log("traffic probe: done")
 
 
-def summarize_pmc(fetch_csv, write_csv, cmd):
+def summarize_pmc(fetch_csv, write_csv, cmd, nonces):
     """Per-dispatch FETCH_SIZE / WRITE_SIZE of the noisy GEMM, each scaled by COPY_BYTES over the
     counter's reading for the calibration copy, into TRAFFIC_FILE."""
     import csv
@@ -524,21 +525,26 @@ def summarize_pmc(fetch_csv, write_csv, cmd):
     out = {}
     for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
         v = per_kernel(path, counter)
-        gemm = [x for name, xs in v.items() if "noisy_gemm256_kernel<true, true, 1>" in name for x in xs]
+        gemm = [x for name, xs in v.items() if "noisy_gemm256_kernel<true, true, 1, true>" in name for x in xs]
         copy = [x for name, xs in v.items() if "copy" in name.lower() for x in xs]  # the runtime's blit kernel
         copy = [x for x in copy if x > 0.5 * COPY_BYTES / 1024]  # the 256 MiB copies, not tensor setup
         gk, ck = statistics.median(gemm), statistics.median(copy)
         factor = COPY_BYTES / (ck * 1024.0)
         out[counter] = dict(gemm_kib=gk, copy_kib=ck, factor=factor, bytes=gk * 1024.0 * factor, n=len(gemm))
     traffic = out["FETCH_SIZE"]["bytes"] + out["WRITE_SIZE"]["bytes"]
+    nonces = int(nonces)
     with open(TRAFFIC_FILE, "w") as f:
-        f.write("HBM traffic of noisy_gemm256_kernel<true, true, 1> (mining, 4096^3, r=64, L=2), bytes per dispatch\n")
+        f.write(f"HBM traffic of noisy_gemm256_kernel<true, true, 1, true> (mining, 4096^3, r=64, L=2), bytes per dispatch "
+                f"of {nonces} nonces\n")
         f.write(f"commands: {cmd}\n")
         for c in ("FETCH_SIZE", "WRITE_SIZE"):
             d = out[c]
             f.write(f"{c}: median {d['gemm_kib']:.1f} KiB per dispatch over {d['n']} dispatches; calibration copy of "
                     f"{COPY_BYTES} B reads {d['copy_kib']:.1f} KiB -> factor {d['factor']:.4f} -> {d['bytes']:.0f} B\n")
         f.write(f"traffic_bytes_per_launch: {traffic:.0f}\n")
+        f.write(f"traffic_bytes_per_nonce: {traffic / nonces:.0f} (read {out['FETCH_SIZE']['bytes'] / nonces:.0f}, "
+                f"written {out['WRITE_SIZE']['bytes'] / nonces:.0f}; algorithmic: A 16.8 MB + B 16.8 MB + corrections "
+                f"2.1 MB read, int32 output 67.1 MB written)\n")
     print(open(TRAFFIC_FILE).read())
 
 
@@ -547,38 +553,42 @@ def gemm_reps(steps: int) -> int:
     return max(8, min(steps, 64))
 
 
-def summarize_trace(trace_csv, out_path, cmd, steps, warmup):
+def summarize_trace(trace_csv, out_path, cmd, steps, warmup, group):
     """A kernel trace (run_kernel_trace.csv) of `bench.py --no-cpu --no-detrt --no-e2e --steps S
-    --warmup W` as text: per kernel of the timed sweep (from the end of the warm-up's last GEMM to
-    the end of the sweep's last GEMM) calls, average and time per nonce, and the average of the
-    back-to-back GEMM launches that give the bench's roofline figure."""
+    --warmup W` (groups of G nonces, one batched GEMM launch per group) as text: per kernel of the
+    timed sweep (from the end of the warm-up's last GEMM launch to the end of the sweep's last)
+    calls, average and time per nonce, and the average of the back-to-back GEMM launches that give
+    the bench's roofline figure."""
     import csv
     import re
-    steps, warmup = int(steps), int(warmup)
+    steps, warmup, group = int(steps), int(warmup), int(group)
     rows = sorted(csv.DictReader(open(trace_csv)), key=lambda r: int(r["Start_Timestamp"]))
     name = lambda r: re.sub(r"\(.*", "", r["Kernel_Name"])  # noqa: E731
     dur = lambda r: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3  # noqa: E731
-    g = [i for i, r in enumerate(rows) if "noisy_gemm256_kernel<true, true, 1>" in r["Kernel_Name"]]
-    t0, t1 = int(rows[g[warmup - 1]]["End_Timestamp"]), int(rows[g[warmup + steps - 1]]["End_Timestamp"])
+    g = [i for i, r in enumerate(rows) if "noisy_gemm256_kernel<true, true, 1, true>" in r["Kernel_Name"]]
+    nw, ns = -(-warmup // group), -(-steps // group)  # launches of the warm-up and of the sweep
+    t0, t1 = int(rows[g[nw - 1]]["End_Timestamp"]), int(rows[g[nw + ns - 1]]["End_Timestamp"])
     per = {}
     for r in rows:
         if t0 < int(r["Start_Timestamp"]) and int(r["End_Timestamp"]) <= t1:
             per.setdefault(name(r), []).append(dur(r))
-    b2b = [dur(rows[i]) for i in g[warmup + steps + 3:warmup + steps + 3 + gemm_reps(steps)]]
+    b2b = [dur(rows[i]) for i in g[nw + ns + 3:nw + ns + 3 + gemm_reps(steps)]]
     with open(out_path, "w") as f:
         f.write(f"rocprofv3 kernel trace, mined forward 4096x4096x4096 r=64 (bench.py workload), sweep of {steps} "
-                f"nonces after {warmup} warm-up nonces\n")
+                f"nonces after {warmup} warm-up nonces, {group} nonces per group\n")
         f.write(f"command: {cmd}\n\n")
         f.write(f"timed sweep: {(t1 - t0) / 1e3 / steps:.2f} us per nonce (kernel trace clock)\n")
         f.write(f"{'kernel':58s} {'calls':>6s} {'avg_us':>9s} {'min_us':>9s} {'max_us':>9s} {'us/nonce':>9s}\n")
         for k_, xs in sorted(per.items(), key=lambda kv: -sum(kv[1])):
             f.write(f"{k_[:58]:58s} {len(xs):6d} {sum(xs) / len(xs):9.2f} {min(xs):9.2f} {max(xs):9.2f} "
                     f"{sum(xs) / steps:9.2f}\n")
-        f.write(f"\nback-to-back noisy_gemm256_kernel<true, true, 1> (the bench's roofline figure): {len(b2b)} calls, "
-                f"avg {sum(b2b) / len(b2b):.2f} us, min {min(b2b):.2f}, max {max(b2b):.2f}\n")
-        f.write("\nPer group of 8 nonces: b3_chunks + b3_reduce (one batched commitment of the group's A), one\n"
-                "nonce_noise (E_A, P_A, selection matrices of all 8); per nonce: side_kernel (noised A, both\n"
-                "projections in limbs), noisy_gemm256_kernel<true, true, 1> (hashed GEMM, exact denoise, int32 out).\n")
+        f.write(f"\nback-to-back noisy_gemm256_kernel<true, true, 1, true> launches of {group} nonces (the bench's "
+                f"roofline figure): {len(b2b)} calls, avg {sum(b2b) / len(b2b):.2f} us = "
+                f"{sum(b2b) / len(b2b) / group:.2f} us per nonce, min {min(b2b):.2f}, max {max(b2b):.2f}\n")
+        f.write(f"\nPer group of {group} nonces: b3_chunks + b3_reduce (one batched commitment of the group's A), one\n"
+                "nonce_noise (E_A, P_A, selection matrices of the group), one side_kernel per nonce (noised A,\n"
+                "both projections in limbs), one noisy_gemm256_kernel<true, true, 1, true> launch (the group's\n"
+                "hashed GEMMs with exact denoise, int32 out; split roles, stores overlapping the next nonce).\n")
     print(open(out_path).read())
 
 
@@ -635,11 +645,11 @@ def main():
     ap.add_argument("--e2e-layers", type=int, default=28)
     ap.add_argument("--e2e-cpu-tokens", type=int, default=256)
     ap.add_argument("--traffic-probe", action="store_true", help="the workload of the FETCH_SIZE / WRITE_SIZE passes")
-    ap.add_argument("--summarize-pmc", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "CMD"),
+    ap.add_argument("--summarize-pmc", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "CMD", "NONCES"),
                     help="write the traffic summary under profiles/ from two counter_collection.csv files")
     ap.add_argument("--summarize-e2e-trace", nargs=3, metavar=("STATS_CSV", "OUT", "CMD"),
                     help="write a configs[4] kernel-trace summary under profiles/")
-    ap.add_argument("--summarize-trace", nargs=5, metavar=("TRACE_CSV", "OUT", "CMD", "STEPS", "WARMUP"),
+    ap.add_argument("--summarize-trace", nargs=6, metavar=("TRACE_CSV", "OUT", "CMD", "STEPS", "WARMUP", "GROUP"),
                     help="write a kernel-trace summary under profiles/ from a run_kernel_trace.csv")
     args = ap.parse_args()
     if args.summarize_trace:

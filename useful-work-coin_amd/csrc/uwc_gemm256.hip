@@ -20,15 +20,22 @@
 //     32-row fragment reads are conflict-free with 32 or 64 banks. The swizzle is applied on the
 //     global side (each lane of a DMA writes a fixed LDS slot and fetches the bytes that belong
 //     there).
-//   * Transcript fold every r along k: a lane XORs its accumulators into 8 partials (hash block
-//     x g & 3) with 3-input v_bitop3 XORs, block by block right before that block's next MFMA
-//     (the fold of chunk c runs inside the first pass of chunk c + 1), then a reduce-scatter
-//     over lane bits 0, 3, 4 (DPP quad_perm and row_ror:8 fused into v_xor, ds_swizzle) leaves
-//     every lane with the full tile XOR of exactly one tile, which it folds into that tile's
-//     16-word message (message slots are static: the chunk loop is unrolled over the 16 slots).
-//     After the k loop every lane digests its own tile.
+//   * Transposed C: the B fragment is the MFMA's A operand, so lane l holds row l & 31 of a
+//     block and four consecutive columns per register group (16-byte epilogue stores).
+//   * Transcript fold every r along k: a lane XORs its accumulators into 4 partials (hash block
+//     x bit 0 of the tile index) with 3-input v_bitop3 XORs, spread over a chunk's last pass
+//     (blocks folded three MFMAs after their last MFMA of the chunk) and the next chunk's first
+//     pass (the rest, before their first MFMA), then a reduce-scatter over lane bits 3 (DPP
+//     row_ror:8 fused into v_xor) and 4 (v_permlane16_swap) leaves every lane with the full tile
+//     XOR of exactly one tile, which it folds into that tile's 16-word message (message slots
+//     are static: the chunk loop is unrolled over the 16 slots). After the k loop every lane
+//     digests its own tile.
 //   * Denoise in four passes over quarters of the wave's block (a 32-register Horner
-//     accumulator), streaming [X_li | EAL] and [EBRt | Y_li] through the same ring.
+//     accumulator), the corrections streamed through the same ring (or, when they fit, loaded
+//     into it before the digest).
+//   * SPLIT (the batched form): several nonces per launch on the same tiles; waves 0-3 issue the
+//     DMA, waves 4-7 store every output (the others' through an LDS hand-off), so one nonce's
+//     stores drain while the next computes (see the kernel).
 #include "uwc_common.h"
 
 // lambdas are always inlined: an out-of-line call would take the accumulator arrays' addresses
