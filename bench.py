@@ -100,7 +100,10 @@ def mining(args, torch, np, ops):
 
     # the sweep runs through MinedWeight.forward_many: one batched commitment and one noise launch
     # per group of nonces, then each nonce's projections and hashed GEMM
-    w.forward_many([As[i % nbuf] for i in range(args.warmup)], ones, outs=[out] * args.warmup, out_mode=ops.OUT_I32,
+    # the warm-up covers at least two groups: forward_many alternates two sets of workspace slots,
+    # which it allocates on first use
+    nwarm = max(args.warmup, 2 * args.group)
+    w.forward_many([As[i % nbuf] for i in range(nwarm)], ones, outs=[out] * nwarm, out_mode=ops.OUT_I32,
                    group=args.group, gemm_group=args.gemm_group)
     torch.cuda.synchronize()
     sweep = [As[(args.warmup + i) % nbuf] for i in range(args.steps)]
@@ -566,7 +569,7 @@ def summarize_trace(trace_csv, out_path, cmd, steps, warmup, group):
     name = lambda r: re.sub(r"\(.*", "", r["Kernel_Name"])  # noqa: E731
     dur = lambda r: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3  # noqa: E731
     g = [i for i, r in enumerate(rows) if "noisy_gemm256_kernel<true, true, 1, true>" in r["Kernel_Name"]]
-    nw, ns = -(-warmup // group), -(-steps // group)  # launches of the warm-up and of the sweep
+    nw, ns = -(-max(warmup, 2 * group) // group), -(-steps // group)  # launches of the warm-up and of the sweep
     t0, t1 = int(rows[g[nw - 1]]["End_Timestamp"]), int(rows[g[nw + ns - 1]]["End_Timestamp"])
     per = {}
     for r in rows:

@@ -322,6 +322,7 @@ def igemm_i32(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None)
 
 # ------------------------------------------------------------------ one mined linear layer
 _WORKSPACE: dict = {}
+_SWEEP_SYNC: dict = {}
 SWEEP_GROUP = 8  # nonces per batched commitment / noise launch in MinedWeight.forward_many
 GEMM_GROUP = 8   # nonces per batched GEMM launch in MinedWeight.forward_many
 
@@ -510,13 +511,14 @@ class MinedWeight:
         """Mined forwards of a sequence of activations (the nonces of a sweep), each equal to
         forward(As[i]) bit for bit. The nonces go in groups of `group` (1..MAX_BATCH): one set of
         launches commits the whole group (BLAKE3 trees and salted seeds) and one launch draws all
-        of its noise, so those latency-bound chains run several waves per SIMD instead of one;
-        then the group's nonces run their projections and hashed GEMMs, `gemm_group` nonces per
+        of its noise, so those latency-bound chains run several waves per SIMD instead of one,
+        and on a second stream one group ahead, beside the previous group's projections; then
+        the group's nonces run their projections and hashed GEMMs, `gemm_group` nonces per
         batched GEMM call (whose output stores overlap the next nonce's tiles; a smaller batch
-        keeps the noised operands it reads in the Infinity Cache). Everything is queued in order
-        on the current stream; Python's cyclic garbage collector is paused while the launches are
-        queued (a full collection can stall the host for tens of milliseconds, longer than the
-        GPU work already queued), and its previous state restored. outs / wins: optional per-item
+        keeps the noised operands it reads in the Infinity Cache). The work is queued behind the
+        current stream, which then waits for all of it. Python's cyclic garbage collector is
+        paused while the launches are queued (a full collection can stall the host for tens of
+        milliseconds, longer than the GPU work already queued), and its previous state restored. outs / wins: optional per-item
         output tensors and win buffers (1 + max_wins * WIN_WORDS int32 each); without wins,
         winners() reports the last item (the others' records go to per-slot buffers). Returns the
         outputs."""
@@ -542,24 +544,55 @@ class MinedWeight:
         return outs
 
     def _sweep(self, As, a_scale, outs, out_mode, hash_tiles, wins, group, gemm_group, m, k, r, c, side):
+        """Group g's commitment and noise go on a side stream, one group ahead, so that they run
+        beside group g - 1's projections (the BLAKE3 chains are VALU-bound, the projections
+        memory-bound, and a CU holds one workgroup of each); groups alternate between two sets of
+        workspace slots, and a group's commitment waits until the GEMM of the group two back, the
+        last user of its set, is done."""
         n_items = len(As)
-        for g0 in range(0, n_items, group):
-            items = list(range(g0, min(g0 + group, n_items)))
-            bufs = []
-            for j, i in enumerate(items):
+        groups = [list(range(g0, min(g0 + group, n_items))) for g0 in range(0, n_items, group)]
+        cur = torch.cuda.current_stream(self.device)
+        sync = _SWEEP_SYNC.get(str(self.device))
+        if sync is None:  # default-priority side stream and four reusable events per device
+            sync = _SWEEP_SYNC[str(self.device)] = (torch.cuda.Stream(device=self.device),
+                                                    [torch.cuda.Event() for _ in range(2)],
+                                                    [torch.cuda.Event() for _ in range(2)])
+        sc, committed, consumed = sync
+        sc.wait_stream(cur)
+
+        def bufs_of(gi):
+            out = []
+            for j, i in enumerate(groups[gi]):
                 # the sweep's last item reports through the weight's own win buffer (slot 0's)
                 wb = wins[i] if wins is not None else (self._buf(m)["wins"] if i == n_items - 1 else None)
-                bufs.append(self._buf(m, slot=j + 1, wins=wb))
-            # 1. commit to every A of the group, a_seed_i = H(b_seed || bind_a(root_Ai, m))
-            #    (ops.py:322-324)
-            b3_root_and_seed_many([As[i].view(-1) for i in items], self.job_key, prefix=self.b_seed, salt=c["SALT_A"],
-                                  dim=m, seed_outs=[b["a_seed"] for b in bufs], scratch=self._sweep_scratch(m, len(items)))
-            # 2. every nonce's noise E_A, P_A and selection matrices; zeroes its maxabs and win count
-            nonce_noise_many([b["EAL"] for b in bufs], [b["PA"] for b in bufs], k, r, c["LABEL_A"],
-                             [b["a_seed"] for b in bufs], Sts=[b["SA"] for b in bufs],
-                             zero0s=[b["maxabs"] for b in bufs], zero1s=[b["wins"][:1] for b in bufs],
-                             SpTs=[b["SpA"] for b in bufs] if side else None)
-            corrBs = [self._slot_corrB(j + 1) for j in range(len(items))]
+                out.append(self._buf(m, slot=1 + (gi % 2) * group + j, wins=wb))
+            return out
+
+        def commit(gi):
+            items, bufs = groups[gi], bufs_of(gi)
+            with torch.cuda.stream(sc):
+                if gi >= 2:
+                    sc.wait_event(consumed[gi % 2])
+                # 1. commit to every A of the group, a_seed_i = H(b_seed || bind_a(root_Ai, m))
+                #    (ops.py:322-324)
+                b3_root_and_seed_many([As[i].view(-1) for i in items], self.job_key, prefix=self.b_seed,
+                                      salt=c["SALT_A"], dim=m, seed_outs=[b["a_seed"] for b in bufs],
+                                      scratch=self._sweep_scratch(m, len(items)))
+                # 2. every nonce's noise E_A, P_A and selection matrices; zeroes its maxabs and win
+                #    count
+                nonce_noise_many([b["EAL"] for b in bufs], [b["PA"] for b in bufs], k, r, c["LABEL_A"],
+                                 [b["a_seed"] for b in bufs], Sts=[b["SA"] for b in bufs],
+                                 zero0s=[b["maxabs"] for b in bufs], zero1s=[b["wins"][:1] for b in bufs],
+                                 SpTs=[b["SpA"] for b in bufs] if side else None)
+                committed[gi % 2].record(sc)
+
+        commit(0)
+        for gi, items in enumerate(groups):
+            if gi + 1 < len(groups):
+                commit(gi + 1)
+            bufs = bufs_of(gi)
+            cur.wait_event(committed[gi % 2])
+            corrBs = [self._slot_corrB(1 + (gi % 2) * group + j) for j in range(len(items))]
             for s0 in range(0, len(items), gemm_group):
                 sub = range(s0, min(s0 + gemm_group, len(items)))
                 # 3.-4. the nonces' noised operands and projections (own slot and corrB copy)
@@ -573,6 +606,8 @@ class MinedWeight:
                           target=self.target, winss=[bufs[j]["wins"] for j in sub], max_wins=self.max_wins,
                           a_scale=a_scale, b_scale=self.b_scale,
                           outs=[outs[items[j]] for j in sub] if out_mode != OUT_NONE else None, out_mode=out_mode)
+            consumed[gi % 2].record(cur)
+        cur.wait_stream(sc)
 
     def noise_mine(self, A: torch.Tensor, dump=None):
         """What a pure noise miner runs per attempt batch: commit A, noise it, hashed GEMM, no output.
