@@ -511,7 +511,7 @@ def traffic_probe(args, torch, ops, O, np):
     forwards at the bench shape (one group: batched GEMM launches of args.gemm_group nonces),
     then a plain device copy of COPY_BYTES three times, whose counter readings calibrate the KiB
     units of both counters."""
-    args.steps, args.warmup = args.gemm_group, args.gemm_group
+    args.steps, args.warmup, args.warmup_seconds = args.gemm_group, args.gemm_group, 0.0
     mining(args, torch, np, ops)
     x = torch.empty(COPY_BYTES, dtype=torch.int8, device="cuda").fill_(1)
     y = torch.empty_like(x)
@@ -567,10 +567,12 @@ def gemm_reps(steps: int) -> int:
 
 def summarize_trace(trace_csv, out_path, cmd, steps, warmup, group):
     """A kernel trace (run_kernel_trace.csv) of `bench.py --no-cpu --no-detrt --no-e2e --steps S
-    --warmup W` (groups of G nonces, one batched GEMM launch per group) as text: per kernel of the
-    timed sweep (from the end of the warm-up's last GEMM launch to the end of the sweep's last)
+    --warmup W ...` (groups of G nonces, one batched GEMM launch per group) as text: per kernel of
+    the timed sweep (from the end of the warm-up's last GEMM launch to the end of the sweep's last)
     calls, average and time per nonce, and the average of the back-to-back GEMM launches that give
-    the bench's roofline figure."""
+    the bench's roofline figure. The warm-up runs for a time, so the sweep is found from the end:
+    its S / G GEMM launches are followed by the capture call's launch, two untimed launches and the
+    timed back-to-back ones."""
     import csv
     import re
     steps, warmup, group = int(steps), int(warmup), int(group)
@@ -578,16 +580,18 @@ def summarize_trace(trace_csv, out_path, cmd, steps, warmup, group):
     name = lambda r: re.sub(r"\(.*", "", r["Kernel_Name"])  # noqa: E731
     dur = lambda r: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3  # noqa: E731
     g = [i for i, r in enumerate(rows) if "noisy_gemm256_kernel<true, true, 1, true>" in r["Kernel_Name"]]
-    nw, ns = -(-max(warmup, 2 * group) // group), -(-steps // group)  # launches of the warm-up and of the sweep
-    t0, t1 = int(rows[g[nw - 1]]["End_Timestamp"]), int(rows[g[nw + ns - 1]]["End_Timestamp"])
+    ns, nb = -(-steps // group), gemm_reps(steps)  # GEMM launches of the sweep, timed back-to-back launches
+    first = len(g) - nb - 3 - ns  # index in g of the sweep's first GEMM launch
+    assert first >= 1, "trace too short for a warm-up, a sweep and the back-to-back launches"
+    t0, t1 = int(rows[g[first - 1]]["End_Timestamp"]), int(rows[g[first + ns - 1]]["End_Timestamp"])
     per = {}
     for r in rows:
         if t0 < int(r["Start_Timestamp"]) and int(r["End_Timestamp"]) <= t1:
             per.setdefault(name(r), []).append(dur(r))
-    b2b = [dur(rows[i]) for i in g[nw + ns + 3:nw + ns + 3 + gemm_reps(steps)]]
+    b2b = [dur(rows[i]) for i in g[len(g) - nb:]]
     with open(out_path, "w") as f:
         f.write(f"rocprofv3 kernel trace, mined forward 4096x4096x4096 r=64 (bench.py workload), sweep of {steps} "
-                f"nonces after {warmup} warm-up nonces, {group} nonces per group\n")
+                f"nonces after {first * group} warm-up nonces, {group} nonces per group\n")
         f.write(f"command: {cmd}\n\n")
         f.write(f"timed sweep: {(t1 - t0) / 1e3 / steps:.2f} us per nonce (kernel trace clock)\n")
         f.write(f"{'kernel':58s} {'calls':>6s} {'avg_us':>9s} {'min_us':>9s} {'max_us':>9s} {'us/nonce':>9s}\n")
