@@ -41,6 +41,11 @@ extern "C" {
 /* Library version (1) and the message of the last failing call on this thread. */
 int uwc_version(void);
 const char* uwc_last_error(void);
+/* The first 16 hex digits of the SHA-256 of the include/uwc.h the library was built from: a
+ * binding compares it with the header it was written against, so a library left over from an
+ * earlier header (changed argument lists) is refused instead of called with the wrong layout.
+ * No counterpart in the reference (its kernels are compiled at import, kernels.cu via CuPy). */
+const char* uwc_header_sha(void);
 
 /*
  * C = A * B^T (A m x k, B n x k, int8, k contiguous, 16-byte aligned; k % 64 == 0), optionally:

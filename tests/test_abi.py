@@ -35,6 +35,15 @@ def test_library_exports_every_declared_symbol():
     assert L.uwc_version() == 1
 
 
+def test_library_built_from_this_header():
+    """The loader refuses a library stamped with another header's hash (argument lists would not
+    match); the stamp is the first 16 hex digits of SHA-256 of include/uwc.h."""
+    import hashlib
+    from uwc_amd import _lib
+    want = hashlib.sha256(open(HEADER, "rb").read()).hexdigest()[:16]
+    assert _lib.lib().uwc_header_sha().decode() == want
+
+
 def test_scratch_words_host_only():
     from uwc_amd import _lib
     L = _lib.lib()
@@ -130,3 +139,15 @@ def test_host_limb_rule_and_bound_words_match_oracle():
         want = O.bound_for_wins(m, n, w)
         got = ops.bound_words(((1 << 256) - 1) * w // ((m // 8) * (n // 16)))
         assert got.dtype == want.dtype and (got == want).all()
+
+
+def test_loader_refuses_library_of_another_header(tmp_path, monkeypatch):
+    """A header that differs from the one the library was built from (one changed byte) makes
+    the loader raise instead of binding the library."""
+    from uwc_amd import _lib
+    other = tmp_path / "uwc.h"
+    other.write_bytes(open(HEADER, "rb").read() + b"\n")
+    monkeypatch.setattr(_lib, "HEADER_PATH", str(other))
+    monkeypatch.setattr(_lib, "_LIB", None)
+    with pytest.raises(ImportError, match="another include/uwc.h"):
+        _lib.lib()

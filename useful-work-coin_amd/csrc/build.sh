@@ -7,7 +7,9 @@ set -e
 cd "$(dirname "$0")"
 OUT=../uwc_amd/libuwc_hip.so
 HIPCC=/opt/rocm/bin/hipcc
-FLAGS="--offload-arch=gfx950 -O3 -std=c++17 -fPIC -ffp-contract=off -Xclang -target-feature -Xclang -packed-fp32-ops -Wno-unused-result -I../../include ${UWC_HIPCC_EXTRA}"
+# the header's hash, which uwc_header_sha() returns and the Python binding checks at load
+SHA=$(sha256sum ../../include/uwc.h | cut -c1-16)
+FLAGS="--offload-arch=gfx950 -O3 -std=c++17 -fPIC -ffp-contract=off -Xclang -target-feature -Xclang -packed-fp32-ops -Wno-unused-result -I../../include -DUWC_HEADER_SHA=\"$SHA\" ${UWC_HIPCC_EXTRA}"
 TMP=$(mktemp -d)
 trap 'rm -rf "$TMP"' EXIT
 pids=""

@@ -26,6 +26,12 @@ extern "C" const char* uwc_last_error(void) { return g_last_error; }
 
 extern "C" int uwc_version(void) { return 1; }
 
+#ifndef UWC_HEADER_SHA
+#define UWC_HEADER_SHA "unstamped"
+#endif
+// build.sh stamps the header's hash in (-DUWC_HEADER_SHA=...)
+extern "C" const char* uwc_header_sha(void) { return UWC_HEADER_SHA; }
+
 // Compute units of the current device, queried once per device (256 on MI355X).
 int uwc_cu_count() {
   static int cached[64] = {0};

@@ -6,10 +6,12 @@ There is no fallback: if the library is missing or a call fails, this module rai
 from __future__ import annotations
 
 import ctypes
+import hashlib
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libuwc_hip.so")
+HEADER_PATH = os.path.join(_HERE, "..", "..", "include", "uwc.h")
 
 vp = ctypes.c_void_p
 i32 = ctypes.c_int
@@ -22,6 +24,7 @@ f32 = ctypes.c_float
 SIGNATURES = {
     "uwc_version": [],
     "uwc_last_error": [],
+    "uwc_header_sha": [],
     "uwc_noisy_gemm": [vp, vp, i32, i32, i32, i32, vp, vp, vp, i32, vp, vp, vp, i32, vp, vp, vp, i32, i32, vp, vp],
     "uwc_noisy_gemm_many": [i32, vp, vp, i32, i32, i32, i32, vp, vp, vp, i32, vp, vp, vp, i32, vp, vp, vp, i32, i32, vp],
     "uwc_igemm_i32": [vp, vp, i32, i32, i32, vp, vp],
@@ -55,7 +58,7 @@ SIGNATURES = {
     "uwc_det_elementwise": [i32, vp, vp, vp, i64, vp],
     "uwc_mfma_rate_probe": [i32, i32, vp, i64, vp],
 }
-_RESTYPE = {"uwc_last_error": ctypes.c_char_p}
+_RESTYPE = {"uwc_last_error": ctypes.c_char_p, "uwc_header_sha": ctypes.c_char_p}
 
 _LIB = None
 
@@ -75,6 +78,13 @@ def lib() -> ctypes.CDLL:
             fn = getattr(L, name)
             fn.argtypes = args
             fn.restype = _RESTYPE.get(name, ctypes.c_int)
+        if os.path.exists(HEADER_PATH):  # the source tree's header: the library must be built from it
+            with open(HEADER_PATH, "rb") as f:
+                want = hashlib.sha256(f.read()).hexdigest()[:16]
+            got = L.uwc_header_sha().decode()
+            if got != want:
+                raise ImportError(f"{LIB_PATH} was built from another include/uwc.h (stamp {got}, header {want}): "
+                                  "rebuild with useful-work-coin_amd/csrc/build.sh (or __graft_entry__.build())")
         _LIB = L
     return _LIB
 
