@@ -94,9 +94,13 @@ def mining(args, torch, np, ops):
         gen.manual_seed(1000 + i)
         As.append(torch.randint(-64, 64, (m, k), dtype=torch.int8, device=dev, generator=gen))
     ones = torch.ones(m, device=dev)
-    out = torch.empty((m, n), dtype=torch.int32, device=dev)
+    # distinct int32 outputs rotated through the sweep (64 MiB each at 4096^2): together larger than
+    # the 256 MB Infinity Cache, so the outputs' write-back is paid as in a real sweep
+    outbufs = [torch.empty((m, n), dtype=torch.int32, device=dev) for _ in range(args.out_buffers)]
+    rot = lambda count, first=0: [outbufs[(first + i) % len(outbufs)] for i in range(count)]  # noqa: E731
     torch.cuda.synchronize()
-    log(f"mining: {m}x{n}x{k} r={r}, {nbuf} distinct A resident, warmup {args.warmup}, steps {args.steps}")
+    log(f"mining: {m}x{n}x{k} r={r}, {nbuf} distinct A resident, {len(outbufs)} output buffers, warmup "
+        f"{args.warmup}, steps {args.steps}")
 
     # the sweep runs through MinedWeight.forward_many: one batched commitment and one noise launch
     # per group of nonces, then each nonce's projections and hashed GEMM
@@ -109,18 +113,19 @@ def mining(args, torch, np, ops):
     warm_list = [As[i % nbuf] for i in range(nwarm)]
     done, tw = 0, time.perf_counter()
     while done < args.warmup or done < 2 * args.group or time.perf_counter() - tw < args.warmup_seconds:
-        w.forward_many(warm_list, ones, outs=[out] * nwarm, out_mode=ops.OUT_I32, group=args.group,
+        w.forward_many(warm_list, ones, outs=rot(nwarm, done), out_mode=ops.OUT_I32, group=args.group,
                        gemm_group=args.gemm_group)
         torch.cuda.synchronize()
         done += nwarm
-    args.warmup = done
+    args.warmup_nonces_run = done
     log(f"mining: warm-up {done} nonces in {time.perf_counter() - tw:.2f} s")
-    sweep = [As[(args.warmup + i) % nbuf] for i in range(args.steps)]
+    sweep = [As[(done + i) % nbuf] for i in range(args.steps)]
     t0 = time.perf_counter()
-    w.forward_many(sweep, ones, outs=[out] * args.steps, out_mode=ops.OUT_I32, group=args.group,
+    w.forward_many(sweep, ones, outs=rot(args.steps), out_mode=ops.OUT_I32, group=args.group,
                    gemm_group=args.gemm_group)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
+    sweep_wins = w.sweep_winners()  # every nonce's winners, read back group by group during the sweep
 
     # the noisy GEMM alone: HIP events on its stream around back-to-back launches of the sweep's
     # last batched GEMM call (one launch = one group of nonces: same operands, corrections, seeds
@@ -130,7 +135,7 @@ def mining(args, torch, np, ops):
     calls = []
     ops.gemm_many = lambda *a, **kw: (calls.append((a, kw)), orig_gemm_many(*a, **kw))[1]
     try:
-        w.forward_many(sweep[-args.group:], ones, outs=[out] * args.group, out_mode=ops.OUT_I32, group=args.group,
+        w.forward_many(sweep[-args.group:], ones, outs=rot(args.group), out_mode=ops.OUT_I32, group=args.group,
                        gemm_group=args.gemm_group)
     finally:
         ops.gemm_many = orig_gemm_many
@@ -162,21 +167,26 @@ def mining(args, torch, np, ops):
     log(f"mining: {dt * 1e3 / args.steps:.3f} ms/nonce, {tops:.1f} TOPS whole path; noisy_gemm {launch_ms * 1e3:.1f} us "
         f"per launch of {per_launch} nonces = {kern_ms * 1e3:.1f} us per nonce = {kern_tops:.1f} TOP/s (L={L})")
     res = dict(m=m, n=n, k=k, r=r, dt=dt, tops=tops, kern_ms=kern_ms, kern_tops=kern_tops, L=L, w=w, As=As,
-               launch_ms=launch_ms, per_launch=per_launch,
-               job_key=job_key, target=target, Bt=Bt)
+               launch_ms=launch_ms, per_launch=per_launch, sweep_winners=sum(len(x) for x in sweep_wins),
+               job_key=job_key, target=target, Bt=Bt, ones=ones)
     return res
 
 
 def parity_and_cpu(args, res, torch, np, ops, O):
-    """Re-run one nonce on the GPU with the tile dump and compare it with the oracle, timing the
-    oracle's full mined forward for the same nonce on the host."""
+    """Re-run one group of the sweep on the GPU, through the same batched split-role GEMM launch the
+    sweep and the roofline time, with a tile dump per nonce, and compare its first nonce with the
+    oracle (output, every tile message and digest, winners), timing the oracle's full mined
+    forward of that nonce on the host."""
     m, n, k, r = res["m"], res["n"], res["k"], res["r"]
     w = res["w"]
-    A = res["As"][0]
-    dump = torch.zeros((m // 64) * 8 * (n // 64) * 4 * ops.DUMP_WORDS, dtype=torch.int32, device="cuda")
-    out = w._forward(A, torch.ones(m, device="cuda"), None, ops.OUT_I32, True, dump=dump)
+    group = [res["As"][i % len(res["As"])] for i in range(args.gemm_group)]
+    dumps = [torch.zeros((m // 64) * 8 * (n // 64) * 4 * ops.DUMP_WORDS, dtype=torch.int32, device="cuda")
+             for _ in group]
+    outs = w.forward_many(group, res["ones"], out_mode=ops.OUT_I32, group=args.group, gemm_group=args.gemm_group,
+                          dumps=dumps)
     torch.cuda.synchronize()
-    wins = set(w.winners(m))
+    wins = set(w.sweep_winners()[0])
+    out, dump, A = outs[0], dumps[0], group[0]
     A_np = A.cpu().numpy()
     Bt_np = res["Bt"].cpu().numpy()
     blk = O.block_side(res["job_key"], Bt_np, r)
@@ -192,7 +202,9 @@ def parity_and_cpu(args, res, torch, np, ops, O):
             break
     t_cpu = time.perf_counter() - t0
     d = dump.cpu().numpy().view(np.uint32).reshape(m // 64, 8, n // 64, 4, ops.DUMP_WORDS)
-    parity = dict(nonces_checked=1, output_exact=bool(np.array_equal(out.cpu().numpy(), ref["out"])),
+    parity = dict(kernel="noisy_gemm256_kernel<true, true, 1, true> (the timed split launch)",
+                  nonces_in_launch=len(group), nonces_checked=1,
+                  output_exact=bool(np.array_equal(out.cpu().numpy(), ref["out"])),
                   tile_digests_equal=bool(np.array_equal(d[..., 16:], ref["digests"])),
                   tile_messages_equal=bool(np.array_equal(d[..., :16], ref["msgs"])),
                   winners_equal=bool(wins == ref["winners"]), winners=len(wins),
@@ -632,15 +644,30 @@ def summarize_e2e_trace(stats_csv, out_path, cmd):
     print(open(out_path).read())
 
 
-def read_traffic():
-    """traffic_bytes_per_launch from the committed summary, or None."""
+def _summary_value(path, key):
+    """The number after `key:` in a committed rocprofv3 summary under profiles/, or None."""
     try:
-        for line in open(TRAFFIC_FILE):
-            if line.startswith("traffic_bytes_per_launch:"):
-                return int(float(line.split(":", 1)[1]))
+        for line in open(path):
+            if line.startswith(key + ":"):
+                return float(line.split(":", 1)[1].split()[0])
     except OSError:
         pass
     return None
+
+
+def read_traffic():
+    """traffic_bytes_per_launch from the committed FETCH_SIZE / WRITE_SIZE summary, or None."""
+    v = _summary_value(TRAFFIC_FILE, "traffic_bytes_per_launch")
+    return None if v is None else int(v)
+
+
+COUNTER_FILE = os.path.join(ROOT, "profiles", "noisy_gemm256_mining_4096_counters.txt")
+
+
+def read_mfma_busy():
+    """The hashed GEMM's matrix-core busy fraction from the committed counter summary:
+    SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x SIMDs), or None."""
+    return _summary_value(COUNTER_FILE, "mfma_busy_frac")
 
 
 def main():
@@ -652,6 +679,7 @@ def main():
     ap.add_argument("--size", type=int, default=4096)
     ap.add_argument("--rank", type=int, default=64)
     ap.add_argument("--distinct", type=int, default=64, help="distinct resident A matrices cycled over")
+    ap.add_argument("--out-buffers", type=int, default=8, help="distinct int32 outputs rotated through the sweep")
     ap.add_argument("--group", type=int, default=8, help="nonces per batched commitment / noise launch")
     ap.add_argument("--gemm-group", type=int, default=8, help="nonces per batched GEMM launch")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -712,6 +740,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_nonces_run": getattr(args, "warmup_nonces_run", None),
         "ms_per_step": round(res["dt"] * 1e3 / args.steps, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -725,11 +754,17 @@ def main():
         "mfma_sustained_tops": ceiling,
         "roofline": {"bound": "mfma", "achieved": round(res["kern_tops"], 2), "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
                      "frac": round(res["kern_tops"] / PEAK_INT8_TOPS, 4), "traffic": read_traffic(),
+                     "traffic_source": "profiles/noisy_gemm256_mining_4096_traffic.txt (rocprofv3 FETCH_SIZE + "
+                                       "WRITE_SIZE passes over bench.py --traffic-probe, copy-calibrated)",
+                     "mfma_busy_frac": read_mfma_busy(),
+                     "mfma_busy_source": "profiles/noisy_gemm256_mining_4096_counters.txt (rocprofv3 "
+                                         "SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x 1024 SIMDs))",
                      "kernel": "noisy_gemm256_kernel<HASH=true, DENOISE=true, OUT_I32, SPLIT=true>",
                      "avg_us": round(res["launch_ms"] * 1e3, 2), "nonces_per_launch": res["per_launch"],
                      "ops_per_launch": res["per_launch"] * (2 * m * n * k + 2 * m * n * 2 * r * res["L"])},
         "cpu_baseline": cpu,
         "parity": parity,
+        "sweep_winners": res["sweep_winners"],
         "detrt_layer": det,
         "detrt_skinny": skinny,
         "llama_prefill": prefill,

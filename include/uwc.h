@@ -73,9 +73,9 @@ int uwc_noisy_gemm(const int8_t* A, const int8_t* B, int m, int n, int k, int r,
 /*
  * `count` GEMMs sharing B (and target, scales, out_mode, flags), item i equal to
  * uwc_noisy_gemm(A[i], B, ..., corrA[i], corrB[i], maxabs[i], ..., key[i], target, wins[i], ...,
- * out[i], ...) without a tile dump. A, corrA, corrB, maxabs, key, wins and out are HOST arrays
- * of `count` device pointers (corrA/corrB/maxabs may be NULL without UWC_FLAG_DENOISE, key
- * without UWC_FLAG_HASH, wins entirely). With HASH | DENOISE, UWC_OUT_I32, m, n % 256 == 0 and
+ * out[i], ..., tile_dump[i]). A, corrA, corrB, maxabs, key, wins, out and tile_dump are HOST
+ * arrays of `count` device pointers (corrA/corrB/maxabs may be NULL without UWC_FLAG_DENOISE, key
+ * without UWC_FLAG_HASH, wins and tile_dump entirely). With HASH | DENOISE, UWC_OUT_I32, m, n % 256 == 0 and
  * count >= 2 the items run up to 16 per launch on the same tiles, the output stores of one item draining
  * while the next computes; otherwise one launch per item. The reference mines one nonce per
  * ops.gemm call (ops.py:185-198 from MinedWeight._forward, ops.py:339-347); this form serves a
@@ -85,7 +85,7 @@ int uwc_noisy_gemm_many(int count, const int8_t* const* A, const int8_t* B, int 
                         const int8_t* const* corrA, const int8_t* const* corrB, const int32_t* const* maxabs, int lmax,
                         const uint32_t* const* key, const uint32_t* target, uint32_t* const* wins, int max_wins,
                         const float* a_scale, const float* b_scale, void* const* out, int out_mode, int flags,
-                        hipStream_t stream);
+                        uint32_t* const* tile_dump, hipStream_t stream);
 
 /* Exact int32 C = A * B^T for any m, n (k % 64 == 0).
  * Replaces DetLinear.int_gemm's GPU path (torch._int_mm / MinedWeight.forward OUT_I32):

@@ -178,8 +178,21 @@ def attention(qq, qs, kq, ks, vq, vs, inv_sqrt: np.float32):
 
     qq (T, H, hd), kq / vq (T, Hkv, hd) integer-valued; qs (T, H, 1), ks / vs (T, Hkv, 1) fp32.
     Returns (sc (H, T, T) with -inf above the diagonal, pi (H, T, T) int32, sp (H, T, 1), o (H, T, hd))."""
-    T, H, hd = qq.shape
-    Hkv = kq.shape[1]
+    return _attend(qq, qs, kq, ks, vq, vs, inv_sqrt, np.arange(qq.shape[0]))
+
+
+def attention_rows(qq, qs, kq, ks, vq, vs, inv_sqrt: np.float32, rows):
+    """attention() for the query positions `rows` only (every key of the sequence is used): the
+    same computation restricted to those rows, without the (H, T, T) arrays, for long sequences.
+    Returns (sc, pi, sp, o) with the row axis of length len(rows)."""
+    rows = np.asarray(rows, np.int64)
+    return _attend(qq[rows], qs[rows], kq, ks, vq, vs, inv_sqrt, rows)
+
+
+def _attend(qq, qs, kq, ks, vq, vs, inv_sqrt, qpos):
+    """Query rows qq (R, H, hd) at positions qpos (R) against all T keys of kq / vq."""
+    H = qq.shape[1]
+    T, Hkv = kq.shape[0], kq.shape[1]
     rep = H // Hkv
     # float64 products are exact here: |q . k| < 2**24 and |sum p v| < 16383 * 127 * T < 2**53
     K = np.repeat(kq.transpose(1, 0, 2), rep, axis=0).astype(F64)   # (H, T, hd)
@@ -189,7 +202,7 @@ def attention(qq, qs, kq, ks, vq, vs, inv_sqrt: np.float32):
     Q, QS = qq.transpose(1, 0, 2).astype(F64), qs.transpose(1, 0, 2)
     sc_int = (Q @ K.transpose(0, 2, 1)).astype(F32)                 # exact: |s| < 2**24
     sc = ((sc_int * QS) * SK.transpose(0, 2, 1)) * inv_sqrt
-    mask = np.arange(T)[None, :] <= np.arange(T)[:, None]
+    mask = np.arange(T)[None, :] <= np.asarray(qpos)[:, None]
     sc = np.where(mask[None], sc, F32(-np.inf)).astype(F32)
     mx = sc.max(axis=-1, keepdims=True)
     with np.errstate(invalid="ignore"):

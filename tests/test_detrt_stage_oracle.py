@@ -175,3 +175,23 @@ def test_exact_rowsum_shift_for_softmax_rows():
     assert (ex == 1).all()
     assert S.det_exp(np.float32(0.0)) == np.float32(1.0)
     assert S.det_exp(np.float32(-np.inf)) == np.float32(0.0)
+
+
+def test_attention_rows_equals_full_attention():
+    """The row-subset attention (used to check T = 8192 rows) is the full attention's rows, bit for
+    bit, at sizes where the full (H, T, T) form runs, with GQA and the first and last positions."""
+    rng = np.random.default_rng(23)
+    T, H, Hkv, hd = 200, 4, 2, 64
+    qq = rng.integers(-127, 128, (T, H, hd)).astype(np.int64)
+    kq = rng.integers(-127, 128, (T, Hkv, hd)).astype(np.int64)
+    vq = rng.integers(-127, 128, (T, Hkv, hd)).astype(np.int64)
+    qs = rng.uniform(1e-3, 3e-2, (T, H, 1)).astype(np.float32)
+    ks = rng.uniform(1e-3, 3e-2, (T, Hkv, 1)).astype(np.float32)
+    vs = rng.uniform(1e-3, 3e-2, (T, Hkv, 1)).astype(np.float32)
+    inv = S.inv_sqrt_hd(hd)
+    full = S.attention(qq, qs, kq, ks, vq, vs, inv)
+    rows = [0, 1, 63, 64, 127, 199, 150]
+    part = S.attention_rows(qq, qs, kq, ks, vq, vs, inv, rows)
+    for f, p in zip(full, part):
+        np.testing.assert_array_equal(f[:, rows].view(np.uint32) if f.dtype == np.float32 else f[:, rows],
+                                      p.view(np.uint32) if p.dtype == np.float32 else p)

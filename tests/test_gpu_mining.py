@@ -117,10 +117,13 @@ def test_noise_generation_matches_oracle(dev, r):
     assert np.array_equal(_u32(P), O.perm_packed(O.SEED_LABEL_B, key, k, r))
 
 
-def test_noise_rows_noising_and_projection(dev):
+@pytest.mark.parametrize("rows,k,r", [(128, 2048, 128), (8, 4, 64), (24, 1000, 64), (16, 4100, 128), (64, 4096, 16)])
+def test_noise_rows_noising_and_projection(dev, rows, k, r):
+    """The general-shape operand pass (rows % 8, k % 4): noised rows, projection limbs, the E copy
+    and max |projection| against the oracle; a second call with only the projection and maxabs
+    (the B side of the LDS-atomic path) gives the same limbs."""
     ops = _ops()
-    rng = np.random.default_rng(3)
-    rows, k, r = 128, 2048, 128
+    rng = np.random.default_rng(3 + rows + k + r)
     A = rng.integers(-64, 65, size=(rows, k), dtype=np.int8)
     E = rng.integers(-32, 32, size=(rows, r), dtype=np.int8)
     Pn = O.perm_packed(O.SEED_LABEL_A, b"\x01" * 32, k, r)
@@ -130,8 +133,9 @@ def test_noise_rows_noising_and_projection(dev):
     L = ops.limbs_for(k)
     corr = torch.zeros((L, rows, 2 * r), dtype=torch.int8, device=dev)
     mx = torch.zeros(1, dtype=torch.int32, device=dev)
-    ops.noise_rows(torch.from_numpy(A).to(dev), rows, k, r, E=torch.from_numpy(E).to(dev), Pn=pack(Pn), dst=dst,
-                   Pp=pack(Pp), corr=corr, corr_off=0, ecopy_off=r, maxabs=mx)
+    Ad = torch.from_numpy(A).to(dev)
+    ops.noise_rows(Ad, rows, k, r, E=torch.from_numpy(E).to(dev), Pn=pack(Pn), dst=dst, Pp=pack(Pp), corr=corr,
+                   corr_off=0, ecopy_off=r, maxabs=mx)
     assert np.array_equal(dst.cpu().numpy(), O.noise_apply(A, E, Pn))
     proj = O.project(A, Pp, r)
     want = np.zeros((L, rows, 2 * r), np.int8)
@@ -140,6 +144,13 @@ def test_noise_rows_noising_and_projection(dev):
         want[li, :, r:] = E
     assert np.array_equal(corr.cpu().numpy(), want)
     assert int(mx.item()) == int(np.abs(proj).max())
+    corr2 = torch.zeros_like(corr)
+    mx2 = torch.full((1,), 3, dtype=torch.int32, device=dev)
+    ops.noise_rows(Ad, rows, k, r, Pp=pack(Pp), corr=corr2, corr_off=r, maxabs=mx2)
+    want2 = np.zeros((L, rows, 2 * r), np.int8)
+    O.write_limbs(proj, want2, r)
+    assert np.array_equal(corr2.cpu().numpy(), want2)
+    assert int(mx2.item()) == max(3, int(np.abs(proj).max()))
 
 
 @pytest.mark.parametrize("m,n,k,r", [(128, 128, 1024, 64), (256, 256, 2048, 64), (256, 384, 2048, 128),

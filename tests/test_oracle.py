@@ -2,6 +2,7 @@
 restatements and brute force, chosen so that a dropped term, a wrong index or a transposed
 operand fails at least one check."""
 import hashlib
+import json
 import os
 
 import numpy as np
@@ -18,6 +19,22 @@ def test_blake3_published_digests():
     assert O.b3(b"").hex() == "af1349b9f5f9a1a6a0404dea36dcc9499bcb25c9adc112b7cc9a93cae41f3262"
     assert O.b3(b"abc").hex() == "6437b3ac38465133ffb63b75273a8db548c558465d79db03fd359c6cd5bd9d85"
     assert py_b3(b"").hex() == "af1349b9f5f9a1a6a0404dea36dcc9499bcb25c9adc112b7cc9a93cae41f3262"
+
+
+def test_blake3_official_test_vectors():
+    """The BLAKE3 team's published vectors (tests/golden/blake3_official_vectors.json): one block
+    (len 0, 1), a full 16-block chunk (1024: chunk chaining, CHUNK_START/END), two chunks under a
+    parent node (1025: chunk counter, PARENT, ROOT placement), and keyed mode (KEYED_HASH flag and
+    the key in place of the IV), for both restatements."""
+    v = json.load(open(os.path.join(GOLDEN, "blake3_official_vectors.json")))
+    key = v["key"].encode()
+    for case in v["cases"]:
+        data = bytes(i % 251 for i in range(case["input_len"]))
+        assert O.b3(data).hex() == case["hash"], case["input_len"]
+        assert py_b3(data).hex() == case["hash"], case["input_len"]
+        if "keyed_hash" in case:
+            assert O.b3(data, key).hex() == case["keyed_hash"], case["input_len"]
+            assert py_b3(data, key).hex() == case["keyed_hash"], case["input_len"]
 
 
 @pytest.mark.parametrize("nchunks", list(range(1, 40)) + [63, 64, 65, 127, 128, 129])

@@ -425,7 +425,7 @@ extern "C" int uwc_igemm_dequant_f32(const int8_t* A, const int8_t* B, int m, in
 int uwc_noisy_gemm256_many(int count, const int8_t* const* A, const int8_t* B, int m, int n, int k, int r,
                            const int8_t* const* corrA, const int8_t* const* corrB, const int32_t* const* maxabs,
                            int lmax, const uint32_t* const* key, const uint32_t* target, uint32_t* const* wins,
-                           int max_wins, void* const* out, hipStream_t stream);
+                           int max_wins, void* const* out, uint32_t* const* tile_dump, hipStream_t stream);
 
 #define GEMM_MANY_MAX 16  // items per split launch (the kernel's item table)
 
@@ -434,7 +434,7 @@ extern "C" int uwc_noisy_gemm_many(int count, const int8_t* const* A, const int8
                                    const int32_t* const* maxabs, int lmax, const uint32_t* const* key,
                                    const uint32_t* target, uint32_t* const* wins, int max_wins, const float* a_scale,
                                    const float* b_scale, void* const* out, int out_mode, int flags,
-                                   hipStream_t stream) {
+                                   uint32_t* const* tile_dump, hipStream_t stream) {
   if (count < 0 || (count > 0 && (!A || !out))) return uwc_fail("uwc_noisy_gemm_many: count=%d or null A / out arrays", count);
   const bool hash = flags & FLAG_HASH, denoise = flags & FLAG_DENOISE;
   if ((hash && !key) || (denoise && (!corrA || !corrB || !maxabs)))
@@ -453,7 +453,7 @@ extern "C" int uwc_noisy_gemm_many(int count, const int8_t* const* A, const int8
       if (int st = uwc_noisy_gemm(A[i], B, m, n, k, r, denoise ? corrA[i] : nullptr, denoise ? corrB[i] : nullptr,
                                   denoise ? maxabs[i] : nullptr, lmax, hash ? key[i] : nullptr, target,
                                   wins ? wins[i] : nullptr, max_wins, a_scale, b_scale, out[i], out_mode, flags,
-                                  nullptr, stream))
+                                  tile_dump ? tile_dump[i] : nullptr, stream))
         return st;
     return 0;
   }
@@ -461,7 +461,8 @@ extern "C" int uwc_noisy_gemm_many(int count, const int8_t* const* A, const int8
   for (int i0 = 0; i0 < count; i0 += GEMM_MANY_MAX) {
     const int c = count - i0 < GEMM_MANY_MAX ? count - i0 : GEMM_MANY_MAX;
     if (int st = uwc_noisy_gemm256_many(c, A + i0, B, m, n, k, r, corrA + i0, corrB + i0, maxabs + i0, lmax, key + i0,
-                                        target, wins ? wins + i0 : no_wins, max_wins, out + i0, stream))
+                                        target, wins ? wins + i0 : no_wins, max_wins, out + i0,
+                                        tile_dump ? tile_dump + i0 : nullptr, stream))
       return st;
   }
   return 0;

@@ -90,6 +90,7 @@ struct Gemm256Item {
   const u32* key;
   u32* wins;
   void* out;
+  u32* dump;  // optional tile dump (messages and digests), NULL to skip
 };
 
 struct Gemm256Params {
@@ -100,7 +101,6 @@ struct Gemm256Params {
   int max_wins;
   const float* a_scale;
   const float* b_scale;
-  u32* dump;
   int ldc;  // output row stride in elements
   int count;
   Gemm256Item it[G256_MAXB];
@@ -709,9 +709,9 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
       for (int i = 0; i < 8; i++) key[i] = ld_uniform(I.key, i);
       b3_keyed64(key, msg, h);
       const int row = bm0 + wm * 128 + hb * 64 + g, col = bn0 + wn * 64 + 2 * t;
-      if (p.dump) {
+      if (I.dump) {
         const long NB = p.n / 64;
-        u32* d = p.dump + ((((long)(row >> 6) * 8 + g) * NB + (col >> 6)) * 4 + t) * DUMP_WORDS;
+        u32* d = I.dump + ((((long)(row >> 6) * 8 + g) * NB + (col >> 6)) * 4 + t) * DUMP_WORDS;
 #pragma unroll
         for (int w = 0; w < 16; w++) d[w] = msg[w];
 #pragma unroll
@@ -893,10 +893,9 @@ int uwc_noisy_gemm256(const int8_t* A, const int8_t* B, int m, int n, int k, int
   p.max_wins = max_wins;
   p.a_scale = a_scale;
   p.b_scale = b_scale;
-  p.dump = hash ? tile_dump : nullptr;
   p.ldc = ldc;
   p.count = 1;
-  p.it[0] = Gemm256Item{A, corrA, corrB, maxabs, key, wins, out};
+  p.it[0] = Gemm256Item{A, corrA, corrB, maxabs, key, wins, out, hash ? tile_dump : nullptr};
   const dim3 grid((m / W_BM) * (n / W_BN));
   if (hash && denoise) out256<true, true>(out_mode, grid, stream, p);
   else if (hash) out256<true, false>(out_mode, grid, stream, p);
@@ -911,7 +910,7 @@ int uwc_noisy_gemm256(const int8_t* A, const int8_t* B, int m, int n, int k, int
 int uwc_noisy_gemm256_many(int count, const int8_t* const* A, const int8_t* B, int m, int n, int k, int r,
                            const int8_t* const* corrA, const int8_t* const* corrB, const int32_t* const* maxabs,
                            int lmax, const uint32_t* const* key, const uint32_t* target, uint32_t* const* wins,
-                           int max_wins, void* const* out, hipStream_t stream) {
+                           int max_wins, void* const* out, uint32_t* const* tile_dump, hipStream_t stream) {
   if (count < 1 || count > G256_MAXB) return uwc_fail("uwc_noisy_gemm256_many: count=%d outside 1..%d", count, G256_MAXB);
   Gemm256Params p{};
   p.B = B;
@@ -921,7 +920,8 @@ int uwc_noisy_gemm256_many(int count, const int8_t* const* A, const int8_t* B, i
   p.max_wins = max_wins;
   p.ldc = n;
   p.count = count;
-  for (int i = 0; i < count; i++) p.it[i] = Gemm256Item{A[i], corrA[i], corrB[i], maxabs[i], key[i], wins[i], out[i]};
+  for (int i = 0; i < count; i++)
+    p.it[i] = Gemm256Item{A[i], corrA[i], corrB[i], maxabs[i], key[i], wins[i], out[i], tile_dump ? tile_dump[i] : nullptr};
   go256<true, true, OUT_I32, true>(dim3((m / W_BM) * (n / W_BN)), stream, p);
   return uwc_launch_status("noisy_gemm256 (split, batched)");
 }

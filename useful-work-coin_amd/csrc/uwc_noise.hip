@@ -1,7 +1,7 @@
 // Per-nonce noise kernels of the cuPOW miner on gfx950 (the commitment is uwc_commit.hip):
 //   uniform noise E and the noise pairs P (kernels.cu:246-301, reference.py:67-93);
 //   operand noising + rank-r projections in balanced base-128 limbs + max |projection|
-//   (kernels.cu:303-372).
+//   (kernels.cu:303-404): a general-shape per-row form and the matrix-core forms.
 #include "uwc_common.h"
 
 // ------------------------------------------------------------------ noise generation
@@ -78,79 +78,82 @@ extern "C" int uwc_noise_perm(uint32_t* out, uint32_t k, uint32_t r, const uint3
 }
 
 // ------------------------------------------------------------------ operand noising + projections
-// For NR_ROWS rows per workgroup, optionally:
-//   dst[l]  = int8(src[l] + E[row][Pn.first(l)] - E[row][Pn.second(l)])           (noising)
-//   proj[j] = sum_l src[l] ([Pp.first(l) == j] - [Pp.second(l) == j])             (projection)
-// then proj in `lmax` balanced base-128 limbs to corr[li][row][corr_off + j] (row stride 2r),
-// E rows copied to corr[li][row][ecopy_off + j] for every limb, and max |proj| into *maxabs.
-// Projection sums use LDS integer atomics: integer addition is associative, so the order in
-// which lanes land does not change the result.
-#define NR_ROWS 8
-__global__ void __launch_bounds__(256) noise_rows_kernel(const i8* __restrict__ src, int rows, int k, int r,
-                                                         const i8* __restrict__ E, const u32* __restrict__ Pn,
-                                                         i8* __restrict__ dst, const u32* __restrict__ Pp,
-                                                         i8* __restrict__ corr, int corr_off, int ecopy_off,
-                                                         i32* __restrict__ maxabs, int lmax) {
-  extern __shared__ __attribute__((aligned(16))) u8 nr_smem[];
-  i8* Es = reinterpret_cast<i8*>(nr_smem);                              // NR_ROWS * r
-  i32* proj = reinterpret_cast<i32*>(nr_smem + NR_ROWS * r);            // NR_ROWS * r
-  const int row0 = blockIdx.x * NR_ROWS, tid = threadIdx.x;
-  if (E)
-    for (int i = tid; i < NR_ROWS * r; i += 256) Es[i] = E[(u64)row0 * r + i];
-  if (Pp)
-    for (int i = tid; i < NR_ROWS * r; i += 256) proj[i] = 0;
+// The general-shape form (rows % 8, k % 4) of the per-row operand pass, for shapes the matrix-core
+// kernels below do not take. Each of the workgroup's 8 waves owns one row and a private LDS
+// region: the row's E entries and its r projection bins. The wave walks the row a dword per lane
+// (4 columns, 256 columns per wave step) and, per column l,
+//   noising:    dst[l] = int8(src[l] + E[row][Pn.first(l)] - E[row][Pn.second(l)])
+//   projection: bin[Pp.first(l)] += src[l], bin[Pp.second(l)] -= src[l]   (LDS integer adds)
+// (kernels.cu:303-372). Integer addition is associative, so the order in which the lanes' adds
+// land does not change a bin. After one barrier each wave writes its row's bins as `lmax`
+// balanced base-128 limbs, copies its E row into every limb, and the workgroup contributes one
+// atomic max of |bin| to *maxabs.
+#define NRW_WAVES 8
+#define NRW_MAXR 256
+
+__device__ __forceinline__ void row_limbs(i8* __restrict__ out, u64 limb_stride, int v, int lmax) {
+  // balanced base-128 digits: d = ((v + 64) mod 128) - 64, v <- (v - d) / 128 (exact)
+  for (int li = 0; li < lmax; li++) {
+    const int d = ((v + 64) & 127) - 64;
+    out[li * limb_stride] = (i8)d;
+    v = (v - d) >> 7;
+  }
+}
+
+__global__ void __launch_bounds__(NRW_WAVES * 64) rows_noise_kernel(
+    const i8* __restrict__ src, int rows, int k, int r, const i8* __restrict__ E, const u32* __restrict__ Pn,
+    i8* __restrict__ dst, const u32* __restrict__ Pp, i8* __restrict__ corr, int corr_off, int ecopy_off,
+    i32* __restrict__ maxabs, int lmax) {
+  __shared__ i32 bins[NRW_WAVES][NRW_MAXR];
+  __shared__ i8 erow[NRW_WAVES][NRW_MAXR];
+  __shared__ int wave_max[NRW_WAVES];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int row = blockIdx.x * NRW_WAVES + w;
+  const i8* srow = src + (u64)row * k;
+  for (int j = lane; j < r; j += 64) {
+    if (E) erow[w][j] = E[(u64)row * r + j];
+    bins[w][j] = 0;
+  }
   __syncthreads();
-  const int quads = k >> 2, total = NR_ROWS * quads;
-  for (int it = tid; it < total; it += 256) {
-    const int rr = it / quads, q = it - rr * quads;
-    const u64 off = (u64)(row0 + rr) * k + 4 * q;
-    const u32 w = *reinterpret_cast<const u32*>(src + off);
-    u32 o = 0;
+  for (int l0 = 4 * lane; l0 < k; l0 += 256) {
+    const u32 word = *reinterpret_cast<const u32*>(srow + l0);
+    u32 noised = 0;
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int l = 4 * q + j;
-      const int x = (int)(i8)(u8)(w >> (8 * j));
+    for (int b = 0; b < 4; b++) {
+      const int x = (int)(i8)(u8)(word >> (8 * b));
       if (dst) {
-        const u32 pn = Pn[l];
-        const int nv = x + (int)Es[rr * r + (pn & 0xFFFF)] - (int)Es[rr * r + (pn >> 16)];
-        o |= ((u32)(u8)nv) << (8 * j);
+        const u32 pn = Pn[l0 + b];
+        noised |= (u32)(u8)(x + erow[w][pn & 0xFFFF] - erow[w][pn >> 16]) << (8 * b);
       }
       if (Pp) {
-        const u32 pp = Pp[l];
-        atomicAdd(&proj[rr * r + (pp & 0xFFFF)], x);
-        atomicSub(&proj[rr * r + (pp >> 16)], x);
+        const u32 pp = Pp[l0 + b];
+        atomicAdd(&bins[w][pp & 0xFFFF], x);
+        atomicAdd(&bins[w][pp >> 16], -x);
       }
     }
-    if (dst) *reinterpret_cast<u32*>(dst + off) = o;
+    if (dst) *reinterpret_cast<u32*>(dst + (u64)row * k + l0) = noised;
   }
   __syncthreads();
-  const u64 limb_stride = (u64)rows * 2 * r;
-  int local_max = 0;
-  for (int i = tid; i < NR_ROWS * r; i += 256) {
-    const int rr = i / r, j = i - rr * r;
-    const u64 base = (u64)(row0 + rr) * 2 * r;
-    if (Pp && corr_off >= 0) {
-      int v = proj[i];
-      local_max = max(local_max, abs(v));
-      for (int li = 0; li < lmax; li++) {
-        const int d = ((v + 64) & 127) - 64;
-        corr[li * limb_stride + base + corr_off + j] = (i8)d;
-        v = (v - d) >> 7;
-      }
+  const u64 limb_stride = (u64)rows * 2 * r, base = (u64)row * 2 * r;
+  int mx = 0;
+  for (int j = lane; j < r; j += 64) {
+    if (Pp) {
+      const int v = bins[w][j];
+      mx = max(mx, abs(v));
+      if (corr_off >= 0) row_limbs(corr + base + corr_off + j, limb_stride, v, lmax);
     }
-    if (E && ecopy_off >= 0) {
-      const i8 e = Es[i];
-      for (int li = 0; li < lmax; li++) corr[li * limb_stride + base + ecopy_off + j] = e;
-    }
+    if (E && ecopy_off >= 0)
+      for (int li = 0; li < lmax; li++) corr[li * limb_stride + base + ecopy_off + j] = erow[w][j];
   }
   if (Pp && maxabs) {
-    // one global atomic per workgroup: same-address atomics serialize in L2
-    __shared__ int wmax[4];
-#pragma unroll
-    for (int s = 32; s > 0; s >>= 1) local_max = max(local_max, __shfl_xor(local_max, s));
-    if ((tid & 63) == 0) wmax[tid >> 6] = local_max;
+    for (int s = 32; s >= 1; s >>= 1) mx = max(mx, __shfl_xor(mx, s));
+    if (lane == 0) wave_max[w] = mx;
     __syncthreads();
-    if (tid == 0) atomicMax(maxabs, max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3])));
+    if (threadIdx.x == 0) {
+      int m = 0;
+      for (int i = 0; i < NRW_WAVES; i++) m = max(m, wave_max[i]);
+      atomicMax(maxabs, m);  // one same-address atomic per workgroup
+    }
   }
 }
 
@@ -158,18 +161,19 @@ extern "C" int uwc_noise_rows(const int8_t* src, int rows, int k, int r, const i
                               int8_t* dst, const uint32_t* Pp, int8_t* corr, int corr_off, int ecopy_off,
                               int32_t* maxabs, int lmax, hipStream_t stream) {
   if (!src || rows <= 0 || k <= 0 || r <= 0) return uwc_fail("uwc_noise_rows: empty or null src");
-  if (rows % NR_ROWS || k % 4) return uwc_fail("uwc_noise_rows: rows=%d must be a multiple of %d and k=%d of 4", rows, NR_ROWS, k);
+  if (rows % NRW_WAVES || k % 4)
+    return uwc_fail("uwc_noise_rows: rows=%d must be a multiple of %d and k=%d of 4", rows, NRW_WAVES, k);
+  if (r > NRW_MAXR) return uwc_fail("uwc_noise_rows: r=%d above %d", r, NRW_MAXR);
   if (((uintptr_t)src & 3u) || (dst && ((uintptr_t)dst & 3u))) return uwc_fail("uwc_noise_rows: src/dst must be 4-byte aligned");
   if (dst && (!E || !Pn)) return uwc_fail("uwc_noise_rows: noising needs E and Pn");
-  if ((corr_off >= 0 && Pp) || (ecopy_off >= 0 && E)) {
-    if (!corr || lmax < 1) return uwc_fail("uwc_noise_rows: limbs need corr and lmax >= 1");
-    if ((corr_off >= 0 && corr_off + r > 2 * r) || (ecopy_off >= 0 && ecopy_off + r > 2 * r))
+  if (!corr) corr_off = ecopy_off = -1;
+  if (corr_off >= 0 || ecopy_off >= 0) {
+    if (lmax < 1 || lmax > 4) return uwc_fail("uwc_noise_rows: limbs need lmax in 1..4");
+    if ((corr_off >= 0 && corr_off != 0 && corr_off != r) || (ecopy_off >= 0 && ecopy_off != 0 && ecopy_off != r))
       return uwc_fail("uwc_noise_rows: corr_off/ecopy_off must be 0 or r");
   }
-  const size_t smem = (size_t)NR_ROWS * r * 5;
-  if (smem > 64 * 1024) return uwc_fail("uwc_noise_rows: r=%d too large", r);
-  hipLaunchKernelGGL(noise_rows_kernel, dim3(rows / NR_ROWS), dim3(256), smem, stream, src, rows, k, r, E, Pn, dst, Pp,
-                     corr, corr ? corr_off : -1, corr ? ecopy_off : -1, maxabs, corr ? lmax : 0);
+  hipLaunchKernelGGL(rows_noise_kernel, dim3(rows / NRW_WAVES), dim3(NRW_WAVES * 64), 0, stream, src, rows, k, r, E, Pn,
+                     dst, Pp, corr, corr_off, ecopy_off, maxabs, corr ? lmax : 0);
   return uwc_launch_status("noise_rows");
 }
 
@@ -295,13 +299,8 @@ __global__ void __launch_bounds__(NP_THREADS) noise_project_kernel(const i8* __r
     const int ro = i / r, j = i - ro * r;
     const u64 base = (u64)(row0 + ro) * 2 * r;
     if (PROJ && corr_off >= 0) {
-      int v = Xs[i];
-      local_max = max(local_max, abs(v));
-      for (int li = 0; li < lmax; li++) {
-        const int d = ((v + 64) & 127) - 64;
-        corr[li * limb_stride + base + corr_off + j] = (i8)d;
-        v = (v - d) >> 7;
-      }
+      local_max = max(local_max, abs(Xs[i]));
+      row_limbs(corr + base + corr_off + j, limb_stride, Xs[i], lmax);
     }
     if (E && ecopy_off >= 0) {
       const i8 e = Es[ro * es + j];

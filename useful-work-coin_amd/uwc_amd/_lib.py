@@ -26,7 +26,7 @@ SIGNATURES = {
     "uwc_last_error": [],
     "uwc_header_sha": [],
     "uwc_noisy_gemm": [vp, vp, i32, i32, i32, i32, vp, vp, vp, i32, vp, vp, vp, i32, vp, vp, vp, i32, i32, vp, vp],
-    "uwc_noisy_gemm_many": [i32, vp, vp, i32, i32, i32, i32, vp, vp, vp, i32, vp, vp, vp, i32, vp, vp, vp, i32, i32, vp],
+    "uwc_noisy_gemm_many": [i32, vp, vp, i32, i32, i32, i32, vp, vp, vp, i32, vp, vp, vp, i32, vp, vp, vp, i32, i32, vp, vp],
     "uwc_igemm_i32": [vp, vp, i32, i32, i32, vp, vp],
     "uwc_igemm_dequant_f32": [vp, vp, i32, i32, i32, vp, vp, vp, vp],
     "uwc_b3_scratch_words": [u64],

@@ -18,6 +18,8 @@ Everything runs on torch's current HIP stream; buffers are torch tensors on the 
 """
 from __future__ import annotations
 
+import hashlib
+
 import numpy as np
 import torch
 
@@ -223,12 +225,41 @@ def merkle_roots(words: torch.Tensor, ntrees: int) -> torch.Tensor:
     return roots
 
 
+# sha256(cos bytes || sin bytes) of detrt's pinned fp32 rope tables (runtime/artifacts/*.npz, built
+# by qwen3.py:49-68; the Qwen3-1.7B one is also recorded as rope_table_sha in
+# results/step2/xdev_cpu.json:4): (theta, head_dim, positions) -> digest.
+PINNED_ROPE_SHA = {
+    (1e6, 128, 8192): "8ee66518240c0e045455c4ff8fb6cf1d959e22872c1e0dbba4bbc18985d3df26",
+    (1e4, 64, 8192): "bfd2634ada10ea33214570446397a3749cf48de85eac0a0fba1531f18abaa79a",
+    (1e4, 32, 64): "2ff462ac8583a2f5ef106fc4a9823cb845ece1243d83d73b5565c53ffee34bc7",
+}
+
+
+def rope_table(theta: float, head_dim: int, max_pos: int) -> tuple[np.ndarray, np.ndarray]:
+    """detrt's fp32 rope tables (max_pos x head_dim): angle(p, i) = p / theta^(2 (i mod hd/2) / hd)
+    in float64, cos and sin in float64 rounded once to float32 (qwen3.py:59-66). The reference
+    loads them from pinned files; here they are computed on the host, and a table with a pinned
+    digest is checked against it, so a host whose libm rounds differently fails loudly instead of
+    silently changing every rotated query and key."""
+    half = np.arange(0, head_dim, 2, dtype=np.float64) / head_dim
+    freq = 1.0 / np.power(float(theta), half)
+    ang = np.outer(np.arange(max_pos, dtype=np.float64), np.tile(freq, 2))
+    cos, sin = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    want = PINNED_ROPE_SHA.get((float(theta), int(head_dim), int(max_pos)))
+    if want is not None:
+        got = hashlib.sha256(cos.tobytes() + sin.tobytes()).hexdigest()
+        if got != want:
+            raise RuntimeError(f"rope_table(theta={theta:g}, hd={head_dim}, pos={max_pos}): this host's table hashes to "
+                               f"{got[:16]}..., not detrt's pinned {want[:16]}...")
+    return cos, sin
+
+
 def digest_bytes(words) -> np.ndarray:
-    """(..., 8) sha256 state words (torch or numpy) -> (..., 32) digest bytes."""
-    if isinstance(words, torch.Tensor):
-        words = words.cpu().numpy()
-    w = np.ascontiguousarray(words).view(np.uint32)
-    return w.byteswap().view(np.uint8).reshape(*w.shape[:-1], 32)
+    """SHA-256 digests as bytes: (..., 8) state words, torch or numpy, to (..., 32) uint8. A digest
+    is its state words in big-endian byte order (FIPS 180-4)."""
+    host = words.detach().to("cpu").numpy() if isinstance(words, torch.Tensor) else np.asarray(words)
+    be = np.ascontiguousarray(host).astype(">u4", copy=False)
+    return be.view(np.uint8).reshape(host.shape[:-1] + (32,))
 
 
 def sout_leaves(out: torch.Tensor) -> np.ndarray:
@@ -345,11 +376,8 @@ class DetModel:
             layers.append(dict(in_norm=nw(D), post_norm=nw(D), q_norm=nw(hd), k_norm=nw(hd),
                                qkv=lin((H + 2 * Hkv) * hd, D), o=lin(D, H * hd), gu=lin(2 * I, D), down=lin(D, I)))
         embed_t = torch.randn((V, D), generator=g, device=device)
-        inv = 1.0 / (cfg.get("theta", 1e6) ** (np.arange(0, hd, 2, dtype=np.float64) / hd))
-        ang = np.arange(cfg.get("max_pos", 8192), dtype=np.float64)[:, None] * inv[None, :]
-        emb = np.concatenate([ang, ang], axis=1)
-        cos = torch.from_numpy(np.cos(emb).astype(np.float32)).to(device)
-        sin = torch.from_numpy(np.sin(emb).astype(np.float32)).to(device)
+        cos_np, sin_np = rope_table(cfg.get("theta", 1e6), hd, cfg.get("max_pos", 8192))
+        cos, sin = torch.from_numpy(cos_np).to(device), torch.from_numpy(sin_np).to(device)
         lm = lin(V, D) if with_lm_head else None
         return cls(cfg, embed_t, layers, cos, sin, nw(D), lm)
 
@@ -386,13 +414,16 @@ def stage_outputs(m, tokens: torch.Tensor | None, x: torch.Tensor | None, l0: in
 
 
 def job_outputs(m, tokens: torch.Tensor, groups: int, upto: int | None = None) -> list[torch.Tensor]:
-    """Every group's output for a batch of sequences, kept on the GPU (detgpu/stages.py:216-225)."""
-    lpg = len(m.layers) // groups
-    upto = groups - 1 if upto is None else upto
-    outs, x = [], None
-    for g in range(upto + 1):
-        x = stage_outputs(m, tokens if g == 0 else None, x, g * lpg, (g + 1) * lpg)
-        outs.append(x)
+    """The outputs of layer groups 0 .. upto (default: all) for a batch of sequences, each (B, T, D)
+    on the GPU: the layers split into `groups` equal runs, each run continuing from the previous
+    run's output (detgpu/stages.py:216-225)."""
+    per = len(m.layers) // groups
+    last = groups - 1 if upto is None else upto
+    bounds = [(g * per, (g + 1) * per) for g in range(last + 1)]
+    outs = []
+    for l0, l1 in bounds:
+        prev = outs[-1] if outs else None
+        outs.append(stage_outputs(m, tokens if prev is None else None, prev, l0, l1))
     return outs
 
 

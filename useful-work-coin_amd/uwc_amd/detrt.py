@@ -54,8 +54,9 @@ class DetLinear:
     """int8 W7A7 linear: W -> Wq = quant_sym(fwht(W, bs), 64), s_w folded by 1/sqrt(bs);
     __call__(x) = (f32(quant_act(x) @ Wq^T) * s_x) * s_w.
 
-    `mine` is accepted for signature compatibility; mining per linear goes through
-    uwc_amd.ops.MinedWeight (setup_block / int_gemm then route through it)."""
+    With mine=True, setup_block() prepares a MinedWeight (r = 128) for the layers detrt mines, and
+    int_gemm() then runs the mined forward (hashed tiles, exact denoise, int32 out) instead of the
+    plain GEMM: the same integers either way (qwen3.py:94-116)."""
 
     def __init__(self, W: torch.Tensor, device, hadamard_block: int, mine: bool = False):
         n, k = W.shape
@@ -87,11 +88,20 @@ class DetLinear:
         self.mine, self.mw = False, None
         return self
 
+    # the layers detrt mines (qwen3.py:96): k >= 2048, k % 128 == 0 and n a multiple of the GEMM
+    # tile's N, which is 128 in the reference's default configuration ("128x3", ops.py:35-37) and
+    # is the hashed GEMM's requirement here (m, n % 128; 256-multiples take the large tiles)
+    MINE_MIN_K = 2048
+
+    def mineable(self) -> bool:
+        return self.k >= self.MINE_MIN_K and self.k % 128 == 0 and self.n % ops.BN == 0
+
     def setup_block(self, job_key_for_k, bound_for_k):
-        """Prepare this weight for mining under a block template (qwen3.py:94-104)."""
+        """Prepare this weight for mining under a block template (qwen3.py:94-104); a layer that
+        cannot be mined stops trying (mine becomes False), as the reference does."""
         if not self.mine:
             return
-        ok = self.k % 128 == 0 and self.n % ops.BN == 0
+        ok = self.mineable()
         if not ok:
             self.mine = False
             return

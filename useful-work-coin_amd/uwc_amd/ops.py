@@ -2,15 +2,22 @@
 stream: the call surface of the reference's miner/ampere/uwc_ampere/ops.py (same names,
 argument meaning and error behaviour), over libuwc_hip.so's C-ABI (include/uwc.h).
 
-Differences a caller can see: the GEMM tile is 128 x 128 (so m and n of hashed GEMMs must be
-multiples of 128, not of the reference's BN), `cfg` is accepted and ignored (one tiling), and
-gemm() can also dump every tile's message and digest (`dump`). OUT_F32 is an extra output mode
-(the fused detrt dequant epilogue).
+Differences a caller can see:
+  * two GEMM tilings, CONFIGS["256x256"] (the default; m and n multiples of 256) and
+    CONFIGS["128x128"] (any m, n for plain GEMMs; m, n multiples of 128 with a transcript), with
+    identical outputs and winners; a hashed GEMM therefore needs m, n % 128 == 0 where the
+    reference needs m % 128 and n % BN;
+  * gemm() can also dump every tile's message and digest (`dump`), and OUT_F32 is an extra output
+    mode (the fused detrt dequant epilogue);
+  * MinedWeight.forward_many runs a sweep of nonces with batched commitments, noise and GEMM
+    launches, and sweep_winners() returns every nonce's winners.
 """
 from __future__ import annotations
 
 import ctypes
+import functools
 import gc
+import sys
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -20,19 +27,21 @@ from . import _lib
 
 BM, BN, BK = 128, 128, 64
 
-
-def limbs_for(k: int) -> int:
-    """Balanced base-128 limbs that always cover |projection| <= 127 * k (ops.py:18-24)."""
-    bound, L, cap = 127 * k, 1, 63
-    while cap < bound:
-        L += 1
-        cap = cap * 128 + 63
-    return L
+# L balanced base-128 limbs, each digit in [-64, 63], represent every |v| <= 63 (1 + 128 + ... +
+# 128^(L-1)) = 63 (128^L - 1) / 127: 63, 8127, 1040319, ... (kernels.cu:357-360, 602-607).
+LIMB_CAPS = tuple(63 * (128 ** L - 1) // 127 for L in range(1, 5))
 
 
 def limbs_for_max(mx: int) -> int:
-    """Limbs the denoise pass uses for a runtime max |projection| mx (kernels.cu:602-607)."""
-    return 1 if mx <= 63 else 2 if mx <= 8127 else 3 if mx <= 1040319 else 4
+    """Limbs the denoise pass uses for a runtime max |projection| mx (kernels.cu:602-607); the
+    kernels stop at 4."""
+    return next((L for L, cap in enumerate(LIMB_CAPS[:3], 1) if mx <= cap), 4)
+
+
+def limbs_for(k: int) -> int:
+    """Limbs that cover any projection of k int8 values, |projection| <= 127 k (ops.py:18-24):
+    the limb count the correction buffers are sized for."""
+    return limbs_for_max(127 * k)
 
 
 def bound_words(bound: int) -> np.ndarray:
@@ -73,29 +82,36 @@ def _stream() -> int:
     return torch.cuda.current_stream().cuda_stream
 
 
+assert sys.byteorder == "little", "the 32-byte values are little-endian u32 words, as the host's int32"
+
+
 def words(b: bytes, device="cuda") -> torch.Tensor:
-    return torch.from_numpy(np.frombuffer(b, dtype="<u4").view(np.int32).copy()).to(device)
+    """A 32-byte value as the 8 int32 words the kernels take (little-endian u32, ops.py:73-78)."""
+    _check(len(b) % 4 == 0, f"words: {len(b)} bytes is not a whole number of 32-bit words")
+    return torch.frombuffer(bytearray(b), dtype=torch.int32).to(device)
 
 
 def words_to_bytes(t: torch.Tensor) -> bytes:
-    return t.detach().cpu().numpy().view(np.uint32).astype("<u4").tobytes()
+    """The inverse of words(): the tensor's 32-bit words as little-endian bytes."""
+    return t.detach().to("cpu", torch.int32).contiguous().numpy().tobytes()
 
 
 LABEL_A = words(SEED_LABEL_A, "cpu")
 LABEL_B = words(SEED_LABEL_B, "cpu")
 SALT_A = words(SEED_SALT_A, "cpu")
 SALT_B = words(SEED_SALT_B, "cpu")
-_CONSTS: dict = {}
+
+
+@functools.lru_cache(maxsize=None)
+def _consts_on(device: str) -> dict:
+    return {"LABEL_A": LABEL_A.to(device), "LABEL_B": LABEL_B.to(device), "SALT_A": SALT_A.to(device),
+            "SALT_B": SALT_B.to(device)}
 
 
 def consts(device) -> dict:
-    """Device copies of the label/salt constants (made once; forward() must not copy H2D)."""
-    key = str(torch.device(device))
-    c = _CONSTS.get(key)
-    if c is None:
-        c = _CONSTS[key] = {n: t.to(device) for n, t in
-                            dict(LABEL_A=LABEL_A, LABEL_B=LABEL_B, SALT_A=SALT_A, SALT_B=SALT_B).items()}
-    return c
+    """The label and salt words resident on `device`, copied there once per device, so that a
+    forward (and a graph capture of it) never copies host to device (ops.py:85-95)."""
+    return _consts_on(str(torch.device(device)))
 
 
 # ------------------------------------------------------------------ BLAKE3
@@ -283,11 +299,11 @@ def gemm(A, B, *, r=128, flags=0, corrA=None, corrB=None, maxabs=None, key=None,
 
 
 def gemm_many(As, B, *, r=128, flags=0, corrAs=None, corrBs=None, maxabss=None, keys=None, target=None, winss=None,
-              max_wins=0, a_scale=None, b_scale=None, outs=None, out_mode=OUT_NONE):
+              max_wins=0, a_scale=None, b_scale=None, outs=None, out_mode=OUT_NONE, dumps=None):
     """gemm() of several operands As[i] against one B, item i with its own corrections, maxabs,
-    seed, win buffer and output. With FLAG_HASH | FLAG_DENOISE, OUT_I32 and m, n % 256 == 0 the
-    items share launches (up to 16 per launch, output stores overlapping the next item);
-    otherwise one launch per item. Results equal separate gemm() calls."""
+    seed, win buffer, output and optional tile dump. With FLAG_HASH | FLAG_DENOISE, OUT_I32 and
+    m, n % 256 == 0 the items share launches (up to 16 per launch, output stores overlapping the
+    next item); otherwise one launch per item. Results equal separate gemm() calls."""
     count = len(As)
     if count == 0:
         return
@@ -299,14 +315,14 @@ def gemm_many(As, B, *, r=128, flags=0, corrAs=None, corrBs=None, maxabss=None, 
         _check(tuple(A.shape) == (m, k) and A.dtype == torch.int8 and A.is_contiguous(),
                "gemm_many: every A must be a contiguous int8 m x k")
     _check(B.dtype == torch.int8 and B.is_contiguous(), "gemm_many: B must be contiguous int8")
-    for xs in (corrAs, corrBs, maxabss, keys, winss, outs):
+    for xs in (corrAs, corrBs, maxabss, keys, winss, outs, dumps):
         _check(xs is None or len(xs) == count, "gemm_many: one entry per item")
     _check(outs is not None or out_mode == OUT_NONE, "gemm_many: outputs needed for this out_mode")
     lmax = corrAs[0].shape[0] if corrAs is not None else 0
     out_arr = _arr(outs) if outs is not None else ctypes.cast((ctypes.c_void_p * count)(), ctypes.c_void_p)
     _lib.call("uwc_noisy_gemm_many", count, _arr(As), _p(B), m, n, k, r, _arr(corrAs), _arr(corrBs), _arr(maxabss),
               lmax, _arr(keys), _p(target), _arr(winss), max_wins, _p(a_scale), _p(b_scale), out_arr, out_mode, flags,
-              _stream())
+              _arr(dumps), _stream())
 
 
 def igemm_i32(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
@@ -347,6 +363,7 @@ class MinedWeight:
     corrB: torch.Tensor | None = None
     SBt: torch.Tensor | None = None
     _bufs: dict = field(default_factory=dict)
+    _block_gen: int = 0  # bumped by every setup_block: per-slot copies of corrB made earlier are stale
 
     @property
     def n(self):
@@ -383,6 +400,7 @@ class MinedWeight:
         else:
             noise_rows(Bt, n, k, r, E=self.EBRt, Pn=self.PB, dst=self.BpEBt, corr=self.corrB, ecopy_off=0)
         self.SBt = proj_matrix(self.PB, k, r)
+        self._block_gen += 1
         del Bt
 
     def _buf(self, m: int, slot: int = 0, wins: torch.Tensor | None = None):
@@ -414,12 +432,18 @@ class MinedWeight:
         return {**ws, "wins": wins}
 
     def _slot_corrB(self, slot: int) -> torch.Tensor:
-        """A per-slot copy of corrB for forward_many: the E copy setup_block wrote, and room for
-        the slot's nonce's Y limbs (the reference's single corrB serves one call at a time)."""
-        cb = self._bufs.get(("corrB", slot))
-        if cb is None or cb.shape != self.corrB.shape or self._bufs.get(("corrB_src", slot)) is not self.corrB:
-            cb = self._bufs[("corrB", slot)] = self.corrB.clone()
-            self._bufs[("corrB_src", slot)] = self.corrB
+        """A per-slot copy of corrB for forward_many: the E_B columns setup_block wrote, and room
+        for the slot's nonce's Y limbs (the reference's single corrB serves one call at a time).
+        The copy is refreshed (on the current stream) whenever setup_block has run since it was
+        made: a new block template rewrites E_B in place."""
+        gen, cb = self._bufs.get(("corrB", slot), (None, None))
+        if cb is None or cb.shape != self.corrB.shape:
+            cb = torch.empty_like(self.corrB)
+            gen = None
+        if gen != self._block_gen:
+            cb.copy_(self.corrB)
+            gen = self._block_gen
+        self._bufs[("corrB", slot)] = (gen, cb)
         return cb
 
     def forward(self, A: torch.Tensor, a_scale: torch.Tensor, out: torch.Tensor | None = None,
@@ -507,21 +531,26 @@ class MinedWeight:
         return self._after_commit(A, b, a_scale, out, out_mode, hash_tiles, cfg=cfg, proj=proj, dump=dump)
 
     def forward_many(self, As, a_scale: torch.Tensor, outs=None, out_mode: int = OUT_BF16, hash_tiles: bool = True,
-                     wins=None, group: int = SWEEP_GROUP, gemm_group: int = GEMM_GROUP):
+                     wins=None, group: int = SWEEP_GROUP, gemm_group: int = GEMM_GROUP, dumps=None):
         """Mined forwards of a sequence of activations (the nonces of a sweep), each equal to
-        forward(As[i]) bit for bit. The nonces go in groups of `group` (1..MAX_BATCH): one set of
-        launches commits the whole group (BLAKE3 trees and salted seeds) and one launch draws all
-        of its noise, so those latency-bound chains run several waves per SIMD instead of one,
-        and on a second stream one group ahead, beside the previous group's projections; then
-        the group's nonces run their projections and hashed GEMMs, `gemm_group` nonces per
-        batched GEMM call (whose output stores overlap the next nonce's tiles; a smaller batch
-        keeps the noised operands it reads in the Infinity Cache). The work is queued behind the
-        current stream, which then waits for all of it. Python's cyclic garbage collector is
-        paused while the launches are queued (a full collection can stall the host for tens of
-        milliseconds, longer than the GPU work already queued), and its previous state restored. outs / wins: optional per-item
-        output tensors and win buffers (1 + max_wins * WIN_WORDS int32 each); without wins,
-        winners() reports the last item (the others' records go to per-slot buffers). Returns the
-        outputs."""
+        forward(As[i]) bit for bit, winners included.
+
+        The nonces go in groups of `group` (1..MAX_BATCH): one set of launches commits the whole
+        group (BLAKE3 trees and salted seeds) and one launch draws all of its noise, so those
+        latency-bound chains run several waves per SIMD instead of one, on a second stream one
+        group ahead, beside the previous group's projections; then the group's nonces run their
+        projections and hashed GEMMs, `gemm_group` nonces per batched GEMM call (whose output
+        stores overlap the next nonce's tiles). The work is queued behind the current stream,
+        which then waits for all of it. Python's cyclic garbage collector is paused while the
+        launches are queued (a full collection can stall the host for tens of milliseconds,
+        longer than the GPU work already queued), and its previous state restored.
+
+        Every nonce records its winners in its own buffer: the caller's `wins` (one int32 tensor
+        of 1 + max_wins * WIN_WORDS words per item), or else rows of a sweep buffer that the
+        weight keeps, copied to pinned host memory group by group on the stream as each group's
+        GEMMs finish; sweep_winners() returns them all. winners(m) keeps reporting the last
+        item, as after forward(). dumps: optional per-item tile dumps (gemm()'s `dump` layout).
+        Returns the outputs."""
         n_items = len(As)
         if n_items == 0:
             return []
@@ -531,19 +560,39 @@ class MinedWeight:
         for A in As:
             self._check_a(A)
             _check(A.shape[0] == m, "MinedWeight.forward_many: every A needs the same shape")
+        _check(wins is None or len(wins) == n_items, "MinedWeight.forward_many: one win buffer per item")
+        _check(dumps is None or len(dumps) == n_items, "MinedWeight.forward_many: one tile dump per item")
         outs = [self._out(m, outs[i] if outs is not None else None, out_mode) for i in range(n_items)]
         c = consts(As[0].device)
         side = side_ok(m, self.n, k, r)
+        host = None
+        if wins is None:
+            wins, host = self._sweep_win_rows(m, n_items)
+        self._sweep_host = (host, n_items) if host is not None else None
         gc_on = gc.isenabled()
         gc.disable()
         try:
-            self._sweep(As, a_scale, outs, out_mode, hash_tiles, wins, group, gemm_group, m, k, r, c, side)
+            self._sweep(As, a_scale, outs, out_mode, hash_tiles, wins, group, gemm_group, m, k, r, c, side, host, dumps)
         finally:
             if gc_on:
                 gc.enable()
         return outs
 
-    def _sweep(self, As, a_scale, outs, out_mode, hash_tiles, wins, group, gemm_group, m, k, r, c, side):
+    def _sweep_win_rows(self, m: int, n_items: int):
+        """Device win buffers for a sweep of n_items nonces (rows of one tensor, grown on demand)
+        and the pinned host copy they are read back into. The last item's row is the weight's own
+        buffer of this m, so winners(m) reports it."""
+        words = 1 + self.max_wins * WIN_WORDS
+        dev_rows, host_rows = self._bufs.get(("sweep_wins", m), (None, None))
+        if dev_rows is None or dev_rows.shape[0] < n_items:
+            dev_rows = torch.zeros((n_items, words), dtype=torch.int32, device=self.device)
+            host_rows = torch.zeros((n_items, words), dtype=torch.int32, pin_memory=True)
+            self._bufs[("sweep_wins", m)] = (dev_rows, host_rows)
+        rows = [dev_rows[i] for i in range(n_items - 1)] + [self._buf(m)["wins"]]
+        return rows, (host_rows, rows)
+
+    def _sweep(self, As, a_scale, outs, out_mode, hash_tiles, wins, group, gemm_group, m, k, r, c, side, host=None,
+               dumps=None):
         """Group g's commitment and noise go on a side stream, one group ahead, so that they run
         beside group g - 1's projections (the BLAKE3 chains are VALU-bound, the projections
         memory-bound, and a CU holds one workgroup of each); groups alternate between two sets of
@@ -553,19 +602,19 @@ class MinedWeight:
         groups = [list(range(g0, min(g0 + group, n_items))) for g0 in range(0, n_items, group)]
         cur = torch.cuda.current_stream(self.device)
         sync = _SWEEP_SYNC.get(str(self.device))
-        if sync is None:  # default-priority side stream and four reusable events per device
+        if sync is None:  # default-priority side and copy streams, four reusable events per device
             sync = _SWEEP_SYNC[str(self.device)] = (torch.cuda.Stream(device=self.device),
                                                     [torch.cuda.Event() for _ in range(2)],
-                                                    [torch.cuda.Event() for _ in range(2)])
-        sc, committed, consumed = sync
+                                                    [torch.cuda.Event() for _ in range(2)],
+                                                    torch.cuda.Stream(device=self.device))
+        sc, committed, consumed, cs = sync
         sc.wait_stream(cur)
+        sc.wait_stream(cs)  # the previous sweep's win copies read buffers this sweep clears
 
         def bufs_of(gi):
             out = []
             for j, i in enumerate(groups[gi]):
-                # the sweep's last item reports through the weight's own win buffer (slot 0's)
-                wb = wins[i] if wins is not None else (self._buf(m)["wins"] if i == n_items - 1 else None)
-                out.append(self._buf(m, slot=1 + (gi % 2) * group + j, wins=wb))
+                out.append(self._buf(m, slot=1 + (gi % 2) * group + j, wins=wins[i]))
             return out
 
         def commit(gi):
@@ -605,8 +654,15 @@ class MinedWeight:
                           maxabss=[bufs[j]["maxabs"] for j in sub], keys=[bufs[j]["a_seed"] for j in sub],
                           target=self.target, winss=[bufs[j]["wins"] for j in sub], max_wins=self.max_wins,
                           a_scale=a_scale, b_scale=self.b_scale,
-                          outs=[outs[items[j]] for j in sub] if out_mode != OUT_NONE else None, out_mode=out_mode)
+                          outs=[outs[items[j]] for j in sub] if out_mode != OUT_NONE else None, out_mode=out_mode,
+                          dumps=[dumps[items[j]] for j in sub] if dumps is not None else None)
             consumed[gi % 2].record(cur)
+            if host is not None:  # this group's win records to the pinned host rows, on the copy
+                host_rows, rows = host  # stream once its GEMMs are done (compute never waits for it)
+                cs.wait_event(consumed[gi % 2])
+                with torch.cuda.stream(cs):
+                    for i in items:
+                        host_rows[i].copy_(rows[i], non_blocking=True)
         cur.wait_stream(sc)
 
     def noise_mine(self, A: torch.Tensor, dump=None):
@@ -629,37 +685,62 @@ class MinedWeight:
              max_wins=self.max_wins, dump=dump)
 
     def winners(self, m: int) -> list[tuple[int, int, bytes]]:
-        """(row_offset, col_offset, hash) for winning tiles of the last forward with this m (syncs)."""
-        w = self._buf(m)["wins"].cpu().numpy().view(np.uint32)
-        cnt = min(int(w[0]), self.max_wins)
-        recs = w[1:1 + cnt * WIN_WORDS].reshape(cnt, WIN_WORDS)
-        return [(int(x[0]), int(x[1]), x[2:].astype("<u4").tobytes()) for x in recs]
+        """(row_offset, col_offset, hash) for winning tiles of the last forward with this m
+        (ops.py:366-371; reads the device buffer, so it waits for the work queued so far)."""
+        return win_records(self._buf(m)["wins"], self.max_wins)
+
+    def sweep_winners(self) -> list[list[tuple[int, int, bytes]]]:
+        """Every nonce's winners of the last forward_many without caller win buffers, in item
+        order: waits for the sweep's queued work, then parses the pinned host copies."""
+        _check(getattr(self, "_sweep_host", None) is not None,
+               "MinedWeight.sweep_winners: no forward_many without caller win buffers has run")
+        (host_rows, _), n_items = self._sweep_host
+        _SWEEP_SYNC[str(self.device)][3].synchronize()
+        return [win_records(host_rows[i], self.max_wins) for i in range(n_items)]
+
+
+def win_records(buf: torch.Tensor, max_wins: int) -> list[tuple[int, int, bytes]]:
+    """Parse a win buffer [count, (row, col, digest[8]) x max_wins] (kernels.cu:586-595): the
+    first min(count, max_wins) records as (row_offset, col_offset, 32-byte digest)."""
+    w = buf.detach().to("cpu").numpy().view(np.uint32)
+    kept = min(int(w[0]), max_wins)
+    out = []
+    for rec in np.split(w[1:1 + kept * WIN_WORDS], kept) if kept else []:
+        out.append((int(rec[0]), int(rec[1]), rec[2:].tobytes()))
+    return out
 
 
 class GraphedForward:
-    """MinedWeight.forward captured as one HIP graph for a fixed m (static input/output buffers).
+    """MinedWeight.forward at a fixed m replayed from one HIP graph (ops.py:374-396): the input,
+    scale and output tensors are the graph's own (copy activations into .A, read .out).
 
-    The graph records no memset node: the win counter and maxabs are cleared by kernels
-    (torch's zero_ fill and noise_uniform's zero_me)."""
+    The captured forward records kernels only: the win counter and maxabs are cleared by the
+    noise launch, never by a memset node. Before capture one eager forward on the capture stream
+    allocates the workspace this (m, k, r) shares and sets the kernels' launch attributes, neither
+    of which may happen inside a capture."""
 
     def __init__(self, w: MinedWeight, m: int, out_mode: int = OUT_BF16):
+        self.w, self.m, self.out_mode = w, m, out_mode
         dev = w.device
-        self.w, self.m = w, m
         self.A = torch.zeros((m, w.k), dtype=torch.int8, device=dev)
         self.a_scale = torch.ones(m, dtype=torch.float32, device=dev)
-        dt = {OUT_BF16: torch.bfloat16, OUT_I32: torch.int32, OUT_F32: torch.float32}[out_mode]
-        self.out = torch.empty((m, w.n), dtype=dt, device=dev)
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            for _ in range(2):
-                w.forward(self.A, self.a_scale, out=self.out, out_mode=out_mode)
-        torch.cuda.current_stream().wait_stream(side)
-        torch.cuda.synchronize()
+        self.out = w._out(m, None, out_mode)
         self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
-            w.forward(self.A, self.a_scale, out=self.out, out_mode=out_mode)
+        self._record(torch.cuda.Stream(device=dev))
 
-    def __call__(self):
+    def _forward(self):
+        self.w.forward(self.A, self.a_scale, out=self.out, out_mode=self.out_mode)
+
+    def _record(self, stream: torch.cuda.Stream):
+        caller = torch.cuda.current_stream(self.w.device)
+        stream.wait_stream(caller)
+        with torch.cuda.stream(stream):
+            self._forward()  # eager: workspace and attributes
+            stream.synchronize()
+            with torch.cuda.graph(self.graph, stream=stream):
+                self._forward()
+        caller.wait_stream(stream)
+
+    def __call__(self) -> torch.Tensor:
         self.graph.replay()
         return self.out
