@@ -120,6 +120,17 @@ int uwc_b3_root_and_seed_many(const uint8_t* const* data, int count, uint64_t nb
                               uint32_t* const* seed_out, uint32_t* scratch, uint64_t scratch_words,
                               hipStream_t stream);
 
+/* uwc_b3_root_and_seed without a scratch argument: the same root and seed, for inputs of at most
+ * 1 GiB (2^30 bytes; larger inputs are rejected with UWC_EINVAL), with the workspace in a static
+ * device array of 131,200 words (513 KiB) that every GPU the library runs on holds until the
+ * process ends. No counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops). It allocates nothing; its first call
+ * on a device looks up that device's workspace address (make it before a capture). Calls that
+ * overlap on one GPU share the workspace and race; calls ordered on one stream do not. */
+int uwc_b3_root_and_seed_static(const uint8_t* data, uint64_t nbytes, const uint32_t* key, const uint32_t* prefix,
+                                const uint32_t* salt, uint32_t dim, uint32_t* root_out, uint32_t* seed_out,
+                                hipStream_t stream);
+
 /* out (nblocks x 32 int8) = (bytes of keyed_BLAKE3(key, msg(index, label)) & 63) - 32; also
  * zeroes zero_me[0..zero_n) (may be NULL with zero_n = 0).
  * Replaces ops.noise_uniform: ops.py:122-125, kernels.cu:259-282. */

@@ -11,6 +11,8 @@
 // This quarters the dependent instruction chain per compression and gives 4x the waves.
 #include "uwc_common.h"
 
+#include <mutex>
+
 #define QROT1 0x39  // quad_perm [1,2,3,0]: lane q takes lane (q+1) & 3
 #define QROT2 0x4E  // quad_perm [2,3,0,1]
 #define QROT3 0x93  // quad_perm [3,0,1,2]
@@ -334,6 +336,77 @@ extern "C" int uwc_b3_root_and_seed_many(const uint8_t* const* data, int count, 
     outs.seed[i] = seed_out ? seed_out[i] : nullptr;
   }
   return b3_launch(in, count, nbytes, key, prefix, salt, dim, outs, scratch, (u64)need, stream);
+}
+
+// ------------------------------------------------------------------ allocation-free commitment
+// uwc_b3_root_and_seed for callers that cannot allocate (code under graph capture, serving loops):
+// the workspace the chunk and reduce kernels pass subtree values through is a file-scope device
+// array instead of a caller's buffer, sized for inputs up to UWC_B3_STATIC_MAX_BYTES. Each GPU
+// the library runs on holds its own copy until the process ends. Host code never uses the
+// array's name as an address: the first call on a device looks its device address up with
+// hipGetSymbolAddress and keeps it per device. Every call on one GPU shares that GPU's array, so
+// calls that overlap on one GPU (on different streams) race; calls on one stream are ordered.
+// Nothing in the workspace needs to start at zero: the chunk kernel writes every value a
+// reduction then reads, and the previous call's contents are overwritten.
+#define UWC_B3_STATIC_MAX_BYTES (1ull << 30)
+#define UWC_MAX_DEVICES 64
+
+constexpr u64 b3_words_for(u64 nbytes) {
+  u64 cnt = (nbytes / 1024 + B3_CHUNKS_PER_WG - 1) / B3_CHUNKS_PER_WG, words = cnt * 8;
+  while (cnt > B3_GROUP) {
+    cnt = (cnt + B3_GROUP - 1) / B3_GROUP;
+    words += cnt * 8;
+  }
+  return words;
+}
+#define B3_STATIC_WORDS b3_words_for(UWC_B3_STATIC_MAX_BYTES)
+static_assert(B3_STATIC_WORDS == 131200, "1 GiB: 16384 subtree values, then 16 group values");
+
+static __device__ __align__(256) u32 b3_static_scratch[B3_STATIC_WORDS];
+
+static std::mutex g_b3_static_mu;
+static u32* g_b3_static_ptr[UWC_MAX_DEVICES];  // device address of b3_static_scratch, per device
+
+// The current device's address of b3_static_scratch (looked up once per device), or NULL after
+// recording the error.
+static u32* b3_static_workspace(const char* fn) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= UWC_MAX_DEVICES) {
+    uwc_fail("%s: no usable current device (%d)", fn, dev);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_b3_static_mu);
+  if (!g_b3_static_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(b3_static_scratch));
+    if (e != hipSuccess || !ptr) {
+      uwc_fail("%s: hipGetSymbolAddress of the static workspace failed on device %d: %s", fn, dev,
+               hipGetErrorString(e));
+      return nullptr;
+    }
+    g_b3_static_ptr[dev] = static_cast<u32*>(ptr);
+  }
+  return g_b3_static_ptr[dev];
+}
+
+extern "C" int uwc_b3_root_and_seed_static(const uint8_t* data, uint64_t nbytes, const uint32_t* key,
+                                           const uint32_t* prefix, const uint32_t* salt, uint32_t dim,
+                                           uint32_t* root_out, uint32_t* seed_out, hipStream_t stream) {
+  static const char* fn = "uwc_b3_root_and_seed_static";
+  if (!data) return uwc_fail("%s: null data", fn);
+  if (int st = b3_check(nbytes, key, prefix, salt, seed_out != nullptr, fn)) return st;
+  if (nbytes > UWC_B3_STATIC_MAX_BYTES)
+    return uwc_fail("%s: %llu bytes exceed the static workspace's maximum of %llu bytes (use uwc_b3_root_and_seed "
+                    "with a scratch buffer)", fn, (unsigned long long)nbytes, (unsigned long long)UWC_B3_STATIC_MAX_BYTES);
+  if (((uintptr_t)data & 15u) != 0) return uwc_fail("%s: data must be 16-byte aligned", fn);
+  u32* ws = b3_static_workspace(fn);
+  if (!ws) return UWC_EINVAL;
+  B3In in{};
+  B3Out outs{};
+  in.data[0] = data;
+  outs.root[0] = root_out;
+  outs.seed[0] = seed_out;
+  return b3_launch(in, 1, nbytes, key, prefix, salt, dim, outs, ws, b3_words_for(nbytes), stream);
 }
 
 // ------------------------------------------------------------------ per-nonce noise in one launch
