@@ -84,7 +84,9 @@ def mining(args, torch, np, ops):
     Bt = torch.from_numpy(rng.integers(-64, 64, size=(n, k), dtype=np.int8)).to(dev)
     job_key = rng.bytes(32)
     target = ops.bound_words(((1 << 256) - 1) * 12 // ((m // 8) * (n // 16)))  # about 12 winning 8 x 16 tiles
-    w = ops.MinedWeight(Bt=Bt, b_scale=torch.ones(n, device=dev), r=r, max_wins=4096)
+    # win records: about 12 winners per nonce are expected; 256 record slots per nonce (the count
+    # itself is exact beyond the cap, as in the reference's buffers)
+    w = ops.MinedWeight(Bt=Bt, b_scale=torch.ones(n, device=dev), r=r, max_wins=256)
     w.setup_block(job_key, target)
     nA = args.steps + args.warmup
     nbuf = min(nA, args.distinct)
@@ -111,6 +113,7 @@ def mining(args, torch, np, ops):
     # and the JSON line reports the nonces actually run.
     nwarm = max(args.warmup, 2 * args.group)
     warm_list = [As[i % nbuf] for i in range(nwarm)]
+    w.reserve_sweep(m, max(nwarm, args.steps))  # the sweep's win rows (device + pinned host), allocated before timing
     done, tw = 0, time.perf_counter()
     while done < args.warmup or done < 2 * args.group or time.perf_counter() - tw < args.warmup_seconds:
         w.forward_many(warm_list, ones, outs=rot(nwarm, done), out_mode=ops.OUT_I32, group=args.group,
@@ -572,6 +575,40 @@ def summarize_pmc(fetch_csv, write_csv, cmd, nonces):
     print(open(TRAFFIC_FILE).read())
 
 
+def summarize_counters(csv_path, cmd, nonces):
+    """Per-dispatch counters of the hashed GEMM (median over its dispatches) from one rocprofv3 --pmc
+    pass over `bench.py --traffic-probe`, into COUNTER_FILE, with the matrix-core busy fraction.
+    SQ_VALU_MFMA_BUSY_CYCLES sums, over every SIMD, the cycles its matrix core works (it equals the
+    dispatch's MFMA work: 8 nonces x 73.0 GMAC / 1024 MAC per cycle); GRBM_GUI_ACTIVE sums the
+    active cycles of the 8 XCDs' graphics blocks. busy fraction = MFMA cycles / (active cycles of
+    one XCD x 1024 SIMDs)."""
+    import csv
+    import statistics
+    vals = {}
+    for row in csv.DictReader(open(csv_path)):
+        if "noisy_gemm256_kernel<true, true, 1, true>" in row["Kernel_Name"]:
+            vals.setdefault(row["Counter_Name"], []).append(float(row["Counter_Value"]))
+    med = {c: statistics.median(v) for c, v in vals.items()}
+    simds, xcds = 256 * 4, 8
+    busy, active = med.get("SQ_VALU_MFMA_BUSY_CYCLES"), med.get("GRBM_GUI_ACTIVE")
+    frac = busy / (active / xcds * simds) if busy and active else None
+    nonces = int(nonces)
+    with open(COUNTER_FILE, "w") as f:
+        f.write(f"rocprofv3 counters of noisy_gemm256_kernel<true, true, 1, true> (mining 4096^3, r=64, {nonces} nonces "
+                f"per dispatch), median per dispatch over {len(next(iter(vals.values())))} dispatches\n")
+        f.write(f"command: {cmd}\n")
+        for c in sorted(med):
+            f.write(f"{c}: {med[c]:.0f}\n")
+        if frac is not None:
+            f.write(f"mfma_busy_frac: {frac:.4f} (SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / {xcds} XCDs x {simds} "
+                    f"SIMDs))\n")
+            f.write(f"active_cycles_per_xcd: {active / xcds:.0f} (divide by the dispatch's duration for the clock)\n")
+        if "SQ_INSTS_VALU_MFMA_MOPS_I8" in med and active:
+            f.write(f"mfma_i8_ops_per_dispatch: {med['SQ_INSTS_VALU_MFMA_MOPS_I8'] * 512:.4g} "
+                    "(SQ_INSTS_VALU_MFMA_MOPS_I8 x 512)\n")
+    print(open(COUNTER_FILE).read())
+
+
 def gemm_reps(steps: int) -> int:
     """Back-to-back launches of the noisy GEMM that time it after the sweep."""
     return max(8, min(steps, 64))
@@ -694,6 +731,8 @@ def main():
     ap.add_argument("--traffic-probe", action="store_true", help="the workload of the FETCH_SIZE / WRITE_SIZE passes")
     ap.add_argument("--summarize-pmc", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "CMD", "NONCES"),
                     help="write the traffic summary under profiles/ from two counter_collection.csv files")
+    ap.add_argument("--summarize-counters", nargs=3, metavar=("COUNTER_CSV", "CMD", "NONCES"),
+                    help="write the hashed GEMM's counter summary under profiles/ from a counter_collection.csv")
     ap.add_argument("--summarize-e2e-trace", nargs=3, metavar=("STATS_CSV", "OUT", "CMD"),
                     help="write a configs[4] kernel-trace summary under profiles/")
     ap.add_argument("--summarize-trace", nargs=6, metavar=("TRACE_CSV", "OUT", "CMD", "STEPS", "WARMUP", "GROUP"),
@@ -707,6 +746,9 @@ def main():
         return
     if args.summarize_pmc:
         summarize_pmc(*args.summarize_pmc)
+        return
+    if args.summarize_counters:
+        summarize_counters(*args.summarize_counters)
         return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the multi-GPU layout "
@@ -758,7 +800,7 @@ def main():
                                        "WRITE_SIZE passes over bench.py --traffic-probe, copy-calibrated)",
                      "mfma_busy_frac": read_mfma_busy(),
                      "mfma_busy_source": "profiles/noisy_gemm256_mining_4096_counters.txt (rocprofv3 "
-                                         "SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x 1024 SIMDs))",
+                                         "SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 XCDs x 1024 SIMDs))",
                      "kernel": "noisy_gemm256_kernel<HASH=true, DENOISE=true, OUT_I32, SPLIT=true>",
                      "avg_us": round(res["launch_ms"] * 1e3, 2), "nonces_per_launch": res["per_launch"],
                      "ops_per_launch": res["per_launch"] * (2 * m * n * k + 2 * m * n * 2 * r * res["L"])},

@@ -546,10 +546,12 @@ class MinedWeight:
         longer than the GPU work already queued), and its previous state restored.
 
         Every nonce records its winners in its own buffer: the caller's `wins` (one int32 tensor
-        of 1 + max_wins * WIN_WORDS words per item), or else rows of a sweep buffer that the
-        weight keeps, copied to pinned host memory group by group on the stream as each group's
-        GEMMs finish; sweep_winners() returns them all. winners(m) keeps reporting the last
-        item, as after forward(). dumps: optional per-item tile dumps (gemm()'s `dump` layout).
+        of 1 + max_wins * WIN_WORDS words per item), or else a row of a device buffer that the
+        weight keeps (reserve_sweep() allocates it ahead of time); sweep_winners() reads all rows
+        back with one copy once the sweep is done. (Copying each group's rows to the host while
+        the sweep runs, on a stream waiting for the group's GEMMs, stalled the host thread in the
+        copy call and with it the queueing of the next groups.) winners(m) reports the last item,
+        as after forward(). dumps: optional per-item tile dumps (gemm()'s `dump` layout).
         Returns the outputs."""
         n_items = len(As)
         if n_items == 0:
@@ -578,18 +580,19 @@ class MinedWeight:
                 gc.enable()
         return outs
 
-    def _sweep_win_rows(self, m: int, n_items: int):
-        """Device win buffers for a sweep of n_items nonces (rows of one tensor, grown on demand)
-        and the pinned host copy they are read back into. The last item's row is the weight's own
-        buffer of this m, so winners(m) reports it."""
+    def reserve_sweep(self, m: int, n_items: int) -> torch.Tensor:
+        """Allocate now the per-nonce win rows that forward_many of n_items nonces of m rows uses,
+        so that the sweep itself allocates nothing."""
         words = 1 + self.max_wins * WIN_WORDS
-        dev_rows, host_rows = self._bufs.get(("sweep_wins", m), (None, None))
-        if dev_rows is None or dev_rows.shape[0] < n_items:
-            dev_rows = torch.zeros((n_items, words), dtype=torch.int32, device=self.device)
-            host_rows = torch.zeros((n_items, words), dtype=torch.int32, pin_memory=True)
-            self._bufs[("sweep_wins", m)] = (dev_rows, host_rows)
-        rows = [dev_rows[i] for i in range(n_items - 1)] + [self._buf(m)["wins"]]
-        return rows, (host_rows, rows)
+        rows = self._bufs.get(("sweep_wins", m))
+        if rows is None or rows.shape[0] < n_items:
+            rows = self._bufs[("sweep_wins", m)] = torch.zeros((n_items, words), dtype=torch.int32, device=self.device)
+        return rows
+
+    def _sweep_win_rows(self, m: int, n_items: int):
+        """Device win buffers for a sweep of n_items nonces: consecutive rows of one tensor."""
+        rows = self.reserve_sweep(m, n_items)
+        return [rows[i] for i in range(n_items)], rows
 
     def _sweep(self, As, a_scale, outs, out_mode, hash_tiles, wins, group, gemm_group, m, k, r, c, side, host=None,
                dumps=None):
@@ -602,14 +605,12 @@ class MinedWeight:
         groups = [list(range(g0, min(g0 + group, n_items))) for g0 in range(0, n_items, group)]
         cur = torch.cuda.current_stream(self.device)
         sync = _SWEEP_SYNC.get(str(self.device))
-        if sync is None:  # default-priority side and copy streams, four reusable events per device
+        if sync is None:  # a default-priority side stream and four reusable events per device
             sync = _SWEEP_SYNC[str(self.device)] = (torch.cuda.Stream(device=self.device),
                                                     [torch.cuda.Event() for _ in range(2)],
-                                                    [torch.cuda.Event() for _ in range(2)],
-                                                    torch.cuda.Stream(device=self.device))
-        sc, committed, consumed, cs = sync
+                                                    [torch.cuda.Event() for _ in range(2)])
+        sc, committed, consumed = sync
         sc.wait_stream(cur)
-        sc.wait_stream(cs)  # the previous sweep's win copies read buffers this sweep clears
 
         def bufs_of(gi):
             out = []
@@ -657,12 +658,8 @@ class MinedWeight:
                           outs=[outs[items[j]] for j in sub] if out_mode != OUT_NONE else None, out_mode=out_mode,
                           dumps=[dumps[items[j]] for j in sub] if dumps is not None else None)
             consumed[gi % 2].record(cur)
-            if host is not None:  # this group's win records to the pinned host rows, on the copy
-                host_rows, rows = host  # stream once its GEMMs are done (compute never waits for it)
-                cs.wait_event(consumed[gi % 2])
-                with torch.cuda.stream(cs):
-                    for i in items:
-                        host_rows[i].copy_(rows[i], non_blocking=True)
+        if host is not None:  # winners(m) reports the sweep's last nonce, as after forward()
+            self._buf(m)["wins"].copy_(host[n_items - 1])
         cur.wait_stream(sc)
 
     def noise_mine(self, A: torch.Tensor, dump=None):
@@ -691,12 +688,12 @@ class MinedWeight:
 
     def sweep_winners(self) -> list[list[tuple[int, int, bytes]]]:
         """Every nonce's winners of the last forward_many without caller win buffers, in item
-        order: waits for the sweep's queued work, then parses the pinned host copies."""
+        order (one device-to-host copy of the sweep's rows; waits for the work queued so far)."""
         _check(getattr(self, "_sweep_host", None) is not None,
                "MinedWeight.sweep_winners: no forward_many without caller win buffers has run")
-        (host_rows, _), n_items = self._sweep_host
-        _SWEEP_SYNC[str(self.device)][3].synchronize()
-        return [win_records(host_rows[i], self.max_wins) for i in range(n_items)]
+        rows, n_items = self._sweep_host
+        host = rows[:n_items].cpu()
+        return [win_records(host[i], self.max_wins) for i in range(n_items)]
 
 
 def win_records(buf: torch.Tensor, max_wins: int) -> list[tuple[int, int, bytes]]:
