@@ -175,6 +175,40 @@ def mining(args, torch, np, ops):
     return res
 
 
+def noise_mining(args, torch, np, ops):
+    """Pure noise mining at the reference miner's shape (miner_loop.py:35-38): m = 8192, n = 16384,
+    k = 4096, r = 128; per attempt MinedWeight.noise_mine (commit A, noise, noised A, hashed GEMM
+    with every tile digested, no output), over resident random A rotated through 4 buffers. The
+    reference's sustained figures for this loop are 70-73 hashed TMAC/s on an RTX 3080 and 320-330
+    on an RTX 5090 (spec/step1-results.md:39-40, 141; results/matrix_q4.txt:5,10)."""
+    dev = "cuda"
+    m, n, k, r = 8192, 16384, 4096, 128
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(77)
+    Bt = torch.randint(-64, 65, (n, k), dtype=torch.int8, device=dev, generator=gen)
+    w = ops.MinedWeight(Bt=Bt, b_scale=torch.ones(n, device=dev), r=r, max_wins=64)
+    w.setup_block(bytes(range(32)), ops.bound_words(((1 << 256) - 1) * 4 // ((m // 8) * (n // 16))))
+    As = [torch.randint(-64, 65, (m, k), dtype=torch.int8, device=dev, generator=gen) for _ in range(4)]
+    for i in range(4):
+        w.noise_mine(As[i % 4])
+    torch.cuda.synchronize()
+    attempts, t0 = 0, time.perf_counter()
+    while attempts < args.mine_attempts or time.perf_counter() - t0 < 1.0:
+        for i in range(8):
+            w.noise_mine(As[(attempts + i) % 4])
+        attempts += 8
+        torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    wins = len(w.winners(m))
+    tmacs = m * n * k * attempts / dt / 1e12
+    out = dict(workload=f"noise_mine {m}x{n}x{k} r={r}: commitment + noise + noised A + hashed GEMM per attempt",
+               attempts=attempts, ms_per_attempt=round(dt * 1e3 / attempts, 4), hashed_tmacs=round(tmacs, 1),
+               int8_tops=round(2 * tmacs, 1), last_attempt_winners=wins,
+               reference_tmacs={"rtx3080": [70, 73], "rtx5090": [320, 330]})
+    log(f"noise mining: {out}")
+    return out
+
+
 def parity_and_cpu(args, res, torch, np, ops, O):
     """Re-run one group of the sweep on the GPU, through the same batched split-role GEMM launch the
     sweep and the roofline time, with a tile dump per nonce, and compare its first nonce with the
@@ -721,6 +755,8 @@ def main():
     ap.add_argument("--gemm-group", type=int, default=8, help="nonces per batched GEMM launch")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--cpu-max-nonces", type=int, default=4)
+    ap.add_argument("--mine-attempts", type=int, default=16, help="noise_mine attempts at the miner's shape")
+    ap.add_argument("--no-mine", action="store_true", help="skip the pure noise-mining leg")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-detrt", action="store_true")
     ap.add_argument("--no-e2e", action="store_true", help="skip configs[4] (the 28-layer forward)")
@@ -769,6 +805,7 @@ def main():
         return
     ceiling = mfma_ceiling(torch)
     res = mining(args, torch, np, ops)
+    mine = None if args.no_mine else noise_mining(args, torch, np, ops)
     parity, cpu = (None, None) if args.no_cpu else parity_and_cpu(args, res, torch, np, ops, O)
     det = None if args.no_detrt else detrt_layer(args, torch, np)
     skinny = None if args.no_detrt else skinny_linears(args, torch, np)
@@ -807,6 +844,7 @@ def main():
         "cpu_baseline": cpu,
         "parity": parity,
         "sweep_winners": res["sweep_winners"],
+        "noise_mining": mine,
         "detrt_layer": det,
         "detrt_skinny": skinny,
         "llama_prefill": prefill,

@@ -204,6 +204,19 @@ int uwc_side_project(const int8_t* A, int m, const int8_t* EA, const int8_t* SpA
                      int8_t* corrA, int corr_a_off, int ecopy_off, const int8_t* Bp, int n, const int8_t* StA,
                      int8_t* corrB, int corr_b_off, int k, int r, int32_t* maxabs, int lmax, hipStream_t stream);
 
+/* uwc_side_project for `count` (1..16) nonces sharing the block side (StB, Bp) in one launch:
+ * item i as uwc_side_project(A[i], m, EA[i], SpA[i], ApEA[i], StB, corrA[i], corr_a_off, ecopy_off,
+ * Bp, n, StA[i], corrB[i], corr_b_off, k, r, maxabs[i], lmax). A, EA, SpA, ApEA, corrA, StA, corrB
+ * and maxabs are HOST arrays of `count` device pointers. m % 128 == 0, n % 128 == 0,
+ * k % 128 == 0, r in {16, 32, 64}; corr offsets 0 or r (ecopy_off may be -1); A, EA, SpA, ApEA,
+ * StA, StB, Bp (and corrA for the E copy) 16-byte aligned.
+ * Batches the per-nonce operand side of MinedWeight._forward (ops.py:331-336) over a sweep's
+ * group of nonces. */
+int uwc_side_project_many(int count, const int8_t* const* A, const int8_t* const* EA, const int8_t* const* SpA,
+                          int8_t* const* ApEA, const int8_t* StB, int8_t* const* corrA, int corr_a_off, int ecopy_off,
+                          const int8_t* Bp, const int8_t* const* StA, int8_t* const* corrB, int corr_b_off, int m,
+                          int n, int k, int r, int32_t* const* maxabs, int lmax, hipStream_t stream);
+
 /* detrt quant_act per row of x (rows x k fp32): q = clamp(rint(fwht_bs(x) / s), -qmax, qmax),
  * s = max(max|y|, 1e-8) / qmax, scale = s * (1 / sqrt(bs)) if bs > 1 else s (bs a power of two
  * dividing k, or 0/1 for none; k % 512 == 0 with bs <= 512, else k <= 40960).

@@ -498,3 +498,49 @@ def test_gemm_many_equals_single_calls(dev, count, m, n, k, out_mode):
         assert winset(wins[i]) == winset(w1), i
         any_win = any_win or bool(winset(w1))
     assert any_win
+
+
+@pytest.mark.parametrize("count,m,n,k,r", [(3, 128, 256, 512, 64), (2, 256, 128, 384, 16), (5, 128, 128, 1152, 32),
+                                           (8, 512, 384, 4096, 64)])
+def test_side_project_many_matches_oracle(dev, count, m, n, k, r):
+    """The batched operand side (one launch for a group of nonces sharing B'): every item's noised
+    operand, X limbs + E copy, Y limbs and both maxima equal the oracle; maxabs is an atomic max
+    into what each buffer held."""
+    ops = _ops()
+    rng = np.random.default_rng(count * 11 + m + n + k + r)
+    Bp = rng.integers(-64, 65, size=(n, k), dtype=np.int8)
+    PB = O.perm_packed(O.SEED_LABEL_B, rng.bytes(32), k, r)
+    pack = lambda P: torch.from_numpy(P.view(np.int32).copy()).to(dev)
+    StB = ops.proj_matrix(pack(PB), k, r)
+    L = ops.limbs_for(k)
+    items = []
+    for i in range(count):
+        A = rng.integers(-64, 65, size=(m, k), dtype=np.int8)
+        E = rng.integers(-32, 32, size=(m, r), dtype=np.int8)
+        PA = O.perm_packed(O.SEED_LABEL_A, rng.bytes(32), k, r)
+        StA = ops.proj_matrix(pack(PA), k, r)
+        SpA = torch.zeros((k, 64), dtype=torch.int8, device=dev)
+        SpA[:, :r] = StA.t()
+        items.append(dict(A=A, E=E, PA=PA, Ad=torch.from_numpy(A).to(dev), Ed=torch.from_numpy(E).to(dev), StA=StA,
+                          SpA=SpA, ApEA=torch.empty((m, k), dtype=torch.int8, device=dev),
+                          corrA=torch.zeros((L, m, 2 * r), dtype=torch.int8, device=dev),
+                          corrB=torch.full((L, n, 2 * r), 7, dtype=torch.int8, device=dev),
+                          mx=torch.tensor([0, 3], dtype=torch.int32, device=dev)))
+    Bd = torch.from_numpy(Bp).to(dev)
+    ops.side_project_many([it["Ad"] for it in items], [it["Ed"] for it in items], [it["SpA"] for it in items],
+                          [it["ApEA"] for it in items], StB, [it["corrA"] for it in items], Bd,
+                          [it["StA"] for it in items], [it["corrB"] for it in items],
+                          maxabss=[it["mx"] for it in items], corr_a_off=0, ecopy_off=r, corr_b_off=r)
+    torch.cuda.synchronize()
+    for i, it in enumerate(items):
+        X, Y = O.project(it["A"], PB, r), O.project(Bp, it["PA"], r)
+        wantA = np.zeros((L, m, 2 * r), np.int8)
+        O.write_limbs(X, wantA, 0)
+        for li in range(L):
+            wantA[li, :, r:] = it["E"]
+        wantB = np.full((L, n, 2 * r), 7, np.int8)
+        O.write_limbs(Y, wantB, r)
+        assert np.array_equal(it["ApEA"].cpu().numpy(), O.noise_apply(it["A"], it["E"], it["PA"])), i
+        assert np.array_equal(it["corrA"].cpu().numpy(), wantA), i
+        assert np.array_equal(it["corrB"].cpu().numpy(), wantB), i
+        assert it["mx"].cpu().tolist() == [int(np.abs(X).max()), max(3, int(np.abs(Y).max()))], i

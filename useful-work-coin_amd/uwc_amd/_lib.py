@@ -42,6 +42,7 @@ SIGNATURES = {
     "uwc_project": [vp, i32, i32, i32, vp, vp, i32, vp, i32, vp],
     "uwc_noise_project": [vp, i32, i32, i32, vp, vp, vp, vp, vp, i32, i32, vp, i32, vp],
     "uwc_side_project": [vp, i32, vp, vp, vp, vp, vp, i32, i32, vp, i32, vp, vp, i32, i32, i32, vp, i32, vp],
+    "uwc_side_project_many": [i32, vp, vp, vp, vp, vp, vp, i32, i32, vp, vp, vp, i32, i32, i32, i32, i32, vp, i32, vp],
     "uwc_quant_act_f32": [vp, i32, i32, i32, i32, vp, vp, vp],
     "uwc_quant_rows_had": [vp, i32, i32, i32, vp, vp, vp],
     "uwc_dequant_f32": [vp, vp, vp, i32, i32, vp, vp],

@@ -266,6 +266,31 @@ def side_project(A, EA, SpA, ApEA, StB, corrA, Bp, StA, corrB, *, maxabs, corr_a
               _p(Bp), n, _p(StA), _p(corrB), corr_b_off, k, r, _p(maxabs), corrA.shape[0], _stream())
 
 
+def side_many_ok(m: int, n: int, k: int, r: int) -> bool:
+    """Shapes uwc_side_project_many takes."""
+    return m % 128 == 0 and n % 128 == 0 and k % 128 == 0 and r in (16, 32, 64)
+
+
+def side_project_many(As, EAs, SpAs, ApEAs, StB, corrAs, Bp, StAs, corrBs, *, maxabss, corr_a_off=0, ecopy_off=-1,
+                      corr_b_off=0):
+    """side_project for a group of nonces sharing the block side (StB, Bp), one launch: item i as
+    side_project(As[i], EAs[i], SpAs[i], ApEAs[i], StB, corrAs[i], Bp, StAs[i], corrBs[i],
+    maxabs=maxabss[i], ...)."""
+    count = len(As)
+    _check(1 <= count <= MAX_BATCH, f"side_project_many: {count} items, need 1..{MAX_BATCH}")
+    m, k = As[0].shape
+    n, r = Bp.shape[0], StAs[0].shape[0]
+    _check(side_many_ok(m, n, k, r), f"side_project_many: m={m} n={n} k={k} r={r} unsupported")
+    for xs in (EAs, SpAs, ApEAs, corrAs, StAs, corrBs, maxabss):
+        _check(len(xs) == count, "side_project_many: one entry per item")
+    for A, SpA in zip(As, SpAs):
+        _check(tuple(A.shape) == (m, k) and SpA.shape == (k, 64), "side_project_many: A must be m x k, SpA k x 64")
+    _check(corrAs[0].shape[0] == corrBs[0].shape[0], "side_project_many: corrA and corrB need the same limb count")
+    _lib.call("uwc_side_project_many", count, _arr(As), _arr(EAs), _arr(SpAs), _arr(ApEAs), _p(StB), _arr(corrAs),
+              corr_a_off, ecopy_off, _p(Bp), _arr(StAs), _arr(corrBs), corr_b_off, m, n, k, r, _arr(maxabss),
+              corrAs[0].shape[0], _stream())
+
+
 # ------------------------------------------------------------------ activation quantizer
 def quant_rows_had(x: torch.Tensor, bs: int, q: torch.Tensor | None = None, scale: torch.Tensor | None = None):
     """x: m x k bf16 (contiguous) -> (int8 q in [-64, 64], float32 per-row scale), block Hadamard of
@@ -603,6 +628,7 @@ class MinedWeight:
         last user of its set, is done."""
         n_items = len(As)
         groups = [list(range(g0, min(g0 + group, n_items))) for g0 in range(0, n_items, group)]
+        many = side_many_ok(m, self.n, k, r)  # one operand-side launch per GEMM batch
         cur = torch.cuda.current_stream(self.device)
         sync = _SWEEP_SYNC.get(str(self.device))
         if sync is None:  # a default-priority side stream and four reusable events per device
@@ -633,7 +659,7 @@ class MinedWeight:
                 nonce_noise_many([b["EAL"] for b in bufs], [b["PA"] for b in bufs], k, r, c["LABEL_A"],
                                  [b["a_seed"] for b in bufs], Sts=[b["SA"] for b in bufs],
                                  zero0s=[b["maxabs"] for b in bufs], zero1s=[b["wins"][:1] for b in bufs],
-                                 SpTs=[b["SpA"] for b in bufs] if side else None)
+                                 SpTs=[b["SpA"] for b in bufs] if side or many else None)
                 committed[gi % 2].record(sc)
 
         commit(0)
@@ -645,9 +671,17 @@ class MinedWeight:
             corrBs = [self._slot_corrB(1 + (gi % 2) * group + j) for j in range(len(items))]
             for s0 in range(0, len(items), gemm_group):
                 sub = range(s0, min(s0 + gemm_group, len(items)))
-                # 3.-4. the nonces' noised operands and projections (own slot and corrB copy)
-                for j in sub:
-                    self._project(As[items[j]], bufs[j], side, corrBs[j])
+                # 3.-4. the nonces' noised operands and projections (own slot and corrB copy): one
+                # launch for the sub-batch, or one per nonce for shapes the batched form does not take
+                if many:
+                    side_project_many([As[items[j]] for j in sub], [bufs[j]["EAL"] for j in sub],
+                                      [bufs[j]["SpA"] for j in sub], [bufs[j]["ApEA"] for j in sub], self.SBt,
+                                      [bufs[j]["corrA"] for j in sub], self.BpEBt, [bufs[j]["SA"] for j in sub],
+                                      [corrBs[j] for j in sub], maxabss=[bufs[j]["maxabs"] for j in sub],
+                                      corr_a_off=0, ecopy_off=r, corr_b_off=r)
+                else:
+                    for j in sub:
+                        self._project(As[items[j]], bufs[j], side, corrBs[j])
                 # 5. their hashed GEMMs with exact denoise: one batched call
                 gemm_many([bufs[j]["ApEA"] for j in sub], self.BpEBt, r=r,
                           flags=(FLAG_HASH if hash_tiles else 0) | FLAG_DENOISE,
