@@ -686,7 +686,8 @@ def summarize_trace(trace_csv, out_path, cmd, steps, warmup, group):
                 f"{sum(b2b) / len(b2b) / group:.2f} us per nonce, min {min(b2b):.2f}, max {max(b2b):.2f}\n")
         f.write(f"\nPer group of {group} nonces: b3_chunks + b3_reduce (one batched commitment of the group's A) and\n"
                 "one nonce_noise (E_A, P_A, selection matrices of the group), on a side stream one group ahead, beside\n"
-                "the previous group's side kernels; one side_kernel per nonce (noised A, both projections in limbs);\n"
+                "the previous group's side work; one side_many_kernel launch (noised A and both projections in limbs\n"
+                "for every nonce of the group);\n"
                 "one noisy_gemm256_kernel<true, true, 1, true> launch (the group's hashed GEMMs with exact denoise,\n"
                 "int32 out; split roles, stores overlapping the next nonce). Kernel times overlap: per-nonce sums\n"
                 "exceed the sweep's wall time per nonce.\n")

@@ -24,8 +24,9 @@ def test_blake3_published_digests():
 def test_blake3_official_test_vectors():
     """The BLAKE3 team's published vectors (tests/golden/blake3_official_vectors.json): one block
     (len 0, 1), a full 16-block chunk (1024: chunk chaining, CHUNK_START/END), two chunks under a
-    parent node (1025: chunk counter, PARENT, ROOT placement), and keyed mode (KEYED_HASH flag and
-    the key in place of the IV), for both restatements."""
+    parent node (1025, 2048: chunk counter, PARENT, ROOT placement), ragged and deep trees (31744 =
+    31 chunks, 102400 = 100 chunks), and keyed mode (KEYED_HASH flag and the key in place of the IV)
+    on one block, one chunk and a parent node (2048), for both restatements."""
     v = json.load(open(os.path.join(GOLDEN, "blake3_official_vectors.json")))
     key = v["key"].encode()
     for case in v["cases"]:
