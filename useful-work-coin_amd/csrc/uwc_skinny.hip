@@ -17,6 +17,8 @@
 //
 // Replaces, for m <= 64, the exact GEMM of DetLinear.int_gemm / __call__
 // (runtime/detrt/qwen3.py:106-126; the reference pads m to 32 and calls torch._int_mm).
+#include <algorithm>
+
 #include "uwc_common.h"
 
 #ifndef SK_U
@@ -364,6 +366,261 @@ static void sk_mt(int mt, int out_mode, dim3 grid, dim3 block, size_t lds, hipSt
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// The DMA-streamed form (k % 1024 == 0): the fastest form wherever the X of a token group fits in
+// LDS next to a weight ring of >= 4 entries. Measured on this part, three facts shape it:
+//   * W must move as whole 128-byte lines: a wave load of 16 rows x 64 bytes (the MFMA operand
+//     layout) streams 25-50% slower than 1 KB contiguous per instruction, while global_load_lds
+//     of 1 KB row pieces runs at the contiguous rate. So W goes to LDS by DMA, one 1 KB piece of
+//     one row per wave instruction, and is read back in the operand layout (rows padded to 1040
+//     bytes: the 16 rows of a fragment read fall in distinct banks);
+//   * requests of a CU return in issue order: an L2 hit issued after HBM misses waits for them.
+//     X (a few KB to 64 KB, L2-resident) is therefore requested before any W;
+//   * X replicated into every CU costs more than streaming W when m k is large (64 x 2048 bytes
+//     per workgroup against 48 KB of W each at configs[0]). Above one group's LDS budget the
+//     tokens are split into ts = 2 groups: each workgroup holds half of X and reads its W rows,
+//     and the two workgroups of a row block run in the same round on one XCD (round-robin
+//     dispatch puts workgroup b on XCD b % 8) so the second read of W is served by that XCD's
+//     L2. The mapping is only a locality hint: any placement gives the same result.
+// Roles: 8 compute waves and 2 helper waves. Compute wave w DMAs rows w and w + 8 of each ring
+// entry (16 rows x 1 KB of one k chunk) and runs the MFMAs of the 128-byte piece w of every
+// chunk: v_mfma_i32_16x16x64_i8 with A = 16 W rows from the ring, B = 16 tokens from the X copy.
+// At a block's end the 8 partial sums go to LDS; helper (block % 2) adds them, applies the
+// epilogue and stores. Only DMAs ever touch the compute waves' vmcnt, so every wait count is
+// static. Stores live in the helpers; the weight scales of the workgroup's blocks are DMA'd to
+// LDS at the start (lane l of a DMA gathers 16 bytes of block l / 4), so a helper's block loop
+// has no global loads, and with blocks alternating between two helpers the register reuse that
+// makes a helper wait for its stores finds them two blocks old.
+#define SD_PITCH 1040  // LDS bytes per W row of a ring entry (1 KB + 16)
+#define SD_ENTRY (16 * SD_PITCH)
+#define SD_MAX_NE 6
+
+typedef void __attribute__((address_space(3)))* sd_lptr;
+
+// wait until at most `younger` ring entries (2 DMAs each) issued after the awaited one are pending
+template <int NE>
+__device__ __forceinline__ void sd_wait_entries(int younger) {
+  switch (younger) {
+    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    case 1: if constexpr (NE >= 3) asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
+    case 2: if constexpr (NE >= 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
+    case 3: if constexpr (NE >= 5) asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
+    default: if constexpr (NE >= 6) asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+  }
+}
+
+template <int MT, int NE, int NPB, int OUT>
+__global__ void __launch_bounds__(640) skinny_dma_kernel(const i8* __restrict__ X, const i8* __restrict__ W, int m, int n,
+                                                         int k, int ts, const float* __restrict__ sx,
+                                                         const float* __restrict__ sw, void* __restrict__ out) {
+  static_assert(NE >= 2 && NE <= SD_MAX_NE, "ring depth");
+  constexpr int PART = 8 * MT * 1024;  // bytes of one partials buffer: [8 waves][MT][64 lanes] v4i
+  extern __shared__ __attribute__((aligned(16))) u8 sd_lds[];
+  const u32 lbase = (u32)(uintptr_t)(sd_lptr)sd_lds;
+  const int cpb = k >> 10;       // 1 KB chunks per row
+  const int mg = m / ts;         // tokens of a group
+  const int xpitch = k + 16;
+  u8* xl = sd_lds + NE * SD_ENTRY;
+  v4i* part = reinterpret_cast<v4i*>(xl + (((long)mg * xpitch + 15) & ~15L));
+  const float* swl = reinterpret_cast<const float*>(part + NPB * (PART / 16));  // [block][16] weight scales
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nblk = (n + 15) >> 4;
+  // tasks (16-row block, token group): workgroup b = 8 l + x takes group h = l % ts and, in round
+  // r, block x + 8 ((r G / 8 + l) / ts)
+  const int x8 = blockIdx.x & 7, l = blockIdx.x >> 3, G8 = gridDim.x >> 3;
+  const int h = l % ts;
+  const int tasks = (x8 < nblk ? (nblk - 1 - x8) / 8 + 1 : 0) * ts;
+  const int nmine = l < tasks ? (tasks - 1 - l) / G8 + 1 : 0;
+  const int E = nmine * cpb;  // ring entries of this workgroup
+  if (E == 0) return;
+  auto block_of = [&](int r) { return x8 + 8 * ((r * G8 + l) / ts); };
+  const i8* Xg = X + (long)h * mg * k;
+
+  if (wave < 8) {
+    // X of the group first (row r by wave r % 8), then the first NE - 1 ring entries
+    for (int r = wave; r < mg; r += 8)
+      for (int c = 0; c < cpb; c++)
+        s2_dma16(Xg + (long)r * k + c * 1024 + lane * 16,
+                 __builtin_amdgcn_readfirstlane(lbase + (u32)(NE * SD_ENTRY + r * xpitch + c * 1024)));
+    auto dma_entry = [&](int e) {
+      const int i = e / cpb, c = e - i * cpb;
+      const int row0 = block_of(i) * 16;
+      const u32 slot = lbase + (u32)((e % NE) * SD_ENTRY);
+#pragma unroll
+      for (int t = 0; t < 2; t++) {
+        const int r = wave + 8 * t;
+        s2_dma16(W + (long)min(row0 + r, n - 1) * k + c * 1024 + lane * 16,
+                 __builtin_amdgcn_readfirstlane(slot + r * SD_PITCH));
+      }
+    };
+    const int pro = min(NE - 1, E);
+    for (int e = 0; e < pro; e++) dma_entry(e);
+    int xo[MT];
+#pragma unroll
+    for (int tg = 0; tg < MT; tg++) xo[tg] = min(16 * tg + (lane & 15), mg - 1) * xpitch + 128 * wave + 16 * (lane >> 4);
+    const int wo = (lane & 15) * SD_PITCH + 128 * wave + 16 * (lane >> 4);
+    v4i acc[MT];
+#pragma unroll
+    for (int tg = 0; tg < MT; tg++) acc[tg] = v4i{0, 0, 0, 0};
+    int i = 0, c = 0;
+    for (int e = 0; e < E; e++) {
+      // entry e landed (the X copy too, being older), in every wave's share
+      sd_wait_entries<NE>(min(NE - 2, E - 1 - e));
+      s2_lds_barrier();
+      if (e + NE - 1 < E) dma_entry(e + NE - 1);
+      const u8* we = sd_lds + (e % NE) * SD_ENTRY + wo;
+#pragma unroll
+      for (int u = 0; u < 2; u++) {
+        const v4i a = *reinterpret_cast<const v4i*>(we + 64 * u);
+        v4i b[MT];
+#pragma unroll
+        for (int tg = 0; tg < MT; tg++) b[tg] = *reinterpret_cast<const v4i*>(xl + xo[tg] + c * 1024 + 64 * u);
+#pragma unroll
+        for (int tg = 0; tg < MT; tg++) acc[tg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[tg], acc[tg], 0, 0, 0);
+      }
+      if (++c == cpb) {
+        v4i* pb = part + (NPB == 2 ? (i & 1) * (PART / 16) : 0);
+#pragma unroll
+        for (int tg = 0; tg < MT; tg++) {
+          pb[(wave * MT + tg) * 64 + lane] = acc[tg];
+          acc[tg] = v4i{0, 0, 0, 0};
+        }
+        s2_lds_barrier();
+        c = 0;
+        i++;
+      }
+    }
+  } else {
+    // helpers: per block, the sum of the 8 partials and the epilogue. Lane l holds outputs
+    // (token 16 tg + (l & 15) of the group, columns 4 (l >> 4) .. + 3 of the block). Every
+    // barrier of a helper waits for its LDS reads first: the partials buffer a helper reads is
+    // written again only after a later barrier.
+    constexpr bool SCALED = OUT != UWC_OUT_I32;
+    const int hw = wave - 8;
+    float sxv[MT];
+#pragma unroll
+    for (int tg = 0; tg < MT; tg++) sxv[tg] = SCALED ? sx[h * mg + min(16 * tg + (lane & 15), mg - 1)] : 0.f;
+    if constexpr (SCALED) {
+      // the blocks' weight scales to LDS: DMA q, lane l -> block 16 q + l / 4, floats 4 (l % 4) ..
+      const u32 swb = lbase + (u32)((const u8*)swl - sd_lds);
+      for (int q = 0; q < (nmine + 15) / 16; q++) {
+        const int bi = min(16 * q + (lane >> 2), nmine - 1);
+        s2_dma16(sw + min(block_of(bi) * 16 + 4 * (lane & 3), n - 4), __builtin_amdgcn_readfirstlane(swb + q * 1024));
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    for (int i = 0; i < nmine; i++) {
+      for (int c = 0; c < cpb; c++) s2_lds_barrier();  // the block's ring entries
+      s2_lds_barrier();                                 // its partials written
+      if ((i & 1) != hw) continue;
+      const int col = block_of(i) * 16 + 4 * (lane >> 4);
+      const v4i* pb = part + (NPB == 2 ? (i & 1) * (PART / 16) : 0);
+      v4i s[MT];
+#pragma unroll
+      for (int tg = 0; tg < MT; tg++) {
+        s[tg] = pb[tg * 64 + lane];
+#pragma unroll
+        for (int w = 1; w < 8; w++) s[tg] += pb[(w * MT + tg) * 64 + lane];
+      }
+      float4 y[MT];
+      if constexpr (SCALED) {
+        const float4 swv = *reinterpret_cast<const float4*>(swl + i * 16 + 4 * (lane >> 4));
+#pragma unroll
+        for (int tg = 0; tg < MT; tg++) {
+          y[tg].x = __fmul_rn(__fmul_rn((float)s[tg][0], sxv[tg]), swv.x);
+          y[tg].y = __fmul_rn(__fmul_rn((float)s[tg][1], sxv[tg]), swv.y);
+          y[tg].z = __fmul_rn(__fmul_rn((float)s[tg][2], sxv[tg]), swv.z);
+          y[tg].w = __fmul_rn(__fmul_rn((float)s[tg][3], sxv[tg]), swv.w);
+        }
+      }
+#pragma unroll
+      for (int tg = 0; tg < MT; tg++) {
+        const int tl = 16 * tg + (lane & 15);
+        if (tl < mg && col < n) {
+          const long o = (long)(h * mg + tl) * n + col;
+          if constexpr (OUT == UWC_OUT_I32) {
+            *reinterpret_cast<v4i*>(reinterpret_cast<i32*>(out) + o) = s[tg];
+          } else if constexpr (OUT == UWC_OUT_F32) {
+            *reinterpret_cast<float4*>(reinterpret_cast<float*>(out) + o) = y[tg];
+          } else {
+            const uint2 b = {sk_bf16_rne(y[tg].x) | (sk_bf16_rne(y[tg].y) << 16),
+                             sk_bf16_rne(y[tg].z) | (sk_bf16_rne(y[tg].w) << 16)};
+            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(out) + o) = b;
+          }
+        }
+      }
+    }
+  }
+}
+
+// LDS bytes of the DMA-streamed form: ring, one group's X (rows of k + 16), partials
+static size_t sd_lds_bytes(int ne, int npb, int mg, int k, int mt, int nmine_max) {
+  return (size_t)ne * SD_ENTRY + ((((size_t)mg * (k + 16)) + 15) & ~(size_t)15) + (size_t)npb * 8 * mt * 1024 +
+         (size_t)((nmine_max + 15) / 16) * 1024;
+}
+
+template <int MT, int NE, int NPB>
+static void sd_launch(int out_mode, int G, size_t lds, hipStream_t s, const i8* X, const i8* W, int m, int n, int k,
+                      int ts, const float* sx, const float* sw, void* out) {
+  auto kern = skinny_dma_kernel<MT, NE, NPB, UWC_OUT_F32>;
+  if (out_mode == UWC_OUT_I32) kern = skinny_dma_kernel<MT, NE, NPB, UWC_OUT_I32>;
+  else if (out_mode == UWC_OUT_BF16) kern = skinny_dma_kernel<MT, NE, NPB, UWC_OUT_BF16>;
+  static bool attr[3] = {false, false, false};
+  const int oi = out_mode == UWC_OUT_I32 ? 0 : out_mode == UWC_OUT_BF16 ? 1 : 2;
+  if (!attr[oi]) {
+    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    attr[oi] = true;
+  }
+  hipLaunchKernelGGL(kern, dim3(G), dim3(640), lds, s, X, W, m, n, k, ts, sx, sw, out);
+}
+
+template <int MT>
+static void sd_ne(int ne, int npb, int out_mode, int G, size_t lds, hipStream_t s, const i8* X, const i8* W, int m,
+                  int n, int k, int ts, const float* sx, const float* sw, void* out) {
+  if (npb == 2) {
+    switch (ne) {
+      case 4: sd_launch<MT, 4, 2>(out_mode, G, lds, s, X, W, m, n, k, ts, sx, sw, out); break;
+      case 5: sd_launch<MT, 5, 2>(out_mode, G, lds, s, X, W, m, n, k, ts, sx, sw, out); break;
+      default: sd_launch<MT, 6, 2>(out_mode, G, lds, s, X, W, m, n, k, ts, sx, sw, out); break;
+    }
+  } else {
+    switch (ne) {
+      case 4: sd_launch<MT, 4, 1>(out_mode, G, lds, s, X, W, m, n, k, ts, sx, sw, out); break;
+      case 5: sd_launch<MT, 5, 1>(out_mode, G, lds, s, X, W, m, n, k, ts, sx, sw, out); break;
+      default: sd_launch<MT, 6, 1>(out_mode, G, lds, s, X, W, m, n, k, ts, sx, sw, out); break;
+    }
+  }
+}
+
+// The DMA-streamed form's plan for (m, n, k), or false when it does not apply: token groups ts
+// (1, else 2), ring depth ne (4..6), partials buffers npb (2, else 1), grid, LDS bytes.
+struct SdPlan {
+  int ts, ne, npb, mt, grid;
+  size_t lds;
+};
+static bool sd_plan(int m, int n, int k, SdPlan* p) {
+  if (k % 1024 != 0 || n % 4 != 0 || m < 1 || m > 64) return false;
+  const int grid = uwc_cu_count() & ~15;  // a multiple of 16: G / 8 is a multiple of ts
+  if (grid < 16) return false;
+  const int nblk = (n + 15) / 16;
+  for (int ts = 1; ts <= 2; ts++) {
+    if (m % ts) continue;
+    const int mg = m / ts, mt = (mg + 15) / 16;
+    // most tasks of a workgroup: tasks of the busiest XCD over its G / 8 workgroups
+    const int nmine_max = ((nblk + 7) / 8 * ts + grid / 8 - 1) / (grid / 8);
+    for (int npb = 2; npb >= 1; npb--)
+      for (int ne = SD_MAX_NE; ne >= 4; ne--) {
+        const size_t lds = sd_lds_bytes(ne, npb, mg, k, mt, nmine_max);
+        if (lds <= 160 * 1024) {
+          // at least 81 KB: one workgroup per CU, so the dispatcher spreads them over every CU
+          *p = SdPlan{ts, ne, npb, mt, grid, std::max(lds, (size_t)81 * 1024)};
+          return true;
+        }
+      }
+  }
+  return false;
+}
+
 #ifndef S2_KS_LOG
 #define S2_KS_LOG -1  // k splits per workgroup (log2); -1 = chosen per shape
 #endif
@@ -378,6 +635,17 @@ static void sk_mt(int mt, int out_mode, dim3 grid, dim3 block, size_t lds, hipSt
 // out_mode I32 / BF16 / F32, operands already checked (16-byte aligned).
 int uwc_skinny_gemm(const int8_t* X, const int8_t* W, int m, int n, int k, const float* sx, const float* sw,
                     void* out, int out_mode, hipStream_t stream) {
+  SdPlan sp;
+  const bool vec_ok = ((uintptr_t)out & 15) == 0 && (out_mode == UWC_OUT_I32 || ((uintptr_t)sw & 15) == 0);
+  if (vec_ok && sd_plan(m, n, k, &sp)) {
+    switch (sp.mt) {
+      case 1: sd_ne<1>(sp.ne, sp.npb, out_mode, sp.grid, sp.lds, stream, X, W, m, n, k, sp.ts, sx, sw, out); break;
+      case 2: sd_ne<2>(sp.ne, sp.npb, out_mode, sp.grid, sp.lds, stream, X, W, m, n, k, sp.ts, sx, sw, out); break;
+      case 3: sd_ne<3>(sp.ne, sp.npb, out_mode, sp.grid, sp.lds, stream, X, W, m, n, k, sp.ts, sx, sw, out); break;
+      default: sd_ne<4>(sp.ne, sp.npb, out_mode, sp.grid, sp.lds, stream, X, W, m, n, k, sp.ts, sx, sw, out); break;
+    }
+    return uwc_launch_status("skinny_dma_gemm");
+  }
   const int mt = (m + 15) / 16;
   // X-stationary form when X (padded rows) and the reduction buffer fit in LDS
   const int xpitch = k + 16;
