@@ -1,9 +1,10 @@
 """GPU parity of the DMA-streamed skinny GEMM form (m <= 64, k % 1024 == 0: W through an LDS
-ring by DMA, X of a token group resident in LDS) through the C-ABI. Shapes are picked to reach
-every branch of its plan: one and two token groups, one and two partials buffers, ring depths
-4..6, ragged n (a partial last 16-row block), n as small as one block, many blocks per workgroup
-(a weight-scale table of several DMAs), 1, 2, 3, 4 and 14 chunks of 1 KB per row, and the odd m
-that must fall back to the other forms. Each result is compared with the 128 x 128 tiled kernel
+ring by DMA, X of a token group resident in LDS or streamed with W) through the C-ABI. Shapes are
+picked to reach every branch of its plan: one and two token groups, X resident or streamed (8 or
+16 X rows per entry), one and two partials buffers, ring depths 4..6, ragged n (a partial last
+16-row block), n as small as one block, many blocks per workgroup (a weight-scale table of several
+DMAs), 1, 2, 3, 4, 14 and 30 chunks of 1 KB per row, and the odd m that must fall back to the
+other forms. Each result is compared with the 128 x 128 tiled kernel
 (UWC_FLAG_TILE128) and, where it is cheap, with the CPU oracle; the fp32 / bf16 epilogues bit for
 bit with the oracle's dequant (runtime/detrt/qwen3.py:106-126)."""
 import numpy as np
@@ -43,6 +44,11 @@ SHAPES = [
     (64, 6144, 2048),
     (32, 6144, 4096),    # Llama-3.1-8B qkv at M = 32
     (33, 300, 4096),     # odd m whose X does not fit one group: the other forms
+    # X streamed through the ring with W (too large to stay resident)
+    (32, 4096, 14336),   # Llama-3.1-8B down at M = 32: two groups of 16, 16 X rows per entry
+    (9, 1000, 14336),    # odd m, one group of 9 (rows 9..15 of the entry repeat row 8)
+    (24, 2000, 14336),   # two groups of 12
+    (6, 256, 30720),     # 8 X rows per entry, 30 chunks per row
 ]
 
 
@@ -77,7 +83,7 @@ def test_skinny_dma_many_blocks_per_workgroup(dev):
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 6144, 2048), (19, 1000, 1024), (64, 6144, 2048), (34, 300, 4096),
-                                   (8, 4096, 14336)])
+                                   (8, 4096, 14336), (32, 4096, 14336), (9, 1000, 14336)])
 def test_skinny_dma_dequant_epilogues(dev, m, n, k):
     """OUT_F32 = fmul(fmul(f32(acc), sx), sw) and OUT_BF16 = its RNE bf16, bit-exact vs the oracle."""
     from uwc_amd import ops

@@ -382,6 +382,10 @@ static void sk_mt(int mt, int out_mode, dim3 grid, dim3 block, size_t lds, hipSt
 //     and the two workgroups of a row block run in the same round on one XCD (round-robin
 //     dispatch puts workgroup b on XCD b % 8) so the second read of W is served by that XCD's
 //     L2. The mapping is only a locality hint: any placement gives the same result.
+// When X is too large to stay resident (e.g. 32 x 14336), it is streamed instead (XS): every ring
+// entry carries, ahead of its W rows, the same 1 KB chunk of the group's X rows (8 XD of them),
+// and each entry is read once. X then crosses each CU once per block instead of once per
+// workgroup, which is the same when a workgroup has one block (n <= 16 x CUs).
 // Roles: 8 compute waves and 2 helper waves. Compute wave w DMAs rows w and w + 8 of each ring
 // entry (16 rows x 1 KB of one k chunk) and runs the MFMAs of the 128-byte piece w of every
 // chunk: v_mfma_i32_16x16x64_i8 with A = 16 W rows from the ring, B = 16 tokens from the X copy.
@@ -397,31 +401,37 @@ static void sk_mt(int mt, int out_mode, dim3 grid, dim3 block, size_t lds, hipSt
 
 typedef void __attribute__((address_space(3)))* sd_lptr;
 
-// wait until at most `younger` ring entries (2 DMAs each) issued after the awaited one are pending
-template <int NE>
+// wait until at most `younger` ring entries (ND DMAs each) issued after the awaited one are pending
+template <int N>
+__device__ __forceinline__ void sd_waitv() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+template <int NE, int ND>
 __device__ __forceinline__ void sd_wait_entries(int younger) {
   switch (younger) {
-    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
-    case 1: if constexpr (NE >= 3) asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
-    case 2: if constexpr (NE >= 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
-    case 3: if constexpr (NE >= 5) asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
-    default: if constexpr (NE >= 6) asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+    case 0: sd_waitv<0>(); break;
+    case 1: if constexpr (NE >= 3) sd_waitv<ND>(); break;
+    case 2: if constexpr (NE >= 4) sd_waitv<2 * ND>(); break;
+    case 3: if constexpr (NE >= 5) sd_waitv<3 * ND>(); break;
+    default: if constexpr (NE >= 6) sd_waitv<4 * ND>(); break;
   }
 }
 
-template <int MT, int NE, int NPB, int OUT>
+// XD: 0 = X resident; > 0 = X streamed, 8 XD X rows per entry (XD DMAs per compute wave)
+template <int MT, int NE, int NPB, int XD, int OUT>
 __global__ void __launch_bounds__(640) skinny_dma_kernel(const i8* __restrict__ X, const i8* __restrict__ W, int m, int n,
                                                          int k, int ts, const float* __restrict__ sx,
                                                          const float* __restrict__ sw, void* __restrict__ out) {
   static_assert(NE >= 2 && NE <= SD_MAX_NE, "ring depth");
-  constexpr int PART = 8 * MT * 1024;  // bytes of one partials buffer: [8 waves][MT][64 lanes] v4i
+  constexpr int PART = 8 * MT * 1024;        // bytes of one partials buffer: [8 waves][MT][64 lanes] v4i
+  constexpr int XR = 8 * XD;                 // X rows of a streamed entry (before its 16 W rows)
+  constexpr int ENTRY = (XR + 16) * SD_PITCH;
+  constexpr int ND = 2 + XD;                 // DMAs per compute wave per entry
   extern __shared__ __attribute__((aligned(16))) u8 sd_lds[];
   const u32 lbase = (u32)(uintptr_t)(sd_lptr)sd_lds;
   const int cpb = k >> 10;       // 1 KB chunks per row
   const int mg = m / ts;         // tokens of a group
-  const int xpitch = k + 16;
-  u8* xl = sd_lds + NE * SD_ENTRY;
-  v4i* part = reinterpret_cast<v4i*>(xl + (((long)mg * xpitch + 15) & ~15L));
+  const int xpitch = XD ? SD_PITCH : k + 16;
+  u8* xl = sd_lds + NE * ENTRY;  // resident X (XD == 0)
+  v4i* part = reinterpret_cast<v4i*>(xl + (XD ? 0 : (((long)mg * xpitch + 15) & ~15L)));
   const float* swl = reinterpret_cast<const float*>(part + NPB * (PART / 16));  // [block][16] weight scales
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nblk = (n + 15) >> 4;
@@ -437,20 +447,28 @@ __global__ void __launch_bounds__(640) skinny_dma_kernel(const i8* __restrict__ 
   const i8* Xg = X + (long)h * mg * k;
 
   if (wave < 8) {
-    // X of the group first (row r by wave r % 8), then the first NE - 1 ring entries
-    for (int r = wave; r < mg; r += 8)
-      for (int c = 0; c < cpb; c++)
-        s2_dma16(Xg + (long)r * k + c * 1024 + lane * 16,
-                 __builtin_amdgcn_readfirstlane(lbase + (u32)(NE * SD_ENTRY + r * xpitch + c * 1024)));
+    // resident X of the group first (row r by wave r % 8), then the first NE - 1 ring entries
+    if constexpr (XD == 0) {
+      for (int r = wave; r < mg; r += 8)
+        for (int c = 0; c < cpb; c++)
+          s2_dma16(Xg + (long)r * k + c * 1024 + lane * 16,
+                   __builtin_amdgcn_readfirstlane(lbase + (u32)(NE * ENTRY + r * xpitch + c * 1024)));
+    }
     auto dma_entry = [&](int e) {
       const int i = e / cpb, c = e - i * cpb;
       const int row0 = block_of(i) * 16;
-      const u32 slot = lbase + (u32)((e % NE) * SD_ENTRY);
+      const u32 slot = lbase + (u32)((e % NE) * ENTRY);
+#pragma unroll
+      for (int t = 0; t < XD; t++) {  // streamed X rows (rows past the group repeat its last one)
+        const int r = wave + 8 * t;
+        s2_dma16(Xg + (long)min(r, mg - 1) * k + c * 1024 + lane * 16,
+                 __builtin_amdgcn_readfirstlane(slot + r * SD_PITCH));
+      }
 #pragma unroll
       for (int t = 0; t < 2; t++) {
         const int r = wave + 8 * t;
         s2_dma16(W + (long)min(row0 + r, n - 1) * k + c * 1024 + lane * 16,
-                 __builtin_amdgcn_readfirstlane(slot + r * SD_PITCH));
+                 __builtin_amdgcn_readfirstlane(slot + (XR + r) * SD_PITCH));
       }
     };
     const int pro = min(NE - 1, E);
@@ -458,23 +476,24 @@ __global__ void __launch_bounds__(640) skinny_dma_kernel(const i8* __restrict__ 
     int xo[MT];
 #pragma unroll
     for (int tg = 0; tg < MT; tg++) xo[tg] = min(16 * tg + (lane & 15), mg - 1) * xpitch + 128 * wave + 16 * (lane >> 4);
-    const int wo = (lane & 15) * SD_PITCH + 128 * wave + 16 * (lane >> 4);
+    const int wo = (XR + (lane & 15)) * SD_PITCH + 128 * wave + 16 * (lane >> 4);
     v4i acc[MT];
 #pragma unroll
     for (int tg = 0; tg < MT; tg++) acc[tg] = v4i{0, 0, 0, 0};
     int i = 0, c = 0;
     for (int e = 0; e < E; e++) {
       // entry e landed (the X copy too, being older), in every wave's share
-      sd_wait_entries<NE>(min(NE - 2, E - 1 - e));
+      sd_wait_entries<NE, ND>(min(NE - 2, E - 1 - e));
       s2_lds_barrier();
       if (e + NE - 1 < E) dma_entry(e + NE - 1);
-      const u8* we = sd_lds + (e % NE) * SD_ENTRY + wo;
+      const u8* slot = sd_lds + (e % NE) * ENTRY;
+      const u8* xc = XD ? slot : xl + c * 1024;  // this chunk's X rows
 #pragma unroll
       for (int u = 0; u < 2; u++) {
-        const v4i a = *reinterpret_cast<const v4i*>(we + 64 * u);
+        const v4i a = *reinterpret_cast<const v4i*>(slot + wo + 64 * u);
         v4i b[MT];
 #pragma unroll
-        for (int tg = 0; tg < MT; tg++) b[tg] = *reinterpret_cast<const v4i*>(xl + xo[tg] + c * 1024 + 64 * u);
+        for (int tg = 0; tg < MT; tg++) b[tg] = *reinterpret_cast<const v4i*>(xc + xo[tg] + 64 * u);
 #pragma unroll
         for (int tg = 0; tg < MT; tg++) acc[tg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[tg], acc[tg], 0, 0, 0);
       }
@@ -554,17 +573,18 @@ __global__ void __launch_bounds__(640) skinny_dma_kernel(const i8* __restrict__ 
 }
 
 // LDS bytes of the DMA-streamed form: ring, one group's X (rows of k + 16), partials
-static size_t sd_lds_bytes(int ne, int npb, int mg, int k, int mt, int nmine_max) {
-  return (size_t)ne * SD_ENTRY + ((((size_t)mg * (k + 16)) + 15) & ~(size_t)15) + (size_t)npb * 8 * mt * 1024 +
+static size_t sd_lds_bytes(int ne, int npb, int xd, int mg, int k, int mt, int nmine_max) {
+  const size_t xres = xd ? 0 : (((size_t)mg * (k + 16)) + 15) & ~(size_t)15;
+  return (size_t)ne * (8 * xd + 16) * SD_PITCH + xres + (size_t)npb * 8 * mt * 1024 +
          (size_t)((nmine_max + 15) / 16) * 1024;
 }
 
-template <int MT, int NE, int NPB>
+template <int MT, int NE, int NPB, int XD>
 static void sd_launch(int out_mode, int G, size_t lds, hipStream_t s, const i8* X, const i8* W, int m, int n, int k,
                       int ts, const float* sx, const float* sw, void* out) {
-  auto kern = skinny_dma_kernel<MT, NE, NPB, UWC_OUT_F32>;
-  if (out_mode == UWC_OUT_I32) kern = skinny_dma_kernel<MT, NE, NPB, UWC_OUT_I32>;
-  else if (out_mode == UWC_OUT_BF16) kern = skinny_dma_kernel<MT, NE, NPB, UWC_OUT_BF16>;
+  auto kern = skinny_dma_kernel<MT, NE, NPB, XD, UWC_OUT_F32>;
+  if (out_mode == UWC_OUT_I32) kern = skinny_dma_kernel<MT, NE, NPB, XD, UWC_OUT_I32>;
+  else if (out_mode == UWC_OUT_BF16) kern = skinny_dma_kernel<MT, NE, NPB, XD, UWC_OUT_BF16>;
   static bool attr[3] = {false, false, false};
   const int oi = out_mode == UWC_OUT_I32 ? 0 : out_mode == UWC_OUT_BF16 ? 1 : 2;
   if (!attr[oi]) {
@@ -574,28 +594,30 @@ static void sd_launch(int out_mode, int G, size_t lds, hipStream_t s, const i8* 
   hipLaunchKernelGGL(kern, dim3(G), dim3(640), lds, s, X, W, m, n, k, ts, sx, sw, out);
 }
 
-template <int MT>
+template <int MT, int XD>
 static void sd_ne(int ne, int npb, int out_mode, int G, size_t lds, hipStream_t s, const i8* X, const i8* W, int m,
                   int n, int k, int ts, const float* sx, const float* sw, void* out) {
   if (npb == 2) {
     switch (ne) {
-      case 4: sd_launch<MT, 4, 2>(out_mode, G, lds, s, X, W, m, n, k, ts, sx, sw, out); break;
-      case 5: sd_launch<MT, 5, 2>(out_mode, G, lds, s, X, W, m, n, k, ts, sx, sw, out); break;
-      default: sd_launch<MT, 6, 2>(out_mode, G, lds, s, X, W, m, n, k, ts, sx, sw, out); break;
+      case 4: sd_launch<MT, 4, 2, XD>(out_mode, G, lds, s, X, W, m, n, k, ts, sx, sw, out); break;
+      case 5: sd_launch<MT, 5, 2, XD>(out_mode, G, lds, s, X, W, m, n, k, ts, sx, sw, out); break;
+      default: sd_launch<MT, 6, 2, XD>(out_mode, G, lds, s, X, W, m, n, k, ts, sx, sw, out); break;
     }
   } else {
     switch (ne) {
-      case 4: sd_launch<MT, 4, 1>(out_mode, G, lds, s, X, W, m, n, k, ts, sx, sw, out); break;
-      case 5: sd_launch<MT, 5, 1>(out_mode, G, lds, s, X, W, m, n, k, ts, sx, sw, out); break;
-      default: sd_launch<MT, 6, 1>(out_mode, G, lds, s, X, W, m, n, k, ts, sx, sw, out); break;
+      case 4: sd_launch<MT, 4, 1, XD>(out_mode, G, lds, s, X, W, m, n, k, ts, sx, sw, out); break;
+      case 5: sd_launch<MT, 5, 1, XD>(out_mode, G, lds, s, X, W, m, n, k, ts, sx, sw, out); break;
+      default: sd_launch<MT, 6, 1, XD>(out_mode, G, lds, s, X, W, m, n, k, ts, sx, sw, out); break;
     }
   }
 }
 
 // The DMA-streamed form's plan for (m, n, k), or false when it does not apply: token groups ts
-// (1, else 2), ring depth ne (4..6), partials buffers npb (2, else 1), grid, LDS bytes.
+// (1, else 2), X resident (xd = 0) or streamed (xd = 1, 2, 4: rows of 8 per entry), ring depth ne
+// (4..6), partials buffers npb (2, else 1), grid, LDS bytes. Resident X is preferred; streaming
+// takes the shapes whose group X does not fit beside a 4-entry ring.
 struct SdPlan {
-  int ts, ne, npb, mt, grid;
+  int ts, xd, ne, npb, mt, grid;
   size_t lds;
 };
 static bool sd_plan(int m, int n, int k, SdPlan* p) {
@@ -603,21 +625,24 @@ static bool sd_plan(int m, int n, int k, SdPlan* p) {
   const int grid = uwc_cu_count() & ~15;  // a multiple of 16: G / 8 is a multiple of ts
   if (grid < 16) return false;
   const int nblk = (n + 15) / 16;
-  for (int ts = 1; ts <= 2; ts++) {
-    if (m % ts) continue;
-    const int mg = m / ts, mt = (mg + 15) / 16;
-    // most tasks of a workgroup: tasks of the busiest XCD over its G / 8 workgroups
-    const int nmine_max = ((nblk + 7) / 8 * ts + grid / 8 - 1) / (grid / 8);
-    for (int npb = 2; npb >= 1; npb--)
-      for (int ne = SD_MAX_NE; ne >= 4; ne--) {
-        const size_t lds = sd_lds_bytes(ne, npb, mg, k, mt, nmine_max);
-        if (lds <= 160 * 1024) {
-          // at least 81 KB: one workgroup per CU, so the dispatcher spreads them over every CU
-          *p = SdPlan{ts, ne, npb, mt, grid, std::max(lds, (size_t)81 * 1024)};
-          return true;
+  for (int stream = 0; stream <= 1; stream++)
+    for (int ts = 1; ts <= 2; ts++) {
+      if (m % ts) continue;
+      const int mg = m / ts, mt = (mg + 15) / 16;
+      const int xd = stream ? (mg <= 8 ? 1 : mg <= 16 ? 2 : mg <= 32 ? 4 : 0) : 0;
+      if (stream && xd == 0) continue;
+      // most tasks of a workgroup: tasks of the busiest XCD over its G / 8 workgroups
+      const int nmine_max = ((nblk + 7) / 8 * ts + grid / 8 - 1) / (grid / 8);
+      for (int npb = 2; npb >= 1; npb--)
+        for (int ne = SD_MAX_NE; ne >= 4; ne--) {
+          const size_t lds = sd_lds_bytes(ne, npb, xd, mg, k, mt, nmine_max);
+          if (lds <= 160 * 1024) {
+            // at least 81 KB: one workgroup per CU, so the dispatcher spreads them over every CU
+            *p = SdPlan{ts, xd, ne, npb, mt, grid, std::max(lds, (size_t)81 * 1024)};
+            return true;
+          }
         }
-      }
-  }
+    }
   return false;
 }
 
@@ -638,12 +663,24 @@ int uwc_skinny_gemm(const int8_t* X, const int8_t* W, int m, int n, int k, const
   SdPlan sp;
   const bool vec_ok = ((uintptr_t)out & 15) == 0 && (out_mode == UWC_OUT_I32 || ((uintptr_t)sw & 15) == 0);
   if (vec_ok && sd_plan(m, n, k, &sp)) {
-    switch (sp.mt) {
-      case 1: sd_ne<1>(sp.ne, sp.npb, out_mode, sp.grid, sp.lds, stream, X, W, m, n, k, sp.ts, sx, sw, out); break;
-      case 2: sd_ne<2>(sp.ne, sp.npb, out_mode, sp.grid, sp.lds, stream, X, W, m, n, k, sp.ts, sx, sw, out); break;
-      case 3: sd_ne<3>(sp.ne, sp.npb, out_mode, sp.grid, sp.lds, stream, X, W, m, n, k, sp.ts, sx, sw, out); break;
-      default: sd_ne<4>(sp.ne, sp.npb, out_mode, sp.grid, sp.lds, stream, X, W, m, n, k, sp.ts, sx, sw, out); break;
+#define SD_GO(MT, XD) sd_ne<MT, XD>(sp.ne, sp.npb, out_mode, sp.grid, sp.lds, stream, X, W, m, n, k, sp.ts, sx, sw, out)
+    if (sp.xd == 0) {
+      switch (sp.mt) {
+        case 1: SD_GO(1, 0); break;
+        case 2: SD_GO(2, 0); break;
+        case 3: SD_GO(3, 0); break;
+        default: SD_GO(4, 0); break;
+      }
+    } else if (sp.xd == 1) {
+      SD_GO(1, 1);
+    } else if (sp.xd == 2) {
+      SD_GO(1, 2);
+    } else if (sp.mt == 1) {
+      SD_GO(1, 4);
+    } else {
+      SD_GO(2, 4);
     }
+#undef SD_GO
     return uwc_launch_status("skinny_dma_gemm");
   }
   const int mt = (m + 15) / 16;
