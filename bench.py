@@ -255,9 +255,13 @@ def parity_and_cpu(args, res, torch, np, ops, O):
 
 
 def detrt_layer(args, torch, np):
-    """qkv, o, gu, down of a Qwen3-1.7B layer at M = 2048 through DetLinear."""
-    from uwc_amd import detrt
+    """qkv, o, gu, down of a Qwen3-1.7B layer at M = 2048 through DetLinear.
+    Device time: the four calls (quant_act + exact GEMM with fused dequant each) captured in a HIP
+    graph and replayed; beside it the GEMM-only time (the four uwc_igemm_dequant_f32 launches on
+    pre-quantized activations, graph-replayed) and the host-timed eager figure."""
+    from uwc_amd import _lib, detrt
     dev = "cuda"
+    L = _lib.lib()
     M, D, I, H, Hkv, hd = 2048, 2048, 6144, 16, 8, 128
     shapes = {"qkv": ((H + 2 * Hkv) * hd, D), "o": (D, H * hd), "gu": (2 * I, D), "down": (D, I)}
     g = torch.Generator(device=dev)
@@ -270,19 +274,45 @@ def detrt_layer(args, torch, np):
     for name in shapes:
         lays[name](xs[name])
     torch.cuda.synchronize()
-    reps = 10
     macs = sum(M * nn * kk for nn, kk in shapes.values())
+    # host-timed eager calls (launch overhead included)
+    reps = 10
     t0 = time.perf_counter()
     for _ in range(reps):
         for name in shapes:
             lays[name](xs[name])
     torch.cuda.synchronize()
-    dt = (time.perf_counter() - t0) / reps
+    host_dt = (time.perf_counter() - t0) / reps
+    # device time of the whole linears: one graph of the four DetLinear calls
+    keep = []
+
+    def call(name):
+        keep.append(lays[name](xs[name]))
+        return 0
+    layer_us = _graph_time_us(torch, [lambda nm=nm: call(nm) for nm in shapes]) * len(shapes)
+    keep.clear()
+    # GEMM-only device time per linear
+    stream_of = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+    gemm_us, per = 0.0, {}
+    for name, (nn, kk) in shapes.items():
+        q, sx = detrt.quant_act(xs[name], lays[name].bs)
+        y = torch.empty((M, nn), dtype=torch.float32, device=dev)
+        lay = lays[name]
+        f = lambda q=q, sx=sx, y=y, lay=lay, nn=nn, kk=kk: L.uwc_igemm_dequant_f32(  # noqa: E731
+            q.data_ptr(), lay.Wq.data_ptr(), M, nn, kk, sx.data_ptr(), lay.sw.data_ptr(), y.data_ptr(), stream_of())
+        us = _graph_time_us(torch, [f] * 8)
+        per[name] = dict(us=round(us, 2), tops=round(2.0 * M * nn * kk / us / 1e6, 1))
+        gemm_us += us
     import oracle as O
     ctops, ct, ran, cores = cpu_linears(torch, np, O, M, shapes, budget_s=3.0)
     out = dict(workload="Qwen3-1.7B layer linears (qkv, o, gu, down) at M=2048, quant_act + exact GEMM + dequant",
-               ms_per_layer=round(dt * 1e3, 4), tops=round(2.0 * macs / dt / 1e12, 2),
-               frac_of_peak=round(2.0 * macs / dt / 1e12 / PEAK_INT8_TOPS, 4),
+               ms_per_layer=round(layer_us / 1e3, 4), tops=round(2.0 * macs / layer_us / 1e6, 2),
+               frac_of_peak=round(2.0 * macs / layer_us / 1e6 / PEAK_INT8_TOPS, 4),
+               timing="device (HIP graph of the four DetLinear calls, replayed)",
+               gemm_only=dict(us_per_layer=round(gemm_us, 2), tops=round(2.0 * macs / gemm_us / 1e6, 1),
+                              frac_of_peak=round(2.0 * macs / gemm_us / 1e6 / PEAK_INT8_TOPS, 4), per_linear=per,
+                              kernel="uwc_igemm_dequant_f32 (exact int8 GEMM, fused fp32 dequant), graph-replayed"),
+               host_ms_per_layer=round(host_dt * 1e3, 4),
                cpu_baseline=dict(value=round(ctops, 4), unit="TOPS", cores=cores, kind="port",
                                  sample=f"quant_act + fp64 matmul + dequant, {ran}, {ct:.2f} s"))
     log(f"detrt layer: {out}")
@@ -344,6 +374,19 @@ def cpu_linears(torch, np, O, m, shapes, budget_s=3.0):
     return tops, t_done, ran, threads
 
 
+def _weight_copies(wb):
+    """Distinct weight buffers a skinny shape rotates over: > 1.2 GB in all, at least 2."""
+    return max(2, -(-(1200 << 20) // wb))
+
+
+def _skinny_launches(wb, reps_cap=48):
+    """Launches in a skinny shape's timing graph."""
+    return min(max(2 * _weight_copies(wb), 16), reps_cap)
+
+
+LLAMA_LINEARS = {"qkv": (6144, 4096), "o": (4096, 4096), "gu": (28672, 4096), "down": (4096, 14336)}
+
+
 def skinny_linears(args, torch, np):
     """BASELINE configs[0] (detrt MLP-up, 64 x 2048 -> 6144) and the decode half of configs[3]
     (Llama-3.1-8B layer linears at M = 1, 8, 32): exact GEMM + fused fp32 dequant through
@@ -360,7 +403,7 @@ def skinny_linears(args, torch, np):
         total_us, total_bytes, per = 0.0, 0, {}
         for name, (n, k) in shapes.items():
             wb = n * k
-            nw = max(2, -(-(1200 << 20) // wb))
+            nw = _weight_copies(wb)
             Ws = [torch.randint(-64, 65, (n, k), dtype=torch.int8, device=dev) for _ in range(nw)]
             X = torch.randint(-64, 65, (m, k), dtype=torch.int8, device=dev)
             sx, sw = torch.rand(m, device=dev) + 0.5, torch.rand(n, device=dev) * 1e-3
@@ -369,7 +412,7 @@ def skinny_linears(args, torch, np):
             def mk(W):
                 return lambda: L.uwc_igemm_dequant_f32(X.data_ptr(), W.data_ptr(), m, n, k, sx.data_ptr(),
                                                        sw.data_ptr(), Y.data_ptr(), stream_of())
-            launches = [mk(Ws[i % nw]) for i in range(min(max(2 * nw, 16), reps_cap))]
+            launches = [mk(Ws[i % nw]) for i in range(_skinny_launches(wb, reps_cap))]
             us = _graph_time_us(torch, launches)
             byt = wb + m * k + 4 * m * n + 4 * (m + n)
             per[name] = dict(us=round(us, 2), gbs=round(byt / us / 1e3, 1))
@@ -388,7 +431,7 @@ def skinny_linears(args, torch, np):
         tops=round(2.0 * 64 * 6144 * 2048 / us / 1e6, 2),
         cpu_baseline=dict(value=round(ctops, 4), unit="TOPS", cores=cores, kind="port",
                           sample=f"quant_act + fp64 matmul + dequant, {ran}, {ct:.2f} s"))
-    llama = {"qkv": (6144, 4096), "o": (4096, 4096), "gu": (28672, 4096), "down": (4096, 14336)}
+    llama = LLAMA_LINEARS
     dec = {}
     for m in (1, 8, 32):
         us, byt, per = run(m, llama)
@@ -716,6 +759,65 @@ def summarize_e2e_trace(stats_csv, out_path, cmd):
     print(open(out_path).read())
 
 
+LINEAR_LABELS = ["configs[1] layer graph: 4 x (quant_act + GEMM)", "configs[1] qkv GEMM 2048x4096x2048",
+                 "configs[1] o GEMM 2048x2048x2048", "configs[1] gu GEMM 2048x12288x2048",
+                 "configs[1] down GEMM 2048x2048x6144", "configs[0] mlp_up 64x6144x2048"] + [
+    f"Llama-3.1-8B decode M={m} {nm}" for m in (1, 8, 32) for nm in ("qkv 6144x4096", "o 4096x4096",
+                                                                      "gu 28672x4096", "down 4096x14336")]
+
+
+def summarize_linears_trace(trace_csv, out_path, cmd):
+    """A kernel trace of `bench.py --linears-only` as text: per graph-timed shape (configs[1]'s layer
+    graph and its four GEMMs, configs[0], the Llama-3.1-8B decode linears) the device durations of
+    its timed replays. Each graph of N launches is run eagerly, replayed once, then replayed three
+    times back to back: dispatch runs are split at idle gaps over 30 us, and each shape's timed run
+    is the next run of exactly 3 N dispatches of this library's kernels (N from the bench's own
+    launch counts; torch's kernels fill the gaps between shapes)."""
+    import csv
+    import re
+    rows = sorted(csv.DictReader(open(trace_csv)), key=lambda r: int(r["Start_Timestamp"]))
+    runs, cur, last_end = [], [], None
+    for r in rows:
+        st, en = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
+        if cur and st - last_end > 30000:
+            runs.append(cur)
+            cur = []
+        cur.append(r)
+        last_end = en
+    if cur:
+        runs.append(cur)
+    ours = lambda r: not re.search(r"at::native|__amd_rocclr", r["Kernel_Name"])  # noqa: E731
+    # the timed run of each shape, in bench order: 3 x the launches of its graph (warm-up and first
+    # replay runs have a third of that)
+    want = [24] * 5 + [3 * _skinny_launches(6144 * 2048)] + [
+        3 * _skinny_launches(nn * kk) for _ in (1, 8, 32) for nn, kk in LLAMA_LINEARS.values()]
+    timed, j = [], 0
+    for w in want:
+        while j < len(runs) and not (len(runs[j]) == w and all(ours(r) for r in runs[j])):
+            j += 1
+        if j == len(runs):
+            break
+        timed.append(runs[j])
+        j += 1
+    with open(out_path, "w") as f:
+        f.write("rocprofv3 kernel trace, graph-timed linears of bench.py (configs[1] at M=2048, configs[0], "
+                "Llama-3.1-8B decode at M=1, 8, 32; weights rotated over > 1.2 GB)\n")
+        f.write(f"command: {cmd}\n\n")
+        f.write(f"{'shape':44s} {'kernel':44s} {'grid':>6s} {'lds':>7s} {'calls':>6s} {'avg_us':>8s} {'min_us':>8s} "
+                f"{'max_us':>8s}\n")
+        for lab, run in zip(LINEAR_LABELS, timed):
+            per = {}
+            for r in run:
+                key = (re.sub(r"\(.*", "", r["Kernel_Name"])[:44], r.get("Grid_Size_X", ""), r.get("LDS_Block_Size", ""))
+                per.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+            for (kn, grid, lds), xs in per.items():
+                f.write(f"{lab[:44]:44s} {kn:44s} {grid:>6s} {lds:>7s} {len(xs):6d} {sum(xs) / len(xs):8.2f} "
+                        f"{min(xs):8.2f} {max(xs):8.2f}\n")
+        f.write("\ngrid = work-items (workgroups x 640 for skinny_dma_kernel); kernel durations exclude the "
+                "~1.8 us launch gap between dependent graph nodes that the bench's per-launch figures include.\n")
+    print(open(out_path).read())
+
+
 def _summary_value(path, key):
     """The number after `key:` in a committed rocprofv3 summary under profiles/, or None."""
     try:
@@ -766,6 +868,9 @@ def main():
     ap.add_argument("--e2e-layers", type=int, default=28)
     ap.add_argument("--e2e-cpu-tokens", type=int, default=256)
     ap.add_argument("--traffic-probe", action="store_true", help="the workload of the FETCH_SIZE / WRITE_SIZE passes")
+    ap.add_argument("--linears-only", action="store_true", help="run only configs[1], configs[0] and the decode linears")
+    ap.add_argument("--summarize-linears-trace", nargs=3, metavar=("TRACE_CSV", "OUT", "CMD"),
+                    help="write the graph-timed linears' kernel-trace summary under profiles/")
     ap.add_argument("--summarize-pmc", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "CMD", "NONCES"),
                     help="write the traffic summary under profiles/ from two counter_collection.csv files")
     ap.add_argument("--summarize-counters", nargs=3, metavar=("COUNTER_CSV", "CMD", "NONCES"),
@@ -777,6 +882,9 @@ def main():
     args = ap.parse_args()
     if args.summarize_trace:
         summarize_trace(*args.summarize_trace)
+        return
+    if args.summarize_linears_trace:
+        summarize_linears_trace(*args.summarize_linears_trace)
         return
     if args.summarize_e2e_trace:
         summarize_e2e_trace(*args.summarize_e2e_trace)
@@ -803,6 +911,9 @@ def main():
         return
     if args.e2e_only:
         print(json.dumps(qwen3_e2e(args, torch, np)))
+        return
+    if args.linears_only:
+        print(json.dumps({"detrt_layer": detrt_layer(args, torch, np), "detrt_skinny": skinny_linears(args, torch, np)}))
         return
     ceiling = mfma_ceiling(torch)
     res = mining(args, torch, np, ops)
