@@ -11,9 +11,12 @@ function is listed in the C file's header and exercised by tests/test_oracle.py.
 
 Parity status: BLAKE3-derived values (commitment roots, seeds, noise E/P, tile digests)
 have no stored vectors in the reference (its only check compares against the `blake3`
-package live, miner/ampere/tests/test_kernels.py:13-20); here they are pinned by BLAKE3's
-published digests plus two independent restatements (C recursive tree, Python streaming
-stack). The Pearl-side job_key/penalised bound (pearl_glue.py:44-62) are "parity unpinned"
+package live, miner/ampere/tests/test_kernels.py:13-20); here they are pinned by the BLAKE3
+team's published test vectors (tests/golden/blake3_official_vectors.json: unkeyed inputs of 0 to
+102400 bytes, i.e. one block, a chunk, a parent node and 31- and 100-chunk trees; keyed inputs of
+0, 1, 1024 and 2048 bytes, the last one two chunks under a keyed parent, the form every
+commitment takes) plus two independent restatements (C recursive tree, Python streaming stack)
+that agree on every tree shape up to 129 chunks, keyed and plain. The Pearl-side job_key/penalised bound (pearl_glue.py:44-62) are "parity unpinned"
 and are not restated: callers pass job_key and target words, as the kernels do.
 """
 from __future__ import annotations

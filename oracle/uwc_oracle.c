@@ -15,12 +15,15 @@
  *   or_igemm_i32        L1 known answer sha256[:20] = bf9394d180bda5b0412c
  *                       (results/xc_cpu.json:4, miner/ampere/bench/crosscheck.py:62-76)
  *                       and the Go-referee linear fixtures (int accumulators).
- *   or_b3_*             BLAKE3 published empty-input and "abc" digests, plus agreement
- *                       with an independent pure-Python restatement (oracle/blake3_py.py)
- *                       over every tree shape up to 70 chunks and ragged lengths.
+ *   or_b3_*             the BLAKE3 team's published test vectors (unkeyed 0..102400 bytes,
+ *                       keyed 0, 1, 1024 and 2048 bytes: one block, a chunk chain, parent
+ *                       nodes, 31- and 100-chunk trees), plus agreement with an independent
+ *                       pure-Python restatement (oracle/blake3_py.py) over every tree shape
+ *                       up to 129 chunks, keyed and plain, and ragged lengths.
  *   or_noise_*          structural invariants (range [-32,31], first != second < r),
- *                       byte layout against a pure-Python random_hash.
- *                       Values themselves: parity unpinned (needs the `blake3` package).
+ *                       byte layout against a pure-Python random_hash. The values rest on the
+ *                       pinned keyed BLAKE3 and the restated message layout (reference.py:67-93);
+ *                       the reference stores no vectors of them.
  *   or_transcript_*     brute-force per-tile recomputation on tiny shapes (explicit
  *                       cumulative sums over each tile's 128 elements).
  *   or_quant_act_f32    Go-referee fixtures N1->QA1, O->QA2, N2->QA3, SM->QA4 bit-exact.
