@@ -73,6 +73,44 @@ __device__ __forceinline__ void quad_compress_m(const u32 m[28], int q, u32 ca, 
   hi = b ^ d;
 }
 
+// The byte offsets of message word j (0..3) of round r for the 4 lanes of a quad, one per byte:
+// lane q extracts byte q (one v_bfe), so no lane keeps a table of 28 offsets in registers.
+__device__ constexpr u32 quad_off_pack(int r, int j) {
+  u32 v = 0;
+  for (int q = 0; q < 4; q++) {
+    const int w = j < 2 ? kB3Sched[r][2 * q + j] : kB3Sched[r][8 + 2 * q + (j - 2)];
+    v |= (u32)(4 * w) << (8 * q);
+  }
+  return v;
+}
+
+// quad_compress_m with the message words read from LDS round by round (4 live words instead of
+// 28, offsets from quad_off_pack). q8 = 8 q; word w is read at msg + ((4 w) ^ xmask), for
+// messages stored with their 16-byte quarters permuted by xmask (0 for a plain message).
+__device__ __forceinline__ void quad_compress_rounds(const u8* msg, u32 q8, u32 xmask, int q, u32 ca, u32 cb,
+                                                     u64 counter, u32 blen, u32 flags, u32& lo, u32& hi) {
+  u32 a = ca, b = cb, c = b3_iv(0), d = (u32)counter;
+  if (q == 1) { c = b3_iv(1); d = (u32)(counter >> 32); }
+  if (q == 2) { c = b3_iv(2); d = blen; }
+  if (q == 3) { c = b3_iv(3); d = flags; }
+#pragma unroll
+  for (int r = 0; r < 7; r++) {
+    u32 o[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) o[j] = __builtin_amdgcn_ubfe(quad_off_pack(r, j), q8, 8) ^ xmask;
+    const u32 m0 = *reinterpret_cast<const u32*>(msg + o[0]);
+    const u32 m1 = *reinterpret_cast<const u32*>(msg + o[1]);
+    const u32 m2 = *reinterpret_cast<const u32*>(msg + o[2]);
+    const u32 m3 = *reinterpret_cast<const u32*>(msg + o[3]);
+    b3_g1(a, b, c, d, m0, m1);
+    b = qperm<QROT1>(b); c = qperm<QROT2>(c); d = qperm<QROT3>(d);
+    b3_g1(a, b, c, d, m2, m3);
+    b = qperm<QROT3>(b); c = qperm<QROT2>(c); d = qperm<QROT1>(d);
+  }
+  lo = a ^ c;
+  hi = b ^ d;
+}
+
 // quad_compress_m on a message in LDS.
 __device__ __forceinline__ void quad_compress(const u8* msg, const QuadMsgOffsets& off, int q, u32 ca, u32 cb,
                                               u64 counter, u32 blen, u32 flags, u32& lo, u32& hi) {
@@ -84,8 +122,7 @@ __device__ __forceinline__ void quad_compress(const u8* msg, const QuadMsgOffset
 // Level-wise pairwise reduction, by quads, of `count` chaining values in LDS (8 words each):
 // pairs (2i, 2i+1) merge, an odd last value carries up. Over a group that starts at a multiple
 // of a power of two covering it, this is exactly BLAKE3's left-complete tree.
-__device__ void quad_level_reduce(u32* cvs, int count, u32 k_lo, u32 k_hi, u32 kflag, bool root_at_end,
-                                  const QuadMsgOffsets& off) {
+__device__ __forceinline__ void quad_level_reduce(u32* cvs, int count, u32 k_lo, u32 k_hi, u32 kflag, bool root_at_end) {
   const int tid = threadIdx.x, q = tid & 3, quad = tid >> 2, nquads = blockDim.x >> 2;
   while (count > 1) {
     const int pairs = count >> 1;
@@ -93,11 +130,11 @@ __device__ void quad_level_reduce(u32* cvs, int count, u32 k_lo, u32 k_hi, u32 k
     // up to 2 pairs per quad (groups of at most 4 * blockDim / 4 values)
     u32 lo0 = 0, hi0 = 0, lo1 = 0, hi1 = 0;
     if (quad < pairs)
-      quad_compress(reinterpret_cast<const u8*>(cvs + quad * 16), off, q, k_lo, k_hi, 0, 64,
-                    B3_PARENT | kflag | (last ? B3_ROOT : 0u), lo0, hi0);
+      quad_compress_rounds(reinterpret_cast<const u8*>(cvs + quad * 16), 8 * q, 0, q, k_lo, k_hi, 0, 64,
+                           B3_PARENT | kflag | (last ? B3_ROOT : 0u), lo0, hi0);
     if (quad + nquads < pairs)
-      quad_compress(reinterpret_cast<const u8*>(cvs + (quad + nquads) * 16), off, q, k_lo, k_hi, 0, 64,
-                    B3_PARENT | kflag, lo1, hi1);
+      quad_compress_rounds(reinterpret_cast<const u8*>(cvs + (quad + nquads) * 16), 8 * q, 0, q, k_lo, k_hi, 0, 64,
+                           B3_PARENT | kflag, lo1, hi1);
     u32 carry = 0;
     const bool has_carry = (count & 1) && tid < 8;
     if (has_carry) carry = cvs[(count - 1) * 8 + tid];
@@ -111,17 +148,11 @@ __device__ void quad_level_reduce(u32* cvs, int count, u32 k_lo, u32 k_hi, u32 k
 }
 
 #define B3_CHUNKS_PER_WG 64
-#define B3_QSTRIDE 80  // LDS bytes per quad's message block (64 + 16 pad: fewer bank conflicts)
+#define B3_RING 4  // blocks of every chunk in flight, per wave (the wait switch below covers up to 4)
+#define B3_QSTRIDE 80  // LDS bytes per quad's message block in nonce_noise (64 + 16 pad: fewer bank conflicts)
 
-// 64 chunks per workgroup (256 threads, one quad per chunk). A chunk is a chain of 16 dependent
-// compressions, so its loads are issued all at once up front (lane q holds bytes [16 q, 16 q + 16)
-// of every 64-byte block: 64 VGPRs) and the chain waits for HBM once, not once per block. Blocks
-// reach the quad's message words through two LDS slots per quad: block b + 1 is written and its
-// words read while block b compresses (a wave's LDS accesses complete in order, and a quad only
-// touches its own slots).
 // Inputs of a batch of equal-size commitments (blockIdx.y = item): one launch commits several
-// operands at once, which gives a latency-bound chain kernel several waves per SIMD to switch
-// between.
+// operands at once.
 #define B3_MAXB 16
 struct B3In {
   const u8* data[B3_MAXB];
@@ -131,43 +162,69 @@ struct B3Out {
   u32* seed[B3_MAXB];
 };
 
+typedef void __attribute__((address_space(3)))* b3_lptr;
+
+__device__ __forceinline__ void b3_dma16(const void* g, u32 lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+template <int N>
+__device__ __forceinline__ void b3_waitv() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+
+// 64 chunks per workgroup (4 waves x 16 quads, one quad per chunk). A chunk is a chain of 16
+// dependent compressions of ~180 dependent instructions each, and a batch of 8 operands is 8
+// waves per SIMD of ~4100 VALU instructions each: at 4 cycles per wave64 VALU instruction the
+// batch is VALU-bound (~63 us for 8 x 16 MiB), so the kernel keeps 6 waves per SIMD resident
+// (78 VGPRs; at 8 the compiler spills) and its LDS reads free of bank conflicts. A wave streams
+// its 16 chunks' blocks through its own LDS ring by DMA, B3_RING blocks ahead (lane l fetches
+// bytes [16 (l & 3), + 16) of block b of chunk l / 4, so one DMA instruction brings one block of
+// all 16 chunks); the ring is the wave's own, so no barrier is needed, only the wave's vmcnt. A
+// lane reads the message words of each round from the ring at its precomputed offsets.
 // Item blockIdx.y hashes bt.data[item] into wg_cvs + item * stride (stride in words).
-__global__ void __launch_bounds__(256) b3_chunks_kernel(B3In bt, u64 nchunks, const u32* __restrict__ key,
-                                                        u32* __restrict__ wg_cvs, u64 stride) {
-  __shared__ __attribute__((aligned(16))) u8 blk[2][B3_CHUNKS_PER_WG * B3_QSTRIDE];
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6)))
+b3_chunks_kernel(B3In bt, u64 nchunks, const u32* __restrict__ key, u32* __restrict__ wg_cvs, u64 stride) {
+  __shared__ __attribute__((aligned(16))) u8 ring[4][B3_RING][1024];  // [wave][slot][16 chunks x 64 bytes]
   __shared__ u32 cvs[B3_CHUNKS_PER_WG * 8];
   const u8* __restrict__ data = bt.data[blockIdx.y];
   wg_cvs += blockIdx.y * stride;
-  const int tid = threadIdx.x, q = tid & 3, c = tid >> 2;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = tid & 3, c = tid >> 2;
   const u64 base = (u64)blockIdx.x * B3_CHUNKS_PER_WG;
   const int count = (int)min((u64)B3_CHUNKS_PER_WG, nchunks - base);
-  const QuadMsgOffsets off = quad_offsets(q);
   const u32 k_lo = key[q], k_hi = key[4 + q];
   const bool active = c < count;
-  const v4i* src = reinterpret_cast<const v4i*>(data + (base + (active ? c : 0)) * 1024ull) + q;
-  v4i d[16];
+  // this lane's 16 bytes of every block (chunks past the end read the first chunk: not stored).
+  // Chunk slot i of a ring entry holds the chunk's block with its 16-byte quarters permuted,
+  // quarter p at position p ^ (i >> 2): lane 4 i + q fetches quarter q ^ (i >> 2). Chunks i and
+  // i + 4 (64 bytes apart: the same banks) then keep any given word in different banks, and the
+  // 16 quads' reads of one message word no longer collide 4 to a bank.
+  const u32 xmask = lane & 48;  // (i >> 2) << 4
+  const u8* src = data + (base + (active ? c : 0)) * 1024ull + ((q * 16) ^ xmask);
+  const u32 rbase = __builtin_amdgcn_readfirstlane((u32)(uintptr_t)(b3_lptr)&ring[wave][0][0]);
 #pragma unroll
-  for (int b = 0; b < 16; b++) d[b] = active ? src[b * 4] : v4i{0, 0, 0, 0};
-  u8* slot[2] = {blk[0] + c * B3_QSTRIDE, blk[1] + c * B3_QSTRIDE};
-  u32 m[2][28];
-  *reinterpret_cast<v4i*>(slot[0] + q * 16) = d[0];
-  __builtin_amdgcn_wave_barrier();
-  quad_msg(slot[0], off, m[0]);
+  for (int b = 0; b < B3_RING; b++) b3_dma16(src + b * 64, rbase + b * 1024);
   u32 lo = k_lo, hi = k_hi;
 #pragma unroll
   for (int b = 0; b < 16; b++) {
-    if (b + 1 < 16) {
-      *reinterpret_cast<v4i*>(slot[(b + 1) & 1] + q * 16) = d[b + 1];
-      __builtin_amdgcn_wave_barrier();
-      quad_msg(slot[(b + 1) & 1], off, m[(b + 1) & 1]);
+    // blocks b .. min(b + B3_RING - 1, 15) are in flight: wait for block b (the count folds to
+    // a constant in the unrolled loop)
+    switch (min(B3_RING - 1, 15 - b)) {
+      case 0: b3_waitv<0>(); break;
+      case 1: b3_waitv<1>(); break;
+      case 2: b3_waitv<2>(); break;
+      default: b3_waitv<3>(); break;
     }
+    const u8* blk = &ring[wave][b % B3_RING][(lane >> 2) * 64];
     const u32 flags = B3_KEYED | (b == 0 ? B3_CHUNK_START : 0u) | (b == 15 ? B3_CHUNK_END : 0u) |
                       ((b == 15 && nchunks == 1) ? B3_ROOT : 0u);
-    quad_compress_m(m[b & 1], q, lo, hi, base + c, 64, flags, lo, hi);
+    quad_compress_rounds(blk, 8 * q, xmask, q, lo, hi, base + c, 64, flags, lo, hi);
+    if (b + B3_RING < 16) {
+      // the slot's reads are done (their values were used above) before the DMA overwrites it
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      b3_dma16(src + (b + B3_RING) * 64, rbase + (b % B3_RING) * 1024);
+    }
   }
   if (active) { cvs[c * 8 + q] = lo; cvs[c * 8 + 4 + q] = hi; }
   __syncthreads();
-  quad_level_reduce(cvs, count, k_lo, k_hi, B3_KEYED, gridDim.x == 1, off);
+  quad_level_reduce(cvs, count, k_lo, k_hi, B3_KEYED, gridDim.x == 1);
   if (tid < 8) wg_cvs[blockIdx.x * 8 + tid] = cvs[tid];
 }
 
@@ -223,7 +280,7 @@ __global__ void __launch_bounds__(256) b3_reduce_kernel(const u32* __restrict__ 
     }
     c2 = pairs + (c2 & 1);
   }
-  quad_level_reduce(cvs, c2, k_lo, k_hi, B3_KEYED, final_level != 0, off);
+  quad_level_reduce(cvs, c2, k_lo, k_hi, B3_KEYED, final_level != 0);
   if (!final_level) {
     if (tid < 8) out_cvs[blockIdx.x * 8 + tid] = cvs[tid];
     return;
