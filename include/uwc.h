@@ -31,6 +31,13 @@ extern "C" {
 #define UWC_FLAG_HASH 1
 #define UWC_FLAG_DENOISE 2
 #define UWC_FLAG_TILE128 0x100  /* force the 128 x 128 tiling (identical results) */
+/* force configuration c (0: 128 x 128 tiles, 4-step ring; 1: 128 x 256, 3 steps; 2: 128 x 128,
+ * 2 steps; 3: 128 x 256, 2 steps; c + 4: the same with each step's DMA spread over the next
+ * step's passes) of the DMA-pipelined plain kernel: UWC_FLAG_PLAIN_CFG(c).
+ * Plain GEMMs only (no HASH / DENOISE / TILE128); m, n multiples of the tile, k % 128 == 0, out
+ * and (for BF16 / F32) b_scale 16-byte aligned, n % 4 == 0; identical results. */
+#define UWC_FLAG_PLAIN 0x200
+#define UWC_FLAG_PLAIN_CFG(c) (UWC_FLAG_PLAIN | ((c) << 12))
 #define UWC_OUT_NONE 0
 #define UWC_OUT_I32 1
 #define UWC_OUT_BF16 2

@@ -64,6 +64,12 @@ def test_scratch_words_host_only():
     (dict(out_mode=7), "unknown out_mode"),
     (dict(out_mode=3, scales=False), "a_scale and b_scale"),
     (dict(flags=8), "unknown flags"),
+    (dict(flags=0x1000), "unknown flags"),                     # a plain configuration without FLAG_PLAIN
+    (dict(flags=0x200 | (9 << 12)), "configuration 9 unknown"),
+    (dict(flags=0x200 | 1, m=128), "FLAG_PLAIN is for plain"),  # with FLAG_HASH
+    (dict(flags=0x300), "FLAG_PLAIN is for plain"),             # with FLAG_TILE128
+    (dict(flags=0x200 | (1 << 12), n=128), "does not take"),    # 128 x 256 tiles, n = 128
+    (dict(flags=0x200, m=192), "does not take"),                # 128-row tiles, m = 192
 ])
 def test_noisy_gemm_rejects_bad_arguments(kwargs, msg):
     from uwc_amd import _lib

@@ -34,6 +34,11 @@
 #define FLAG_HASH 1
 #define FLAG_DENOISE 2
 #define FLAG_TILE128 0x100  // force the 128 x 128 kernel (same results; for tests and small shapes)
+// force configuration c of the plain DMA kernel (uwc_gemm_plain.hip) for a plain GEMM:
+// FLAG_PLAIN | c << FLAG_PLAIN_SHIFT (same results; for tests and tuning)
+#define FLAG_PLAIN 0x200
+#define FLAG_PLAIN_SHIFT 12
+#define FLAG_PLAIN_MASK (0xF << FLAG_PLAIN_SHIFT)
 #define OUT_NONE 0
 #define OUT_I32 1
 #define OUT_BF16 2
@@ -321,6 +326,10 @@ int uwc_noisy_gemm256(const int8_t* A, const int8_t* B, int m, int n, int k, int
 
 int uwc_skinny_gemm(const int8_t* X, const int8_t* W, int m, int n, int k, const float* sx, const float* sw,
                     void* out, int out_mode, hipStream_t stream);
+int uwc_plain_cfg_count();
+bool uwc_plain_fits(int cfg, int m, int n, int k, int ldc, const void* out, int out_mode, const float* b_scale);
+int uwc_gemm_plain(int cfg, const int8_t* A, const int8_t* B, int m, int n, int k, const float* a_scale,
+                   const float* b_scale, void* out, int out_mode, int ldc, hipStream_t stream);
 
 template <bool H, bool D>
 static void launch_out(int out_mode, dim3 grid, hipStream_t s, const GemmParams& p) {
@@ -340,7 +349,17 @@ static int gemm_check(const int8_t* A, const int8_t* B, int m, int n, int k, int
                       uint32_t* wins, int max_wins, const float* a_scale, const float* b_scale, void* out, int out_mode,
                       int flags) {
   const bool hash = flags & FLAG_HASH, denoise = flags & FLAG_DENOISE;
-  if (flags & ~(FLAG_HASH | FLAG_DENOISE | FLAG_TILE128)) return uwc_fail("uwc_noisy_gemm: unknown flags %d", flags);
+  if (flags & ~(FLAG_HASH | FLAG_DENOISE | FLAG_TILE128 | FLAG_PLAIN | FLAG_PLAIN_MASK) ||
+      ((flags & FLAG_PLAIN_MASK) && !(flags & FLAG_PLAIN)))
+    return uwc_fail("uwc_noisy_gemm: unknown flags %d", flags);
+  if (flags & FLAG_PLAIN) {
+    const int cfg = (flags & FLAG_PLAIN_MASK) >> FLAG_PLAIN_SHIFT;
+    if (hash || denoise || (flags & FLAG_TILE128))
+      return uwc_fail("uwc_noisy_gemm: FLAG_PLAIN is for plain GEMMs without FLAG_TILE128 (flags %d)", flags);
+    if (cfg >= uwc_plain_cfg_count()) return uwc_fail("uwc_noisy_gemm: plain configuration %d unknown", cfg);
+    if (!uwc_plain_fits(cfg, m, n, k, n, out, out_mode, b_scale))
+      return uwc_fail("uwc_noisy_gemm: plain configuration %d does not take m=%d n=%d k=%d", cfg, m, n, k);
+  }
   if (!A || !B || m <= 0 || n <= 0 || k <= 0) return uwc_fail("uwc_noisy_gemm: empty or null operands (m=%d n=%d k=%d)", m, n, k);
   if (k % G_BK) return uwc_fail("uwc_noisy_gemm: k=%d must be a multiple of %d", k, G_BK);
   if (!aligned16(A) || !aligned16(B)) return uwc_fail("uwc_noisy_gemm: A and B must be 16-byte aligned");
@@ -374,11 +393,18 @@ extern "C" int uwc_noisy_gemm(const int8_t* A, const int8_t* B, int m, int n, in
     return st;
   const bool hash = flags & FLAG_HASH, denoise = flags & FLAG_DENOISE;
   const bool plain = !hash && !denoise;
+  if (flags & FLAG_PLAIN)  // checked: a plain GEMM the forced configuration takes
+    return uwc_gemm_plain((flags & FLAG_PLAIN_MASK) >> FLAG_PLAIN_SHIFT, A, B, m, n, k, a_scale, b_scale, out,
+                          out_mode, n, stream);
   if (plain && m <= 64 && out_mode != OUT_NONE && !(flags & FLAG_TILE128))
     return uwc_skinny_gemm(A, B, m, n, k, a_scale, b_scale, out, out_mode, stream);
-  // 256 x 256 tiles when they fill the 256 CUs (or when hashing: one tiling per nonce shape);
-  // a plain GEMM with fewer 256 x 256 tiles than CUs runs faster on 128 x 128 tiles.
-  const bool fills = (long)(m / 256) * (n / 256) >= 256;
+  // 256 x 256 tiles when hashing (one tiling per nonce shape), or for a plain GEMM when they keep
+  // the CUs busy: at least one tile per CU and the last round of tiles at least 90% full (2048 x
+  // 12288 gives 384 tiles on 256 CUs, a half-empty second round, and runs faster on the plain
+  // kernel's 128 x 128 tiles).
+  const int cus = uwc_cu_count();
+  const long t256 = (long)(m / 256) * (n / 256), rounds256 = (t256 + cus - 1) / cus;
+  const bool fills = t256 >= cus && t256 * 10 >= rounds256 * cus * 9;
   const bool k256 = k % 128 == 0 && k <= (1 << 24);  // the 256 x 256 DMA adds 32-bit lane offsets (255 k + 112)
   // the 256 x 256 epilogue writes 16-byte (8-byte for bf16) row segments: rows must start aligned
   const bool vec_out = out_mode == OUT_NONE || (aligned16(out) && n % 4 == 0);
@@ -400,6 +426,15 @@ extern "C" int uwc_noisy_gemm(const int8_t* A, const int8_t* B, int m, int n, in
     const dim3 g2(((m + G_BM - 1) / G_BM) * ((n - n256 + G_BN - 1) / G_BN));
     launch_out<false, false>(out_mode, g2, stream, q);
     return uwc_launch_status("noisy_gemm (column tail)");
+  }
+  // Any other plain GEMM of whole 128 x 128 tiles: the DMA-pipelined plain kernel with each
+  // step's DMA spread over the next step's passes; a 4-step ring (one workgroup per CU) when there
+  // is at most one tile per CU, else a 2-step ring (two workgroups per CU). Measured at the
+  // Qwen3-1.7B layer linears (M = 2048): the first for o and down, the second for qkv and gate_up.
+  if (plain && !(flags & FLAG_TILE128)) {
+    const int cfg = (long)(m / 128) * (n / 128) <= cus ? 4 : 6;
+    if (uwc_plain_fits(cfg, m, n, k, n, out, out_mode, b_scale))
+      return uwc_gemm_plain(cfg, A, B, m, n, k, a_scale, b_scale, out, out_mode, n, stream);
   }
   GemmParams p{A, B, m, n, k, r, corrA, corrB, maxabs, lmax, key, target, wins, max_wins, a_scale, b_scale, out,
                hash ? tile_dump : nullptr, n};

@@ -54,6 +54,14 @@ DUMP_WORDS = 24
 CHUNKS_PER_CTA = 64
 FLAG_HASH, FLAG_DENOISE = 1, 2
 FLAG_TILE128 = 0x100  # force the 128 x 128 tiling (identical results)
+FLAG_PLAIN = 0x200  # force a configuration of the plain DMA kernel: plain_cfg(c) (identical results)
+
+
+def plain_cfg(c: int) -> int:
+    """Flags forcing configuration c of the plain DMA kernel (0: 128 x 128 tiles, 4-step ring;
+    1: 128 x 256, 3 steps; 2: 128 x 128, 2 steps; 3: 128 x 256, 2 steps; c + 4: the same with
+    each step's DMA spread over the next step's passes)."""
+    return FLAG_PLAIN | (c << 12)
 OUT_NONE, OUT_I32, OUT_BF16, OUT_F32 = 0, 1, 2, 3
 # GEMM tilings: (tile M = N, pipeline stages, waves per SIMD). "256x256" serves m, n % 256 == 0
 # and falls back to "128x128" otherwise; every tiling gives identical outputs and winners.
