@@ -249,6 +249,43 @@ __global__ void __launch_bounds__(256) quant_act_wave_kernel(const T* __restrict
   if (lane == 0) scale[row] = lbs > 0 ? __fmul_rn(s, __fdiv_rn(1.0f, uwc_sqrt_rn((float)(1 << lbs)))) : s;
 }
 
+// The same quant_act with one workgroup per row and one wave per 512-element group (k % 512 == 0,
+// k / 512 <= QA_GMAX, bs <= 512): the groups transform independently (a Hadamard block never
+// spans two groups), the waves combine their max|y| through LDS, and each quantizes its own
+// group. A row of 2048 then runs on 4 waves instead of 1: at M = 2048 the one-wave form leaves
+// half the SIMDs without a wave and the rest with one, whose dependent transform and division
+// chains then run at their full latency.
+template <typename T>
+__global__ void __launch_bounds__(64 * QA_GMAX) quant_act_group_kernel(const T* __restrict__ x, int k, int lbs,
+                                                                       int qmax, i8* __restrict__ q,
+                                                                       float* __restrict__ scale) {
+  __shared__ float wmax[QA_GMAX];
+  const int lane = threadIdx.x & 63, g = threadIdx.x >> 6, G = blockDim.x >> 6;
+  const u64 row = blockIdx.x;
+  float y[1][8];
+  load8(x + row * k + g * 512 + lane * 8, y[0]);
+  fwht512_rows<1>(y, 1, lane, lbs);
+  float mx = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; j++) mx = fmaxf(mx, fabsf(y[0][j]));
+#pragma unroll
+  for (int s = 32; s > 0; s >>= 1) mx = fmaxf(mx, __shfl_xor(mx, s, 64));
+  if (lane == 0) wmax[g] = mx;
+  __syncthreads();
+  mx = wmax[0];
+  for (int i = 1; i < G; i++) mx = fmaxf(mx, wmax[i]);
+  const float fq = (float)qmax;
+  const float s = __fdiv_rn(fmaxf(mx, 1e-8f), fq);
+  u64 packed = 0;
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const float t = fminf(fmaxf(rintf(__fdiv_rn(y[0][j], s)), -fq), fq);
+    packed |= (u64)(u8)(i8)(int)t << (8 * j);
+  }
+  *reinterpret_cast<u64*>(q + row * k + g * 512 + lane * 8) = packed;
+  if (threadIdx.x == 0) scale[row] = lbs > 0 ? __fmul_rn(s, __fdiv_rn(1.0f, uwc_sqrt_rn((float)(1 << lbs)))) : s;
+}
+
 // y = (f32(acc) * sx[row]) * sw[col], each product rounded once (qwen3.py:125).
 __global__ void dequant_kernel(const i32* __restrict__ acc, const float* __restrict__ sx, const float* __restrict__ sw,
                                int n, u64 total, float* __restrict__ y) {
@@ -271,7 +308,8 @@ static int quant_rows(const char* fn, const T* x, int rows, int k, int bs, int q
     const int lbs = 31 - __builtin_clz((unsigned)bse);
     const dim3 grid((unsigned)((rows + 3) / 4));
     if (k <= 512 * QA_GMAX)
-      hipLaunchKernelGGL((quant_act_wave_kernel<true, T>), grid, dim3(256), 0, stream, x, rows, k, lbs, qmax, q, scale);
+      hipLaunchKernelGGL(quant_act_group_kernel<T>, dim3((unsigned)rows), dim3(64 * (k >> 9)), 0, stream, x, k, lbs,
+                         qmax, q, scale);
     else
       hipLaunchKernelGGL((quant_act_wave_kernel<false, T>), grid, dim3(256), 0, stream, x, rows, k, lbs, qmax, q, scale);
     return uwc_launch_status(fn);
