@@ -808,7 +808,8 @@ def summarize_linears_trace(trace_csv, out_path, cmd):
         for lab, run in zip(LINEAR_LABELS, timed):
             per = {}
             for r in run:
-                key = (re.sub(r"\(.*", "", r["Kernel_Name"])[:44], r.get("Grid_Size_X", ""), r.get("LDS_Block_Size", ""))
+                name = r["Kernel_Name"].replace("(anonymous namespace)::", "")
+                key = (re.sub(r"\(.*", "", name)[:44], r.get("Grid_Size_X", ""), r.get("LDS_Block_Size", ""))
                 per.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
             for (kn, grid, lds), xs in per.items():
                 f.write(f"{lab[:44]:44s} {kn:44s} {grid:>6s} {lds:>7s} {len(xs):6d} {sum(xs) / len(xs):8.2f} "
