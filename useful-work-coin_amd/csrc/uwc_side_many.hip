@@ -82,7 +82,10 @@ struct SmGeom {
   static constexpr int STAGE = SRC + STB + SPT;
   static constexpr int NSEG = STAGE / 1024;                 // 1 KiB DMA segments per chunk
   static constexpr int SPW = (NSEG + SM_PROD - 1) / SM_PROD;  // per producer wave (the last repeats)
-  static constexpr int NS = (144 * 1024) / STAGE < 6 ? (144 * 1024) / STAGE : 6;  // ring stages
+  // ring stages: two (64 KiB at r = 64). A deeper ring measured no faster alone, and the batched
+  // commitment of the next group, queued beside this launch on another stream, then fits on the
+  // same CUs (five of its 18 KiB workgroups next to one of these; one next to a 4-stage ring)
+  static constexpr int NS = 2;
   static constexpr int LDS = NS * STAGE;
 };
 
