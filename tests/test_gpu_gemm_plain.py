@@ -102,3 +102,24 @@ def test_plain_repeated_calls_distinct_weights(dev):
         for a, b, B in zip(first, again, Bs):
             assert torch.equal(a, b)
             assert torch.equal(a, _gemm(A, B, ops.OUT_I32, flags=ops.FLAG_TILE128))
+
+
+@pytest.mark.parametrize("k", [384, 1152])
+def test_large_tile_plain_odd_k_steps(dev, k):
+    """The 256 x 256 kernel's plain form (4096 x 4096: one tile per CU) with an odd number of
+    128-wide k steps, so its last step runs outside the two-stage main loop; int32, fp32 and bf16
+    outputs against the generic 128 x 128 kernel, the int32 rows sampled against the oracle."""
+    from uwc_amd import ops
+    m = n = 4096
+    A, B = _rand(dev, k, m, k), _rand(dev, k + 1, n, k)
+    sx = torch.rand(m, device=dev) * 1e-2 + 1e-4
+    sw = torch.rand(n, device=dev) * 1e-3 + 1e-5
+    C = _gemm(A, B, ops.OUT_I32)
+    assert torch.equal(C, _gemm(A, B, ops.OUT_I32, flags=ops.FLAG_TILE128))
+    rows = np.r_[0:4, 2047:2051, m - 4:m]
+    assert np.array_equal(C.cpu().numpy()[rows], O.igemm(A.cpu().numpy()[rows], B.cpu().numpy()))
+    for mode in (ops.OUT_F32, ops.OUT_BF16):
+        Y = _gemm(A, B, mode, sx=sx, sw=sw)
+        Yr = _gemm(A, B, mode, flags=ops.FLAG_TILE128, sx=sx, sw=sw)
+        assert torch.equal(Y.view(torch.int16) if mode == ops.OUT_BF16 else Y.view(torch.int32),
+                           Yr.view(torch.int16) if mode == ops.OUT_BF16 else Yr.view(torch.int32))

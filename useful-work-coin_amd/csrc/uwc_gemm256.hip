@@ -736,7 +736,13 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
       int kt = 0;
       for (; kt + W_STAGES <= KT; kt += W_STAGES)
         static_for<W_STAGES>([&](auto stc) UWC_AI { step(NoFold{}, stc, kt + decltype(stc)::value, unused, unused); });
-      for (; kt < KT; kt++) step_rt(NoFold{}, kt, unused, unused);
+      // the last KT % W_STAGES steps: kt is a multiple of W_STAGES here, so step kt + s sits in
+      // stage s (a loop over step_rt instead made the compiler spill the DMA offsets, whose
+      // reloads then wait for every DMA in flight)
+      static_for<W_STAGES - 1>([&](auto sc) UWC_AI {
+        constexpr int s = decltype(sc)::value;
+        if (kt + s < KT) step(NoFold{}, sc, kt + s, unused, unused);
+      });
     }
 
     // A finished quarter (blocks (2h, nb), (2h + 1, nb)): stored at once, or, in the split
@@ -744,38 +750,92 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
     // writes its quarter to slot w (block i, register group j, lane l at 16 ((4 i + j) 64 + l)),
     // storer w + 4 reads it and stores it as wave (0, w). Two barriers per quarter: the slot is
     // written, the slot is read. The loaders never store an output.
+    // A quarter's two blocks through LDS, stored by rows. The slot holds blocks i = 0, 1 as
+    // 16-byte pieces: register group j (columns 8 j + 4 hh .. + 3) of the MFMA layout's lane
+    // hh 32 + rr (row rr) at piece (4 i + j) 64 + hh 32 + (rr ^ 2 (2 j + hh)). It is read back by
+    // rows: for store instruction jj, lane l takes row 8 jj + l / 8, columns 4 (l % 8) .. + 3, so
+    // each store writes 8 whole row segments of the block (the MFMA layout stored directly
+    // writes 32 rows x 16 bytes per instruction, and a launch's output burst then drains slower:
+    // 81.8 -> 77.6 us per nonce in the batched mining launch). The XOR spreads both the writes
+    // (16 consecutive rows) and the row reads (2 rows x 8 pieces) of 16 lanes over 16 distinct
+    // 16-byte bank groups.
+    auto put = [&](u8* slot, const v16i& a0, const v16i& a1) UWC_AI {
+      const int hh = lane >> 5, rr = lane & 31;
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const v16i& v = i ? a1 : a0;
+          *reinterpret_cast<v4i*>(slot + ((4 * i + j) * 64 + hh * 32 + (rr ^ (2 * (2 * j + hh)))) * 16) =
+              v4i{v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]};
+        }
+    };
+    // block 2 h + i of wave row swm (column half nb of wave column wn), from the slot
+    auto store_rows = [&](const u8* slot, int swm, int h, int nb, int i) UWC_AI {
+      if constexpr (OUT != OUT_NONE) {
+        constexpr int ES = OUT == OUT_BF16 ? 2 : 4;  // output element bytes
+        const int j = (lane & 7) >> 1, hh = lane & 1;
+        const int row0 = bm0 + swm * 128 + (2 * h + i) * 32, col = bn0 + wn * 64 + nb * 32 + 4 * (lane & 7);
+        u8* base = reinterpret_cast<u8*>(I.out) + ((long)row0 * p.ldc + col) * ES;
+        float4 sw{};
+        if constexpr (OUT != OUT_I32) sw = float4{p.b_scale[col], p.b_scale[col + 1], p.b_scale[col + 2], p.b_scale[col + 3]};
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) {
+          const int rr = 8 * jj + (lane >> 3);
+          const v4i x = *reinterpret_cast<const v4i*>(slot + ((4 * i + j) * 64 + hh * 32 + (rr ^ (2 * (2 * j + hh)))) * 16);
+          u8* dst = base + (long)rr * p.ldc * ES;
+          if constexpr (OUT == OUT_I32) {
+            *reinterpret_cast<v4i*>(dst) = x;
+          } else {
+            const float asc = p.a_scale[row0 + rr];
+            const float y0 = __fmul_rn(__fmul_rn((float)x[0], asc), sw.x);
+            const float y1 = __fmul_rn(__fmul_rn((float)x[1], asc), sw.y);
+            const float y2 = __fmul_rn(__fmul_rn((float)x[2], asc), sw.z);
+            const float y3 = __fmul_rn(__fmul_rn((float)x[3], asc), sw.w);
+            if constexpr (OUT == OUT_F32) {
+              *reinterpret_cast<float4*>(dst) = float4{y0, y1, y2, y3};
+            } else {
+              *reinterpret_cast<uint2*>(dst) =
+                  uint2{bf16_rne(y0) | (bf16_rne(y1) << 16), bf16_rne(y2) | (bf16_rne(y3) << 16)};
+            }
+          }
+        }
+      }
+    };
+
+    // A finished quarter (blocks (2h, nb), (2h + 1, nb)). Without SPLIT: with DENOISE the ring
+    // holds the corrections while the quarters finish, so the blocks are stored directly;
+    // otherwise through this wave's own 16 KiB of the idle ring (the caller's barrier ends the k
+    // loop's reads of it). In the split kernel the storers store everything, the loaders'
+    // quarters through a hand-off slot past the ring: loader w puts its quarter in slot w, storer
+    // w + 4 stores it as wave (0, w), then puts and stores its own through the same slot. Two
+    // barriers per quarter: the slot is written, the slot is done with. The loaders never store
+    // an output.
     auto quarter_done = [&](int h, int nb, const v16i& v0, const v16i& v1) UWC_AI {
       if constexpr (!SPLIT) {
-        store_block(lane, I.out, wm, wn, 2 * h, nb, v0);
-        store_block(lane, I.out, wm, wn, 2 * h + 1, nb, v1);
-      } else {
-        u8* slot = wsm + W_LDS + (wave & 3) * 8192;
-        if constexpr (loader) {
-#pragma unroll
-          for (int i = 0; i < 2; i++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-              const v16i& v = i ? v1 : v0;
-              *reinterpret_cast<v4i*>(slot + ((4 * i + j) * 64 + lane) * 16) =
-                  v4i{v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]};
-            }
-        } else {
+        if constexpr (DENOISE) {
           store_block(lane, I.out, wm, wn, 2 * h, nb, v0);
           store_block(lane, I.out, wm, wn, 2 * h + 1, nb, v1);
+        } else if constexpr (OUT != OUT_NONE) {
+          u8* slot = wsm + wave * 16384;
+          put(slot, v0, v1);
+          store_rows(slot, wm, h, nb, 0);
+          store_rows(slot, wm, h, nb, 1);
         }
+      } else {
+        static_assert(OUT == OUT_I32, "the split kernels store int32 outputs");
+        u8* slot = wsm + W_LDS + (wave & 3) * 8192;
+        if constexpr (loader) put(slot, v0, v1);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
         if constexpr (!loader) {
-#pragma unroll
-          for (int i = 0; i < 2; i++) {
-            v16i v;
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-              const v4i x = *reinterpret_cast<const v4i*>(slot + ((4 * i + j) * 64 + lane) * 16);
-              v[4 * j] = x[0], v[4 * j + 1] = x[1], v[4 * j + 2] = x[2], v[4 * j + 3] = x[3];
-            }
-            store_block(lane, I.out, wm - 1, wn, 2 * h + i, nb, v);
-          }
+          // the loader's quarter, then this wave's own through the same slot (a wave's LDS
+          // operations execute in order: the writes follow the reads they overwrite)
+          store_rows(slot, wm - 1, h, nb, 0);
+          store_rows(slot, wm - 1, h, nb, 1);
+          put(slot, v0, v1);
+          store_rows(slot, wm, h, nb, 0);
+          store_rows(slot, wm, h, nb, 1);
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
@@ -838,6 +898,10 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
         }
       }
     } else {
+      if constexpr (!SPLIT) {  // every wave is done reading the ring before it takes a slot of it
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+      }
 #pragma unroll
       for (int q = 0; q < 4; q++) quarter_done(q >> 1, q & 1, acc[2 * (q >> 1)][q & 1], acc[2 * (q >> 1) + 1][q & 1]);
     }
