@@ -12,7 +12,8 @@
 //     so the 32-row fragment reads are conflict-free; the swizzle is applied on the global side.
 //   * Two fragment sets: the reads of pass p + 1 go out before the MFMAs of pass p.
 //   * Transposed C (the B fragment is the MFMA's first operand): lane l holds row l & 31 of a
-//     32 x 32 block and 4 consecutive columns per register group, one 16-byte store each.
+//     32 x 32 block and 4 consecutive columns per register group; the epilogue turns pairs of
+//     blocks around through LDS so that each store instruction writes whole row segments.
 //   * int32 sums are exact, so any tiling and k order gives the same accumulators as the other
 //     GEMM kernels of this library.
 #include <type_traits>
@@ -234,37 +235,58 @@ __global__ void __launch_bounds__(P_THREADS) plain_gemm_kernel(PlainParams p) {
     });
   }
 
-  // epilogue: block (i, j) of the wave: lane holds row (lane & 31) and, in registers
-  // 4 g .. 4 g + 3, columns 8 g + 4 (lane >> 5) .. + 3
+  // epilogue: the wave's blocks, two at a time, through its own 8 KiB of the idle ring, stored by
+  // rows. In the MFMA layout lane hh 32 + rr holds row rr of a block and, in register group j,
+  // columns 8 j + 4 hh .. + 3; that piece goes to slot piece (4 b + j) 64 + hh 32 + (rr ^ 2 (2 j +
+  // hh)) for block b of the pair. Store instruction jj then has lane l take row 8 jj + l / 8,
+  // columns 4 (l % 8) .. + 3 of a block: 8 whole row segments per instruction instead of 32 rows
+  // of 16 bytes (the output burst at the end of a launch drains faster). The XOR keeps the 16
+  // lanes of each write (16 rows) and of each read (2 rows x 8 pieces) on distinct 16-byte bank
+  // groups.
   if constexpr (OUT != P_OUT_NONE) {
     constexpr int ES = OUT == P_OUT_BF16 ? 2 : 4;
-    const int lr = lane & 31, lc = 4 * (lane >> 5);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();  // every wave is done reading the ring
+    u8* slot = sm + wave * 8192;
+    const int hh = lane >> 5, rr = lane & 31;
+    const int rj = (lane & 7) >> 1, rh = lane & 1;  // the piece a row read takes
 #pragma unroll
     for (int i = 0; i < MB; i++) {
-      const int row = bm0 + wm * WM + i * 32 + lr;
-      float asc = 0.f;
-      if constexpr (OUT != P_OUT_I32) asc = p.a_scale[row];
-      u8* orow = reinterpret_cast<u8*>(p.out) + (long)row * p.ldc * ES;
 #pragma unroll
-      for (int j = 0; j < NB; j++) {
-        const v16i& v = acc[i][j];
+      for (int j0 = 0; j0 < NB; j0 += 2) {
 #pragma unroll
-        for (int g = 0; g < 4; g++) {
-          const int col = bn0 + wn * WN + j * 32 + 8 * g + lc;
-          u8* dst = orow + (long)col * ES;
-          if constexpr (OUT == P_OUT_I32) {
-            *reinterpret_cast<v4i*>(dst) = v4i{v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]};
-          } else {
-            const float4 sw = *reinterpret_cast<const float4*>(p.b_scale + col);
-            const float y0 = __fmul_rn(__fmul_rn((float)v[4 * g], asc), sw.x);
-            const float y1 = __fmul_rn(__fmul_rn((float)v[4 * g + 1], asc), sw.y);
-            const float y2 = __fmul_rn(__fmul_rn((float)v[4 * g + 2], asc), sw.z);
-            const float y3 = __fmul_rn(__fmul_rn((float)v[4 * g + 3], asc), sw.w);
-            if constexpr (OUT == P_OUT_F32) {
-              *reinterpret_cast<float4*>(dst) = float4{y0, y1, y2, y3};
+        for (int b = 0; b < 2; b++)
+#pragma unroll
+          for (int g = 0; g < 4; g++) {
+            const v16i& v = acc[i][j0 + b];
+            *reinterpret_cast<v4i*>(slot + ((4 * b + g) * 64 + hh * 32 + (rr ^ (2 * (2 * g + hh)))) * 16) =
+                v4i{v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]};
+          }
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+          const int row0 = bm0 + wm * WM + i * 32, col = bn0 + wn * WN + (j0 + b) * 32 + 4 * (lane & 7);
+          u8* base = reinterpret_cast<u8*>(p.out) + ((long)row0 * p.ldc + col) * ES;
+          float4 sw{};
+          if constexpr (OUT != P_OUT_I32) sw = *reinterpret_cast<const float4*>(p.b_scale + col);
+#pragma unroll
+          for (int jj = 0; jj < 4; jj++) {
+            const int r = 8 * jj + (lane >> 3);
+            const v4i x = *reinterpret_cast<const v4i*>(slot + ((4 * b + rj) * 64 + rh * 32 + (r ^ (2 * (2 * rj + rh)))) * 16);
+            u8* dst = base + (long)r * p.ldc * ES;
+            if constexpr (OUT == P_OUT_I32) {
+              *reinterpret_cast<v4i*>(dst) = x;
             } else {
-              *reinterpret_cast<uint2*>(dst) =
-                  uint2{p_bf16_rne(y0) | (p_bf16_rne(y1) << 16), p_bf16_rne(y2) | (p_bf16_rne(y3) << 16)};
+              const float asc = p.a_scale[row0 + r];
+              const float y0 = __fmul_rn(__fmul_rn((float)x[0], asc), sw.x);
+              const float y1 = __fmul_rn(__fmul_rn((float)x[1], asc), sw.y);
+              const float y2 = __fmul_rn(__fmul_rn((float)x[2], asc), sw.z);
+              const float y3 = __fmul_rn(__fmul_rn((float)x[3], asc), sw.w);
+              if constexpr (OUT == P_OUT_F32) {
+                *reinterpret_cast<float4*>(dst) = float4{y0, y1, y2, y3};
+              } else {
+                *reinterpret_cast<uint2*>(dst) =
+                    uint2{p_bf16_rne(y0) | (p_bf16_rne(y1) << 16), p_bf16_rne(y2) | (p_bf16_rne(y3) << 16)};
+              }
             }
           }
         }
