@@ -169,9 +169,12 @@ def test_qkv_post(dev, B, T, H, Hkv, hd, qknorm):
     assert Tp % 64 == 0
 
 
+@pytest.mark.parametrize("stored", [False, True])
 @pytest.mark.parametrize("B,T,H,Hkv,hd", [(1, 1, 1, 1, 32), (1, 12, 4, 2, 32), (2, 70, 4, 2, 64),
                                           (1, 300, 2, 1, 128), (1, 129, 16, 8, 128)])
-def test_attention(dev, B, T, H, Hkv, hd):
+def test_attention(dev, B, T, H, Hkv, hd, stored):
+    """Both forms of the kernel (exponentials recomputed per pass, or kept in the scratch of
+    uwc_attention_ws) against the oracle's attention, bit for bit."""
     from uwc_amd import detgpu
     rng = np.random.default_rng(T * 7 + hd)
     N = B * T
@@ -183,12 +186,32 @@ def test_attention(dev, B, T, H, Hkv, hd):
     vs = rng.uniform(1e-3, 3e-2, (N, Hkv, 1)).astype(np.float32)
     inv = S.inv_sqrt_hd(hd)
     o = detgpu.attention(_t(qq, dev), _t(qs, dev), _t(kq, dev), _t(ks, dev), _t(vq, dev), _t(vs, dev), B, T, H, Hkv,
-                         float(inv)).cpu().numpy()
+                         float(inv), stored_exp=stored).cpu().numpy()
     for b in range(B):
         sl = slice(b * T, (b + 1) * T)
         _, _, _, ref = S.attention(qq[sl].astype(np.int64), qs[sl], kq[sl].astype(np.int64), ks[sl],
                                    vq[sl].astype(np.int64), vs[sl], inv)
         np.testing.assert_array_equal(_u32(o[sl]), _u32(ref.transpose(1, 0, 2).reshape(T, H * hd)))
+
+
+@pytest.mark.parametrize("B,T,H,Hkv,hd", [(1, 2048, 16, 8, 128), (2, 1000, 4, 4, 64), (1, 777, 8, 2, 32)])
+def test_attention_stored_equals_recomputed(dev, B, T, H, Hkv, hd):
+    """The stored-exponentials form equals the recomputing one bit for bit at sizes the oracle
+    would take minutes for (the oracle comparison above covers both at small T)."""
+    from uwc_amd import detgpu
+    g = torch.Generator(device=dev)
+    g.manual_seed(T + hd)
+    N = B * T
+    qq = torch.randint(-127, 128, (N, H, hd), dtype=torch.int8, device=dev, generator=g)
+    kq = torch.randint(-127, 128, (N, Hkv, hd), dtype=torch.int8, device=dev, generator=g)
+    vq = torch.randint(-127, 128, (N, Hkv, hd), dtype=torch.int8, device=dev, generator=g)
+    qs = torch.rand((N, H, 1), device=dev, generator=g) * 3e-2 + 1e-3
+    ks = torch.rand((N, Hkv, 1), device=dev, generator=g) * 3e-2 + 1e-3
+    vs = torch.rand((N, Hkv, 1), device=dev, generator=g) * 3e-2 + 1e-3
+    inv = float(S.inv_sqrt_hd(hd))
+    a = detgpu.attention(qq, qs, kq, ks, vq, vs, B, T, H, Hkv, inv, stored_exp=False)
+    b = detgpu.attention(qq, qs, kq, ks, vq, vs, B, T, H, Hkv, inv, stored_exp=True)
+    assert torch.equal(a.view(torch.int32), b.view(torch.int32))
 
 
 def _fixture_model(name, dev):

@@ -32,6 +32,9 @@
 #include "uwc_rows.h"
 
 #define AT_PLEVELS 16383.0f
+// lambdas are always inlined: an out-of-line call would take the address of the register arrays
+// they capture (private memory)
+#define AT_AI __attribute__((always_inline))
 
 __device__ __forceinline__ v4i at_zero4() { return v4i{0, 0, 0, 0}; }
 
@@ -98,11 +101,23 @@ __device__ __forceinline__ float at_get(const float4& v, int i) {
   return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
 }
 
-template <int HD>
-__global__ void __launch_bounds__(256, 3) attention_kernel(const i8* __restrict__ qq, const float* __restrict__ qs,
+// Exp tiles of the stored form: wave block wq (queries 16 wq .. + 15) of a (sequence, head) owns
+// tiles 0 .. wq / 4 (its key tiles), the blocks' tiles back to back: block wq starts at tile
+// (a + 1)(2 a + b) for wq = 4 a + b, and a (sequence, head) holds at_tiles(Tp) of them.
+__host__ __device__ constexpr u64 at_tile0(u64 wq) { return (wq / 4 + 1) * (2 * (wq / 4) + wq % 4); }
+__host__ __device__ constexpr u64 at_tiles(u64 Tp) { return at_tile0(Tp / 16); }
+
+// ES (exp stored): sweep 2 writes every e_ij it computes to escr (one 4 KiB tile per wave and key
+// tile, 16 floats per lane as four float4 at lane and piece offsets), and sweeps 3 and 4 read them
+// back instead of recomputing the scores and det_exp (about two thirds of the VALU work per score
+// element), two tiles ahead. The same values go through the same operations, so both forms give
+// the same bits.
+template <int HD, bool ES>
+__global__ void __launch_bounds__(256, ES && HD == 128 ? 2 : 3) attention_kernel(const i8* __restrict__ qq, const float* __restrict__ qs,
                                                         const i8* __restrict__ kq, const float* __restrict__ ks,
                                                         const i8* __restrict__ vt, const float* __restrict__ vs, int T,
-                                                        int Tp, int H, int Hkv, float inv_sqrt, float* __restrict__ o) {
+                                                        int Tp, int H, int Hkv, float inv_sqrt, float* __restrict__ o,
+                                                        float* __restrict__ escr) {
   constexpr int NC = (HD + 63) / 64;  // 64-dim chunks of the score product
   constexpr int ND = HD / 16;         // 16-dim blocks of the output
   __shared__ __attribute__((aligned(16))) float at_slot[4][2][64];
@@ -129,6 +144,10 @@ __global__ void __launch_bounds__(256, 3) attention_kernel(const i8* __restrict_
   const int kmax = min(T, q0 + 16);  // keys any query of the wave sees
   const int nkt = (kmax + 63) / 64;
   const i8* kbase = kq + (size_t)hk * HD;
+  // stored form: this wave's exp tiles (tile kt at + 1024 kt floats, piece b at + 256 b)
+  float* ewave = nullptr;
+  if constexpr (ES)
+    ewave = escr + ((u64)(bseq * H + h) * at_tiles((u64)Tp) + at_tile0((u64)(q0 >> 4))) * 1024 + lane * 4;
 
   // integer scores of key tile kt: acc[b][i] = q_qi . k_j, j = 64 kt + 16 b + 4 g + i
   auto iscores = [&](int kt, v4i acc[4]) {
@@ -194,18 +213,72 @@ __global__ void __launch_bounds__(256, 3) attention_kernel(const i8* __restrict_
     scores(kt, S, skv, mask);
     double part = 0.0;
 #pragma unroll
-    for (int b = 0; b < 4; b++)
+    for (int b = 0; b < 4; b++) {
+      float e[4];
 #pragma unroll
-      for (int i = 0; i < 4; i++) part += at_fix41(at_exp(__fsub_rn(S[b][i], mx)));
+      for (int i = 0; i < 4; i++) {
+        e[i] = at_exp(__fsub_rn(S[b][i], mx));
+        part += at_fix41(e[i]);
+      }
+      if constexpr (ES) *reinterpret_cast<float4*>(ewave + kt * 1024 + b * 256) = float4{e[0], e[1], e[2], e[3]};
+    }
     dsum += (u64)part;
   });
   dsum = at_sum_groups(dsum);
   const float den = (float)ldexp((double)dsum, -41);
   const double rden = 1.0 / (double)den;
 
+  // stored form: tile loads for sweeps 3 and 4, and the V scales of a tile (lane's key
+  // 64 kt + lane, staged through the wave's LDS slot as at_stage_scales does)
+  auto eload = [&](int kt, float4 (&ev)[4]) AT_AI {
+#pragma unroll
+    for (int b = 0; b < 4; b++) ev[b] = *reinterpret_cast<const float4*>(ewave + kt * 1024 + b * 256);
+  };
+  auto vsload = [&](int kt) AT_AI { return vs[sc_base + (u32)min(kt * 64 + lane, T - 1) * (u32)Hkv]; };
+  auto vsstage = [&](float v, float4 out[4]) AT_AI {
+    sv_slot[lane] = v;
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int b = 0; b < 4; b++) out[b] = *reinterpret_cast<const float4*>(sv_slot + 16 * b + 4 * g);
+    __builtin_amdgcn_wave_barrier();
+  };
+  // over tiles 0 .. nkt - 1 with loads two tiles ahead: prefetch(kt, slot) loads tile kt into
+  // register set slot, body(kt, slot) uses it (slot is a compile-time 0 or 1)
+  auto pipelined = [&](auto prefetch, auto body) AT_AI {
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    if (nkt > 0) prefetch(0, S0{});
+    if (nkt > 1) prefetch(1, S1{});
+    for (int kt = 0; kt < nkt; kt += 2) {
+      body(kt, S0{});
+      if (kt + 2 < nkt) prefetch(kt + 2, S0{});
+      if (kt + 1 < nkt) {
+        body(kt + 1, S1{});
+        if (kt + 3 < nkt) prefetch(kt + 3, S1{});
+      }
+    }
+  };
+
   // sweep 3: max of the V-scaled probabilities
   float pm = 0.f;
-  sweep([&](int kt, auto mask) {
+  if constexpr (ES) {
+    float4 eb[2][4];
+    float vb[2];
+    pipelined(
+        [&](int kt, auto sl) AT_AI {
+          eload(kt, eb[decltype(sl)::value]);
+          vb[decltype(sl)::value] = vsload(kt);
+        },
+        [&](int kt, auto sl) AT_AI {
+          constexpr int L = decltype(sl)::value;
+          float4 svv[4];
+          vsstage(vb[L], svv);
+#pragma unroll
+          for (int b = 0; b < 4; b++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) pm = fmaxf(pm, __fmul_rn(at_div(at_get(eb[L][b], i), rden), at_get(svv[b], i)));
+        });
+  } else sweep([&](int kt, auto mask) {
     float S[4][4];
     float4 skv[4], svv[4];
     scores(kt, S, skv, mask);
@@ -227,19 +300,15 @@ __global__ void __launch_bounds__(256, 3) attention_kernel(const i8* __restrict_
 #pragma unroll
   for (int d = 0; d < ND; d++) ohi[d] = olo[d] = at_zero4();
   const i8* vbase = vt + (size_t)(bseq * Hkv + hk) * HD * Tp;
-  sweep([&](int kt, auto mask) {
-    float S[4][4];
-    float4 skv[4], svv[4];
-    scores(kt, S, skv, mask);
-    at_stage_scales(vs, sc_base, Hkv, kt * 64, T, sv_slot, lane, svv);
+  // P of one tile from its exp values e[b][i] and V scales, times the tile's V rows (vf[d])
+  auto pv_tile = [&](const float (&e)[4][4], const float4 (&svv)[4], const v4i (&vf)[ND]) AT_AI {
     v4i bhi, blo;
 #pragma unroll
     for (int b = 0; b < 4; b++) {
       u32 ph = 0, pl = 0;
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const float e = at_exp(__fsub_rn(S[b][i], mx));
-        const float pv = __fmul_rn(at_div(e, rden), at_get(svv[b], i));
+        const float pv = __fmul_rn(at_div(e[b][i], rden), at_get(svv[b], i));
         const int p = (int)fminf(fmaxf(rintf(at_div(pv, rsp)), 0.0f), AT_PLEVELS);
         ph |= (u32)(p >> 7) << (8 * i);
         pl |= (u32)(p & 127) << (8 * i);
@@ -249,10 +318,49 @@ __global__ void __launch_bounds__(256, 3) attention_kernel(const i8* __restrict_
     }
 #pragma unroll
     for (int d = 0; d < ND; d++) {
-      const v4i vf = *reinterpret_cast<const v4i*>(vbase + (u32)(16 * d + ql) * (u32)Tp + kt * 64 + 16 * g);
-      ohi[d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(vf, bhi, ohi[d], 0, 0, 0);
-      olo[d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(vf, blo, olo[d], 0, 0, 0);
+      ohi[d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(vf[d], bhi, ohi[d], 0, 0, 0);
+      olo[d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(vf[d], blo, olo[d], 0, 0, 0);
     }
+  };
+  auto vload = [&](int kt, v4i (&vf)[ND]) AT_AI {
+#pragma unroll
+    for (int d = 0; d < ND; d++)
+      vf[d] = *reinterpret_cast<const v4i*>(vbase + (u32)(16 * d + ql) * (u32)Tp + kt * 64 + 16 * g);
+  };
+  if constexpr (ES) {
+    float4 eb[2][4];
+    float vb[2];
+    pipelined(
+        [&](int kt, auto sl) AT_AI {
+          eload(kt, eb[decltype(sl)::value]);
+          vb[decltype(sl)::value] = vsload(kt);
+        },
+        [&](int kt, auto sl) AT_AI {
+          constexpr int L = decltype(sl)::value;
+          v4i vf[ND];
+          vload(kt, vf);  // issued first: its latency overlaps the staging and the quantization
+          float4 svv[4];
+          vsstage(vb[L], svv);
+          float e[4][4];
+#pragma unroll
+          for (int b = 0; b < 4; b++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) e[b][i] = at_get(eb[L][b], i);
+          pv_tile(e, svv, vf);
+        });
+  } else sweep([&](int kt, auto mask) {
+    float S[4][4];
+    float4 skv[4], svv[4];
+    scores(kt, S, skv, mask);
+    at_stage_scales(vs, sc_base, Hkv, kt * 64, T, sv_slot, lane, svv);
+    float e[4][4];
+#pragma unroll
+    for (int b = 0; b < 4; b++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) e[b][i] = at_exp(__fsub_rn(S[b][i], mx));
+    v4i vf[ND];
+    vload(kt, vf);
+    pv_tile(e, svv, vf);
   });
   if (qi >= T) return;
   // lane holds dims 16 d + 4 g + i of query qi
@@ -270,10 +378,15 @@ __global__ void __launch_bounds__(256, 3) attention_kernel(const i8* __restrict_
   }
 }
 
-extern "C" int uwc_attention(const int8_t* qq, const float* qs, const int8_t* kq, const float* ks, const int8_t* vt,
-                             const float* vs, int B, int T, int H, int Hkv, int hd, float inv_sqrt_hd, float* o,
-                             hipStream_t stream) {
-  const char* fn = "uwc_attention";
+extern "C" uint64_t uwc_attention_scratch_bytes(int B, int T, int H) {
+  if (B <= 0 || T <= 0 || H <= 0) return 0;
+  const u64 Tp = ((u64)T + 63) / 64 * 64;
+  return (u64)B * (u64)H * at_tiles(Tp) * 4096;
+}
+
+static int attention_go(const char* fn, const int8_t* qq, const float* qs, const int8_t* kq, const float* ks,
+                        const int8_t* vt, const float* vs, int B, int T, int H, int Hkv, int hd, float inv_sqrt_hd,
+                        float* o, float* escratch, uint64_t escratch_bytes, hipStream_t stream) {
   if (!qq || !qs || !kq || !ks || !vt || !vs || !o) return uwc_fail("%s: null arguments", fn);
   if (B < 0 || T <= 0 || T > 131072 || H <= 0 || Hkv <= 0 || H % Hkv)
     return uwc_fail("%s: bad B=%d T=%d H=%d Hkv=%d (T <= 131072)", fn, B, T, H, Hkv);
@@ -286,14 +399,37 @@ extern "C" int uwc_attention(const int8_t* qq, const float* qs, const int8_t* kq
     return uwc_fail("%s: B * T * H * hd must be below 2^31 (32-bit offsets)", fn);
   const int Tp = ((T + 63) / 64) * 64;
   const dim3 grid((unsigned)(Tp / 64), (unsigned)H, (unsigned)B);
-  if (hd == 32)
-    hipLaunchKernelGGL(attention_kernel<32>, grid, dim3(256), 0, stream, qq, qs, kq, ks, vt, vs, T, Tp, H, Hkv,
-                       inv_sqrt_hd, o);
-  else if (hd == 64)
-    hipLaunchKernelGGL(attention_kernel<64>, grid, dim3(256), 0, stream, qq, qs, kq, ks, vt, vs, T, Tp, H, Hkv,
-                       inv_sqrt_hd, o);
-  else
-    hipLaunchKernelGGL(attention_kernel<128>, grid, dim3(256), 0, stream, qq, qs, kq, ks, vt, vs, T, Tp, H, Hkv,
-                       inv_sqrt_hd, o);
+  if (escratch) {
+    if (escratch_bytes < uwc_attention_scratch_bytes(B, T, H))
+      return uwc_fail("%s: escratch holds %llu bytes, %llu needed", fn, (unsigned long long)escratch_bytes,
+                      (unsigned long long)uwc_attention_scratch_bytes(B, T, H));
+    if ((uintptr_t)escratch & 15) return uwc_fail("%s: escratch must be 16-byte aligned", fn);
+  }
+  auto go = [&](auto hdc, auto esc) {
+    hipLaunchKernelGGL((attention_kernel<decltype(hdc)::value, decltype(esc)::value>), grid, dim3(256), 0, stream, qq,
+                       qs, kq, ks, vt, vs, T, Tp, H, Hkv, inv_sqrt_hd, o, escratch);
+  };
+  auto go_hd = [&](auto esc) {
+    if (hd == 32) go(std::integral_constant<int, 32>{}, esc);
+    else if (hd == 64) go(std::integral_constant<int, 64>{}, esc);
+    else go(std::integral_constant<int, 128>{}, esc);
+  };
+  if (escratch) go_hd(std::true_type{});
+  else go_hd(std::false_type{});
   return uwc_launch_status(fn);
+}
+
+extern "C" int uwc_attention(const int8_t* qq, const float* qs, const int8_t* kq, const float* ks, const int8_t* vt,
+                             const float* vs, int B, int T, int H, int Hkv, int hd, float inv_sqrt_hd, float* o,
+                             hipStream_t stream) {
+  return attention_go("uwc_attention", qq, qs, kq, ks, vt, vs, B, T, H, Hkv, hd, inv_sqrt_hd, o, nullptr, 0, stream);
+}
+
+extern "C" int uwc_attention_ws(const int8_t* qq, const float* qs, const int8_t* kq, const float* ks,
+                                const int8_t* vt, const float* vs, int B, int T, int H, int Hkv, int hd,
+                                float inv_sqrt_hd, float* o, float* escratch, uint64_t escratch_bytes,
+                                hipStream_t stream) {
+  if (!escratch) return uwc_fail("uwc_attention_ws: null escratch");
+  return attention_go("uwc_attention_ws", qq, qs, kq, ks, vt, vs, B, T, H, Hkv, hd, inv_sqrt_hd, o, escratch,
+                      escratch_bytes, stream);
 }

@@ -52,6 +52,8 @@ SIGNATURES = {
     "uwc_vt_tokens": [i32],
     "uwc_v_transpose": [vp, i32, i32, i32, i32, vp, vp],
     "uwc_attention": [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, f32, vp, vp],
+    "uwc_attention_scratch_bytes": [i32, i32, i32],
+    "uwc_attention_ws": [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, f32, vp, vp, u64, vp],
     "uwc_swiglu_quant": [vp, vp, vp, i32, i32, i32, vp, vp, vp],
     "uwc_dequant_residual": [vp, vp, vp, vp, i32, i32, vp, vp],
     "uwc_embed_rows": [vp, i64, i32, vp, i32, vp, vp, vp],
@@ -60,7 +62,8 @@ SIGNATURES = {
     "uwc_det_elementwise": [i32, vp, vp, vp, i64, vp],
     "uwc_mfma_rate_probe": [i32, i32, vp, i64, vp],
 }
-_RESTYPE = {"uwc_last_error": ctypes.c_char_p, "uwc_header_sha": ctypes.c_char_p}
+_RESTYPE = {"uwc_last_error": ctypes.c_char_p, "uwc_header_sha": ctypes.c_char_p,
+            "uwc_attention_scratch_bytes": ctypes.c_uint64}
 
 _LIB = None
 

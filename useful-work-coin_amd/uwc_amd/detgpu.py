@@ -116,10 +116,30 @@ def qkv_post(acc, s1, sw, qnw, knw, cos, sin, T: int, H: int, Hkv: int, eps: flo
     return qkv_post_vt(acc, s1, sw, qnw, knw, cos, sin, T, H, Hkv, eps, qknorm)[:6]
 
 
-def attention(qq, qs, kq, ks, vq, vs, B: int, T: int, H: int, Hkv: int, inv_sqrt_hd_f32: float, vt=None):
+# The exponentials scratch of the stored-exp attention: one device buffer per device, grown to the
+# largest call so far and reused (a 28-layer forward allocates it once). Calls whose scratch would
+# exceed ATTN_SCRATCH_MAX bytes recompute the exponentials instead.
+ATTN_SCRATCH_MAX = 16 << 30
+_ESCRATCH: dict = {}
+
+
+def attention_scratch(nbytes: int, device) -> torch.Tensor:
+    """The cached exponentials scratch of at least nbytes on device (float32, 16-byte aligned)."""
+    key = str(device)
+    buf = _ESCRATCH.get(key)
+    if buf is None or buf.numel() * 4 < nbytes:
+        _ESCRATCH.pop(key, None)
+        buf = _ESCRATCH[key] = torch.empty((nbytes + 3) // 4, dtype=F32, device=device)
+    return buf
+
+
+def attention(qq, qs, kq, ks, vq, vs, B: int, T: int, H: int, Hkv: int, inv_sqrt_hd_f32: float, vt=None,
+              stored_exp=None):
     """detrt's attention from quantized q, k, v: qq (N, H, hd), kq and vq (N, Hkv, hd) int8, qs
     (N, H, 1), ks and vs (N, Hkv, 1). Returns o as (N, H*hd) float32 (detgpu/kernels.py:731-770).
-    vt (from qkv_post_vt) skips the transpose of vq."""
+    vt (from qkv_post_vt) skips the transpose of vq. stored_exp: keep the softmax exponentials in
+    a device scratch between the kernel's passes (uwc_attention_ws) instead of recomputing them;
+    None takes it when the scratch is at most ATTN_SCRATCH_MAX bytes. Either way the same bits."""
     N, _, hd = qq.shape
     if N != B * T or kq.shape != (N, Hkv, hd) or vq.shape != (N, Hkv, hd):
         raise AssertionError("attention: shapes (B*T, H, hd) / (B*T, Hkv, hd)")
@@ -131,8 +151,16 @@ def attention(qq, qs, kq, ks, vq, vs, B: int, T: int, H: int, Hkv: int, inv_sqrt
         vt = torch.zeros((B, Hkv, hd, vt_tokens(T)), dtype=torch.int8, device=qq.device)
         _lib.call("uwc_v_transpose", vq.data_ptr(), B, T, Hkv, hd, vt.data_ptr(), _stream())
     o = torch.empty((N, H * hd), dtype=F32, device=qq.device)
-    _lib.call("uwc_attention", qq.data_ptr(), qs.data_ptr(), kq.data_ptr(), ks.data_ptr(), vt.data_ptr(), vs.data_ptr(),
-              B, T, H, Hkv, hd, float(np.float32(inv_sqrt_hd_f32)), o.data_ptr(), _stream())
+    nbytes = int(_lib.lib().uwc_attention_scratch_bytes(B, T, H))
+    if stored_exp is None:
+        stored_exp = 0 < nbytes <= ATTN_SCRATCH_MAX
+    args = (qq.data_ptr(), qs.data_ptr(), kq.data_ptr(), ks.data_ptr(), vt.data_ptr(), vs.data_ptr(), B, T, H, Hkv,
+            hd, float(np.float32(inv_sqrt_hd_f32)), o.data_ptr())
+    if stored_exp and nbytes > 0:
+        es = attention_scratch(nbytes, qq.device)
+        _lib.call("uwc_attention_ws", *args, es.data_ptr(), es.numel() * 4, _stream())
+    else:
+        _lib.call("uwc_attention", *args, _stream())
     return o
 
 
