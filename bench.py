@@ -749,7 +749,7 @@ def summarize_e2e_trace(stats_csv, out_path, cmd):
         f.write(f"command: {cmd}\n\n")
         f.write(f"{'kernel':58s} {'calls':>6s} {'avg_us':>9s} {'ms/fwd':>8s} {'share':>6s}\n")
         for r in rows:
-            name = re.sub(r"\(.*", "", r["Name"])[:58]
+            name = re.sub(r"\(.*", "", r["Name"].replace("(anonymous namespace)::", ""))[:58]
             f.write(f"{name:58s} {int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:9.2f} "
                     f"{float(r['TotalDurationNs']) / 3e6:8.2f} {float(r['Percentage']):5.1f}%\n")
         f.write("\nPer forward: 28 x (rmsnorm_kernel<true> x 2, noisy_gemm256_kernel<false, false, 1> x 4 (qkv, o, gu, "
