@@ -753,7 +753,7 @@ def summarize_e2e_trace(stats_csv, out_path, cmd):
             f.write(f"{name:58s} {int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:9.2f} "
                     f"{float(r['TotalDurationNs']) / 3e6:8.2f} {float(r['Percentage']):5.1f}%\n")
         f.write("\nPer forward: 28 x (rmsnorm_kernel<true> x 2, noisy_gemm256_kernel<false, false, 1> x 4 (qkv, o, gu, "
-                "down), qkv_post_kernel, attention_kernel<128>, quant_act_wave_kernel, dequant_residual x 2, "
+                "down), qkv_post_kernel, attention_kernel<128, true> (exponentials stored), quant_act_group_kernel, dequant_residual x 2, "
                 "swiglu_quant, sha_* for the layer's stage-output root), then rmsnorm_quant + the lm_head GEMM "
                 "(256x256 tiles + a 128-wide column tail) + the logits' Merkle root; ms/fwd = total / 3.\n")
     print(open(out_path).read())
