@@ -323,10 +323,13 @@ def test_sha_row_roots_and_trace_roots(dev):
     from uwc_amd import detgpu
     rng = np.random.default_rng(11)
     # row roots for lengths around the 1 KiB block and message-padding boundaries
-    for w in (1, 13, 14, 15, 16, 17, 255, 256, 257, 300, 512, 2048, 2049, 6144):
-        rows = rng.integers(-2**31, 2**31 - 1, (5, w), dtype=np.int64).astype(np.int32)
+    # (up to 64 blocks per row: a quad per row, 16 rows per workgroup; 65 and more: a thread per
+    # row), with row counts that leave a workgroup partly empty
+    for w, nr in ((1, 5), (13, 5), (14, 5), (15, 5), (16, 5), (17, 5), (255, 5), (256, 5), (257, 5), (300, 5),
+                  (512, 5), (2048, 37), (2049, 5), (6144, 17), (16384, 3), (16385, 3), (40000, 2)):
+        rows = rng.integers(-2**31, 2**31 - 1, (nr, w), dtype=np.int64).astype(np.int32)
         got = detgpu.digest_bytes(detgpu.row_roots(_t(rows, dev)))
-        for i in range(5):
+        for i in range(nr):
             assert bytes(got[i]) == S.row_root(rows[i]), (w, i)
     # stage-output roots for several tree sizes
     for T in (1, 2, 3, 5, 8, 12, 33, 512, 513, 700, 1100, 2048):  # > 512: the two-phase tree

@@ -90,38 +90,51 @@ __device__ __forceinline__ void sha_node(const u32* l, const u32* r, u32 out[8])
   sha_short<16>(1u, z, out);
 }
 
+// The raw data words 16 b .. 16 b + 15 of a block of n words at p (zero past n).
+template <bool VEC>
+__device__ __forceinline__ void sha_load16(const u32* __restrict__ p, int n, int b, u32 d[16]) {
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const int j0 = 16 * b + 4 * q;
+    if (VEC && j0 + 4 <= n) {
+      const uint4 v = *reinterpret_cast<const uint4*>(p + j0);
+      d[4 * q] = v.x; d[4 * q + 1] = v.y; d[4 * q + 2] = v.z; d[4 * q + 3] = v.w;
+    } else {
+#pragma unroll
+      for (int t = 0; t < 4; t++) d[4 * q + t] = j0 + t < n ? p[j0 + t] : 0u;
+    }
+  }
+}
+
 // H(0x00 || block) of n little-endian data words at p (n <= 256); VEC: p is 16-byte aligned.
+// The next 64-byte piece's words are loaded before the current one is compressed, so the load
+// latency hides behind a compression (one wave per SIMD runs these chains: the leaves of a
+// 8192 x 2048 stage output are 65,536 chains).
 template <bool VEC>
 __device__ void sha_block_leaf(const u32* __restrict__ p, int n, u32 out[8]) {
   const int nb = (4 * n + 1 + 1 + 8 + 63) / 64;
   sha_init(out);
   u32 prev = 0;  // the 0x00 prefix
+  u32 d[16];
+  sha_load16<VEC>(p, n, 0, d);
   for (int b = 0; b < nb; b++) {
+    u32 nxt[16];
+    if (b + 1 < nb) sha_load16<VEC>(p, n, b + 1, nxt);
     u32 w[16];
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-      const int j0 = 16 * b + 4 * q;
-      u32 d[4];
-      if (VEC && j0 + 4 <= n) {
-        const uint4 v = *reinterpret_cast<const uint4*>(p + j0);
-        d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
-      } else {
-#pragma unroll
-        for (int t = 0; t < 4; t++) d[t] = j0 + t < n ? p[j0 + t] : 0u;
-      }
-#pragma unroll
-      for (int t = 0; t < 4; t++) {
-        const int j = j0 + t;
-        u32 cur;
-        if (j < n) cur = __builtin_bswap32(d[t]) >> 8;
-        else if (j == n) cur = 0x00800000u;
-        else cur = 0;
-        w[4 * q + t] = (j <= n ? (prev << 24) : 0u) | cur;
-        prev = j < n ? __builtin_bswap32(d[t]) : 0u;
-      }
+    for (int t = 0; t < 16; t++) {
+      const int j = 16 * b + t;
+      u32 cur;
+      if (j < n) cur = __builtin_bswap32(d[t]) >> 8;
+      else if (j == n) cur = 0x00800000u;
+      else cur = 0;
+      w[t] = (j <= n ? (prev << 24) : 0u) | cur;
+      prev = j < n ? __builtin_bswap32(d[t]) : 0u;
     }
     if (b == nb - 1) w[15] = (u32)((4 * n + 1) * 8);
     sha_compress(out, w);
+#pragma unroll
+    for (int t = 0; t < 16; t++) d[t] = nxt[t];
   }
 }
 
@@ -165,6 +178,76 @@ __global__ void sha_row_leaf_kernel(u32* __restrict__ leaves, long nrows, int nb
     }
     n = half + (n & 1);
   }
+  u32 root[8];
+#pragma unroll
+  for (int k = 0; k < 8; k++) root[k] = lv[k];
+  if (roots) {
+#pragma unroll
+    for (int k = 0; k < 8; k++) roots[r * 8 + k] = root[k];
+  }
+  if (out) {
+    u32 idx = base + (u32)r;
+    if (mod) idx %= mod;
+    u32 z[10];
+    z[0] = tag;
+    z[1] = __builtin_bswap32(idx);  // u32 little-endian bytes as a big-endian word
+#pragma unroll
+    for (int k = 0; k < 8; k++) z[2 + k] = root[k];
+    u32 h[8];
+    sha_short<10>(0u, z, h);
+#pragma unroll
+    for (int k = 0; k < 8; k++) out[r * 8 + k] = h[k];
+  }
+}
+
+// The same with one quad per row (16 rows per 64-thread workgroup) for rows of at most
+// SHA_QUAD_MAXBLK blocks: the row's block leaves are copied to LDS and each level of the row tree
+// is computed by the quad's lanes, node i by lane i % 4. A lane reads both children of its node
+// inside sha_node before any lane of the wave writes a parent (the lanes issue the same
+// instructions in order, and a wave's LDS operations complete in order); a level's parent i
+// overwrites child slot i, which only parents <= i / 2 of earlier iterations read. The chain per
+// row is then log2 of the block count in node pairs instead of the block count, and a wave holds
+// 16 rows instead of 64 (4x the waves for the 8192 rows of a stage output).
+#define SHA_QUAD_MAXBLK 64
+#define SHA_QUAD_ROWS 16
+__global__ void __launch_bounds__(64) sha_row_leaf_quad_kernel(const u32* __restrict__ leaves, long nrows, int nblk,
+                                                               u32 tag, u32 base, u32 mod, u32* __restrict__ roots,
+                                                               u32* __restrict__ out) {
+  __shared__ u32 lds[SHA_QUAD_ROWS * SHA_QUAD_MAXBLK * 8];
+  const int q = threadIdx.x & 3, rl = threadIdx.x >> 2;
+  const long r = (long)blockIdx.x * SHA_QUAD_ROWS + rl;
+  const bool live = r < nrows;  // no early return: the lanes of a quad stay together
+  u32* lv = lds + rl * SHA_QUAD_MAXBLK * 8;
+  if (live)
+    for (int w = q; w < nblk * 8; w += 4) lv[w] = leaves[r * nblk * 8 + w];
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's LDS writes are done
+  __builtin_amdgcn_wave_barrier();
+  int n = nblk;
+  while (n > 1) {
+    const int half = n >> 1;
+    for (int i0 = 0; i0 < half; i0 += 4) {
+      const int i = i0 + q;
+      u32 h[8];
+      if (live && i < half) {
+        sha_node(lv + 16 * i, lv + 16 * i + 8, h);
+#pragma unroll
+        for (int k = 0; k < 8; k++) lv[8 * i + k] = h[k];
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_wave_barrier();
+    }
+    if (n & 1) {  // the odd last node moves up: words q and q + 4 by lane q
+      u32 c0 = 0, c1 = 0;
+      if (live) { c0 = lv[8 * (n - 1) + q]; c1 = lv[8 * (n - 1) + 4 + q]; }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_wave_barrier();
+      if (live) { lv[8 * half + q] = c0; lv[8 * half + 4 + q] = c1; }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_wave_barrier();
+    }
+    n = half + (n & 1);
+  }
+  if (!live || q != 0) return;
   u32 root[8];
 #pragma unroll
   for (int k = 0; k < 8; k++) root[k] = lv[k];
@@ -267,8 +350,12 @@ extern "C" int uwc_sha_row_leaves(const uint32_t* rows, int64_t nrows, int row_w
     hipLaunchKernelGGL(sha_block_leaves_kernel<false>, grid, dim3(128), 0, stream, rows, (long)nrows, row_words, nblk, scratch);
   int st = uwc_launch_status("sha_block_leaves");
   if (st) return st;
-  hipLaunchKernelGGL(sha_row_leaf_kernel, dim3((unsigned)((nrows + 63) / 64)), dim3(64), 0, stream, scratch, (long)nrows,
-                     nblk, tag, index_base, index_mod, row_roots, leaves_out);
+  if (nblk <= SHA_QUAD_MAXBLK)
+    hipLaunchKernelGGL(sha_row_leaf_quad_kernel, dim3((unsigned)((nrows + SHA_QUAD_ROWS - 1) / SHA_QUAD_ROWS)), dim3(64),
+                       0, stream, scratch, (long)nrows, nblk, tag, index_base, index_mod, row_roots, leaves_out);
+  else
+    hipLaunchKernelGGL(sha_row_leaf_kernel, dim3((unsigned)((nrows + 63) / 64)), dim3(64), 0, stream, scratch,
+                       (long)nrows, nblk, tag, index_base, index_mod, row_roots, leaves_out);
   return uwc_launch_status("sha_row_leaf");
 }
 
