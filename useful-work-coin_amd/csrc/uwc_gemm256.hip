@@ -756,7 +756,7 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
     // rows: for store instruction jj, lane l takes row 8 jj + l / 8, columns 4 (l % 8) .. + 3, so
     // each store writes 8 whole row segments of the block (the MFMA layout stored directly
     // writes 32 rows x 16 bytes per instruction, and a launch's output burst then drains slower:
-    // 81.8 -> 77.6 us per nonce in the batched mining launch). The XOR spreads both the writes
+    // 77.9 -> 75.9 us per nonce in the batched mining launch). The XOR spreads both the writes
     // (16 consecutive rows) and the row reads (2 rows x 8 pieces) of 16 lanes over 16 distinct
     // 16-byte bank groups.
     auto put = [&](u8* slot, const v16i& a0, const v16i& a1) UWC_AI {
