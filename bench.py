@@ -830,10 +830,11 @@ def _summary_value(path, key):
     return None
 
 
-def read_traffic():
-    """traffic_bytes_per_launch from the committed FETCH_SIZE / WRITE_SIZE summary, or None."""
-    v = _summary_value(TRAFFIC_FILE, "traffic_bytes_per_launch")
-    return None if v is None else int(v)
+def read_traffic(nonces_per_launch):
+    """HBM bytes of one launch of nonces_per_launch nonces: the committed FETCH_SIZE / WRITE_SIZE
+    summary's bytes per nonce times the launch's nonces, or None."""
+    v = _summary_value(TRAFFIC_FILE, "traffic_bytes_per_nonce")
+    return None if v is None else int(v * nonces_per_launch)
 
 
 COUNTER_FILE = os.path.join(ROOT, "profiles", "noisy_gemm256_mining_4096_counters.txt")
@@ -855,8 +856,9 @@ def main():
     ap.add_argument("--rank", type=int, default=64)
     ap.add_argument("--distinct", type=int, default=64, help="distinct resident A matrices cycled over")
     ap.add_argument("--out-buffers", type=int, default=8, help="distinct int32 outputs rotated through the sweep")
-    ap.add_argument("--group", type=int, default=8, help="nonces per batched commitment / noise launch")
-    ap.add_argument("--gemm-group", type=int, default=8, help="nonces per batched GEMM launch")
+    ap.add_argument("--group", type=int, default=None,
+                    help="nonces per batched commitment / noise launch (default: forward_many's, equal groups of <= 16)")
+    ap.add_argument("--gemm-group", type=int, default=None, help="nonces per batched GEMM launch (default: the group)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--cpu-max-nonces", type=int, default=4)
     ap.add_argument("--mine-attempts", type=int, default=16, help="noise_mine attempts at the miner's shape")
@@ -907,6 +909,10 @@ def main():
     import oracle as O
     from uwc_amd import ops
 
+    if args.group is None:  # forward_many's own choice for a sweep of args.steps nonces
+        args.group = ops.sweep_group(args.steps)
+    if args.gemm_group is None:
+        args.gemm_group = min(args.group, ops.GEMM_GROUP)
     if args.traffic_probe:
         traffic_probe(args, torch, ops, O, np)
         return
@@ -945,9 +951,10 @@ def main():
                    "m": m, "n": n, "k": k, "r": r, "noise": "reference rules (E in [-32,31], +-1 pairs)"},
         "mfma_sustained_tops": ceiling,
         "roofline": {"bound": "mfma", "achieved": round(res["kern_tops"], 2), "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
-                     "frac": round(res["kern_tops"] / PEAK_INT8_TOPS, 4), "traffic": read_traffic(),
+                     "frac": round(res["kern_tops"] / PEAK_INT8_TOPS, 4), "traffic": read_traffic(res["per_launch"]),
                      "traffic_source": "profiles/noisy_gemm256_mining_4096_traffic.txt (rocprofv3 FETCH_SIZE + "
-                                       "WRITE_SIZE passes over bench.py --traffic-probe, copy-calibrated)",
+                                       "WRITE_SIZE passes over bench.py --traffic-probe, copy-calibrated; bytes per "
+                                       "nonce x nonces per launch)",
                      "mfma_busy_frac": read_mfma_busy(),
                      "mfma_busy_source": "profiles/noisy_gemm256_mining_4096_counters.txt (rocprofv3 "
                                          "SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 XCDs x 1024 SIMDs))",
