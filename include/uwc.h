@@ -83,7 +83,7 @@ int uwc_noisy_gemm(const int8_t* A, const int8_t* B, int m, int n, int k, int r,
  * out[i], ..., tile_dump[i]). A, corrA, corrB, maxabs, key, wins, out and tile_dump are HOST
  * arrays of `count` device pointers (corrA/corrB/maxabs may be NULL without UWC_FLAG_DENOISE, key
  * without UWC_FLAG_HASH, wins and tile_dump entirely). With HASH | DENOISE, UWC_OUT_I32, m, n % 256 == 0 and
- * count >= 2 the items run up to 16 per launch on the same tiles, the output stores of one item draining
+ * count >= 2 the items run up to 32 per launch on the same tiles, the output stores of one item draining
  * while the next computes; otherwise one launch per item. The reference mines one nonce per
  * ops.gemm call (ops.py:185-198 from MinedWeight._forward, ops.py:339-347); this form serves a
  * sweep of nonces whose operands are all prepared up front.
@@ -115,7 +115,7 @@ int uwc_b3_root_and_seed(const uint8_t* data, uint64_t nbytes, const uint32_t* k
                          const uint32_t* salt, uint32_t dim, uint32_t* root_out, uint32_t* seed_out,
                          uint32_t* scratch, uint64_t scratch_words, hipStream_t stream);
 
-/* uwc_b3_root_and_seed over `count` (1..16) inputs of nbytes each, in one set of launches:
+/* uwc_b3_root_and_seed over `count` (1..32) inputs of nbytes each, in one set of launches:
  * data, root_out and seed_out are HOST arrays of `count` device pointers (root_out / seed_out
  * may be NULL arrays; their entries may not be NULL). Item i uses scratch words
  * [i * s, (i + 1) * s) with s = uwc_b3_scratch_words(nbytes). Results equal `count` separate
@@ -158,7 +158,7 @@ int uwc_noise_perm(uint32_t* out, uint32_t k, uint32_t r, const uint32_t* label,
 int uwc_nonce_noise(int8_t* E, int rows, int r, uint32_t* P, int k, int8_t* St, int8_t* SpT, const uint32_t* label,
                     const uint32_t* key, int32_t* zero0, int n0, int32_t* zero1, int n1, hipStream_t stream);
 
-/* uwc_nonce_noise for `count` (1..16) nonces in one launch: E, P, St, SpT, key, zero0, zero1 are
+/* uwc_nonce_noise for `count` (1..32) nonces in one launch: E, P, St, SpT, key, zero0, zero1 are
  * HOST arrays of `count` device pointers (St, SpT, zero0, zero1 may be NULL arrays; entries of a
  * given array may not be NULL). Same label for every item. Results equal `count` separate calls.
  * Batches the per-nonce noise of ops.py:328-336 over a sweep of nonces. */
@@ -211,7 +211,7 @@ int uwc_side_project(const int8_t* A, int m, const int8_t* EA, const int8_t* SpA
                      int8_t* corrA, int corr_a_off, int ecopy_off, const int8_t* Bp, int n, const int8_t* StA,
                      int8_t* corrB, int corr_b_off, int k, int r, int32_t* maxabs, int lmax, hipStream_t stream);
 
-/* uwc_side_project for `count` (1..16) nonces sharing the block side (StB, Bp) in one launch:
+/* uwc_side_project for `count` (1..32) nonces sharing the block side (StB, Bp) in one launch:
  * item i as uwc_side_project(A[i], m, EA[i], SpA[i], ApEA[i], StB, corrA[i], corr_a_off, ecopy_off,
  * Bp, n, StA[i], corrB[i], corr_b_off, k, r, maxabs[i], lmax). A, EA, SpA, ApEA, corrA, StA, corrB
  * and maxabs are HOST arrays of `count` device pointers. m % 128 == 0, n % 128 == 0,

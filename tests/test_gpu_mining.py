@@ -454,7 +454,8 @@ def test_forward_many_grouped_equals_forward(dev, group, n_items):
     assert set(w.winners(m)) == ref[-1][1]
 
 
-@pytest.mark.parametrize("count,m,n,k,out_mode", [(3, 512, 512, 1024, 1), (17, 256, 512, 512, 1), (2, 256, 256, 1024, 2)])
+@pytest.mark.parametrize("count,m,n,k,out_mode", [(3, 512, 512, 1024, 1), (17, 256, 512, 512, 1), (33, 256, 256, 512, 1),
+                                                   (2, 256, 256, 1024, 2)])
 def test_gemm_many_equals_single_calls(dev, count, m, n, k, out_mode):
     """gemm_many (hashed, denoised GEMMs sharing B: the split-role batched kernel for int32 outputs,
     one launch per item otherwise) gives every item's output and winner set exactly as its own

@@ -153,7 +153,7 @@ __device__ __forceinline__ void quad_level_reduce(u32* cvs, int count, u32 k_lo,
 
 // Inputs of a batch of equal-size commitments (blockIdx.y = item): one launch commits several
 // operands at once.
-#define B3_MAXB 16
+#define B3_MAXB 32
 struct B3In {
   const u8* data[B3_MAXB];
 };

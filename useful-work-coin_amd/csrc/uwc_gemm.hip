@@ -462,7 +462,7 @@ int uwc_noisy_gemm256_many(int count, const int8_t* const* A, const int8_t* B, i
                            int lmax, const uint32_t* const* key, const uint32_t* target, uint32_t* const* wins,
                            int max_wins, void* const* out, uint32_t* const* tile_dump, hipStream_t stream);
 
-#define GEMM_MANY_MAX 16  // items per split launch (the kernel's item table)
+#define GEMM_MANY_MAX 32  // items per split launch (the kernel's item table)
 
 extern "C" int uwc_noisy_gemm_many(int count, const int8_t* const* A, const int8_t* B, int m, int n, int k, int r,
                                    const int8_t* const* corrA, const int8_t* const* corrB,

@@ -81,7 +81,7 @@ static_assert(W_LDS + W_LDS_HANDOFF <= 160 * 1024, "LDS exceeds 160 KiB (gfx950 
 // One item of a launch: a nonce's operand, corrections, seed, win records and output. Every item
 // shares B, the shape, the target and the scales; a launch runs its items one after another on
 // the same tiles.
-#define G256_MAXB 16
+#define G256_MAXB 32
 struct Gemm256Item {
   const i8* A;
   const i8* corrA;

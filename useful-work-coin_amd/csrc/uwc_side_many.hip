@@ -29,7 +29,7 @@
 #define SM_WAVES 8                       // compute waves (16 rows each)
 #define SM_PROD 4                        // producer (DMA) waves
 #define SM_THREADS (64 * (SM_WAVES + SM_PROD))
-#define SM_MAXB 16
+#define SM_MAXB 32
 
 struct SideManyItem {
   const i8* A;

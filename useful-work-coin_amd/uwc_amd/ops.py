@@ -148,7 +148,7 @@ def _ptrs(ts) -> "ctypes.Array | None":
     return (ctypes.c_void_p * len(ts))(*[t.data_ptr() for t in ts])
 
 
-MAX_BATCH = 16  # items per batched commitment / noise launch (the C-ABI's limit)
+MAX_BATCH = 32  # items per batched commitment / noise launch (the C-ABI's limit)
 
 
 def b3_root_and_seed_many(datas, key: torch.Tensor, *, prefix=None, salt=None, dim: int = 0, root_outs=None,
@@ -335,7 +335,7 @@ def gemm_many(As, B, *, r=128, flags=0, corrAs=None, corrBs=None, maxabss=None, 
               max_wins=0, a_scale=None, b_scale=None, outs=None, out_mode=OUT_NONE, dumps=None):
     """gemm() of several operands As[i] against one B, item i with its own corrections, maxabs,
     seed, win buffer, output and optional tile dump. With FLAG_HASH | FLAG_DENOISE, OUT_I32 and
-    m, n % 256 == 0 the items share launches (up to 16 per launch, output stores overlapping the
+    m, n % 256 == 0 the items share launches (up to 32 per launch, output stores overlapping the
     next item); otherwise one launch per item. Results equal separate gemm() calls."""
     count = len(As)
     if count == 0:
@@ -373,16 +373,16 @@ def igemm_i32(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None)
 _WORKSPACE: dict = {}
 _SWEEP_SYNC: dict = {}
 # nonces per batched commitment / noise launch and per batched GEMM launch in
-# MinedWeight.forward_many: at most SWEEP_GROUP, the sweep split into equal groups (measured on a
-# warmed-up box, 4096^3 r = 64: 0.0966 ms per nonce at 16 against 0.1007 at 8 over 256 nonces, and
-# 0.1056 at 10 against 0.1068 at 16 + 4 over 20)
-SWEEP_GROUP = 16
-GEMM_GROUP = 16
+# MinedWeight.forward_many: at most SWEEP_GROUP, the sweep split into equal groups (measured on
+# warmed-up boxes, 4096^3 r = 64, 256 nonces: 0.1007 ms per nonce at 8, 0.0966-0.0984 at 16,
+# 0.0973 at 24 and 32; 20 nonces: 0.1068 as one group, 0.1072 as 2 x 10, 0.1081 as 16 + 4)
+SWEEP_GROUP = 32
+GEMM_GROUP = 32
 
 
 def sweep_group(n_items: int, most: int = SWEEP_GROUP) -> int:
     """The group size forward_many takes for n_items nonces: the fewest groups of at most `most`,
-    as equal as possible (20 nonces: 2 x 10, 256: 16 x 16)."""
+    as equal as possible (20 nonces: one group, 40: 2 x 20, 256: 8 x 32)."""
     ngroups = -(-n_items // most)
     return -(-n_items // ngroups)
 
