@@ -32,7 +32,9 @@
 //     digests its own tile.
 //   * Denoise in four passes over quarters of the wave's block (a 32-register Horner
 //     accumulator), the corrections streamed through the same ring (or, when they fit, loaded
-//     into it before the digest).
+//     into it before the digest). The split kernel, when the corrections fill the ring exactly,
+//     goes stage by stage instead (each stage's product shifted by its limb), so that stage 0 is
+//     free for the next nonce's first k step while stage 1's MFMAs and the output hand-off run.
 //   * SPLIT (the batched form): several nonces per launch on the same tiles; waves 0-3 issue the
 //     DMA, waves 4-7 store every output (the others' through an LDS hand-off), so one nonce's
 //     stores drain while the next computes (see the kernel).
@@ -397,6 +399,18 @@ __device__ __forceinline__ void step_mma_quarter(v16i tmp[2], const FragBase& fb
   }
 }
 
+// a -= t << sh element by element (a vector shift by a scalar count would splat the count into
+// a vector of registers), pinned where it stands: otherwise the subtraction is sunk to a's next
+// use and t's registers stay live until then
+__device__ __forceinline__ void sub_shl(v16i& a, const v16i& t, int sh) {
+#pragma unroll
+  for (int e = 0; e < 16; e++) {
+    int x = a[e] - (t[e] << sh);
+    asm volatile("" : "+v"(x));
+    a[e] = x;
+  }
+}
+
 __device__ __forceinline__ u32 rotl13(u32 x) { return __builtin_amdgcn_alignbit(x, x, 19); }
 
 // Lane-permuted copy of x (DPP control CTRL). bound_ctrl with a zero old value lets the compiler
@@ -515,6 +529,7 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
   const int count = SPLIT ? p.count : 1;  // the single-item kernels compile without the item loop
   // One item, for a wave of role LOADER (a compile-time constant, so that neither role's code
   // carries the other's branches or registers; both take the same barriers in the same order).
+  bool pre0 = false;  // the ring's stage 0 already holds (or is loading) this item's k step 0
   auto run_item = [&](int item, auto role) UWC_AI {
     constexpr bool loader = decltype(role)::value;
     const Gemm256Item& I = p.it[item];
@@ -531,12 +546,15 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
 #pragma unroll
       for (int j = 0; j < 2; j++) acc[i][j] = v16i{};
     const i8* a_win = I.A + (long)bm0 * k;  // + k0: this workgroup's operand windows
-    // prologue: every stage of the ring loading, then step 0 resident and its first pass read
+    // prologue: every stage of the ring loading (step 0 may already be, issued by the previous
+    // item's denoise), then step 0 resident and its first pass read
     if constexpr (loader) {
 #pragma unroll
       for (int s = 0; s < W_STAGES; s++)
-        if (s < KT) dma_step_s<SPL, 0, SPL>(lds_a(s), lds_b(s), doff, a_win + s * W_BK, b_win + s * W_BK, wave);
+        if (s < KT && !(s == 0 && pre0))
+          dma_step_s<SPL, 0, SPL>(lds_a(s), lds_b(s), doff, a_win + s * W_BK, b_win + s * W_BK, wave);
     }
+    pre0 = false;
     wait_step<SPL>(min(KT - 1, W_STAGES - 1), loader);
     // transcript fold partials, carried from a chunk's TAIL pass to the next chunk's HEAD pass;
     // zero before chunk 0, so the HEAD pass of the first k step folds nothing into slot 15
@@ -858,6 +876,49 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
         }
         if constexpr (loader) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // also drains the hash phase's stores
         __builtin_amdgcn_s_barrier();
+        if constexpr (SPLIT && W_STAGES == 2) {
+          if (CT == W_STAGES) {
+            // Stage by stage instead of quarter by quarter: corr stage t belongs to limb
+            // L - 1 - t / CPL, and acc - sum_t (P_t << 7 li(t)) equals the Horner form mod 2^32.
+            // Once every wave has read stage 0 it takes the next item's k step 0, whose latency
+            // then hides behind stage 1's MFMAs and the output hand-off.
+            const int sh0 = 7 * (L - 1), sh1 = 7 * (L - 1 - 1 / CPL);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+              const int h = q >> 1, nb = q & 1;
+              v16i tmp[2] = {v16i{}, v16i{}};
+              step_mma_quarter(tmp, fbase, 0, h, nb);
+              sub_shl(acc[2 * h][nb], tmp[0], sh0);
+              sub_shl(acc[2 * h + 1][nb], tmp[1], sh0);
+              // one quarter's fragments live at a time: the scheduler would otherwise hoist all
+              // four quarters' reads and spill
+              __builtin_amdgcn_sched_barrier(0);
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // every read of stage 0 is complete
+            __builtin_amdgcn_s_barrier();
+            if (item + 1 < count) {
+              if constexpr (loader) {
+                // the offsets recomputed from an opaque lane index, so that the k loop's copy
+                // is not kept live across the digest
+                int z2;
+                asm volatile("v_mov_b32 %0, 0" : "=v"(z2));
+                const DmaOff<SPL> doff2 = dma_offsets<SPL>(k, wave, lane0 + z2);
+                dma_step_s<SPL, 0, SPL>(lds_a(0), lds_b(0), doff2, p.it[item + 1].A + (long)bm0 * k, b_win, wave);
+              }
+              pre0 = true;
+            }
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+              const int h = q >> 1, nb = q & 1;
+              v16i tmp[2] = {v16i{}, v16i{}};
+              step_mma_quarter(tmp, fbase, 1, h, nb);
+              sub_shl(acc[2 * h][nb], tmp[0], sh1);
+              sub_shl(acc[2 * h + 1][nb], tmp[1], sh1);
+              quarter_done(h, nb, acc[2 * h][nb], acc[2 * h + 1][nb]);
+            }
+            return;
+          }
+        }
 #pragma unroll
         for (int q = 0; q < 4; q++) {
           const int h = q >> 1, nb = q & 1;
