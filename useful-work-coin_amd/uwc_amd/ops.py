@@ -178,6 +178,12 @@ def _arr(ts):
     return None if a is None else ctypes.cast(a, ctypes.c_void_p)
 
 
+def _ptr_array(addrs) -> ctypes.c_void_p:
+    """A host array of device addresses (ints), as the void* the C-ABI's array arguments take
+    (the cast keeps the array alive)."""
+    return ctypes.cast((ctypes.c_void_p * len(addrs))(*addrs), ctypes.c_void_p)
+
+
 # ------------------------------------------------------------------ noise
 def noise_uniform(out: torch.Tensor, label: torch.Tensor, key: torch.Tensor, zero_me=None, zero_n: int = 0):
     _check(out.numel() % 32 == 0, "noise_uniform: out size must be a multiple of 32")
@@ -453,6 +459,17 @@ class MinedWeight:
         slot (1, 2, ...): noise, noised operand, corrections and commitment scratch, so that a
         group's projections all run before its GEMMs. Win records are per weight (or the caller's
         buffer); slots > 0 carry their own."""
+        ws = self._ws(m, slot)
+        if wins is None:
+            wkey = (m, slot)
+            wins = self._bufs.get(wkey)
+            if wins is None:
+                wins = self._bufs[wkey] = torch.zeros(1 + self.max_wins * WIN_WORDS, dtype=torch.int32,
+                                                      device=self.device)
+        return {**ws, "wins": wins}
+
+    def _ws(self, m: int, slot: int) -> dict:
+        """The (m, k, r, slot) workspace buffers (allocated on first use, then kept)."""
         dev, k, r = self.device, self.k, self.r
         key = (str(dev), m, k, r, slot)
         ws = _WORKSPACE.get(key)
@@ -468,12 +485,26 @@ class MinedWeight:
                 maxabs=torch.zeros(2, dtype=torch.int32, device=dev),
                 scratch=torch.empty(max(8, b3_scratch_words(m * k)), dtype=torch.int32, device=dev),
             )
-        if wins is None:
-            wkey = (m, slot)
-            wins = self._bufs.get(wkey)
-            if wins is None:
-                wins = self._bufs[wkey] = torch.zeros(1 + self.max_wins * WIN_WORDS, dtype=torch.int32, device=dev)
-        return {**ws, "wins": wins}
+        return ws
+
+    def _slot_set(self, m: int, parity: int, group: int, count: int) -> dict:
+        """forward_many's workspace slots 1 + parity * group + j (j < count) as device-pointer
+        arrays, one per buffer kind, built once per (m, slot set, count) and block template: the
+        buffers stay where they are from sweep to sweep, so a group's launches only need the
+        arrays of its operands, outputs and win rows. Building it refreshes the slots' corrB
+        copies (on the current stream)."""
+        key = ("slot_set", m, parity, group, count)
+        ss = self._bufs.get(key)
+        if ss is not None and ss["gen"] == self._block_gen:
+            return ss
+        slots = [1 + parity * group + j for j in range(count)]
+        ws = [self._ws(m, sl) for sl in slots]
+        ss = {"gen": self._block_gen, "limbs": ws[0]["corrA"].shape[0],
+              "corrB": _ptr_array([self._slot_corrB(sl).data_ptr() for sl in slots])}
+        for name in ("a_seed", "EAL", "PA", "SA", "SpA", "ApEA", "corrA", "maxabs"):
+            ss[name] = _ptr_array([w[name].data_ptr() for w in ws])
+        self._bufs[key] = ss
+        return ss
 
     def _slot_corrB(self, slot: int) -> torch.Tensor:
         """A per-slot copy of corrB for forward_many: the E_B columns setup_block wrote, and room
@@ -607,23 +638,40 @@ class MinedWeight:
             gemm_group = min(group, GEMM_GROUP)
         _check(1 <= group <= MAX_BATCH, f"MinedWeight.forward_many: group={group}, need 1..{MAX_BATCH}")
         _check(gemm_group >= 1, f"MinedWeight.forward_many: gemm_group={gemm_group}")
-        m, k, r = As[0].shape[0], self.k, self.r
-        for A in As:
-            self._check_a(A)
-            _check(A.shape[0] == m, "MinedWeight.forward_many: every A needs the same shape")
+        A0 = As[0]
+        self._check_a(A0)
+        m, k, r = A0.shape[0], self.k, self.r
+        shape, i8 = A0.shape, torch.int8
+        for A in As:  # the kernels assume every operand's shape, type and layout
+            if A.shape != shape or A.dtype != i8 or not A.is_contiguous():
+                self._check_a(A)
+                _check(False, "MinedWeight.forward_many: every A needs the same shape")
         _check(wins is None or len(wins) == n_items, "MinedWeight.forward_many: one win buffer per item")
         _check(dumps is None or len(dumps) == n_items, "MinedWeight.forward_many: one tile dump per item")
-        outs = [self._out(m, outs[i] if outs is not None else None, out_mode) for i in range(n_items)]
-        c = consts(As[0].device)
-        side = side_ok(m, self.n, k, r)
-        host = None
-        if wins is None:
-            wins, host = self._sweep_win_rows(m, n_items)
-        self._sweep_host = (host, n_items) if host is not None else None
+        c = consts(A0.device)
         gc_on = gc.isenabled()
         gc.disable()
         try:
-            self._sweep(As, a_scale, outs, out_mode, hash_tiles, wins, group, gemm_group, m, k, r, c, side, host, dumps)
+            if gemm_group >= group and side_many_ok(m, self.n, k, r):
+                host = None
+                if wins is None:  # row i of the sweep's win rows, by address
+                    host = self.reserve_sweep(m, n_items)
+                    base, pitch = host.data_ptr(), host.stride(0) * host.element_size()
+                    win_ptrs = [base + i * pitch for i in range(n_items)]
+                else:
+                    win_ptrs = [wb.data_ptr() for wb in wins]
+                self._sweep_host = (host, n_items) if host is not None else None
+                outs = self._sweep_fast(As, a_scale, outs, out_mode, hash_tiles, win_ptrs, group, m, k, r, c, dumps,
+                                        host)
+            else:
+                outs = [self._out(m, outs[i] if outs is not None else None, out_mode) for i in range(n_items)]
+                side = side_ok(m, self.n, k, r)
+                host = None
+                if wins is None:
+                    wins, host = self._sweep_win_rows(m, n_items)
+                self._sweep_host = (host, n_items) if host is not None else None
+                self._sweep(As, a_scale, outs, out_mode, hash_tiles, wins, group, gemm_group, m, k, r, c, side, host,
+                            dumps)
         finally:
             if gc_on:
                 gc.enable()
@@ -654,12 +702,7 @@ class MinedWeight:
         groups = [list(range(g0, min(g0 + group, n_items))) for g0 in range(0, n_items, group)]
         many = side_many_ok(m, self.n, k, r)  # one operand-side launch per GEMM batch
         cur = torch.cuda.current_stream(self.device)
-        sync = _SWEEP_SYNC.get(str(self.device))
-        if sync is None:  # a default-priority side stream and four reusable events per device
-            sync = _SWEEP_SYNC[str(self.device)] = (torch.cuda.Stream(device=self.device),
-                                                    [torch.cuda.Event() for _ in range(2)],
-                                                    [torch.cuda.Event() for _ in range(2)])
-        sc, committed, consumed = sync
+        sc, committed, consumed = self._sweep_sync()
         sc.wait_stream(cur)
 
         def bufs_of(gi):
@@ -707,18 +750,100 @@ class MinedWeight:
                     for j in sub:
                         self._project(As[items[j]], bufs[j], side, corrBs[j])
                 # 5. their hashed GEMMs with exact denoise: one batched call
-                gemm_many([bufs[j]["ApEA"] for j in sub], self.BpEBt, r=r,
-                          flags=(FLAG_HASH if hash_tiles else 0) | FLAG_DENOISE,
-                          corrAs=[bufs[j]["corrA"] for j in sub], corrBs=[corrBs[j] for j in sub],
-                          maxabss=[bufs[j]["maxabs"] for j in sub], keys=[bufs[j]["a_seed"] for j in sub],
-                          target=self.target, winss=[bufs[j]["wins"] for j in sub], max_wins=self.max_wins,
-                          a_scale=a_scale, b_scale=self.b_scale,
-                          outs=[outs[items[j]] for j in sub] if out_mode != OUT_NONE else None, out_mode=out_mode,
-                          dumps=[dumps[items[j]] for j in sub] if dumps is not None else None)
+                gargs = ([bufs[j]["ApEA"] for j in sub], self.BpEBt)
+                gkw = dict(r=r, flags=(FLAG_HASH if hash_tiles else 0) | FLAG_DENOISE,
+                           corrAs=[bufs[j]["corrA"] for j in sub], corrBs=[corrBs[j] for j in sub],
+                           maxabss=[bufs[j]["maxabs"] for j in sub], keys=[bufs[j]["a_seed"] for j in sub],
+                           target=self.target, winss=[bufs[j]["wins"] for j in sub], max_wins=self.max_wins,
+                           a_scale=a_scale, b_scale=self.b_scale,
+                           outs=[outs[items[j]] for j in sub] if out_mode != OUT_NONE else None, out_mode=out_mode,
+                           dumps=[dumps[items[j]] for j in sub] if dumps is not None else None)
+                gemm_many(*gargs, **gkw)
+                self._last_gemm = (len(sub), functools.partial(gemm_many, *gargs, **gkw))
             consumed[gi % 2].record(cur)
         if host is not None:  # winners(m) reports the sweep's last nonce, as after forward()
             self._buf(m)["wins"].copy_(host[n_items - 1])
         cur.wait_stream(sc)
+
+    def last_gemm_launch(self):
+        """(nonces, launch) of the last batched GEMM call forward_many queued: launch() queues the
+        same call again on the current stream (same operands, corrections, seeds, target, win rows
+        and outputs; the win rows then collect the repeats' records too). For timing the GEMM
+        alone."""
+        _check(getattr(self, "_last_gemm", None) is not None, "MinedWeight.last_gemm_launch: no forward_many has run")
+        return self._last_gemm
+
+    def _sweep_sync(self):
+        """A default-priority side stream and four reusable events per device."""
+        sync = _SWEEP_SYNC.get(str(self.device))
+        if sync is None:
+            sync = _SWEEP_SYNC[str(self.device)] = (torch.cuda.Stream(device=self.device),
+                                                    [torch.cuda.Event() for _ in range(2)],
+                                                    [torch.cuda.Event() for _ in range(2)])
+        return sync
+
+    def _sweep_fast(self, As, a_scale, outs, out_mode, hash_tiles, win_ptrs, group, m, k, r, c, dumps, host):
+        """_sweep for the shapes the batched operand side takes, one GEMM launch per group, with
+        the launches' array arguments passed as device addresses: the workspace slots' from
+        _slot_set (built once), the group's operands, outputs and win rows per call. The first
+        commitment is therefore queued after a few tens of microseconds of host work instead of
+        after every nonce's bookkeeping (a 20-nonce sweep lost ~0.2 ms of GPU time to that).
+        Same launches, streams, events and order as _sweep. Returns the outputs."""
+        n_items, n = len(As), self.n
+        _check(m % BM == 0 and n % BN == 0 and k % BK == 0 and r % BK == 0 and k % r == 0, (m, n, k, r))
+        bounds = [(g0, min(g0 + group, n_items)) for g0 in range(0, n_items, group)]
+        cur = torch.cuda.current_stream(self.device)
+        sc, committed, consumed = self._sweep_sync()
+        sc.wait_stream(cur)
+        a_ptrs = [A.data_ptr() for A in As]
+        scratch = self._sweep_scratch(m, group)
+        key, prefix, salt, label = _p(self.job_key), _p(self.b_seed), _p(c["SALT_A"]), _p(c["LABEL_A"])
+
+        def commit(gi):
+            g0, g1 = bounds[gi]
+            with torch.cuda.stream(sc):
+                if gi >= 2:
+                    sc.wait_event(consumed[gi % 2])
+                ss = self._slot_set(m, gi % 2, group, g1 - g0)
+                st = sc.cuda_stream
+                # 1. commit to every A of the group, a_seed_i = H(b_seed || bind_a(root_Ai, m))
+                #    (ops.py:322-324)
+                _lib.call("uwc_b3_root_and_seed_many", _ptr_array(a_ptrs[g0:g1]), g1 - g0, m * k, key, prefix, salt, m,
+                          None, ss["a_seed"], scratch.data_ptr(), scratch.numel(), st)
+                # 2. every nonce's noise E_A, P_A and selection matrices; zeroes its maxabs (2
+                #    words) and win count (1 word)
+                _lib.call("uwc_nonce_noise_many", g1 - g0, ss["EAL"], m, r, ss["PA"], k, ss["SA"], ss["SpA"], label,
+                          ss["a_seed"], ss["maxabs"], 2, _ptr_array(win_ptrs[g0:g1]), 1, st)
+                committed[gi % 2].record(sc)
+
+        commit(0)
+        outs = [self._out(m, outs[i] if outs is not None else None, out_mode) for i in range(n_items)]
+        out_ptrs = [o.data_ptr() for o in outs] if out_mode != OUT_NONE else [0] * n_items
+        dump_ptrs = [d.data_ptr() for d in dumps] if dumps is not None else None
+        flags = (FLAG_HASH if hash_tiles else 0) | FLAG_DENOISE
+        B, SBt, target = _p(self.BpEBt), _p(self.SBt), _p(self.target)
+        asc, bsc = _p(a_scale), _p(self.b_scale)
+        for gi, (g0, g1) in enumerate(bounds):
+            if gi + 1 < len(bounds):
+                commit(gi + 1)
+            cnt = g1 - g0
+            ss = self._slot_set(m, gi % 2, group, cnt)
+            cur.wait_event(committed[gi % 2])
+            st = cur.cuda_stream
+            # 3.-4. the nonces' noised operands and projections (own slot and corrB copy), one launch
+            _lib.call("uwc_side_project_many", cnt, _ptr_array(a_ptrs[g0:g1]), ss["EAL"], ss["SpA"], ss["ApEA"], SBt,
+                      ss["corrA"], 0, r, B, ss["SA"], ss["corrB"], r, m, n, k, r, ss["maxabs"], ss["limbs"], st)
+            # 5. their hashed GEMMs with exact denoise, one batched call
+            gargs = (cnt, ss["ApEA"], B, m, n, k, r, ss["corrA"], ss["corrB"], ss["maxabs"], ss["limbs"], ss["a_seed"],
+                     target, _ptr_array(win_ptrs[g0:g1]), self.max_wins, asc, bsc, _ptr_array(out_ptrs[g0:g1]),
+                     out_mode, flags, _ptr_array(dump_ptrs[g0:g1]) if dump_ptrs is not None else None)
+            _lib.call("uwc_noisy_gemm_many", *gargs, st)
+            consumed[gi % 2].record(cur)
+        self._last_gemm = (cnt, lambda: _lib.call("uwc_noisy_gemm_many", *gargs, _stream()))
+        if host is not None:  # winners(m) reports the sweep's last nonce, as after forward()
+            self._buf(m)["wins"].copy_(host[n_items - 1])
+        cur.wait_stream(sc)
+        return outs
 
     def noise_mine(self, A: torch.Tensor, dump=None):
         """What a pure noise miner runs per attempt batch: commit A, noise it, hashed GEMM, no output.
