@@ -513,16 +513,13 @@ def qwen3_e2e(args, torch, np):
     toks = rng.integers(0, cfg["V"], size=T)
     tokens = torch.from_numpy(toks[None]).to(dev)
 
+    louts = torch.empty((NL, T, cfg["D"]), dtype=torch.float32, device=dev)  # every layer's output
+
     def forward(tok):
-        Tn = tok.shape[1]
-        x = detgpu.embed(m.embed, tok)
-        roots = []
-        for L in m.layers:
-            x = detgpu.layer_fused(m, L, x, 1, Tn)
-            roots.append(detgpu.stage_roots_gpu(x.reshape(1, Tn, cfg["D"])))
+        x, roots = detgpu.forward_stage_roots(m, tok, outs=louts)
         acc, _ = detgpu.final_logits(m, x)
         lroot = detgpu.merkle_roots(detgpu._row_leaf_words(acc, detgpu.TAG_SOUT, 0, 0), 1)
-        return x, torch.cat(roots), acc, lroot
+        return x, roots, acc, lroot
 
     forward(tokens)  # warm-up
     torch.cuda.synchronize()
@@ -548,7 +545,7 @@ def qwen3_e2e(args, torch, np):
                first_layer_root=bytes(layer_roots[0]).hex()[:20],
                logits_root=bytes(detgpu.digest_bytes(lroot)[0]).hex()[:20])
     log(f"e2e: {out}")
-    del x, roots, acc, lroot
+    del x, roots, acc, lroot, louts
     torch.cuda.empty_cache()
     # parity at T = 64: two layers + lm_head vs the oracle
     Tp = 64

@@ -264,6 +264,32 @@ def test_fixture_stages_on_gpu(dev, name):
             assert np.array_equal(qrow(vqn[t, h], vsn[t, h, 0]), R[("VQ", 0, t, h)])
 
 
+def test_forward_stage_roots_batched(dev):
+    """forward_stage_roots (every layer's output kept, all stage-output roots hashed in one batched
+    set of launches) gives each layer's output and root exactly as the layer-by-layer forward with
+    stage_roots_gpu per layer does, and the fixture model's roots equal the oracle's."""
+    from uwc_amd import detgpu
+    d, m, gm = _fixture_model("stage_tiny_qwen3", dev)
+    toks = d["s0_tokens"]
+    x, roots = detgpu.forward_stage_roots(gm, _t(toks[None], dev))
+    xo = m.embed[toks]
+    for l in range(len(gm.layers)):
+        xo = S.layer(m, l, xo)
+        assert bytes(detgpu.digest_bytes(roots)[l]) == S.stage_output_root(xo), l
+    assert np.array_equal(_u32(x), _u32(xo))
+    # a random model of 5 layers at T = 300 (ragged trees), against the per-layer forward
+    cfg = dict(D=256, H=4, Hkv=2, hd=64, I=512, L=5, V=1000, eps=1e-6, Bs=128, max_pos=512, theta=1e6, arch=0)
+    rm = detgpu.DetModel.random(cfg, seed=3, device=dev, with_lm_head=False)
+    T = 300
+    tok = torch.from_numpy(np.random.default_rng(5).integers(0, cfg["V"], size=(1, T))).to(dev)
+    xb, rb = detgpu.forward_stage_roots(rm, tok)
+    xs = detgpu.embed(rm.embed, tok)
+    for l, L in enumerate(rm.layers):
+        xs = detgpu.layer_fused(rm, L, xs, 1, T)
+        assert torch.equal(detgpu.stage_roots_gpu(xs.reshape(1, T, cfg["D"]))[0], rb[l]), l
+    assert torch.equal(xb, xs)
+
+
 def test_qwen3_1p7b_rows_on_gpu(dev):
     """The non-GEMM ops at the real shape (hd 128, 16 / 8 heads, I 6144) from the fixture's inputs."""
     from uwc_amd import detgpu

@@ -36,6 +36,12 @@ __device__ __forceinline__ void sha_init(u32 s[8]) {
 
 __device__ __forceinline__ u32 ror(u32 x, int n) { return __builtin_amdgcn_alignbit(x, x, n); }
 
+// The three-input bitwise functions as single v_bitop3_b32 instructions (truth tables over the
+// operand masks 0xF0, 0xCC, 0xAA): x ^ y ^ z, Ch(x, y, z) = x ? y : z, Maj(x, y, z).
+__device__ __forceinline__ u32 sha_xor3(u32 x, u32 y, u32 z) { return __builtin_amdgcn_bitop3_b32(x, y, z, 0x96); }
+__device__ __forceinline__ u32 sha_ch(u32 x, u32 y, u32 z) { return __builtin_amdgcn_bitop3_b32(x, y, z, 0xCA); }
+__device__ __forceinline__ u32 sha_maj(u32 x, u32 y, u32 z) { return __builtin_amdgcn_bitop3_b32(x, y, z, 0xE8); }
+
 // One compression of the 16-word block w (big-endian words) into s.
 __device__ __forceinline__ void sha_compress(u32 s[8], u32 w[16]) {
   u32 a = s[0], b = s[1], c = s[2], d = s[3], e = s[4], f = s[5], g = s[6], h = s[7];
@@ -46,15 +52,15 @@ __device__ __forceinline__ void sha_compress(u32 s[8], u32 w[16]) {
       wi = w[i];
     } else {
       const u32 w15 = w[(i + 1) & 15], w2 = w[(i + 14) & 15];
-      const u32 s0 = ror(w15, 7) ^ ror(w15, 18) ^ (w15 >> 3);
-      const u32 s1 = ror(w2, 17) ^ ror(w2, 19) ^ (w2 >> 10);
+      const u32 s0 = sha_xor3(ror(w15, 7), ror(w15, 18), w15 >> 3);
+      const u32 s1 = sha_xor3(ror(w2, 17), ror(w2, 19), w2 >> 10);
       wi = w[i & 15] = w[i & 15] + s0 + w[(i + 9) & 15] + s1;
     }
-    const u32 S1 = ror(e, 6) ^ ror(e, 11) ^ ror(e, 25);
-    const u32 ch = (e & f) ^ (~e & g);
+    const u32 S1 = sha_xor3(ror(e, 6), ror(e, 11), ror(e, 25));
+    const u32 ch = sha_ch(e, f, g);
     const u32 t1 = h + S1 + ch + kSha256K[i] + wi;
-    const u32 S0 = ror(a, 2) ^ ror(a, 13) ^ ror(a, 22);
-    const u32 mj = (a & b) ^ (a & c) ^ (b & c);
+    const u32 S0 = sha_xor3(ror(a, 2), ror(a, 13), ror(a, 22));
+    const u32 mj = sha_maj(a, b, c);
     h = g; g = f; f = e; e = d + t1; d = c; c = b; b = a; a = t1 + S0 + mj;
   }
   s[0] += a; s[1] += b; s[2] += c; s[3] += d; s[4] += e; s[5] += f; s[6] += g; s[7] += h;
@@ -270,6 +276,60 @@ __global__ void __launch_bounds__(64) sha_row_leaf_quad_kernel(const u32* __rest
   }
 }
 
+// One 256-thread workgroup per row for rows of SHA_QUAD_MAXBLK .. SHA_ROWTREE_MAXBLK blocks (e.g.
+// the int32 logits rows of a 151,936-entry vocabulary: 594 blocks): the row's block leaves in LDS,
+// each level's parents computed in parallel into a second LDS buffer (an odd last node moves up),
+// then the tagged leaf. A thread per row would run its 2 (nblk - 1) compressions one after another.
+#define SHA_ROWTREE_MAXBLK 1024
+__global__ void __launch_bounds__(256) sha_row_tree_kernel(const u32* __restrict__ leaves, long nrows, int nblk,
+                                                           u32 tag, u32 base, u32 mod, u32* __restrict__ roots,
+                                                           u32* __restrict__ out) {
+  extern __shared__ u32 rt_lds[];  // two buffers of nblk x 8 words
+  const long r = blockIdx.x;
+  u32* cur = rt_lds;
+  u32* nxt = rt_lds + nblk * 8;
+  const u32* src = leaves + r * nblk * 8;
+  for (int i = threadIdx.x; i < nblk * 8; i += blockDim.x) cur[i] = src[i];
+  __syncthreads();
+  int n = nblk;
+  while (n > 1) {
+    const int half = n >> 1;
+    for (int i = threadIdx.x; i < half; i += blockDim.x) {
+      u32 h[8];
+      sha_node(cur + 16 * i, cur + 16 * i + 8, h);
+#pragma unroll
+      for (int k = 0; k < 8; k++) nxt[8 * i + k] = h[k];
+    }
+    if ((n & 1) && threadIdx.x < 8) nxt[8 * half + threadIdx.x] = cur[8 * (n - 1) + threadIdx.x];
+    __syncthreads();
+    u32* t = cur;
+    cur = nxt;
+    nxt = t;
+    n = half + (n & 1);
+  }
+  if (threadIdx.x != 0) return;
+  u32 root[8];
+#pragma unroll
+  for (int k = 0; k < 8; k++) root[k] = cur[k];
+  if (roots) {
+#pragma unroll
+    for (int k = 0; k < 8; k++) roots[r * 8 + k] = root[k];
+  }
+  if (out) {
+    u32 idx = base + (u32)r;
+    if (mod) idx %= mod;
+    u32 z[10];
+    z[0] = tag;
+    z[1] = __builtin_bswap32(idx);  // u32 little-endian bytes as a big-endian word
+#pragma unroll
+    for (int k = 0; k < 8; k++) z[2 + k] = root[k];
+    u32 h[8];
+    sha_short<10>(0u, z, h);
+#pragma unroll
+    for (int k = 0; k < 8; k++) out[r * 8 + k] = h[k];
+  }
+}
+
 // One workgroup per tree of n leaves: the Merkle root, bottom-up through scratch.
 __global__ void __launch_bounds__(256) sha_tree_kernel(const u32* __restrict__ leaves, int n0, u32* __restrict__ a,
                                                        u32* __restrict__ b, u32* __restrict__ roots) {
@@ -353,6 +413,9 @@ extern "C" int uwc_sha_row_leaves(const uint32_t* rows, int64_t nrows, int row_w
   if (nblk <= SHA_QUAD_MAXBLK)
     hipLaunchKernelGGL(sha_row_leaf_quad_kernel, dim3((unsigned)((nrows + SHA_QUAD_ROWS - 1) / SHA_QUAD_ROWS)), dim3(64),
                        0, stream, scratch, (long)nrows, nblk, tag, index_base, index_mod, row_roots, leaves_out);
+  else if (nblk <= SHA_ROWTREE_MAXBLK && nrows <= 0x7FFFFFFFL)
+    hipLaunchKernelGGL(sha_row_tree_kernel, dim3((unsigned)nrows), dim3(256), (size_t)nblk * 64, stream, scratch,
+                       (long)nrows, nblk, tag, index_base, index_mod, row_roots, leaves_out);
   else
     hipLaunchKernelGGL(sha_row_leaf_kernel, dim3((unsigned)((nrows + 63) / 64)), dim3(64), 0, stream, scratch,
                        (long)nrows, nblk, tag, index_base, index_mod, row_roots, leaves_out);

@@ -171,11 +171,15 @@ def _scales(acc, *scales):
     return [None if fp else s.contiguous().data_ptr() for s in scales]
 
 
-def dequant_residual(acc, s, sw, x):
-    """x + fmul(fmul(f32(acc), s), sw) (detgpu/kernels.py:805-813); x + acc for float32 acc (s = sw = None)."""
+def dequant_residual(acc, s, sw, x, out=None):
+    """x + fmul(fmul(f32(acc), s), sw) (detgpu/kernels.py:805-813); x + acc for float32 acc (s = sw = None).
+    out: an optional contiguous (N, k) float32 destination that does not overlap x or acc."""
     acc, x = acc.contiguous(), x.contiguous()
     N, k = acc.shape
-    out = torch.empty((N, k), dtype=F32, device=acc.device)
+    if out is None:
+        out = torch.empty((N, k), dtype=F32, device=acc.device)
+    elif out.shape != (N, k) or out.dtype != F32 or not out.is_contiguous():
+        raise AssertionError(f"dequant_residual: out must be a contiguous float32 {N} x {k} tensor")
     ps, psw = _scales(acc, s, sw)
     _lib.call("uwc_dequant_residual", acc.data_ptr(), ps, psw, x.data_ptr(), N, k, out.data_ptr(), _stream())
     return out
@@ -410,9 +414,9 @@ class DetModel:
         return cls(cfg, embed_t, layers, cos, sin, nw(D), lm)
 
 
-def layer_fused(m, L, x: torch.Tensor, B: int, T: int) -> torch.Tensor:
+def layer_fused(m, L, x: torch.Tensor, B: int, T: int, out: torch.Tensor | None = None) -> torch.Tensor:
     """One decoder layer: x (N, D) float32 -> (N, D) float32, bit-identical to detrt
-    (detgpu/stages.py:154-168)."""
+    (detgpu/stages.py:154-168); out: optional (N, D) float32 destination, not overlapping x."""
     H, Hkv = m.H, m.Hkv
     q1, s1 = rmsnorm_quant(x, L["in_norm"], m.eps, L["qkv"].bs)
     qq, qs, kq, ks, vq, vs, vt = qkv_post_vt(L["qkv"].int_gemm(q1), s1, L["qkv"].sw, L["q_norm"], L["k_norm"],
@@ -422,7 +426,7 @@ def layer_fused(m, L, x: torch.Tensor, B: int, T: int) -> torch.Tensor:
     r1 = dequant_residual(L["o"].int_gemm(q2), s2, L["o"].sw, x)
     q3, s3 = rmsnorm_quant(r1, L["post_norm"], m.eps, L["gu"].bs)
     q4, s4 = swiglu_quant(L["gu"].int_gemm(q3), s3, L["gu"].sw, L["down"].bs)
-    return dequant_residual(L["down"].int_gemm(q4), s4, L["down"].sw, r1)
+    return dequant_residual(L["down"].int_gemm(q4), s4, L["down"].sw, r1, out=out)
 
 
 @torch.no_grad()
@@ -439,6 +443,29 @@ def stage_outputs(m, tokens: torch.Tensor | None, x: torch.Tensor | None, l0: in
     for l in range(l0, l1):
         x = layer_fused(m, m.layers[l], x, B, T)
     return x.reshape(B, T, m.D)
+
+
+@torch.no_grad()
+def forward_stage_roots(m, tokens: torch.Tensor, outs: torch.Tensor | None = None):
+    """Every layer of one sequence (tokens (1, T)) with every layer's stage-output root: the layer
+    outputs land in one (L, T, D) float32 buffer (outs, or a new one), and all L roots are then
+    hashed by one batched set of launches, as stage_roots_gpu over L stages. Per layer, the 1 KiB
+    SHA-256 chains of a stage output (8 per 8 KiB row: 65,536 at T = 8192) give every SIMD one
+    wave, whose dependent rounds leave the VALU mostly idle; the L layers together give each SIMD
+    L waves. Returns (the last layer's output (T, D), roots (L, 8) int32 words), the same roots as
+    stage_roots_gpu of each layer's output."""
+    B, T = tokens.shape
+    if B != 1:
+        raise AssertionError("forward_stage_roots: one sequence")
+    nl = len(m.layers)
+    if outs is None:
+        outs = torch.empty((nl, T, m.D), dtype=F32, device=m.device)
+    elif outs.shape != (nl, T, m.D) or outs.dtype != F32 or not outs.is_contiguous():
+        raise AssertionError(f"forward_stage_roots: outs must be a contiguous float32 ({nl}, {T}, {m.D}) tensor")
+    x = embed(m.embed, tokens)
+    for l, L in enumerate(m.layers):
+        x = layer_fused(m, L, x, 1, T, out=outs[l])
+    return x, stage_roots_gpu(outs)
 
 
 def job_outputs(m, tokens: torch.Tensor, groups: int, upto: int | None = None) -> list[torch.Tensor]:
