@@ -75,7 +75,7 @@ def test_fp32_ops_match_ieee_and_detrt(dev):
         assert same.all(), (op, np.nonzero(~same)[0][:5], got[~same][:3], r[~same][:3])
 
 
-@pytest.mark.parametrize("k,bs", [(128, 64), (2048, 512), (6144, 512), (1000, 8), (96, 0)])
+@pytest.mark.parametrize("k,bs", [(128, 64), (2048, 512), (6144, 512), (1024, 64), (512, 1), (1536, 0), (1000, 8), (96, 0)])
 def test_rmsnorm_quant_and_rmsnorm(dev, k, bs):
     from uwc_amd import detgpu
     rng = np.random.default_rng(k + bs)
@@ -91,7 +91,7 @@ def test_rmsnorm_quant_and_rmsnorm(dev, k, bs):
     assert np.array_equal(_u32(y), _u32(ref_h))
 
 
-@pytest.mark.parametrize("I,bs", [(256, 64), (6144, 512), (300, 4)])
+@pytest.mark.parametrize("I,bs", [(256, 64), (6144, 512), (1024, 8), (512, 2), (300, 4)])
 def test_swiglu_quant(dev, I, bs):
     from uwc_amd import detgpu
     rng = np.random.default_rng(I)

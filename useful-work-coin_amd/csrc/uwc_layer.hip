@@ -30,7 +30,10 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const float* __restrict__ 
   __syncthreads();
   dx_rmsnorm_lds(dx_row, k, w, inv_d, eps, red);
   if constexpr (QUANT) {
-    dx_quant_lds(dx_row, k, bs, 64, q + r * k, scale + r, red);
+    if (k % 512 == 0 && bs <= 512 && (bs <= 1 || (bs & (bs - 1)) == 0))
+      dx_quant_lds_g(dx_row, k, bs > 1 ? __builtin_ctz(bs) : 0, 64, q + r * k, scale + r, red);
+    else
+      dx_quant_lds(dx_row, k, bs, 64, q + r * k, scale + r, red);
   } else {
     float* yr = y + r * k;
     for (int i = threadIdx.x; i < k; i += 256) yr[i] = dx_row[i];
@@ -62,7 +65,10 @@ __global__ void __launch_bounds__(256) swiglu_quant_kernel(const void* __restric
     dx_row[i] = __fmul_rn(dx_silu(g), u);
   }
   __syncthreads();
-  dx_quant_lds(dx_row, I, bs, 64, q + r * (long)I, scale + r, red);
+  if (I % 512 == 0 && bs <= 512 && (bs <= 1 || (bs & (bs - 1)) == 0))
+    dx_quant_lds_g(dx_row, I, bs > 1 ? __builtin_ctz(bs) : 0, 64, q + r * (long)I, scale + r, red);
+  else
+    dx_quant_lds(dx_row, I, bs, 64, q + r * (long)I, scale + r, red);
 }
 
 // ------------------------------------------------------------------ residual

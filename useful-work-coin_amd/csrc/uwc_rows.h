@@ -9,6 +9,7 @@
 // and the lane / workgroup split cannot change a bit.
 #pragma once
 #include "uwc_common.h"
+#include "uwc_fwht.h"
 
 // detrt's float32 constants (core.py:101-105), rounded once from the float64 literals.
 #define DX_LOG2E 0x1.715476p+0f
@@ -128,6 +129,43 @@ __device__ __forceinline__ void dx_rmsnorm_lds(float* row, int k, const float* _
   const float r = __fdiv_rn(1.0f, uwc_sqrt_rn(__fadd_rn(__fmul_rn(ss, inv_d), eps)));
   for (int i = tid; i < k; i += 256) row[i] = __fmul_rn(__fmul_rn(row[i], r), w[i]);
   __syncthreads();
+}
+
+// dx_quant_lds for k % 512 == 0 and 1 <= bs = 2^lbs <= 512: each wave takes the 512-element groups
+// g = wave, wave + 4, ... of the LDS row, transforms them in registers (fwht512_rows: the same
+// adds and subtracts in the same order, so the same bits) and writes them back; after the row's
+// max the wave quantizes its own groups, 8 elements per lane and one 8-byte store. Nine LDS
+// passes with a barrier each become one read and one write.
+__device__ __forceinline__ void dx_quant_lds_g(float* row, int k, int lbs, int qmax, i8* __restrict__ q,
+                                               float* __restrict__ scale, DxRed& red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, G = k >> 9;
+  float mx = 0.f;
+  for (int g = wave; g < G; g += 4) {
+    float4* p = reinterpret_cast<float4*>(row + g * 512 + lane * 8);
+    const float4 a = p[0], b = p[1];
+    float y[1][8] = {{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w}};
+    fwht512_rows<1>(y, 1, lane, lbs);
+#pragma unroll
+    for (int j = 0; j < 8; j++) mx = fmaxf(mx, fabsf(y[0][j]));
+    p[0] = float4{y[0][0], y[0][1], y[0][2], y[0][3]};
+    p[1] = float4{y[0][4], y[0][5], y[0][6], y[0][7]};
+  }
+  mx = block_max256(mx, red);
+  const float fq = (float)qmax;
+  const float s = __fdiv_rn(fmaxf(mx, 1e-8f), fq);
+  for (int g = wave; g < G; g += 4) {
+    const float4* p = reinterpret_cast<const float4*>(row + g * 512 + lane * 8);
+    const float4 a = p[0], b = p[1];
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    u64 packed = 0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const float t = fminf(fmaxf(rintf(__fdiv_rn(v[j], s)), -fq), fq);
+      packed |= (u64)(u8)(i8)(int)t << (8 * j);
+    }
+    *reinterpret_cast<u64*>(q + g * 512 + lane * 8) = packed;
+  }
+  if (threadIdx.x == 0) *scale = lbs > 0 ? __fmul_rn(s, __fdiv_rn(1.0f, uwc_sqrt_rn((float)(1 << lbs)))) : s;
 }
 
 // quant_act on an LDS row (core.py:169-193): block FWHT of size bs (stages h = 1, 2, 4, ...,
