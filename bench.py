@@ -744,8 +744,11 @@ def summarize_e2e_trace(stats_csv, out_path, cmd):
                     f"{float(r['TotalDurationNs']) / 3e6:8.2f} {float(r['Percentage']):5.1f}%\n")
         f.write("\nPer forward: 28 x (rmsnorm_kernel<true> x 2, noisy_gemm256_kernel<false, false, 1> x 4 (qkv, o, gu, "
                 "down), qkv_post_kernel, attention_kernel<128, true> (exponentials stored), quant_act_group_kernel, dequant_residual x 2, "
-                "swiglu_quant, sha_* for the layer's stage-output root), then rmsnorm_quant + the lm_head GEMM "
-                "(256x256 tiles + a 128-wide column tail) + the logits' Merkle root; ms/fwd = total / 3.\n")
+                "swiglu_quant), then one batched set of sha_* launches for all 28 layers' stage-output roots "
+                "(sha_block_leaves, sha_row_leaf_quad, sha_group, sha_tree), rmsnorm_quant + the lm_head GEMM "
+                "(256x256 tiles + a 128-wide column tail) + the logits' Merkle root (sha_block_leaves, sha_row_tree, "
+                "sha_group, sha_tree); ms/fwd = total / 3 (the buffer copies and the random-number kernels are model "
+                "set-up and the oracle's weight copies, outside the timed forwards).\n")
     print(open(out_path).read())
 
 
