@@ -48,6 +48,9 @@
 #ifndef W_BK
 #define W_BK 128
 #endif
+#ifndef W_MULTI
+#define W_MULTI 4  // plain int32 GEMMs of >= W_MULTI tiles per CU take the persistent multi-tile form
+#endif
 #ifndef W_STAGES
 #define W_STAGES (W_BK == 64 ? 4 : 2)
 #endif
@@ -105,6 +108,7 @@ struct Gemm256Params {
   const float* b_scale;
   int ldc;  // output row stride in elements
   int count;
+  int tiles;  // > 0: the plain multi-tile form (item i is tile blockIdx.x + i * gridDim.x of it[0])
   Gemm256Item it[G256_MAXB];
 };
 
@@ -454,9 +458,8 @@ __device__ __forceinline__ u32 bf16_rne(float f) {
 
 // Workgroup id -> tile: XCD-contiguous runs (ids are dispatched round-robin over 8 XCDs),
 // rastered in groups of 4 tile rows.
-__device__ __forceinline__ void tile256(int m, int n, int& bm0, int& bn0) {
+__device__ __forceinline__ void tile256_of(int m, int n, int pid, int& bm0, int& bn0) {
   const int npm = m / W_BM, npn = n / W_BN, total = npm * npn;
-  int pid = blockIdx.x;
   if ((total & 7) == 0) pid = (pid & 7) * (total >> 3) + (pid >> 3);
   constexpr int GROUP_M = 4;
   const int grp = GROUP_M * npn, gid = pid / grp, first = gid * GROUP_M;
@@ -464,6 +467,7 @@ __device__ __forceinline__ void tile256(int m, int n, int& bm0, int& bn0) {
   bm0 = (first + in % gsz) * W_BM;
   bn0 = (in / gsz) * W_BN;
 }
+__device__ __forceinline__ void tile256(int m, int n, int& bm0, int& bn0) { tile256_of(m, n, blockIdx.x, bm0, bn0); }
 
 // SPLIT: the launch's items follow each other on the same tiles, and the output stores of item
 // i drain while item i + 1 computes. On gfx9 a wave's vmcnt counts its stores as well as its
@@ -526,13 +530,20 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
     }
   };
 
-  const int count = SPLIT ? p.count : 1;  // the single-item kernels compile without the item loop
+  // the single-item kernels compile without the item loop; the multi-tile form (plain GEMMs of at
+  // least two tiles per workgroup) takes tiles blockIdx.x, blockIdx.x + gridDim.x, ... of one GEMM
+  const bool multi = SPLIT && p.tiles > 0;
+  const int count = SPLIT ? (multi ? (p.tiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x : p.count) : 1;
   // One item, for a wave of role LOADER (a compile-time constant, so that neither role's code
   // carries the other's branches or registers; both take the same barriers in the same order).
-  bool pre0 = false;  // the ring's stage 0 already holds (or is loading) this item's k step 0
+  int pre = 0;  // ring stages 0 .. pre - 1 already hold (or are loading) this item's first k steps
   auto run_item = [&](int item, auto role) UWC_AI {
     constexpr bool loader = decltype(role)::value;
-    const Gemm256Item& I = p.it[item];
+    if (multi) {
+      tile256_of(p.m, p.n, (int)blockIdx.x + item * (int)gridDim.x, bm0, bn0);
+      b_win = p.B + (long)bn0 * k;
+    }
+    const Gemm256Item& I = p.it[multi ? 0 : item];
     // The lane index through an opaque zero: everything derived from it is recomputed per item
     // instead of being hoisted out of the item loop and kept live across it.
     int z;
@@ -551,10 +562,10 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
     if constexpr (loader) {
 #pragma unroll
       for (int s = 0; s < W_STAGES; s++)
-        if (s < KT && !(s == 0 && pre0))
+        if (s < KT && s >= pre)
           dma_step_s<SPL, 0, SPL>(lds_a(s), lds_b(s), doff, a_win + s * W_BK, b_win + s * W_BK, wave);
     }
-    pre0 = false;
+    pre = 0;
     wait_step<SPL>(min(KT - 1, W_STAGES - 1), loader);
     // transcript fold partials, carried from a chunk's TAIL pass to the next chunk's HEAD pass;
     // zero before chunk 0, so the HEAD pass of the first k step folds nothing into slot 15
@@ -841,7 +852,6 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
           store_rows(slot, wm, h, nb, 1);
         }
       } else {
-        static_assert(OUT == OUT_I32, "the split kernels store int32 outputs");
         u8* slot = wsm + W_LDS + (wave & 3) * 8192;
         if constexpr (loader) put(slot, v0, v1);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -905,7 +915,7 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
                 const DmaOff<SPL> doff2 = dma_offsets<SPL>(k, wave, lane0 + z2);
                 dma_step_s<SPL, 0, SPL>(lds_a(0), lds_b(0), doff2, p.it[item + 1].A + (long)bm0 * k, b_win, wave);
               }
-              pre0 = true;
+              pre = 1;
             }
 #pragma unroll
             for (int q = 0; q < 4; q++) {
@@ -962,6 +972,27 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
       if constexpr (!SPLIT) {  // every wave is done reading the ring before it takes a slot of it
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
+      } else {
+        // every wave is done reading the ring: the loaders start the next tile's first k steps,
+        // whose latency then hides behind the output hand-off (the hand-off slots are past the
+        // ring); its window and the DMA offsets are recomputed here rather than kept live
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        if (multi && item + 1 < count) {
+          if constexpr (loader) {
+            int nbm0, nbn0;
+            tile256_of(p.m, p.n, (int)blockIdx.x + (item + 1) * (int)gridDim.x, nbm0, nbn0);
+            int z2;
+            asm volatile("v_mov_b32 %0, 0" : "=v"(z2));
+            const DmaOff<SPL> doff2 = dma_offsets<SPL>(k, wave, lane0 + z2);
+            const i8* na = I.A + (long)nbm0 * k;
+            const i8* nb = p.B + (long)nbn0 * k;
+#pragma unroll
+            for (int s = 0; s < W_STAGES; s++)
+              if (s < KT) dma_step_s<SPL, 0, SPL>(lds_a(s), lds_b(s), doff2, na + s * W_BK, nb + s * W_BK, wave);
+          }
+          pre = W_STAGES;
+        }
       }
 #pragma unroll
       for (int q = 0; q < 4; q++) quarter_done(q >> 1, q & 1, acc[2 * (q >> 1)][q & 1], acc[2 * (q >> 1) + 1][q & 1]);
@@ -1022,6 +1053,21 @@ int uwc_noisy_gemm256(const int8_t* A, const int8_t* B, int m, int n, int k, int
   p.count = 1;
   p.it[0] = Gemm256Item{A, corrA, corrB, maxabs, key, wins, out, hash ? tile_dump : nullptr};
   const dim3 grid((m / W_BM) * (n / W_BN));
+  // A plain int32 GEMM of at least W_MULTI tiles per CU: one persistent workgroup per CU takes
+  // its tiles in turn on the split-role kernel, so a tile's output stores drain while the next
+  // one computes and the next tile's first k steps load during the hand-off. Measured against one
+  // workgroup per tile: 8192 x 151808 x 2048 (74 tiles per CU) 2942 -> 2813 us, 8192 x 12288 x
+  // 2048 (6) 240 -> 233 us, but 2 tiles per CU 74 -> 78 us, and the fp32 dequant epilogue, which
+  // only the 4 storer waves run in this form, was 3-10% slower at every prefill shape.
+  const int G = uwc_cu_count() & ~7;
+  const long tiles = (long)(m / W_BM) * (n / W_BN);
+  if (W_MULTI > 0 && !hash && !denoise && out_mode == OUT_I32 && G >= 8 && tiles >= (long)W_MULTI * G &&
+      tiles <= 0x7FFFFFFFL) {
+    p.tiles = (int)tiles;
+    p.count = 0;
+    go256<false, false, OUT_I32, true>(dim3(G), stream, p);
+    return uwc_launch_status("noisy_gemm256 (plain, multi-tile)");
+  }
   if (hash && denoise) out256<true, true>(out_mode, grid, stream, p);
   else if (hash) out256<true, false>(out_mode, grid, stream, p);
   else if (denoise) out256<false, true>(out_mode, grid, stream, p);
