@@ -129,16 +129,8 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(
   const long W = (long)NH * HD;
   const bool act = HD >= 64 || lane < HD;
   const float sx = FP ? 1.0f : s1[n];
-  for (int hh = wave; hh < NH; hh += 4) {
-    const int col0 = hh * HD;
-    float v[NV];
-#pragma unroll
-    for (int j = 0; j < NV; j++) {
-      const int d = lane + 64 * j;
-      if (!act) v[j] = 0.0f;
-      else if constexpr (FP) v[j] = static_cast<const float*>(acc)[n * W + col0 + d];
-      else v[j] = dx_deq(static_cast<const i32*>(acc)[n * W + col0 + d], sx, sw[col0 + d]);
-    }
+  // One head of the token (wave-uniform hh) from its dequantized values v.
+  auto head = [&](int hh, float (&v)[NV]) {
     const bool isq = hh < H, isv = hh >= H + Hkv;
     if (!isv) {
       if (qknorm) {  // det_rmsnorm over the head (qwen3.py:214-216)
@@ -203,6 +195,27 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(
 #pragma unroll
       for (int j = 0; j < NV; j++) col[(long)(lane + 64 * j) * Tp] = qv[j];
     }
+  };
+  // A wave takes heads wave, wave + 4, ...: the loads of QH of its heads are issued together
+  // (indices clamped in range, values of heads past NH unused), so the wave waits for memory once
+  // per QH heads instead of once per head.
+  constexpr int QH = 4;
+  for (int h0 = wave; h0 < NH; h0 += 4 * QH) {
+    float vv[QH][NV];
+#pragma unroll
+    for (int c = 0; c < QH; c++) {
+      const int col0 = min(h0 + 4 * c, NH - 1) * HD;
+#pragma unroll
+      for (int j = 0; j < NV; j++) {
+        const int d = act ? lane + 64 * j : 0;
+        if constexpr (FP) vv[c][j] = static_cast<const float*>(acc)[n * W + col0 + d];
+        else vv[c][j] = dx_deq(static_cast<const i32*>(acc)[n * W + col0 + d], sx, sw[col0 + d]);
+        if (!act) vv[c][j] = 0.0f;
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < QH; c++)
+      if (h0 + 4 * c < NH) head(h0 + 4 * c, vv[c]);
   }
 }
 
