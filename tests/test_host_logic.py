@@ -79,3 +79,42 @@ def test_rope_tables_pinned():
         assert cos.shape == (pos, hd) and cos.dtype == np.float32
         assert hashlib.sha256(cos.tobytes() + sin.tobytes()).hexdigest() == want
     assert detgpu.PINNED_ROPE_SHA[(1e6, 128, 8192)].startswith("8ee66518240c0e04")
+
+
+def test_division_by_float64_reciprocal_is_correctly_rounded():
+    """The kernels divide many float32 values by one per-row float32 constant d as
+    float32(float64(x) * (1 / float64(d))) (uwc_div_rd, the attention's at_div): equal to the
+    correctly rounded float32 quotient x / d for every float32 x and normal d > 0. Checked here
+    against IEEE float32 division on 4 M random pairs over every exponent, quotients next to
+    rounding midpoints (x = fl(q d) for q just off a midpoint), exact quotients and the
+    quantizers' ranges."""
+    rng = np.random.default_rng(2024)
+    n = 1 << 22
+    # random bit patterns: finite x of any exponent (incl. subnormal), normal positive d
+    xb = rng.integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32)
+    x = xb.view(np.float32).copy()
+    x[~np.isfinite(x)] = np.float32(1.5)
+    db = rng.integers(0x00800000, 0x7F800000, n, dtype=np.uint64).astype(np.uint32)
+    d = db.view(np.float32).copy()
+    # keep the quotient finite and normal-range so that both sides are ordinary float32 values
+    with np.errstate(over="ignore", under="ignore", invalid="ignore", divide="ignore"):
+        ok = np.isfinite(x / d) & (np.abs(x / d) < np.float32(1e38)) & (np.abs(x / d) > np.float32(1e-37))
+    x, d = x[ok], d[ok]
+    # quantizer-like: |x| <= amax, d = amax / 127 (or / 64)
+    amax = (rng.random(n // 4) * 100 + 1e-3).astype(np.float32)
+    xq = (amax * (rng.random(n // 4) * 2 - 1)).astype(np.float32)
+    dq = (amax / np.float32(127)).astype(np.float32)
+    # near midpoints: x = fl(q d) with q = (2 k + 1) 2^-25 (1 + tiny), k random
+    q = ((2 * rng.integers(2**23, 2**24, n // 4) + 1).astype(np.float64) * 2.0**-25) * (1 + 1e-15)
+    dm = (rng.random(n // 4) + 0.5).astype(np.float32)
+    xm = (q * dm.astype(np.float64)).astype(np.float32)
+    # exact quotients
+    de = (rng.random(n // 8) + 0.5).astype(np.float32)
+    xe = (de * rng.integers(-127, 128, n // 8).astype(np.float32)).astype(np.float32)
+    X = np.concatenate([x, xq, xm, xe])
+    D = np.concatenate([d, dq, dm, de])
+    with np.errstate(over="ignore", under="ignore"):
+        want = X / D  # IEEE float32 division, correctly rounded
+        rd = 1.0 / D.astype(np.float64)
+        got = (X.astype(np.float64) * rd).astype(np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))

@@ -22,6 +22,16 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 // the library builds with -ffp-contract=off so they are never fused.)
 __device__ __forceinline__ float uwc_sqrt_rn(float x) { return (float)__builtin_sqrt((double)x); }
 
+// x / d correctly rounded to float32, for float32 x and a normal float32 d > 0 given as
+// rd = 1.0 / (double)d (correctly rounded in float64): the float64 product x * rd is within
+// 2^-52 (relative) of x / d, while a quotient of two float32 values is never a float32 rounding
+// midpoint and lies more than 2^-49 (relative) from every midpoint (with x = X 2^a, d = D 2^b and
+// a midpoint M 2^c, M odd of 25 bits: x - M 2^c d is a nonzero multiple of 2^(b+c), so the
+// quotient's distance from the midpoint is at least 2^c / D > 2^(c-24), against M 2^c < 2^(c+25)),
+// so rounding the product to float32 rounds the exact quotient. Three instructions instead of the
+// IEEE division sequence, for divisions of many values by one per-row constant.
+__device__ __forceinline__ float uwc_div_rd(float x, double rd) { return (float)((double)x * rd); }
+
 // Records a message for uwc_last_error() and returns UWC_EINVAL.
 int uwc_fail(const char* fmt, ...);
 // hipGetLastError() after a launch, converted to a status (and a message on failure).

@@ -169,9 +169,10 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(
 #pragma unroll
     for (int j = 0; j < NV; j++) am = fmaxf(am, fabsf(v[j]));
     const float s = __fdiv_rn(fmaxf(wave_max(am), 1e-8f), 127.0f);
+    const double rs = 1.0 / (double)s;
     i8 qv[NV];
 #pragma unroll
-    for (int j = 0; j < NV; j++) qv[j] = (i8)(int)fminf(fmaxf(rintf(__fdiv_rn(v[j], s)), -127.f), 127.f);
+    for (int j = 0; j < NV; j++) qv[j] = (i8)(int)fminf(fmaxf(rintf(uwc_div_rd(v[j], rs)), -127.f), 127.f);
     i8* qo;
     float* so;
     if (isq) {

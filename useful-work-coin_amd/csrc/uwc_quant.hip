@@ -46,9 +46,10 @@ __global__ void __launch_bounds__(256) quant_act_kernel(const T* __restrict__ x,
   const float amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const float fq = (float)qmax;
   const float s = __fdiv_rn(fmaxf(amax, 1e-8f), fq);
+  const double rs = 1.0 / (double)s;
   i8* qr = q + (u64)row * k;
   for (int i = tid; i < k; i += 256) {
-    const float v = fminf(fmaxf(rintf(__fdiv_rn(rowf[i], s)), -fq), fq);
+    const float v = fminf(fmaxf(rintf(uwc_div_rd(rowf[i], rs)), -fq), fq);
     qr[i] = (i8)(int)v;
   }
   if (tid == 0) scale[row] = bs > 1 ? __fmul_rn(s, __fdiv_rn(1.0f, uwc_sqrt_rn((float)bs))) : s;
@@ -143,12 +144,13 @@ __global__ void __launch_bounds__(256) quant_act_wave_kernel(const T* __restrict
   for (int s = 32; s > 0; s >>= 1) mx = fmaxf(mx, __shfl_xor(mx, s, 64));
   const float fq = (float)qmax;
   const float s = __fdiv_rn(fmaxf(mx, 1e-8f), fq);
+  const double rs = 1.0 / (double)s;
   i8* qr = q + (u64)row * k + lane * 8;
   auto emit = [&](const float v[8], int g) {
     u64 packed = 0;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
-      const float t = fminf(fmaxf(rintf(__fdiv_rn(v[j], s)), -fq), fq);
+      const float t = fminf(fmaxf(rintf(uwc_div_rd(v[j], rs)), -fq), fq);
       packed |= (u64)(u8)(i8)(int)t << (8 * j);
     }
     *reinterpret_cast<u64*>(qr + g * 512) = packed;
@@ -194,10 +196,11 @@ __global__ void __launch_bounds__(64 * QA_GMAX) quant_act_group_kernel(const T* 
   for (int i = 1; i < G; i++) mx = fmaxf(mx, wmax[i]);
   const float fq = (float)qmax;
   const float s = __fdiv_rn(fmaxf(mx, 1e-8f), fq);
+  const double rs = 1.0 / (double)s;
   u64 packed = 0;
 #pragma unroll
   for (int j = 0; j < 8; j++) {
-    const float t = fminf(fmaxf(rintf(__fdiv_rn(y[0][j], s)), -fq), fq);
+    const float t = fminf(fmaxf(rintf(uwc_div_rd(y[0][j], rs)), -fq), fq);
     packed |= (u64)(u8)(i8)(int)t << (8 * j);
   }
   *reinterpret_cast<u64*>(q + row * k + g * 512 + lane * 8) = packed;

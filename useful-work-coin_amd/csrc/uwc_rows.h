@@ -153,6 +153,7 @@ __device__ __forceinline__ void dx_quant_lds_g(float* row, int k, int lbs, int q
   mx = block_max256(mx, red);
   const float fq = (float)qmax;
   const float s = __fdiv_rn(fmaxf(mx, 1e-8f), fq);
+  const double rs = 1.0 / (double)s;
   for (int g = wave; g < G; g += 4) {
     const float4* p = reinterpret_cast<const float4*>(row + g * 512 + lane * 8);
     const float4 a = p[0], b = p[1];
@@ -160,7 +161,7 @@ __device__ __forceinline__ void dx_quant_lds_g(float* row, int k, int lbs, int q
     u64 packed = 0;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
-      const float t = fminf(fmaxf(rintf(__fdiv_rn(v[j], s)), -fq), fq);
+      const float t = fminf(fmaxf(rintf(uwc_div_rd(v[j], rs)), -fq), fq);
       packed |= (u64)(u8)(i8)(int)t << (8 * j);
     }
     *reinterpret_cast<u64*>(q + g * 512 + lane * 8) = packed;
@@ -191,8 +192,9 @@ __device__ __forceinline__ void dx_quant_lds(float* row, int k, int bs, int qmax
   mx = block_max256(mx, red);
   const float fq = (float)qmax;
   const float s = __fdiv_rn(fmaxf(mx, 1e-8f), fq);
+  const double rs = 1.0 / (double)s;
   for (int i = tid; i < k; i += 256) {
-    const float v = fminf(fmaxf(rintf(__fdiv_rn(row[i], s)), -fq), fq);
+    const float v = fminf(fmaxf(rintf(uwc_div_rd(row[i], rs)), -fq), fq);
     q[i] = (i8)(int)v;
   }
   if (tid == 0) *scale = bs > 1 ? __fmul_rn(s, __fdiv_rn(1.0f, uwc_sqrt_rn((float)bs))) : s;
