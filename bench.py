@@ -763,34 +763,49 @@ def summarize_linears_trace(trace_csv, out_path, cmd):
     """A kernel trace of `bench.py --linears-only` as text: per graph-timed shape (configs[1]'s layer
     graph and its four GEMMs, configs[0], the Llama-3.1-8B decode linears) the device durations of
     its timed replays. Each graph of N launches is run eagerly, replayed once, then replayed three
-    times back to back: dispatch runs are split at idle gaps over 30 us, and each shape's timed run
-    is the next run of exactly 3 N dispatches of this library's kernels (N from the bench's own
-    launch counts; torch's kernels fill the gaps between shapes)."""
+    times back to back (N from the bench's own launch counts); a shape whose timed replays are not
+    found is left out of the table."""
     import csv
     import re
     rows = sorted(csv.DictReader(open(trace_csv)), key=lambda r: int(r["Start_Timestamp"]))
+    ours = lambda r: not re.search(r"at::native|__amd_rocclr", r["Kernel_Name"])  # noqa: E731
+    # configs[1]'s graphs: runs of this library's dispatches split at idle gaps; a shape's timed run
+    # is 3 x the launches of its graph, right after the first replay's run of a third of that
     runs, cur, last_end = [], [], None
     for r in rows:
         st, en = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
-        if cur and st - last_end > 30000:
+        if cur and (st - last_end > 30000 or not ours(r)):
             runs.append(cur)
             cur = []
-        cur.append(r)
+        if ours(r):
+            cur.append(r)
         last_end = en
     if cur:
         runs.append(cur)
-    ours = lambda r: not re.search(r"at::native|__amd_rocclr", r["Kernel_Name"])  # noqa: E731
-    # the timed run of each shape, in bench order: 3 x the launches of its graph (warm-up and first
-    # replay runs have a third of that)
-    want = [24] * 5 + [3 * _skinny_launches(6144 * 2048)] + [
-        3 * _skinny_launches(nn * kk) for _ in (1, 8, 32) for nn, kk in LLAMA_LINEARS.values()]
-    timed, j = [], 0
-    for w in want:
-        while j < len(runs) and not (len(runs[j]) == w and all(ours(r) for r in runs[j])):
+    timed, j = [], 1
+    for w in [24] * 5:
+        while j < len(runs) and not (len(runs[j]) == w and len(runs[j - 1]) == w // 3):
             j += 1
-        if j == len(runs):
-            break
-        timed.append(runs[j])
+        timed.append(runs[j] if j < len(runs) else None)
+        j += 1
+    # the skinny shapes: each rotates N launches over its weights; torch's own kernels (the input's
+    # set-up) bracket the eager run, and then the first replay and the three timed ones (4 N launches
+    # with no torch kernel among them, however the profiler's stalls split them in time)
+    segs, cur = [], []
+    for r in rows[rows.index(timed[-1][-1]) + 1 if timed[-1] else 0:]:
+        if ours(r):
+            cur.append(r)
+        elif cur:
+            segs.append(cur)
+            cur = []
+    if cur:
+        segs.append(cur)
+    j = 0
+    for n in [_skinny_launches(6144 * 2048)] + [
+            _skinny_launches(nn * kk) for _ in (1, 8, 32) for nn, kk in LLAMA_LINEARS.values()]:
+        while j < len(segs) and len(segs[j]) != 4 * n:
+            j += 1
+        timed.append(segs[j][n:] if j < len(segs) else None)
         j += 1
     with open(out_path, "w") as f:
         f.write("rocprofv3 kernel trace, graph-timed linears of bench.py (configs[1] at M=2048, configs[0], "
@@ -799,6 +814,8 @@ def summarize_linears_trace(trace_csv, out_path, cmd):
         f.write(f"{'shape':44s} {'kernel':44s} {'grid':>6s} {'lds':>7s} {'calls':>6s} {'avg_us':>8s} {'min_us':>8s} "
                 f"{'max_us':>8s}\n")
         for lab, run in zip(LINEAR_LABELS, timed):
+            if run is None:
+                continue
             per = {}
             for r in run:
                 name = r["Kernel_Name"].replace("(anonymous namespace)::", "")
