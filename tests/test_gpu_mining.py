@@ -48,10 +48,13 @@ def test_seed_derivation_matches_oracle(dev):
     assert ops.words_to_bytes(as_) == a_seed
 
 
-@pytest.mark.parametrize("count,nchunks", [(1, 65), (3, 1), (5, 130), (16, 64), (4, 4097), (2, 65537)])
+@pytest.mark.parametrize("count,nchunks", [(1, 65), (3, 1), (5, 130), (16, 64), (4, 4097), (2, 65537), (32, 2049),
+                                           (4, 16384), (8, 8193)])
 def test_batched_commitment_matches_oracle(dev, count, nchunks):
     """b3_root_and_seed_many: every item's root and salted seed equal the oracle's (and the
-    single-input entry point's), whatever the batch size and tree shape."""
+    single-input entry point's), whatever the batch size and tree shape; from 65536 chunks per
+    launch on (the last three cases and (2, 65537)) the chunks go one per lane, 256 per workgroup,
+    with a partial last workgroup in all but (4, 16384)."""
     ops = _ops()
     rng = np.random.default_rng(count * 1000 + nchunks)
     datas = [rng.integers(0, 256, size=nchunks * 1024, dtype=np.uint8) for _ in range(count)]

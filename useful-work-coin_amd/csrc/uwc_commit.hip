@@ -2,13 +2,17 @@
 // (miner/ampere/uwc_ampere/kernels.cu:138-244, reference.py:41-64, ops.py:99-118).
 //
 // BLAKE3 over 16 MiB is 16384 independent chunk chains of 16 compressions each, then a
-// 14-level tree: the work is latency-bound, not throughput-bound. One compression is therefore
+// 14-level tree. One operand alone is latency-bound, not throughput-bound: for small batches one
+// compression is therefore
 // spread over the 4 lanes of a quad: lane q holds column q of the 4 x 4 state
 // (a = v[q], b = v[4+q], c = v[8+q], d = v[12+q]), runs the column G on it, and the diagonal
 // step rotates b, c, d across the quad with DPP quad permutes (v0 v5 v10 v15 ... become one
 // lane's a b c d). Message words reach each lane from LDS at precomputed per-lane offsets
 // (lane q of round r reads words S[r][2q], S[r][2q+1], S[r][8+2q], S[r][9+2q]).
-// This quarters the dependent instruction chain per compression and gives 4x the waves.
+// This quarters the dependent instruction chain per compression and gives 4x the waves. Batches
+// of four or more 16 MiB operands have the waves anyway and run one chunk per lane instead
+// (b3_lanes_kernel: measured over 16 MiB operands, 20 per launch 157 -> 130 us, 32 per launch
+// 228 -> 194 us; 1 per launch 31 -> 39 us, 2 per launch 38 -> 41 us).
 #include "uwc_common.h"
 
 #include <mutex>
@@ -228,6 +232,60 @@ b3_chunks_kernel(B3In bt, u64 nchunks, const u32* __restrict__ key, u32* __restr
   if (tid < 8) wg_cvs[blockIdx.x * 8 + tid] = cvs[tid];
 }
 
+// The same chunk values with one chunk per lane, for batches large enough to give every SIMD
+// several waves: a lane runs the plain 16-word compression (b3_compress), so a compression costs
+// 64 lanes' ~700 VALU instructions per 64 chunks instead of the quad form's ~1290 lane
+// instructions per chunk (its DPP rotations and per-round LDS message reads are gone), at 4x
+// the dependent chain per wave. A lane reads its chunk's 64-byte blocks straight from memory
+// (four 16-byte loads; the next block's loads are issued before the current block's
+// compression), and 256 chunks per workgroup reduce to one subtree value in LDS.
+#define B3L_CHUNKS_PER_WG 256
+#ifndef B3_LANES_MIN_CHUNKS
+#define B3_LANES_MIN_CHUNKS (1u << 16)  // 4 operands of 16 MiB (1 wave per SIMD): from there on the lane form is faster
+#endif
+
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6)))
+b3_lanes_kernel(B3In bt, u64 nchunks, const u32* __restrict__ key, u32* __restrict__ wg_cvs, u64 stride) {
+  __shared__ u32 cvs[B3L_CHUNKS_PER_WG * 8];
+  const u8* __restrict__ data = bt.data[blockIdx.y];
+  wg_cvs += blockIdx.y * stride;
+  const int tid = threadIdx.x, q = tid & 3;
+  const u64 base = (u64)blockIdx.x * B3L_CHUNKS_PER_WG;
+  const int count = (int)min((u64)B3L_CHUNKS_PER_WG, nchunks - base);
+  const bool active = tid < count;
+  // chunks past the end read the first chunk of the workgroup (not stored)
+  const uint4* __restrict__ src = reinterpret_cast<const uint4*>(data + (base + (active ? tid : 0)) * 1024ull);
+  u32 cv[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) cv[i] = key[i];
+  uint4 nx[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) nx[j] = src[j];
+  const u64 chunk = base + tid;
+#pragma unroll 1
+  for (int b = 0; b < 16; b++) {
+    u32 m[16];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      m[4 * j] = nx[j].x; m[4 * j + 1] = nx[j].y; m[4 * j + 2] = nx[j].z; m[4 * j + 3] = nx[j].w;
+    }
+    if (b < 15) {
+#pragma unroll
+      for (int j = 0; j < 4; j++) nx[j] = src[4 * (b + 1) + j];
+    }
+    const u32 flags = B3_KEYED | (b == 0 ? B3_CHUNK_START : 0u) | (b == 15 ? B3_CHUNK_END : 0u) |
+                      ((b == 15 && nchunks == 1) ? B3_ROOT : 0u);
+    b3_compress(cv, m, chunk, 64, flags, cv);
+  }
+  if (active) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) cvs[tid * 8 + i] = cv[i];
+  }
+  __syncthreads();
+  quad_level_reduce(cvs, count, key[q], key[4 + q], B3_KEYED, gridDim.x == 1);
+  if (tid < 8) wg_cvs[blockIdx.x * 8 + tid] = cvs[tid];
+}
+
 #define B3_GROUP 1024
 // Reduces aligned groups of up to 1024 chaining values (256 threads = 64 quads). With a single
 // group (final), the last merge carries ROOT and the salted seed may follow:
@@ -324,9 +382,17 @@ extern "C" int uwc_b3_scratch_words(uint64_t nbytes) {
 // [i * stride, (i + 1) * stride).
 static int b3_launch(const B3In& in, int count, u64 nbytes, const u32* key, const u32* prefix, const u32* salt, u32 dim,
                      const B3Out& outs, u32* scratch, u64 stride, hipStream_t stream) {
+  // subtree values per item: one per workgroup, in at most the words uwc_b3_scratch_words counts
+  // (a workgroup of the lane form covers more chunks than one of the quad form)
   const u64 nch = nbytes / 1024;
-  int cnt = (int)((nch + B3_CHUNKS_PER_WG - 1) / B3_CHUNKS_PER_WG);
-  hipLaunchKernelGGL(b3_chunks_kernel, dim3(cnt, count), dim3(256), 0, stream, in, nch, key, scratch, stride);
+  int cnt;
+  if ((u64)count * nch >= B3_LANES_MIN_CHUNKS) {
+    cnt = (int)((nch + B3L_CHUNKS_PER_WG - 1) / B3L_CHUNKS_PER_WG);
+    hipLaunchKernelGGL(b3_lanes_kernel, dim3(cnt, count), dim3(256), 0, stream, in, nch, key, scratch, stride);
+  } else {
+    cnt = (int)((nch + B3_CHUNKS_PER_WG - 1) / B3_CHUNKS_PER_WG);
+    hipLaunchKernelGGL(b3_chunks_kernel, dim3(cnt, count), dim3(256), 0, stream, in, nch, key, scratch, stride);
+  }
   int st = uwc_launch_status("b3_chunks");
   if (st) return st;
   u32* cur = scratch;

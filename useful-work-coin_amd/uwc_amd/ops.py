@@ -788,13 +788,19 @@ class MinedWeight:
         _slot_set (built once), the group's operands, outputs and win rows per call. The first
         commitment is therefore queued after a few tens of microseconds of host work instead of
         after every nonce's bookkeeping (a 20-nonce sweep lost ~0.2 ms of GPU time to that).
-        Same launches, streams, events and order as _sweep. Returns the outputs."""
+        Same launches and order as _sweep; a sweep of one group, which has nothing to overlap its
+        commitment with, queues everything on the current stream (no cross-stream waits, each of
+        which left the GPU idle ~10 us). Returns the outputs."""
         n_items, n = len(As), self.n
         _check(m % BM == 0 and n % BN == 0 and k % BK == 0 and r % BK == 0 and k % r == 0, (m, n, k, r))
         bounds = [(g0, min(g0 + group, n_items)) for g0 in range(0, n_items, group)]
         cur = torch.cuda.current_stream(self.device)
+        single = len(bounds) == 1
         sc, committed, consumed = self._sweep_sync()
-        sc.wait_stream(cur)
+        if single:
+            sc = cur
+        else:
+            sc.wait_stream(cur)
         a_ptrs = [A.data_ptr() for A in As]
         scratch = self._sweep_scratch(m, group)
         key, prefix, salt, label = _p(self.job_key), _p(self.b_seed), _p(c["SALT_A"]), _p(c["LABEL_A"])
@@ -814,7 +820,8 @@ class MinedWeight:
                 #    words) and win count (1 word)
                 _lib.call("uwc_nonce_noise_many", g1 - g0, ss["EAL"], m, r, ss["PA"], k, ss["SA"], ss["SpA"], label,
                           ss["a_seed"], ss["maxabs"], 2, _ptr_array(win_ptrs[g0:g1]), 1, st)
-                committed[gi % 2].record(sc)
+                if not single:
+                    committed[gi % 2].record(sc)
 
         commit(0)
         outs = [self._out(m, outs[i] if outs is not None else None, out_mode) for i in range(n_items)]
@@ -828,7 +835,8 @@ class MinedWeight:
                 commit(gi + 1)
             cnt = g1 - g0
             ss = self._slot_set(m, gi % 2, group, cnt)
-            cur.wait_event(committed[gi % 2])
+            if not single:
+                cur.wait_event(committed[gi % 2])
             st = cur.cuda_stream
             # 3.-4. the nonces' noised operands and projections (own slot and corrB copy), one launch
             _lib.call("uwc_side_project_many", cnt, _ptr_array(a_ptrs[g0:g1]), ss["EAL"], ss["SpA"], ss["ApEA"], SBt,
@@ -838,11 +846,13 @@ class MinedWeight:
                      target, _ptr_array(win_ptrs[g0:g1]), self.max_wins, asc, bsc, _ptr_array(out_ptrs[g0:g1]),
                      out_mode, flags, _ptr_array(dump_ptrs[g0:g1]) if dump_ptrs is not None else None)
             _lib.call("uwc_noisy_gemm_many", *gargs, st)
-            consumed[gi % 2].record(cur)
+            if not single:
+                consumed[gi % 2].record(cur)
         self._last_gemm = (cnt, lambda: _lib.call("uwc_noisy_gemm_many", *gargs, _stream()))
         if host is not None:  # winners(m) reports the sweep's last nonce, as after forward()
             self._buf(m)["wins"].copy_(host[n_items - 1])
-        cur.wait_stream(sc)
+        if not single:
+            cur.wait_stream(sc)
         return outs
 
     def noise_mine(self, A: torch.Tensor, dump=None):
