@@ -717,7 +717,8 @@ def summarize_trace(trace_csv, out_path, cmd, steps, warmup, group):
         f.write(f"\nback-to-back noisy_gemm256_kernel<true, true, 1, true> launches of {group} nonces (the bench's "
                 f"roofline figure): {len(b2b)} calls, avg {sum(b2b) / len(b2b):.2f} us = "
                 f"{sum(b2b) / len(b2b) / group:.2f} us per nonce, min {min(b2b):.2f}, max {max(b2b):.2f}\n")
-        f.write(f"\nPer group of {group} nonces: b3_chunks + b3_reduce (one batched commitment of the group's A) and\n"
+        f.write(f"\nPer group of {group} nonces: b3_lanes (or, below 4 operands, b3_chunks) + b3_reduce (one batched "
+                "commitment of the group's A) and\n"
                 "one nonce_noise (E_A, P_A, selection matrices of the group), on a side stream one group ahead, beside\n"
                 "the previous group's side work; one side_many_kernel launch (noised A and both projections in limbs\n"
                 "for every nonce of the group);\n"
