@@ -15,9 +15,12 @@
 // waves, and each St / SpA byte staged in LDS serves the 8 row tiles of the workgroup. The noise
 // of a 64-column step is four MFMAs of SpA rows x the wave's E rows whose A-operand rows are
 // permuted so that each lane's 16 results are the noise of its own 16 source bytes, added with
-// a byte-wise SWAR add. A group of nonces is one launch of count x (m + n) / 128 workgroups:
-// enough to keep every CU loading while others compute (the per-nonce form keeps one
-// latency-bound workgroup per CU).
+// a byte-wise SWAR add. A group of nonces is one launch of count x m / 128 A-side and
+// ceil(count / 2) x n / 128 B-side workgroups: enough to keep every CU loading while others
+// compute (the per-nonce form keeps one latency-bound workgroup per CU). A B-side workgroup
+// projects its 128 rows of B' for two nonces (their St tiles take the stage space the A side
+// gives to SpA), so each row of B' is read once per nonce pair (32 nonces per launch: 11.6 ->
+// 10.9 us per nonce for both sides).
 //
 // LDS rows of 128 bytes keep 16-byte chunk c of row R at c ^ ((R ^ (R >> 3)) & 7); 64-byte SpA
 // rows keep chunk c of row R at c ^ ((R >> 4) & 3): the 16 lanes of a fragment read hit
@@ -76,10 +79,11 @@ __device__ __forceinline__ u32 sm_add_bytes(u32 a, u32 c) {
 template <int NB, bool ASIDE>
 struct SmGeom {
   static constexpr int r = NB * 16;
+  static constexpr int NST = ASIDE ? 1 : 2;                 // selection matrices (B side: a nonce pair's)
   static constexpr int SRC = SM_ROWS * SM_CH;               // source rows of a chunk
-  static constexpr int STB = r * SM_CH;                     // St rows of a chunk
+  static constexpr int STB = r * SM_CH;                     // St rows of a chunk, per selection matrix
   static constexpr int SPT = ASIDE ? SM_CH * 64 : 0;        // SpA rows of a chunk
-  static constexpr int STAGE = SRC + STB + SPT;
+  static constexpr int STAGE = SRC + NST * STB + SPT;
   static constexpr int NSEG = STAGE / 1024;                 // 1 KiB DMA segments per chunk
   static constexpr int SPW = (NSEG + SM_PROD - 1) / SM_PROD;  // per producer wave (the last repeats)
   // ring stages: two (64 KiB at r = 64). A deeper ring measured no faster alone, and the batched
@@ -95,11 +99,14 @@ constexpr int sm_lds() {
 }
 
 // One workgroup: 128 rows (row0 ..) of src over the full k, with the selection matrix St and, on
-// the A side, the noise (E, SpA) into dst.
+// the A side, the noise (E, SpA) into dst. The B side projects its rows of B' for two nonces at
+// once (St, corr, maxabs and St2, corr2, maxabs2; corr2 NULL: no second nonce, St2 = St), so a
+// group reads each row of B' half as often.
 template <int NB, bool ASIDE>
 __device__ __forceinline__ void sm_side(u8* ring, const i8* src, const i8* St, const i8* SpA, const i8* E, i8* dst,
-                                        i8* corr, int corr_off, int ecopy_off, i32* maxabs, int rows, int row0, int k,
-                                        int lmax, int wave, int lane, int* wmax) {
+                                        i8* corr, int corr_off, int ecopy_off, i32* maxabs, const i8* St2, i8* corr2,
+                                        i32* maxabs2, int rows, int row0, int k, int lmax, int wave, int lane,
+                                        int* wmax) {
   using G = SmGeom<NB, ASIDE>;
   constexpr int r = G::r;
   const int NC = k / SM_CH;
@@ -118,13 +125,15 @@ __device__ __forceinline__ void sm_side(u8* ring, const i8* src, const i8* St, c
         const int g = min(t * SM_PROD + pw, G::NSEG - 1);
         const u32 lds = __builtin_amdgcn_readfirstlane(stage + (u32)g * 1024u);
         const void* gp;
-        if (g < (G::SRC + G::STB) / 1024) {
+        if (g < (G::SRC + G::NST * G::STB) / 1024) {
           const bool is_src = g < G::SRC / 1024;
-          const int R = (is_src ? g : g - G::SRC / 1024) * 8 + (lane >> 3);
+          const int gs = g - G::SRC / 1024;  // St segment; on the B side segments STB / 1024 on are St2's
+          const int R = (is_src ? g : gs % (G::STB / 1024)) * 8 + (lane >> 3);
           const int col = col0 + (((lane & 7) ^ sm_swz(R)) << 4);
-          gp = is_src ? (const void*)(src + (u64)(row0 + R) * k + col) : (const void*)(St + (u64)R * k + col);
+          const i8* stp = (G::NST == 2 && gs >= G::STB / 1024) ? St2 : St;
+          gp = is_src ? (const void*)(src + (u64)(row0 + R) * k + col) : (const void*)(stp + (u64)R * k + col);
         } else {
-          const int g2 = g - (G::SRC + G::STB) / 1024;
+          const int g2 = g - (G::SRC + G::NST * G::STB) / 1024;
           gp = SpA + (u64)(col0 + 16 * g2 + (lane >> 2)) * 64 + (((lane & 3) ^ (g2 & 3)) << 4);
         }
         sm_dma16(gp, lds);
@@ -141,9 +150,9 @@ __device__ __forceinline__ void sm_side(u8* ring, const i8* src, const i8* St, c
   } else {
     const int rr = lane & 15, q = lane >> 4;
     const int lrow = wave * 16 + rr;  // this lane's source row in the tile (fragment and noise)
-    v4i acc[NB];
+    v4i acc[NB], acc2[NB];  // acc2: the B side's second nonce
 #pragma unroll
-    for (int b = 0; b < NB; b++) acc[b] = v4i{0, 0, 0, 0};
+    for (int b = 0; b < NB; b++) acc[b] = acc2[b] = v4i{0, 0, 0, 0};
     static_assert(SM_CH == 128, "a chunk is two 64-column noise steps per row");
     v4i ef = v4i{0, 0, 0, 0};  // the noise MFMA's B operand: E[row][16 q, 16 q + 16)
     v4i o0 = v4i{0, 0, 0, 0};  // the noised bytes of the chunk's first 64 columns
@@ -161,13 +170,18 @@ __device__ __forceinline__ void sm_side(u8* ring, const i8* src, const i8* St, c
           const int R = b * 16 + rr;
           const v4i sf = *reinterpret_cast<const v4i*>(st + G::SRC + R * SM_CH + ((lc ^ sm_swz(R)) << 4));
           acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, sf, acc[b], 0, 0, 0);
+          if constexpr (!ASIDE) {
+            const v4i sf2 =
+                *reinterpret_cast<const v4i*>(st + G::SRC + G::STB + R * SM_CH + ((lc ^ sm_swz(R)) << 4));
+            acc2[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, sf2, acc2[b], 0, 0, 0);
+          }
         }
         if constexpr (ASIDE) {
           // noise MFMA t: A-operand row rr = SpA row 64 s + 16 (rr >> 2) + 4 t + (rr & 3) of the
           // chunk, so C element e of lane (rr, q) is the noise of column 16 q + 4 t + e of the
           // step for source row rr: this lane's byte 4 t + e
           const int R0 = 64 * s + 16 * (rr >> 2) + (rr & 3);
-          const u8* sp = st + G::SRC + G::STB + R0 * 64 + ((q ^ ((R0 >> 4) & 3)) << 4);
+          const u8* sp = st + G::SRC + G::NST * G::STB + R0 * 64 + ((q ^ ((R0 >> 4) & 3)) << 4);
           v4i o;
 #pragma unroll
           for (int t = 0; t < 4; t++) {
@@ -198,20 +212,33 @@ __device__ __forceinline__ void sm_side(u8* ring, const i8* src, const i8* St, c
     // C layout of the 16 x 16 x 64 MFMA: lane (j, q) holds rows 4 q + e of the wave's tile,
     // column 16 b + j of the projection
     const u64 limb_stride = (u64)rows * 2 * r;
-    int mx = 0;
+    auto emit = [&](const v4i* ac, i8* cp) {
+      int mx = 0;
 #pragma unroll
-    for (int b = 0; b < NB; b++)
+      for (int b = 0; b < NB; b++)
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        int v = acc[b][e];
-        mx = max(mx, abs(v));
-        i8* out = corr + (u64)(row0 + wave * 16 + 4 * q + e) * 2 * r + corr_off + 16 * b + rr;
-        for (int li = 0; li < lmax; li++) {
-          const int d = ((v + 64) & 127) - 64;
-          out[li * limb_stride] = (i8)d;
-          v = (v - d) >> 7;
+        for (int e = 0; e < 4; e++) {
+          int v = ac[b][e];
+          mx = max(mx, abs(v));
+          i8* out = cp + (u64)(row0 + wave * 16 + 4 * q + e) * 2 * r + corr_off + 16 * b + rr;
+          for (int li = 0; li < lmax; li++) {
+            const int d = ((v + 64) & 127) - 64;
+            out[li * limb_stride] = (i8)d;
+            v = (v - d) >> 7;
+          }
         }
+#pragma unroll
+      for (int s = 32; s > 0; s >>= 1) mx = max(mx, __shfl_xor(mx, s));
+      return mx;
+    };
+    const int mx = emit(acc, corr);
+    if (lane == 0) wmax[wave] = mx;
+    if constexpr (!ASIDE) {
+      if (corr2) {
+        const int mx2 = emit(acc2, corr2);
+        if (lane == 0) wmax[SM_WAVES + wave] = mx2;
       }
+    }
     if (ASIDE && ecopy_off >= 0) {
       // the wave's 16 E rows (r bytes each) into every limb: lane -> row lane / (r / 16) ... in
       // 16-byte pieces
@@ -223,9 +250,6 @@ __device__ __forceinline__ void sm_side(u8* ring, const i8* src, const i8* St, c
           *reinterpret_cast<v4i*>(corr + li * limb_stride + (u64)row * 2 * r + ecopy_off + col) = e;
       }
     }
-#pragma unroll
-    for (int s = 32; s > 0; s >>= 1) mx = max(mx, __shfl_xor(mx, s));
-    if (lane == 0) wmax[wave] = mx;
   }
   __syncthreads();
   if (threadIdx.x == 0 && maxabs) {
@@ -234,24 +258,35 @@ __device__ __forceinline__ void sm_side(u8* ring, const i8* src, const i8* St, c
     for (int w = 0; w < SM_WAVES; w++) m = max(m, wmax[w]);
     atomicMax(maxabs, m);
   }
+  if (!ASIDE && threadIdx.x == 0 && corr2 && maxabs2) {
+    int m = 0;
+#pragma unroll
+    for (int w = 0; w < SM_WAVES; w++) m = max(m, wmax[SM_WAVES + w]);
+    atomicMax(maxabs2, m);
+  }
 }
 
 template <int NB>
 __global__ void __launch_bounds__(SM_THREADS) side_many_kernel(SideManyParams p) {
   extern __shared__ __attribute__((aligned(1024))) u8 ring[];
-  __shared__ int wmax[SM_WAVES];
+  __shared__ int wmax[2 * SM_WAVES];
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int tA = p.m / SM_ROWS, tB = p.n / SM_ROWS, nA = p.count * tA;
   const int b = blockIdx.x;
   if (b < nA) {
     const SideManyItem& I = p.it[b / tA];
-    sm_side<NB, true>(ring, I.A, p.StB, I.SpA, I.EA, I.ApEA, I.corrA, p.corr_a_off, p.ecopy_off, I.maxabs, p.m,
-                      (b % tA) * SM_ROWS, p.k, p.lmax, wave, lane, wmax);
+    sm_side<NB, true>(ring, I.A, p.StB, I.SpA, I.EA, I.ApEA, I.corrA, p.corr_a_off, p.ecopy_off, I.maxabs, nullptr,
+                      nullptr, nullptr, p.m, (b % tA) * SM_ROWS, p.k, p.lmax, wave, lane, wmax);
   } else {
-    const SideManyItem& I = p.it[(b - nA) / tB];
+    // B side: nonces 2 j and 2 j + 1 (if any) of pair j = (b - nA) / tB
+    const int i0 = 2 * ((b - nA) / tB);
+    const SideManyItem& I = p.it[i0];
+    const bool two = i0 + 1 < p.count;
+    const SideManyItem& J = p.it[two ? i0 + 1 : i0];
     sm_side<NB, false>(ring, p.Bp, I.StA, nullptr, nullptr, nullptr, I.corrB, p.corr_b_off, -1,
-                       I.maxabs ? I.maxabs + 1 : nullptr, p.n, ((b - nA) % tB) * SM_ROWS, p.k, p.lmax, wave, lane,
-                       wmax);
+                       I.maxabs ? I.maxabs + 1 : nullptr, J.StA, two ? J.corrB : nullptr,
+                       two && J.maxabs ? J.maxabs + 1 : nullptr, p.n, ((b - nA) % tB) * SM_ROWS, p.k, p.lmax, wave,
+                       lane, wmax);
   }
 }
 
@@ -299,7 +334,7 @@ extern "C" int uwc_side_project_many(int count, const int8_t* const* A, const in
       return uwc_fail("%s: item %d: A, EA, SpA, ApEA, StA (and corrA for the E copy) must be 16-byte aligned", fn, i);
     p.it[i] = SideManyItem{A[i], EA[i], SpA[i], ApEA[i], corrA[i], StA[i], corrB[i], maxabs[i]};
   }
-  const dim3 grid(count * (m / SM_ROWS + n / SM_ROWS));
+  const dim3 grid(count * (m / SM_ROWS) + (count + 1) / 2 * (n / SM_ROWS));
   switch (r) {
     case 16: sm_go<1>(grid, stream, p); break;
     case 32: sm_go<2>(grid, stream, p); break;
