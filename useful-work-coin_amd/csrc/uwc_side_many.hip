@@ -112,8 +112,9 @@ __device__ __forceinline__ void sm_side(u8* ring, const i8* src, const i8* St, c
   const int NC = k / SM_CH;
   const u32 ring_base = __builtin_amdgcn_readfirstlane((u32)(uintptr_t)(sm_lptr_t)ring);
   if (wave >= SM_WAVES) {
-    // producer: chunk c into stage c % NS; segment g holds 8 rows of 128 bytes (source, then St)
-    // or 16 rows of 64 bytes (SpA): lane i -> row 8 g + (i >> 3), physical chunk i & 7 (logical
+    // producer: chunk c into stage c % NS; segment g holds 8 rows of 128 bytes (source, then St,
+    // then on the B side St2) or 16 rows of 64 bytes (A side: SpA): lane i -> row 8 g + (i >> 3)
+    // (St rows counted from each matrix's first segment), physical chunk i & 7 (logical
     // chunk (i & 7) ^ swz(row)); SpA: row 16 g' + (i >> 2), physical chunk i & 3 (logical chunk
     // (i & 3) ^ (g' & 3))
     const int pw = wave - SM_WAVES;
