@@ -614,7 +614,8 @@ class MinedWeight:
         groups of at most SWEEP_GROUP): one set of launches commits the whole
         group (BLAKE3 trees and salted seeds) and one launch draws all of its noise, so those
         latency-bound chains run several waves per SIMD instead of one, on a second stream one
-        group ahead, beside the previous group's projections; then the group's nonces run their
+        group ahead, beside the previous group's projections (a sweep of one group queues them
+        on the current stream); then the group's nonces run their
         projections and hashed GEMMs, `gemm_group` (by default the group) nonces per batched GEMM call (whose output
         stores overlap the next nonce's tiles). The work is queued behind the current stream,
         which then waits for all of it. Python's cyclic garbage collector is paused while the
