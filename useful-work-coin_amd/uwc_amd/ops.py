@@ -14,6 +14,7 @@ Differences a caller can see:
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import functools
 import gc
@@ -808,7 +809,8 @@ class MinedWeight:
 
         def commit(gi):
             g0, g1 = bounds[gi]
-            with torch.cuda.stream(sc):
+            # the side stream current while the slot set may allocate (a one-group sweep has none)
+            with contextlib.nullcontext() if single else torch.cuda.stream(sc):
                 if gi >= 2:
                     sc.wait_event(consumed[gi % 2])
                 ss = self._slot_set(m, gi % 2, group, g1 - g0)
