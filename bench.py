@@ -676,6 +676,62 @@ def summarize_counters(csv_path, cmd, nonces):
     print(open(COUNTER_FILE).read())
 
 
+def summarize_side_counters(sq_csv, fetch_csv, write_csv, out_path, cmd, nonces):
+    """Per-dispatch counters (median over the dispatches) of the sweep's operand-side and
+    commitment kernels from three rocprofv3 --pmc passes over `bench.py --traffic-probe` (SQ
+    counters, then FETCH_SIZE, then WRITE_SIZE; the byte counters scaled by what they read for the
+    calibration copy of COPY_BYTES), with the VALU busy fraction (wave-instructions x 4 cycles over
+    the SIMDs' active cycles) and the fraction of wave cycles spent waiting."""
+    import csv
+    import statistics
+    kernels = ("side_many_kernel<4>", "b3_lanes_kernel")
+
+    def per_dispatch(path):
+        d = {}
+        for row in csv.DictReader(open(path)):
+            key = (row["Dispatch_Id"], row["Kernel_Name"])
+            d.setdefault(key, {})
+            d[key][row["Counter_Name"]] = d[key].get(row["Counter_Name"], 0.0) + float(row["Counter_Value"])
+        return d
+
+    def medians(d, pat):
+        rows = [c for (_, kn), c in d.items() if pat in kn]
+        return {c: statistics.median(r.get(c, 0.0) for r in rows) for c in rows[0]} if rows else {}, len(rows)
+
+    byte_factor = {}
+    for ctr, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        d = per_dispatch(path)
+        copies = [c[ctr] for (_, kn), c in d.items() if "copy" in kn.lower() and c.get(ctr, 0) > 0.5 * COPY_BYTES / 1024]
+        byte_factor[ctr] = (d, COPY_BYTES / (statistics.median(copies) * 1024.0))
+    sq = per_dispatch(sq_csv)
+    simds, xcds, nonces = 256 * 4, 8, int(nonces)
+    with open(out_path, "w") as f:
+        f.write(f"rocprofv3 counters of the mining sweep's operand side and commitment (4096^3, r=64, {nonces} nonces "
+                "per dispatch), median per dispatch\n")
+        f.write(f"commands: {cmd}\n")
+        for kname in kernels:
+            med, n = medians(sq, kname)
+            if not med:
+                continue
+            f.write(f"\n{kname} ({n} dispatches)\n")
+            for c in sorted(med):
+                f.write(f"  {c}: {med[c]:.0f}\n")
+            active = med.get("GRBM_GUI_ACTIVE", 0.0) / xcds
+            if active and "SQ_INSTS_VALU" in med:
+                f.write(f"  valu_busy_frac: {med['SQ_INSTS_VALU'] * 4 / (active * simds):.3f} (SQ_INSTS_VALU x 4 / "
+                        f"(GRBM_GUI_ACTIVE / {xcds} x {simds}))\n")
+            if med.get("SQ_WAVE_CYCLES"):
+                f.write(f"  wait_any_frac: {med.get('SQ_WAIT_ANY', 0) / med['SQ_WAVE_CYCLES']:.3f}, wait_inst_any_frac: "
+                        f"{med.get('SQ_WAIT_INST_ANY', 0) / med['SQ_WAVE_CYCLES']:.3f} (of SQ_WAVE_CYCLES)\n")
+            for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+                d, fac = byte_factor[ctr]
+                bm, _ = medians(d, kname)
+                if ctr in bm:
+                    f.write(f"  {ctr}: {bm[ctr]:.0f} KiB x {fac:.4f} = {bm[ctr] * 1024 * fac / 1e6:.1f} MB per dispatch, "
+                            f"{bm[ctr] * 1024 * fac / 1e6 / nonces:.2f} MB per nonce\n")
+    print(open(out_path).read())
+
+
 def gemm_reps(steps: int) -> int:
     """Back-to-back launches of the noisy GEMM that time it after the sweep."""
     return max(8, min(steps, 64))
@@ -887,6 +943,9 @@ def main():
                     help="write the graph-timed linears' kernel-trace summary under profiles/")
     ap.add_argument("--summarize-pmc", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "CMD", "NONCES"),
                     help="write the traffic summary under profiles/ from two counter_collection.csv files")
+    ap.add_argument("--summarize-side-counters", nargs=6,
+                    metavar=("SQ_CSV", "FETCH_CSV", "WRITE_CSV", "OUT", "CMD", "NONCES"),
+                    help="write the operand side's and commitment's counter summary")
     ap.add_argument("--summarize-counters", nargs=3, metavar=("COUNTER_CSV", "CMD", "NONCES"),
                     help="write the hashed GEMM's counter summary under profiles/ from a counter_collection.csv")
     ap.add_argument("--summarize-e2e-trace", nargs=3, metavar=("STATS_CSV", "OUT", "CMD"),
@@ -905,6 +964,9 @@ def main():
         return
     if args.summarize_pmc:
         summarize_pmc(*args.summarize_pmc)
+        return
+    if args.summarize_side_counters:
+        summarize_side_counters(*args.summarize_side_counters)
         return
     if args.summarize_counters:
         summarize_counters(*args.summarize_counters)
