@@ -238,13 +238,15 @@ b3_chunks_kernel(B3In bt, u64 nchunks, const u32* __restrict__ key, u32* __restr
 // instructions per chunk (its DPP rotations and per-round LDS message reads are gone), at 4x
 // the dependent chain per wave. A lane reads its chunk's 64-byte blocks straight from memory
 // (four 16-byte loads; the next block's loads are issued before the current block's
-// compression), and 256 chunks per workgroup reduce to one subtree value in LDS.
+// compression), and 256 chunks per workgroup reduce to one subtree value in LDS. 61 VGPRs, so 8
+// waves per SIMD: 32 operands (8,192 waves) run in one round instead of 7 waves per SIMD and a
+// partial second round (measured 196.7 -> 193.4 us for 32, 135.6 -> 132.4 us for 20).
 #define B3L_CHUNKS_PER_WG 256
 #ifndef B3_LANES_MIN_CHUNKS
 #define B3_LANES_MIN_CHUNKS (1u << 16)  // 4 operands of 16 MiB (1 wave per SIMD): from there on the lane form is faster
 #endif
 
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8)))
 b3_lanes_kernel(B3In bt, u64 nchunks, const u32* __restrict__ key, u32* __restrict__ wg_cvs, u64 stride) {
   __shared__ u32 cvs[B3L_CHUNKS_PER_WG * 8];
   const u8* __restrict__ data = bt.data[blockIdx.y];
