@@ -539,11 +539,14 @@ extern "C" int uwc_b3_root_and_seed_static(const uint8_t* data, uint64_t nbytes,
 // of P) and SpT (its transpose as k rows of 64 bytes, zero past r) from one keyed random_hash
 // per quad (reference.py:67-93, kernels.cu:246-301, ops.py:152-158), and zeroes two counter
 // ranges, in a single latency-bound launch instead of four. Workgroups [0, nE) make E blocks
-// (one quad per 32-byte block); the rest make 8 pairs per quad. A P wave owns 128 consecutive
+// (one lane per 32-byte block: the plain compression issues about half the instructions of the
+// quad form, and a group's thousands of blocks give every SIMD waves anyway); the rest make 8
+// pairs per quad. A P wave owns 128 consecutive
 // columns: it builds their St rows (r x 128 bytes) and SpT rows (128 x 64 bytes) in LDS by a
 // zero fill and a 2-byte scatter per pair, then writes them with 16-byte stores (column-wise
 // byte stores of St cost several times more).
 #define NN_COLS 128  // columns per P wave
+#define NN_EBLK 256  // E blocks per workgroup (one per lane)
 
 __device__ __forceinline__ void pair_of(u32 u, u32 r, u32& first, u32& second) {
   first = u & (r - 1);
@@ -579,34 +582,41 @@ __global__ void __launch_bounds__(256) nonce_noise_kernel(NNBatch nb, u32 eblock
     if (z0 && tid < n0) z0[tid] = 0;
     if (z1 && tid < n1) z1[tid] = 0;
   }
-  const bool pblk = blockIdx.x >= nE;
-  const u32 index = pblk ? (blockIdx.x - nE) * 64 + lq : blockIdx.x * 64 + lq;  // E block or pair octet
-  const int prepend = pblk ? 1 : 0;
-  // message words 4q..4q+3 of msg: 0 except word `prepend` = 1 + index; words 8..15 = label
+  if (blockIdx.x < nE) {
+    // E block `index` (32 bytes) per lane: the keyed digest of message word 0 = 1 + index, words
+    // 8..15 = label, the rest 0, as one lane's plain compression; digest bytes -> (y & 63) - 32:
+    // the 6-bit value (y & 63) ^ 32 sign-extended per byte
+    const u32 index = blockIdx.x * NN_EBLK + tid;
+    if (index < eblocks) {
+      u32 m[16], kv[8], o[8];
+      m[0] = 1u + index;
+#pragma unroll
+      for (int i = 1; i < 8; i++) m[i] = 0u;
+#pragma unroll
+      for (int i = 0; i < 8; i++) { m[8 + i] = label[i]; kv[i] = key[i]; }
+      b3_compress(kv, m, 0, 64, B3_CHUNK_START | B3_CHUNK_END | B3_ROOT | B3_KEYED, o);
+      u32* dst = reinterpret_cast<u32*>(E + (u64)index * 32);
+#pragma unroll
+      for (int w = 0; w < 8; w++) {
+        const u32 z = (o[w] & 0x3F3F3F3Fu) ^ 0x20202020u, sg = z & 0x20202020u;
+        dst[w] = z | (sg << 1) | (sg << 2);
+      }
+    }
+    return;
+  }
+  const u32 index = (blockIdx.x - nE) * 64 + lq;  // pair octet
+  // message words 4q..4q+3 of msg: 0 except word 1 = 1 + index; words 8..15 = label
   u32* mw = reinterpret_cast<u32*>(msgs + lq * B3_QSTRIDE);
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int w = 4 * q + i;
-    mw[w] = w >= 8 ? label[w - 8] : (w == prepend ? 1u + index : 0u);
+    mw[w] = w >= 8 ? label[w - 8] : (w == 1 ? 1u + index : 0u);
   }
   __builtin_amdgcn_wave_barrier();
   const QuadMsgOffsets off = quad_offsets(q);
   u32 lo, hi;
   quad_compress(msgs + lq * B3_QSTRIDE, off, q, key[q], key[4 + q], 0, 64,
                 B3_CHUNK_START | B3_CHUNK_END | B3_ROOT | B3_KEYED, lo, hi);
-  if (!pblk) {
-    if (index < eblocks) {
-      // digest bytes -> (y & 63) - 32: the 6-bit value (y & 63) ^ 32 sign-extended per byte
-      u32 z = (lo & 0x3F3F3F3Fu) ^ 0x20202020u, sg = z & 0x20202020u;
-      const u32 elo = z | (sg << 1) | (sg << 2);
-      z = (hi & 0x3F3F3F3Fu) ^ 0x20202020u; sg = z & 0x20202020u;
-      const u32 ehi = z | (sg << 1) | (sg << 2);
-      u32* dst = reinterpret_cast<u32*>(E + (u64)index * 32);
-      dst[q] = elo;
-      dst[4 + q] = ehi;
-    }
-    return;
-  }
   // pairs l = 8 index + q + 4 h
   u32 f[2], sc[2];
   bool v[2];
@@ -677,7 +687,7 @@ static int nn_launch(const NNBatch& nb, int count, int rows, int r, int k, bool 
     if (st && !nb.St[i]) return uwc_fail("%s: St[%d] is null", fn, i);
     if ((n0 && !nb.z0[i]) || (n1 && !nb.z1[i])) return uwc_fail("%s: zero range of item %d without a pointer", fn, i);
   }
-  const u64 eblocks = (u64)rows * r / 32, nE = (eblocks + 63) / 64, nP = (((u64)k + 7) / 8 + 63) / 64;
+  const u64 eblocks = (u64)rows * r / 32, nE = (eblocks + NN_EBLK - 1) / NN_EBLK, nP = (((u64)k + 7) / 8 + 63) / 64;
   const u64 blocks = nE + nP > 0 ? nE + nP : 1;
   if (blocks > 0x7fffffff) return uwc_fail("%s: too large", fn);
   const size_t smem = r <= 128 ? (size_t)4 * ((st ? (size_t)r * NN_COLS : 0) + (spt ? NN_COLS * 64 : 0)) : 0;
