@@ -924,7 +924,7 @@ def main():
     ap.add_argument("--distinct", type=int, default=64, help="distinct resident A matrices cycled over")
     ap.add_argument("--out-buffers", type=int, default=8, help="distinct int32 outputs rotated through the sweep")
     ap.add_argument("--group", type=int, default=None,
-                    help="nonces per batched commitment / noise launch (default: forward_many's, equal groups of <= 16)")
+                    help="nonces per batched commitment / noise launch (default: forward_many's, equal groups of <= 32)")
     ap.add_argument("--gemm-group", type=int, default=None, help="nonces per batched GEMM launch (default: the group)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--cpu-max-nonces", type=int, default=4)

@@ -9,15 +9,22 @@ this module composes it into the reference's algorithms, each citing the referen
 file:line it restates (paths relative to the reference repository root). What pins each
 function is listed in the C file's header and exercised by tests/test_oracle.py.
 
-Parity status: BLAKE3-derived values (commitment roots, seeds, noise E/P, tile digests)
-have no stored vectors in the reference (its only check compares against the `blake3`
-package live, miner/ampere/tests/test_kernels.py:13-20); here they are pinned by the BLAKE3
-team's published test vectors (tests/golden/blake3_official_vectors.json: unkeyed inputs of 0 to
-102400 bytes, i.e. one block, a chunk, a parent node and 31- and 100-chunk trees; keyed inputs of
-0, 1, 1024 and 2048 bytes, the last one two chunks under a keyed parent, the form every
-commitment takes) plus two independent restatements (C recursive tree, Python streaming stack)
-that agree on every tree shape up to 129 chunks, keyed and plain. The Pearl-side job_key/penalised bound (pearl_glue.py:44-62) are "parity unpinned"
-and are not restated: callers pass job_key and target words, as the kernels do.
+Parity status. BLAKE3 itself is pinned by the BLAKE3 team's published test vectors
+(tests/golden/blake3_official_vectors.json: unkeyed inputs of 0 to 102400 bytes, keyed inputs of 0,
+1, 1024 and 2048 bytes) and by two independent restatements (C recursive tree, Python streaming
+stack) that agree on every tree shape up to 129 chunks. Those vectors pin the hash function only,
+not the messages this path feeds it. The reference stores no vectors of its BLAKE3-derived values
+(its only check compares against the `blake3` package live, miner/ampere/tests/test_kernels.py:13-20,
+and that package is not installed here), so these rest on restatement alone and are
+PARITY UNPINNED:
+  * the random_hash message layout behind E and P (reference.py:67-93, kernels.cu:246-301; the
+    value rules derived from it are checked by distribution: E uniform on [-32, 31], P's first index
+    uniform and its XOR distance uniform on [1, r - 1]);
+  * the salted seed chain a_seed / b_seed (reference.py:41-64: root binding, salts, labels);
+  * the tile-message encoding fed to the tile digest (reference.py:124-125, kernels.cu:574-596; the
+    fold itself is checked by brute force).
+Pearl's job_key serialization and penalised bound (pearl_glue.py:44-62) are not restated: callers
+pass job_key and target words, as the kernels do.
 """
 from __future__ import annotations
 
@@ -126,6 +133,22 @@ def limbs_for(k: int) -> int:
 def limbs_needed(mx: int) -> int:
     """Limbs the denoise pass uses for a runtime max |projection| (kernels.cu:602-607)."""
     return 1 if mx <= 63 else 2 if mx <= 8127 else 3 if mx <= 1040319 else 4
+
+
+def denoise(noisy: np.ndarray, corrA: np.ndarray, corrB: np.ndarray, maxabs, lmax: int | None = None) -> np.ndarray:
+    """The exact denoise of kernels.cu:598-673: L from the runtime max |projection| (:602-607,
+    capped at lmax = the correction buffers' limb count), then
+    noisy - sum_{li < L} 128^li corrA[li] @ corrB[li]^T, Horner over the limbs from L - 1 down, all
+    mod 2^32. noisy is the int32 (or wider) noisy product; corrA (lmax, m, 2r), corrB (lmax, n, 2r)
+    int8."""
+    lmax = corrA.shape[0] if lmax is None else lmax
+    L = min(limbs_needed(max(int(maxabs[0]), int(maxabs[1]))), lmax)
+    tmp = np.zeros(noisy.shape, np.int64)
+    for li in range(L - 1, -1, -1):
+        # |corrA corrB^T| <= 64 * 64 * 2r: exact in float64 for any r here
+        part = corrA[li].astype(np.float64) @ corrB[li].astype(np.float64).T
+        tmp = (tmp << 7) + part.astype(np.int64)
+    return ((noisy.astype(np.int64) - tmp) & 0xFFFFFFFF).astype(np.uint32).view(np.int32)
 
 
 def pad_to_chunk(data: bytes) -> bytes:

@@ -318,6 +318,46 @@ def layer(m: Model, l: int, x: np.ndarray, put=None) -> np.ndarray:
     return r2.astype(F32)
 
 
+def layer_rows(m: Model, l: int, x: np.ndarray, rows) -> np.ndarray:
+    """layer(m, l, x)[rows] without the other rows' outputs: the keys and values of every position
+    (rmsnorm, the k / v columns of the qkv linear, k norm, rope, int8 quant) and everything else for
+    the query rows only. Rows are independent in every step but attention (stage.py:146-233), so
+    this is the same arithmetic restricted to the rows; for long sequences. Returns (len(rows), D)."""
+    cfg = m.cfg
+    H, Hkv, hd = cfg["H"], cfg["Hkv"], cfg["hd"]
+    T = x.shape[0]
+    rows = np.asarray(rows, np.int64)
+    nrm, lin = m.norms[l], m.lins[l]
+    eps = m.eps32
+    Wq, sw = lin["qkv"]
+    h1 = det_rmsnorm(x, nrm["in_norm"], eps)
+    q1, s1 = quant_act(h1, m.bs(h1.shape[1]))
+    kv = slice(H * hd, (H + 2 * Hkv) * hd)
+    kvo = dequant(int_gemm(q1, Wq[kv]), s1, sw[kv])                  # (T, 2 Hkv hd)
+    k, v = kvo[:, :Hkv * hd], kvo[:, Hkv * hd:]
+    qo = dequant(int_gemm(q1[rows], Wq[:H * hd]), s1[rows], sw[:H * hd])  # (R, H hd)
+    if cfg["arch"] == 0:
+        qn = det_rmsnorm(qo.reshape(len(rows), H, hd), nrm["q_norm"], eps)
+        kn = det_rmsnorm(k.reshape(T, Hkv, hd), nrm["k_norm"], eps)
+    else:
+        qn, kn = qo.reshape(len(rows), H, hd), k.reshape(T, Hkv, hd)
+    qr = rope(qn, m.cos[rows][:, None, :], m.sin[rows][:, None, :])
+    kr = rope(kn, m.cos[:T][:, None, :], m.sin[:T][:, None, :])
+    kq, ks = quant_sym(kr, 127)
+    vq, vs = quant_sym(v.reshape(T, Hkv, hd), 127)
+    qq, qs = quant_sym(qr, 127)
+    *_, o = _attend(qq, qs, kq, ks, vq, vs, inv_sqrt_hd(hd), rows)
+    oc = o.transpose(1, 0, 2).reshape(len(rows), H * hd)
+    _, _, op = linear(oc, *lin["o"], m.bs(oc.shape[1]))
+    r1 = x[rows] + op
+    h2 = det_rmsnorm(r1, nrm["post_norm"], eps)
+    _, _, gu = linear(h2, *lin["gu"], m.bs(h2.shape[1]))
+    I_ = gu.shape[1] // 2
+    sm = det_silu(gu[:, :I_]) * gu[:, I_:]
+    _, _, dn = linear(sm, *lin["down"], m.bs(sm.shape[1]))
+    return (r1 + dn).astype(F32)
+
+
 def final_logits(m: Model, x: np.ndarray):
     """lm_head(det_rmsnorm(x, norm)) (qwen3.py:300, :306): (int32 accumulators, fp32 logits)."""
     h = det_rmsnorm(x, m.final_norm, m.eps32)

@@ -20,15 +20,19 @@
  *                       nodes, 31- and 100-chunk trees), plus agreement with an independent
  *                       pure-Python restatement (oracle/blake3_py.py) over every tree shape
  *                       up to 129 chunks, keyed and plain, and ragged lengths.
- *   or_noise_*          structural invariants (range [-32,31], first != second < r),
- *                       byte layout against a pure-Python random_hash. The values rest on the
- *                       pinned keyed BLAKE3 and the restated message layout (reference.py:67-93);
- *                       the reference stores no vectors of them.
+ *   or_noise_*          structural invariants (range [-32,31], first != second < r) and the
+ *                       rules' distributions (E uniform on [-32,31]; P's first index uniform, its
+ *                       XOR distance uniform on [1,r-1]), byte layout against a pure-Python
+ *                       random_hash. PARITY UNPINNED: the values rest on the pinned keyed BLAKE3
+ *                       and the restated message layout (reference.py:67-93); the reference stores
+ *                       no vectors of them, nor of the seeds or tile digests built the same way.
  *   or_transcript_*     brute-force per-tile recomputation on tiny shapes (explicit
  *                       cumulative sums over each tile's 128 elements).
  *   or_quant_act_f32    Go-referee fixtures N1->QA1, O->QA2, N2->QA3, SM->QA4 bit-exact.
  *   or_dequant_f32      Go-referee fixtures QA1 x W -> QKV etc. bit-exact
  *                       (chain/patches/0003-*.patch:618-634 linearElem).
+ *   or_scale_bf16       torch's fp32 -> bf16 conversion (round to nearest even) of the same fp32
+ *                       products, random values and exact ties of both kept-bit parities.
  */
 #include <stdint.h>
 #include <stdlib.h>

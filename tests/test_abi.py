@@ -109,6 +109,11 @@ def test_other_entry_points_reject_bad_arguments():
     assert "multiple of 1024" in L.uwc_last_error().decode()
     assert L.uwc_noise_perm(fake, 64, 96, fake, fake, None) == -1
     assert L.uwc_noise_rows(fake, 12, 64, 64, None, None, None, None, None, -1, -1, None, 0, None) == -1
+    # requested limbs or E copy without a corr buffer to write them into
+    assert L.uwc_noise_rows(fake, 16, 64, 64, None, None, None, fake, None, 0, -1, None, 3, None) == -1
+    assert "need corr" in L.uwc_last_error().decode()
+    assert L.uwc_noise_rows(fake, 16, 64, 64, fake, fake, fake, None, None, -1, 0, None, 3, None) == -1
+    assert "need corr" in L.uwc_last_error().decode()
     assert L.uwc_quant_act_f32(fake, 4, 96, 64, 64, fake, fake, None) == -1
     assert "power of two" in L.uwc_last_error().decode()
     assert L.uwc_quant_act_f32(fake, 4, 64, 0, 200, fake, fake, None) == -1

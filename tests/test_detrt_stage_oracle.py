@@ -195,3 +195,21 @@ def test_attention_rows_equals_full_attention():
     for f, p in zip(full, part):
         np.testing.assert_array_equal(f[:, rows].view(np.uint32) if f.dtype == np.float32 else f[:, rows],
                                       p.view(np.uint32) if p.dtype == np.float32 else p)
+
+
+@pytest.mark.parametrize("name", ["stage_tiny_qwen3", "stage_tiny_llama"])
+def test_layer_rows_equals_full_layer(name):
+    """layer_rows (the sampled-row form used to check every layer of the T = 8192 forward) is the
+    full layer's rows, bit for bit, on the referee fixtures' models (Qwen3 with q/k norms, Llama
+    without), first and last positions included; the full layer is pinned by the fixtures."""
+    d = _load(name)
+    m = S.model_from_fixture(d)
+    rng = np.random.default_rng(5)
+    T, D = 48, m.cfg["D"]
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    rows = [0, 1, 17, 30, 47]
+    for l in range(len(m.lins)):
+        full = S.layer(m, l, x)
+        part = S.layer_rows(m, l, x, rows)
+        np.testing.assert_array_equal(_u32(full[rows]), _u32(part))
+        x = full

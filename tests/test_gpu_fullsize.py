@@ -7,9 +7,11 @@ miner/ampere/bench/crosscheck.py:62-76):
               mined forward (exact output, all 131,072 tile messages and digests, ~2000 winners),
               every nonce's output and winners against the single-nonce path;
   configs[1]  the four linears of a Qwen3-1.7B layer at M = 2048 through DetLinear;
-  configs[3]  Llama-3.1-8B o and gate_up linears at M = 8192 (sampled rows: rows are independent);
+  configs[3]  the four Llama-3.1-8B linears at M = 8192 as int32 GEMMs, and qkv / down through
+              DetLinear with the 128-wide Hadamard block (sampled rows: rows are independent);
   configs[4]  exact attention at T = 8192 (16 / 8 heads, hd 128) on sampled query rows, one whole
-              decoder layer at T = 2048 with its stage-output root, and the pinned rope table;
+              decoder layer at T = 2048 with its stage-output root, and the pinned rope table (the
+              28-layer forward at T = 8192 is checked layer by layer in test_gpu_e2e.py);
 plus DetLinear's mined path and a sweep after a new block template.
 
 The oracle work is bounded to tens of seconds per test on the GPU box's host cores."""
@@ -134,13 +136,14 @@ def test_qwen3_layer_linears_2048(dev):
 
 
 def test_llama_prefill_8192_sampled_rows(dev):
-    """configs[3] prefill: Llama-3.1-8B o (4096 -> 4096) and gate_up (4096 -> 28672) at M = 8192;
-    the whole product runs on the GPU, sampled rows (first, last, random) are checked."""
+    """configs[3] prefill: the four Llama-3.1-8B linears at M = 8192, qkv (4096 -> 6144), o
+    (4096 -> 4096), gate_up (4096 -> 28672) and down (14336 -> 4096); the whole product runs on the
+    GPU, sampled rows (first, last, random) are checked."""
     from uwc_amd import ops
-    M, k = 8192, 4096
+    M = 8192
     rng = np.random.default_rng(8192)
     rows = np.unique(np.concatenate([np.arange(64), np.arange(M - 64, M), rng.integers(0, M, 128)]))
-    for nm, n in (("o", 4096), ("gu", 28672)):
+    for nm, n, k in (("qkv", 6144, 4096), ("o", 4096, 4096), ("gu", 28672, 4096), ("down", 4096, 14336)):
         X = rng.integers(-64, 65, size=(M, k), dtype=np.int8)
         W = rng.integers(-64, 65, size=(n, k), dtype=np.int8)
         C = ops.igemm_i32(torch.from_numpy(X).to(dev), torch.from_numpy(W).to(dev))
@@ -149,6 +152,29 @@ def test_llama_prefill_8192_sampled_rows(dev):
         torch.cuda.empty_cache()
         say(f"llama prefill: {nm} {M}x{k} -> {n}, {len(rows)} rows on the oracle")
         assert np.array_equal(sampled, O.igemm(X[rows], W)), nm
+
+
+@pytest.mark.parametrize("nm,n,k", [("qkv", 6144, 4096), ("down", 4096, 14336)])
+def test_llama_prefill_8192_detlinear(dev, nm, n, k):
+    """configs[3] prefill through DetLinear (quant_act with Llama's 128-wide Hadamard block, exact
+    GEMM, fused dequant; results/rules4/arch-llama3.1-8b-5090.json:4) at M = 8192: fp32 outputs of
+    sampled rows bit for bit against the oracle's detrt linear (rows are independent)."""
+    from uwc_amd import detrt
+    M = 8192
+    g = torch.Generator(device=dev)
+    g.manual_seed(n + k)
+    lin = detrt.DetLinear(torch.randn((n, k), device=dev, generator=g) * 0.02, dev, 128)
+    assert lin.bs == 128
+    x = torch.randn((M, k), device=dev, generator=g)
+    y = lin(x)
+    rng = np.random.default_rng(k)
+    rows = np.unique(np.concatenate([np.arange(16), np.arange(M - 16, M), rng.integers(0, M, 64)]))
+    rd = torch.from_numpy(rows).to(dev)
+    got = y[rd].cpu().numpy()
+    xs = x[rd].cpu().numpy()
+    say(f"llama prefill detlinear: {nm} {M}x{k} -> {n}, {len(rows)} rows on the oracle")
+    want = O.det_linear(xs, lin.Wq.cpu().numpy(), lin.sw.cpu().numpy(), lin.bs)[-1]
+    assert np.array_equal(_u32(got), _u32(want)), nm
 
 
 def test_attention_8192_sampled_rows(dev):

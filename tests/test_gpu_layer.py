@@ -214,6 +214,36 @@ def test_attention_stored_equals_recomputed(dev, B, T, H, Hkv, hd):
     assert torch.equal(a.view(torch.int32), b.view(torch.int32))
 
 
+def test_attention_stored_on_two_streams(dev):
+    """Stored-exponentials attention calls queued on two streams at once, of different sizes, each
+    equal to the recomputing form: every call has its own scratch (stream-ordered allocation)."""
+    from uwc_amd import detgpu
+    g = torch.Generator(device=dev)
+    g.manual_seed(2)
+    H, Hkv, hd = 8, 4, 128
+    inv = float(S.inv_sqrt_hd(hd))
+    cases = []
+    for T in (1500, 900):
+        mk = lambda *s: torch.randint(-127, 128, s, dtype=torch.int8, device=dev, generator=g)  # noqa: E731
+        sc = lambda *s: torch.rand(s, device=dev, generator=g) * 3e-2 + 1e-3  # noqa: E731
+        cases.append((T, (mk(T, H, hd), sc(T, H, 1), mk(T, Hkv, hd), sc(T, Hkv, 1), mk(T, Hkv, hd), sc(T, Hkv, 1))))
+    want = [detgpu.attention(*a, 1, T, H, Hkv, inv, stored_exp=False) for T, a in cases]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = []
+    for _ in range(3):
+        got = []
+        for st, (T, a) in zip(streams, cases):
+            st.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(st):
+                got.append(detgpu.attention(*a, 1, T, H, Hkv, inv, stored_exp=True))
+        outs.append(got)
+    torch.cuda.synchronize()
+    for got in outs:
+        for x, y in zip(got, want):
+            assert torch.equal(x.view(torch.int32), y.view(torch.int32))
+
+
 def _fixture_model(name, dev):
     from uwc_amd import detgpu
     d = np.load(os.path.join(GOLDEN, name + ".npz"))

@@ -103,6 +103,52 @@ def test_noise_perm_matches_python_and_invariants(r):
         assert np.array_equal(first[8 * i:8 * i + n], f[:n]) and np.array_equal(second[8 * i:8 * i + n], s[:n])
 
 
+def test_noise_distributions():
+    """The noise rules' distributions at large counts (reference.py:74-93): E = (byte & 63) - 32 takes
+    each of the 64 values in [-32, 31] equally often, and the pair rule gives a uniform first index
+    and a uniform nonzero XOR distance first ^ second in [1, r - 1]. A wrong mask, offset or pair
+    formula (e.g. byte % 63, or second = first + 1 + ...) fails the chi-square bounds (p < 1e-6)."""
+    key = bytes(range(7, 39))
+    E = O.uniform_matrix(O.SEED_LABEL_A, key, 4096, 64).ravel()
+    cnt = np.bincount(E.astype(np.int64) + 32, minlength=64)
+    assert cnt.size == 64 and cnt.min() > 0
+    exp = E.size / 64
+    assert ((cnt - exp) ** 2 / exp).sum() < 140  # chi-square, 63 dof: p ~ 1e-7 at 140
+    for r in (64, 128):
+        P = O.perm_packed(O.SEED_LABEL_B, key, 1 << 18, r)
+        first, second = (P & 0xFFFF).astype(np.int64), (P >> 16).astype(np.int64)
+        cf = np.bincount(first, minlength=r)
+        dist = np.bincount(first ^ second, minlength=r)
+        assert cf.size == r and dist[0] == 0 and dist.size == r
+        e1, e2 = first.size / r, first.size / (r - 1)
+        lim = r - 1 + 7 * np.sqrt(2 * (r - 1))  # mean + 7 sd of chi-square with r - 1 dof
+        assert ((cf - e1) ** 2 / e1).sum() < lim
+        assert ((dist[1:] - e2) ** 2 / e2).sum() < lim
+
+
+def test_scale_bf16_against_torch_cast():
+    """The OUT_BF16 epilogue (kernels.cu:440-445, 687-704): f32(acc) * a_scale * b_scale, each
+    product rounded to fp32, then to bf16 by round-to-nearest-even. Pinned by torch's own
+    fp32 -> bf16 conversion of the same fp32 products, on random values and on exact ties (low 16
+    bits 0x8000) with the kept bit 0 and 1, both signs."""
+    import torch
+    rng = np.random.default_rng(16)
+    m, n = 64, 512
+    acc = rng.integers(-2 ** 31, 2 ** 31, size=(m, n), dtype=np.int64).astype(np.int32)
+    ties = np.array([2 ** 24 + 2 ** 16, 2 ** 24 + 2 ** 17 + 2 ** 16, 2 ** 23 + 2 ** 15, 2 ** 23 + 2 ** 16 + 2 ** 15,
+                     2 ** 30 + 2 ** 22, 2 ** 30 + 2 ** 23 + 2 ** 22], np.int64)
+    acc[0, :len(ties)] = ties
+    acc[0, len(ties):2 * len(ties)] = -ties
+    a_scale = rng.uniform(1e-4, 2.0, m).astype(np.float32)
+    b_scale = rng.uniform(1e-4, 2.0, n).astype(np.float32)
+    a_scale[0] = 1.0
+    b_scale[:2 * len(ties)] = 1.0
+    f = (acc.astype(np.float32) * a_scale[:, None]) * b_scale[None, :]
+    assert ((f[0, :2 * len(ties)].view(np.uint32) & 0xFFFF) == 0x8000).all()
+    want = torch.from_numpy(f).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(O.scale_bf16(acc, a_scale, b_scale), want)
+
+
 def test_noise_apply_and_projection_brute_force():
     rng = np.random.default_rng(3)
     rows, k, r = 16, 256, 64
@@ -249,6 +295,45 @@ def test_mined_forward_denoise_exact():
     noisy = O.igemm(res["ApEA"], res["BpEBt"]).astype(np.int64)
     assert np.array_equal(((noisy - corr) & 0xFFFFFFFF).astype(np.uint32).view(np.int32), res["out"])
     assert 0 < len(res["winners"]) < 64
+    # the composed denoise (limb count from maxabs, Horner over limbs) gives the same exact product
+    assert np.array_equal(O.denoise(noisy, res["corrA"], res["corrB"], res["maxabs"]), res["out"])
+
+
+@pytest.mark.parametrize("L", [1, 2, 3, 4])
+def test_denoise_every_limb_count_closed_form(L):
+    """O.denoise (kernels.cu:598-673) at each limb count: projections X, Y whose max |value| lands
+    in limb range L, written as balanced base-128 limbs beside noise copies E_A, E_B, make the
+    denoise equal the closed form noisy - X E_B^T - E_A Y^T exactly. A limb count one too small,
+    or Horner shifts of 6 instead of 7, breaks it (a dropped limb or a wrong radix fails here)."""
+    rng = np.random.default_rng(40 + L)
+    m, n, r = 64, 96, 64
+    caps = (63, 8127, 1040319, 127 * 262144)
+    lo, hi = (0, *caps[:3])[L - 1], caps[L - 1]
+    X = rng.integers(-hi, hi + 1, size=(m, r)).astype(np.int32)
+    Y = rng.integers(-hi, hi + 1, size=(n, r)).astype(np.int32)
+    X[3, 5] = hi  # max |X| in (lo, hi]: exactly L limbs
+    assert lo < np.abs(X).max() <= hi and np.abs(Y).max() <= hi
+    EA = rng.integers(-32, 32, size=(m, r), dtype=np.int8)
+    EB = rng.integers(-32, 32, size=(n, r), dtype=np.int8)
+    corrA = np.zeros((4, m, 2 * r), np.int8)
+    corrB = np.zeros((4, n, 2 * r), np.int8)
+    O.write_limbs(X, corrA, 0)
+    O.write_limbs(Y, corrB, r)
+    corrA[:, :, r:] = EA
+    corrB[:, :, :r] = EB
+    noisy = rng.integers(-2 ** 31, 2 ** 31, size=(m, n)).astype(np.int64)
+    mx = np.array([np.abs(X).max(), np.abs(Y).max()], np.int32)
+    want = noisy - X.astype(np.int64) @ EB.astype(np.int64).T - EA.astype(np.int64) @ Y.astype(np.int64).T
+    want = (want & 0xFFFFFFFF).astype(np.uint32).view(np.int32)
+    assert O.limbs_needed(int(mx.max())) == L
+    assert np.array_equal(O.denoise(noisy, corrA, corrB, mx), want)
+    if L > 1:
+        assert not np.array_equal(O.denoise(noisy, corrA, corrB, mx, lmax=L - 1), want)
+        # a wrong radix in the Horner step
+        bad = np.zeros((m, n), np.int64)
+        for li in range(L - 1, -1, -1):
+            bad = (bad << 6) + corrA[li].astype(np.int64) @ corrB[li].astype(np.int64).T
+        assert not np.array_equal(((noisy - bad) & 0xFFFFFFFF).astype(np.uint32).view(np.int32), want)
 
 
 # ------------------------------------------------------------------ detrt golden fixtures

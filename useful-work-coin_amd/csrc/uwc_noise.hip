@@ -166,7 +166,9 @@ extern "C" int uwc_noise_rows(const int8_t* src, int rows, int k, int r, const i
   if (r > NRW_MAXR) return uwc_fail("uwc_noise_rows: r=%d above %d", r, NRW_MAXR);
   if (((uintptr_t)src & 3u) || (dst && ((uintptr_t)dst & 3u))) return uwc_fail("uwc_noise_rows: src/dst must be 4-byte aligned");
   if (dst && (!E || !Pn)) return uwc_fail("uwc_noise_rows: noising needs E and Pn");
-  if (!corr) corr_off = ecopy_off = -1;
+  if (!corr && ((corr_off >= 0 && Pp) || (ecopy_off >= 0 && E)))
+    return uwc_fail("uwc_noise_rows: the limbs (corr_off) and the E copy (ecopy_off) need corr");
+  if (!corr) corr_off = ecopy_off = -1;  // nothing to write them from: no projection, no E
   if (corr_off >= 0 || ecopy_off >= 0) {
     if (lmax < 1 || lmax > 4) return uwc_fail("uwc_noise_rows: limbs need lmax in 1..4");
     if ((corr_off >= 0 && corr_off != 0 && corr_off != r) || (ecopy_off >= 0 && ecopy_off != 0 && ecopy_off != r))

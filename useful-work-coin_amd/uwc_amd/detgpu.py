@@ -116,21 +116,12 @@ def qkv_post(acc, s1, sw, qnw, knw, cos, sin, T: int, H: int, Hkv: int, eps: flo
     return qkv_post_vt(acc, s1, sw, qnw, knw, cos, sin, T, H, Hkv, eps, qknorm)[:6]
 
 
-# The exponentials scratch of the stored-exp attention: one device buffer per device, grown to the
-# largest call so far and reused (a 28-layer forward allocates it once). Calls whose scratch would
-# exceed ATTN_SCRATCH_MAX bytes recompute the exponentials instead.
+# The exponentials scratch of the stored-exp attention is allocated per call from torch's caching
+# allocator on the current stream: stream-ordered (two calls on two streams never share it, and a
+# buffer freed after a call is reused only by work queued after that call) and, after the first
+# call of a size, without a device allocation. Calls whose scratch would exceed ATTN_SCRATCH_MAX
+# bytes recompute the exponentials instead.
 ATTN_SCRATCH_MAX = 16 << 30
-_ESCRATCH: dict = {}
-
-
-def attention_scratch(nbytes: int, device) -> torch.Tensor:
-    """The cached exponentials scratch of at least nbytes on device (float32, 16-byte aligned)."""
-    key = str(device)
-    buf = _ESCRATCH.get(key)
-    if buf is None or buf.numel() * 4 < nbytes:
-        _ESCRATCH.pop(key, None)
-        buf = _ESCRATCH[key] = torch.empty((nbytes + 3) // 4, dtype=F32, device=device)
-    return buf
 
 
 def attention(qq, qs, kq, ks, vq, vs, B: int, T: int, H: int, Hkv: int, inv_sqrt_hd_f32: float, vt=None,
@@ -157,7 +148,7 @@ def attention(qq, qs, kq, ks, vq, vs, B: int, T: int, H: int, Hkv: int, inv_sqrt
     args = (qq.data_ptr(), qs.data_ptr(), kq.data_ptr(), ks.data_ptr(), vt.data_ptr(), vs.data_ptr(), B, T, H, Hkv,
             hd, float(np.float32(inv_sqrt_hd_f32)), o.data_ptr())
     if stored_exp and nbytes > 0:
-        es = attention_scratch(nbytes, qq.device)
+        es = torch.empty((nbytes + 3) // 4, dtype=F32, device=qq.device)
         _lib.call("uwc_attention_ws", *args, es.data_ptr(), es.numel() * 4, _stream())
     else:
         _lib.call("uwc_attention", *args, _stream())

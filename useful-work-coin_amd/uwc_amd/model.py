@@ -181,24 +181,26 @@ class MinedLinear(nn.Module):
 class _SharedOutput:
     """The fused output of one MinedLinear for the input it was last called with, handed out a
     slice at a time to the modules that stand in for the original linears. A slice is served
-    from the cache while the input is the same tensor (object and version); once every part has
-    taken its slice the cache is dropped, so no activation outlives its layer."""
+    from the cache while the input is the same tensor object at the same version (the cache
+    holds the input itself, so a later tensor that reuses its address never matches); once
+    every part has taken its slice the cache and the input are dropped, so no activation
+    outlives its layer."""
 
     def __init__(self, ml: MinedLinear):
         self.ml = ml
-        self._key = None
+        self._x = None
+        self._version = None
         self._parts = None
         self._pending = 0
 
     def part(self, x: torch.Tensor, index: int) -> torch.Tensor:
-        key = (id(x), x._version)
-        if self._parts is None or self._key != key:
+        if self._parts is None or self._x is not x or self._version != x._version:
             self._parts = torch.split(self.ml(x), self.ml.splits, dim=-1)
-            self._key, self._pending = key, len(self._parts)
+            self._x, self._version, self._pending = x, x._version, len(self._parts)
         y = self._parts[index]
         self._pending -= 1
         if self._pending == 0:
-            self._parts = self._key = None
+            self._parts = self._x = self._version = None
         return y
 
 
