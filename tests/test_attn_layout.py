@@ -173,3 +173,34 @@ def test_attention_layout_matches_oracle(B, T, H, Hkv, hd):
     assert maxaddr["qq"] < N * H * hd and maxaddr["kq"] < N * Hkv * hd
     assert maxaddr["vt"] < B * Hkv * hd * Tp and maxaddr["o"] < N * H * hd
     assert maxaddr["ks"] < N * Hkv and maxaddr["qs"] < N * H
+
+
+def _at_block(i, ntiles, H, Hkv, B):
+    """uwc_attn.hip at_block: block id -> (q tile, head, sequence)."""
+    G, units = H // Hkv, B * Hkv
+    if units % 8 == 0:
+        x, j = i & 7, i >> 3
+        per_tile = units // 8 * G
+        qt = ntiles - 1 - j // per_tile
+        r = j % per_tile
+        u = x + 8 * (r // G)
+        return qt, (u % Hkv) * G + r % G, u // Hkv
+    return ntiles - 1 - i % ntiles, (i // ntiles) % H, i // (ntiles * H)
+
+
+@pytest.mark.parametrize("ntiles,H,Hkv,B", [(128, 16, 8, 1), (64, 32, 8, 1), (5, 8, 8, 2), (3, 4, 2, 4),
+                                            (7, 6, 3, 1), (16, 16, 16, 1), (2, 8, 1, 3)])
+def test_block_mapping_is_a_bijection_and_xcd_local(ntiles, H, Hkv, B):
+    """Every (q tile, head, sequence) gets exactly one block; when the kv units split over the 8
+    XCDs (id % 8), each XCD's blocks read the keys of its own units only, and within an XCD the
+    q tiles come longest first."""
+    total = ntiles * H * B
+    got = [_at_block(i, ntiles, H, Hkv, B) for i in range(total)]
+    assert sorted(got) == sorted((qt, h, b) for qt in range(ntiles) for h in range(H) for b in range(B))
+    if B * Hkv % 8 == 0:
+        G = H // Hkv
+        for x in range(8):
+            mine = [got[i] for i in range(x, total, 8)]
+            assert {(b, h // G) for _, h, b in mine} == {((u // Hkv), u % Hkv) for u in range(x, B * Hkv, 8)}
+            qts = [qt for qt, _, _ in mine]
+            assert qts == sorted(qts, reverse=True)

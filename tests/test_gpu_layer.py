@@ -194,6 +194,30 @@ def test_attention(dev, B, T, H, Hkv, hd, stored):
         np.testing.assert_array_equal(_u32(o[sl]), _u32(ref.transpose(1, 0, 2).reshape(T, H * hd)))
 
 
+@pytest.mark.parametrize("stored", [False, True])
+@pytest.mark.parametrize("period,T,hd", [(7, 300, 64), (3, 200, 128), (64, 260, 32)])
+def test_attention_repeated_keys(dev, period, T, hd, stored):
+    """Keys, values and their scales repeating every `period` positions give exact ties in e * vs
+    between keys (the case in which the kernel's candidate tracking for the row statistic pm
+    must fall back to the full sweep), mixed with rows that have none (period 64 with 16-key lane
+    groups): both forms against the oracle's attention, bit for bit."""
+    from uwc_amd import detgpu
+    rng = np.random.default_rng(period * 31 + T)
+    H, Hkv = 4, 2
+    qq = rng.integers(-127, 128, (T, H, hd)).astype(np.int8)
+    base = lambda *shape: rng.integers(-127, 128, (period,) + shape).astype(np.int8)  # noqa: E731
+    kq = np.resize(base(Hkv, hd), (T, Hkv, hd)).astype(np.int8)
+    vq = np.resize(base(Hkv, hd), (T, Hkv, hd)).astype(np.int8)
+    qs = rng.uniform(1e-3, 3e-2, (T, H, 1)).astype(np.float32)
+    ks = np.resize(rng.uniform(1e-3, 3e-2, (period, Hkv, 1)).astype(np.float32), (T, Hkv, 1))
+    vs = np.resize(rng.uniform(1e-3, 3e-2, (period, Hkv, 1)).astype(np.float32), (T, Hkv, 1))
+    inv = S.inv_sqrt_hd(hd)
+    o = detgpu.attention(_t(qq, dev), _t(qs, dev), _t(kq, dev), _t(ks, dev), _t(vq, dev), _t(vs, dev), 1, T, H, Hkv,
+                         float(inv), stored_exp=stored).cpu().numpy()
+    _, _, _, ref = S.attention(qq.astype(np.int64), qs, kq.astype(np.int64), ks, vq.astype(np.int64), vs, inv)
+    np.testing.assert_array_equal(_u32(o), _u32(ref.transpose(1, 0, 2).reshape(T, H * hd)))
+
+
 @pytest.mark.parametrize("B,T,H,Hkv,hd", [(1, 2048, 16, 8, 128), (2, 1000, 4, 4, 64), (1, 777, 8, 2, 32)])
 def test_attention_stored_equals_recomputed(dev, B, T, H, Hkv, hd):
     """The stored-exponentials form equals the recomputing one bit for bit at sizes the oracle

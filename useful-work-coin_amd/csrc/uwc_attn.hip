@@ -101,6 +101,28 @@ __device__ __forceinline__ float at_get(const float4& v, int i) {
   return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
 }
 
+// Block id -> (q tile, head, sequence). Workgroups are dispatched round-robin over the 8 XCDs
+// (id % 8). When the (sequence, kv head) units split evenly over them, XCD x takes units x,
+// x + 8, ..., so every key and value tile an XCD reads belongs to its own units: at T = 8192 one
+// kv head's K and V (1 MiB each) stay in the XCD's 4 MB L2, where the plain order had every XCD
+// read all 8 kv heads' 8 MiB from the Infinity Cache for each 16-query wave. Within an XCD the
+// longest rows (highest q tile) go first.
+__device__ __forceinline__ void at_block(int id, int ntiles, int H, int Hkv, int B, int& qt, int& h, int& bseq) {
+  const int G = H / Hkv, units = B * Hkv;
+  if (units % 8 == 0) {
+    const int x = id & 7, j = id >> 3;
+    const int per_tile = units / 8 * G;  // this XCD's blocks of one q tile
+    qt = ntiles - 1 - j / per_tile;
+    const int r = j % per_tile, u = x + 8 * (r / G);
+    h = (u % Hkv) * G + r % G;
+    bseq = u / Hkv;
+  } else {
+    qt = ntiles - 1 - id % ntiles;
+    h = (id / ntiles) % H;
+    bseq = id / (ntiles * H);
+  }
+}
+
 // Exp tiles of the stored form: wave block wq (queries 16 wq .. + 15) of a (sequence, head) owns
 // tiles 0 .. wq / 4 (its key tiles), the blocks' tiles back to back: block wq starts at tile
 // (a + 1)(2 a + b) for wq = 4 a + b, and a (sequence, head) holds at_tiles(Tp) of them.
@@ -113,7 +135,7 @@ __host__ __device__ constexpr u64 at_tiles(u64 Tp) { return at_tile0(Tp / 16); }
 // element), two tiles ahead. The same values go through the same operations, so both forms give
 // the same bits.
 template <int HD, bool ES>
-__global__ void __launch_bounds__(256, ES && HD == 128 ? 2 : 3) attention_kernel(const i8* __restrict__ qq, const float* __restrict__ qs,
+__global__ void __launch_bounds__(256, HD == 128 ? 2 : 3) attention_kernel(const i8* __restrict__ qq, const float* __restrict__ qs,
                                                         const i8* __restrict__ kq, const float* __restrict__ ks,
                                                         const i8* __restrict__ vt, const float* __restrict__ vs, int T,
                                                         int Tp, int H, int Hkv, float inv_sqrt, float* __restrict__ o,
@@ -123,10 +145,11 @@ __global__ void __launch_bounds__(256, ES && HD == 128 ? 2 : 3) attention_kernel
   __shared__ __attribute__((aligned(16))) float at_slot[4][2][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int ql = lane & 15, g = lane >> 4;
-  // longest rows first: the q tile index counts down
-  const int q0 = (gridDim.x - 1 - blockIdx.x) * 64 + wave * 16;
+  int qt, h, bseq;
+  at_block((int)blockIdx.x, Tp / 64, H, Hkv, (int)(gridDim.x / (u32)(Tp / 64 * H)), qt, h, bseq);
+  const int q0 = qt * 64 + wave * 16;
   if (q0 >= T) return;  // whole waves only; the kernel has no workgroup barriers
-  const int h = blockIdx.y, bseq = blockIdx.z, hk = h / (H / Hkv);
+  const int hk = h / (H / Hkv);
   // 32-bit offsets: the host checks B * T * max(H, Hkv) * HD < 2^31
   const u32 nb = (u32)(bseq * T);
   const int qi = q0 + ql, qc = min(qi, T - 1);
@@ -190,13 +213,84 @@ __global__ void __launch_bounds__(256, ES && HD == 128 ? 2 : 3) attention_kernel
     for (int kt = 0; kt < nfull; kt++) body(kt, std::false_type{});
     for (int kt = nfull; kt < nkt; kt++) body(kt, std::true_type{});
   };
+  // over tiles 0 .. nkt - 1 with loads two tiles ahead: prefetch(kt, slot) loads tile kt into
+  // register set slot, body(kt, slot) uses it (slot is a compile-time 0 or 1)
+  auto pipelined = [&](auto prefetch, auto body) AT_AI {
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    if (nkt > 0) prefetch(0, S0{});
+    if (nkt > 1) prefetch(1, S1{});
+    for (int kt = 0; kt < nkt; kt += 2) {
+      body(kt, S0{});
+      if (kt + 2 < nkt) prefetch(kt + 2, S0{});
+      if (kt + 1 < nkt) {
+        body(kt + 1, S1{});
+        if (kt + 3 < nkt) prefetch(kt + 3, S1{});
+      }
+    }
+  };
+  // The K fragments and the key scale of one 64-key tile, fetched two tiles ahead of their use in
+  // sweeps 1 and 2 (each tile's loads then overlap the previous tiles' work instead of stalling
+  // the wave: with two waves per SIMD a wave's own loads are its main wait)
+  struct KTile {
+    v4i kf[4][NC];
+    float ks, vs;
+  };
+  auto kfetch = [&](int kt, KTile& t) AT_AI {
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+      const int kr = min(kt * 64 + 16 * b + ql, T - 1);
+      const i8* kp = kbase + (nb + kr) * (u32)(Hkv * HD);
+#pragma unroll
+      for (int c = 0; c < NC; c++) {
+        const int d0 = 64 * c + 16 * g;
+        t.kf[b][c] = d0 < HD ? *reinterpret_cast<const v4i*>(kp + d0) : at_zero4();
+      }
+    }
+    t.ks = ks[sc_base + (u32)min(kt * 64 + lane, T - 1) * (u32)Hkv];
+    t.vs = vs[sc_base + (u32)min(kt * 64 + lane, T - 1) * (u32)Hkv];
+  };
+  // scores(kt, ...) from a fetched tile: the same MFMAs, scales and mask
+  auto scores_t = [&](int kt, const KTile& t, float S[4][4], auto mask) AT_AI {
+    constexpr bool MASK = decltype(mask)::value;
+    float4 skv[4];
+    sk_slot[lane] = t.ks;
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int b = 0; b < 4; b++) skv[b] = *reinterpret_cast<const float4*>(sk_slot + 16 * b + 4 * g);
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+      v4i acc = at_zero4();
+#pragma unroll
+      for (int c = 0; c < NC; c++) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(t.kf[b][c], qf[c], acc, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float sv = __fmul_rn(__fmul_rn(__fmul_rn((float)acc[i], my_qs), at_get(skv[b], i)), inv_sqrt);
+        if constexpr (MASK) {
+          const int j = kt * 64 + 16 * b + 4 * g + i;
+          S[b][i] = (j <= qi && j < T) ? sv : -__int_as_float(0x7f800000);
+        } else {
+          S[b][i] = sv;
+        }
+      }
+    }
+  };
+  // a sweep over the key tiles with the tiles fetched two ahead; full tiles unmasked
+  auto ksweep = [&](auto body) AT_AI {
+    KTile kb[2];
+    pipelined([&](int kt, auto sl) AT_AI { kfetch(kt, kb[decltype(sl)::value]); },
+              [&](int kt, auto sl) AT_AI {
+                float S[4][4];
+                if (kt < nfull) scores_t(kt, kb[decltype(sl)::value], S, std::false_type{});
+                else scores_t(kt, kb[decltype(sl)::value], S, std::true_type{});
+                body(kt, S, kb[decltype(sl)::value]);
+              });
+  };
 
   // sweep 1: row max
   float mx = -__int_as_float(0x7f800000);
-  sweep([&](int kt, auto mask) {
-    float S[4][4];
-    float4 skv[4];
-    scores(kt, S, skv, mask);
+  ksweep([&](int kt, const float (&S)[4][4], const KTile&) AT_AI {
 #pragma unroll
     for (int b = 0; b < 4; b++)
 #pragma unroll
@@ -206,11 +300,26 @@ __global__ void __launch_bounds__(256, ES && HD == 128 ? 2 : 3) attention_kernel
 
   // sweep 2: exact denominator (fixed point at 2^41); masked entries give det_exp(-inf) = 0.
   // A tile's 16 terms per lane sum exactly in float64 (< 2^46), then join a u64 total.
+  //
+  // Sweep 3's statistic pm = max_j fl(fl(e_j / den) vs_j) is found here from candidates: every
+  // lane keeps the largest fp32 product p1 = fl(e vs) of its keys with that key's e and vs, and
+  // the largest product p2 among its other keys. With q_j = fl(e_j / den) and pv_j = fl(q_j vs_j),
+  // pv_j lies within a factor (1 +- 2^-24)^2 of e_j vs_j / den, and fl(e vs) within (1 +- 2^-24)
+  // of e vs; so a key whose product is at most p1 (1 - 2^-21) cannot have a larger pv than the
+  // lane's best key (products are normal numbers: the best is at least vs >= 1e-8 / 127, and a
+  // key whose product underflows is far below it). When every lane of the wave has
+  // p2 <= fl(p1 (1 - 2^-16)) (stricter than needed), pm is the max over the lanes' best keys of
+  // their pv, the same bits sweep 3 gives; otherwise (a near tie, e.g. repeated keys) the wave
+  // runs sweep 3.
   u64 dsum = 0;
-  sweep([&](int kt, auto mask) {
-    float S[4][4];
-    float4 skv[4];
-    scores(kt, S, skv, mask);
+  float p1 = -1.f, p2 = -1.f, e1 = 0.f, v1 = 0.f;
+  ksweep([&](int kt, const float (&S)[4][4], const KTile& t) AT_AI {
+    float4 svv[4];
+    sv_slot[lane] = t.vs;
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int b = 0; b < 4; b++) svv[b] = *reinterpret_cast<const float4*>(sv_slot + 16 * b + 4 * g);
+    __builtin_amdgcn_wave_barrier();
     double part = 0.0;
 #pragma unroll
     for (int b = 0; b < 4; b++) {
@@ -219,6 +328,12 @@ __global__ void __launch_bounds__(256, ES && HD == 128 ? 2 : 3) attention_kernel
       for (int i = 0; i < 4; i++) {
         e[i] = at_exp(__fsub_rn(S[b][i], mx));
         part += at_fix41(e[i]);
+        const float vsj = at_get(svv[b], i), pr = __fmul_rn(e[i], vsj);
+        const bool nb = pr > p1;
+        p2 = nb ? p1 : fmaxf(p2, pr);
+        p1 = nb ? pr : p1;
+        e1 = nb ? e[i] : e1;
+        v1 = nb ? vsj : v1;
       }
       if constexpr (ES) *reinterpret_cast<float4*>(ewave + kt * 1024 + b * 256) = float4{e[0], e[1], e[2], e[3]};
     }
@@ -242,26 +357,12 @@ __global__ void __launch_bounds__(256, ES && HD == 128 ? 2 : 3) attention_kernel
     for (int b = 0; b < 4; b++) out[b] = *reinterpret_cast<const float4*>(sv_slot + 16 * b + 4 * g);
     __builtin_amdgcn_wave_barrier();
   };
-  // over tiles 0 .. nkt - 1 with loads two tiles ahead: prefetch(kt, slot) loads tile kt into
-  // register set slot, body(kt, slot) uses it (slot is a compile-time 0 or 1)
-  auto pipelined = [&](auto prefetch, auto body) AT_AI {
-    using S0 = std::integral_constant<int, 0>;
-    using S1 = std::integral_constant<int, 1>;
-    if (nkt > 0) prefetch(0, S0{});
-    if (nkt > 1) prefetch(1, S1{});
-    for (int kt = 0; kt < nkt; kt += 2) {
-      body(kt, S0{});
-      if (kt + 2 < nkt) prefetch(kt + 2, S0{});
-      if (kt + 1 < nkt) {
-        body(kt + 1, S1{});
-        if (kt + 3 < nkt) prefetch(kt + 3, S1{});
-      }
-    }
-  };
-
-  // sweep 3: max of the V-scaled probabilities
+  // sweep 3: max of the V-scaled probabilities, only for waves with a near tie (see sweep 2)
   float pm = 0.f;
-  if constexpr (ES) {
+  const bool near_tie = p2 > __fmul_rn(p1, 0x1.fffep-1f);
+  if (__ballot(near_tie) == 0) {
+    pm = fmaxf(0.f, __fmul_rn(at_div(e1, rden), v1));
+  } else if constexpr (ES) {
     float4 eb[2][4];
     float vb[2];
     pipelined(
@@ -330,15 +431,16 @@ __global__ void __launch_bounds__(256, ES && HD == 128 ? 2 : 3) attention_kernel
   if constexpr (ES) {
     float4 eb[2][4];
     float vb[2];
+    v4i vfb[2][ND];  // the tile's V rows, fetched two tiles ahead with its exponentials and scales
     pipelined(
         [&](int kt, auto sl) AT_AI {
           eload(kt, eb[decltype(sl)::value]);
           vb[decltype(sl)::value] = vsload(kt);
+          vload(kt, vfb[decltype(sl)::value]);
         },
         [&](int kt, auto sl) AT_AI {
           constexpr int L = decltype(sl)::value;
-          v4i vf[ND];
-          vload(kt, vf);  // issued first: its latency overlaps the staging and the quantization
+          const v4i (&vf)[ND] = vfb[L];
           float4 svv[4];
           vsstage(vb[L], svv);
           float e[4][4];
@@ -398,7 +500,7 @@ static int attention_go(const char* fn, const int8_t* qq, const float* qs, const
   if ((int64_t)B * T * (H > Hkv ? H : Hkv) * hd >= (1LL << 31))
     return uwc_fail("%s: B * T * H * hd must be below 2^31 (32-bit offsets)", fn);
   const int Tp = ((T + 63) / 64) * 64;
-  const dim3 grid((unsigned)(Tp / 64), (unsigned)H, (unsigned)B);
+  const dim3 grid((unsigned)((long)(Tp / 64) * H * B));
   if (escratch) {
     if (escratch_bytes < uwc_attention_scratch_bytes(B, T, H))
       return uwc_fail("%s: escratch holds %llu bytes, %llu needed", fn, (unsigned long long)escratch_bytes,

@@ -91,3 +91,65 @@ __device__ __forceinline__ void fwht512_rows(float y[NG][8], int G, int lane, in
   }
 }
 
+
+// ------------------------------------------------------------------ the 16-per-lane layout
+// A wave holds two 512-element groups, lane bit 2 choosing the group; inside a group, lane L
+// holds the 16 consecutive elements 16 i .. 16 i + 15 with i = b0 + 2 b1 + 4 b3 + 8 b4 + 16 b5
+// (b = the bits of L). Stages h = 1, 2, 4, 8 then pair elements inside a lane, and stages
+// h = 16 .. 256 pair lane L with L ^ 1, ^ 2, ^ 8, ^ 16, ^ 32: lane bit 2, the one exchange the
+// VALU cannot do in one DPP operand, is never crossed. A cross-lane stage is one sign flip and
+// one add per element: the lower lane of a pair computes o + v = v + o (a + b), the upper one
+// o + (-v) = o - v (a - b), the same single rounded IEEE operation on the same two operands as
+// the reference's pair (a + b, a - b), with the partner's value o read through a DPP operand of
+// the add (or exchanged by v_permlane16/32_swap).
+__device__ __forceinline__ int fw16_index(int lane) {
+  return (lane & 3) | ((lane >> 1) & 0x1C);  // b0 + 2 b1 + 4 b3 + 8 b4 + 16 b5
+}
+
+// y[0..15]: the lane's elements of one double group; lbs = log2(bs), bs <= 512. Every lane of the
+// wave must be active.
+__device__ __forceinline__ void fwht16(float y[16], int lane, int lbs) {
+#pragma unroll
+  for (int lh = 0; lh < 4; lh++) {
+    if (lh < lbs) {
+      const int h = 1 << lh;
+#pragma unroll
+      for (int j = 0; j < 16; j++)
+        if (!(j & h)) {
+          const float a = y[j], b = y[j + h];
+          y[j] = __fadd_rn(a, b);
+          y[j + h] = __fsub_rn(a, b);
+        }
+    }
+  }
+  // stages h = 16, 32, 64 (lane bits 0, 1, 3): DPP quad_perm [1,0,3,2], [2,3,0,1], row_ror:8
+#pragma unroll
+  for (int lh = 4; lh < 7; lh++) {
+    if (lh < lbs) {
+      const int bit = lh == 4 ? 0 : lh == 5 ? 1 : 3;
+      const u32 sgn = (lane >> bit) & 1 ? 0x80000000u : 0u;
+#pragma unroll
+      for (int j = 0; j < 16; j++) {
+        const float v = y[j];
+        const float sv = __uint_as_float(__float_as_uint(v) ^ sgn);
+        const float o = lh == 4 ? qa_dpp<0xB1>(v) : lh == 5 ? qa_dpp<0x4E>(v) : qa_dpp<0x128>(v);
+        y[j] = __fadd_rn(o, sv);
+      }
+    }
+  }
+  // stages h = 128, 256 (lane bits 4, 5): the swap hands every lane both values of its pair
+#pragma unroll
+  for (int lh = 7; lh < 9; lh++) {
+    if (lh < lbs) {
+      const u32 sgn = (lane >> (lh - 3)) & 1 ? 0x80000000u : 0u;
+#pragma unroll
+      for (int j = 0; j < 16; j++) {
+        const u32 v = __float_as_uint(y[j]);
+        const auto ab = lh == 7 ? __builtin_amdgcn_permlane16_swap(v, v, false, false)
+                                : __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        // lower lane: a + b; upper lane: a + (-b)
+        y[j] = __fadd_rn(__uint_as_float(ab[0]), __uint_as_float(ab[1] ^ sgn));
+      }
+    }
+  }
+}
