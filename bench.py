@@ -49,6 +49,31 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def host_cpu() -> dict:
+    """The host the CPU baselines ran on: the CPU model (lscpu, else /proc/cpuinfo), os.cpu_count()
+    and the cores this process may run on."""
+    model = None
+    try:
+        import subprocess
+        for line in subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout.splitlines():
+            if line.startswith("Model name:"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except Exception:
+        model = None
+    if model is None:
+        try:
+            with open("/proc/cpuinfo") as f:
+                model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), None)
+        except OSError:
+            model = None
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        avail = None
+    return dict(cpu_model=model, cpu_count=os.cpu_count(), cpus_available=avail)
+
+
 def mfma_ceiling(torch):
     """Sustained int8 MFMA rate of the part (uwc_mfma_rate_probe: a register-only MFMA loop on every
     SIMD), with constant and with random operands, in TOP/s. The random-operand rate is the
@@ -239,7 +264,7 @@ def parity_and_cpu(args, res, torch, np, ops, O):
                   tile_messages_equal=bool(np.array_equal(d[..., :16], ref["msgs"])),
                   winners_equal=bool(wins == ref["winners"]), winners=len(wins),
                   tiles=int(d.shape[0] * 8 * d.shape[2] * 4))
-    cpu = dict(value=round(2.0 * m * n * k * nonces / t_cpu / 1e12, 4), unit="TOPS", cores=threads, kind="port",
+    cpu = dict(value=round(2.0 * m * n * k * nonces / t_cpu / 1e12, 4), unit="TOPS", cores=threads, kind="port", **host_cpu(),
                sample=f"{nonces} full mined forward(s) (commit, noise, projections, transcript of every tile, "
                       f"digests, denoise) at {m}x{n}x{k} r={r}, {t_cpu:.1f} s, oracle/uwc_oracle.c with {threads} "
                       f"OpenMP threads")
@@ -306,7 +331,7 @@ def detrt_layer(args, torch, np):
                               frac_of_peak=round(2.0 * macs / gemm_us / 1e6 / PEAK_INT8_TOPS, 4), per_linear=per,
                               kernel="uwc_igemm_dequant_f32 (exact int8 GEMM, fused fp32 dequant), graph-replayed"),
                host_ms_per_layer=round(host_dt * 1e3, 4),
-               cpu_baseline=dict(value=round(ctops, 4), unit="TOPS", cores=cores, kind="port",
+               cpu_baseline=dict(value=round(ctops, 4), unit="TOPS", cores=cores, kind="port", **host_cpu(),
                                  sample=f"quant_act + fp64 matmul + dequant, {ran}, {ct:.2f} s"))
     log(f"detrt layer: {out}")
     return out
@@ -422,7 +447,7 @@ def skinny_linears(args, torch, np):
     out["config1_mlp_up_64x2048x6144"] = dict(
         us=round(us, 2), bytes=byt, gbs=round(byt / us / 1e3, 1), hbm_frac=round(byt / us / 1e3 / PEAK_HBM_GBS, 4),
         tops=round(2.0 * 64 * 6144 * 2048 / us / 1e6, 2),
-        cpu_baseline=dict(value=round(ctops, 4), unit="TOPS", cores=cores, kind="port",
+        cpu_baseline=dict(value=round(ctops, 4), unit="TOPS", cores=cores, kind="port", **host_cpu(),
                           sample=f"quant_act + fp64 matmul + dequant, {ran}, {ct:.2f} s"))
     llama = LLAMA_LINEARS
     dec = {}
@@ -431,7 +456,7 @@ def skinny_linears(args, torch, np):
         ctops, ct, ran, cores = cpu_linears(torch, np, O, m, llama, budget_s=2.0)
         dec[f"M{m}"] = dict(us_per_layer=round(us, 2), bytes_per_layer=byt, gbs=round(byt / us / 1e3, 1),
                             hbm_frac=round(byt / us / 1e3 / PEAK_HBM_GBS, 4), per_linear=per,
-                            cpu_baseline=dict(value=round(ctops, 5), unit="TOPS", cores=cores, kind="port",
+                            cpu_baseline=dict(value=round(ctops, 5), unit="TOPS", cores=cores, kind="port", **host_cpu(),
                                               sample=f"quant_act + fp64 matmul + dequant, {ran}, {ct:.2f} s"))
     out["config4_llama8b_decode"] = dec
     log(f"skinny linears: {json.dumps(out)}")
@@ -464,7 +489,7 @@ def llama_prefill(args, torch, np):
     ctops, ct, ran, cores = cpu_linears(torch, np, O, 2048, {"o": (4096, 4096)}, budget_s=1.0)
     out = dict(us_per_layer=round(total_us, 1), tops=round(ops / total_us / 1e6, 1),
                frac_of_peak=round(ops / total_us / 1e6 / PEAK_INT8_TOPS, 4), per_linear=per,
-               cpu_baseline=dict(value=round(ctops, 4), unit="TOPS", cores=cores, kind="port",
+               cpu_baseline=dict(value=round(ctops, 4), unit="TOPS", cores=cores, kind="port", **host_cpu(),
                                  sample=f"quant_act + fp64 matmul + dequant of the o linear at M=2048 "
                                         f"(a quarter of the prefill rows), {ct:.2f} s"))
     log(f"llama prefill: {out}")
@@ -576,7 +601,7 @@ def qwen3_e2e(args, torch, np):
     ct = time.perf_counter() - t0
     cl_ops = 2.0 * Tc * D * ((H + 2 * Hkv) * hd + H * hd + 2 * I) + 2.0 * Tc * I * D
     out["cpu_baseline"] = dict(value=round(cl_ops / ct / 1e12, 5), unit="TOPS (linear ops / whole-layer time)",
-                               cores=threads, kind="port",
+                               cores=threads, kind="port", **host_cpu(),
                                sample=f"one decoder layer at T={Tc} through oracle/detrt_stage.py (numpy fp32 "
                                       f"ops, float64 BLAS GEMMs), {ct:.2f} s")
     out["gemm_tops_unit"] = "TOPS (linear + lm_head ops / whole-forward time)"
