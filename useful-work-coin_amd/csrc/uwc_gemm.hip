@@ -405,7 +405,9 @@ extern "C" int uwc_noisy_gemm(const int8_t* A, const int8_t* B, int m, int n, in
   const int cus = uwc_cu_count();
   const long t256 = (long)(m / 256) * (n / 256), rounds256 = (t256 + cus - 1) / cus;
   const bool fills = t256 >= cus && t256 * 10 >= rounds256 * cus * 9;
-  const bool k256 = k % 128 == 0 && k <= (1 << 24);  // the 256 x 256 DMA adds 32-bit lane offsets (255 k + 112)
+  // the 256 x 256 DMA adds 32-bit lane offsets (255 k + 112) and its row stores 32-bit offsets
+  // (31 ldc elements of 4 bytes): k and the output row stride stay below 2^24
+  const bool k256 = k % 128 == 0 && k <= (1 << 24) && n <= (1 << 24);
   // the 256 x 256 epilogue writes 16-byte (8-byte for bf16) row segments: rows must start aligned
   const bool vec_out = out_mode == OUT_NONE || (aligned16(out) && n % 4 == 0);
   if (m % 256 == 0 && n % 256 == 0 && k256 && vec_out && !(flags & FLAG_TILE128) && (!plain || fills))
@@ -475,7 +477,7 @@ extern "C" int uwc_noisy_gemm_many(int count, const int8_t* const* A, const int8
   if ((hash && !key) || (denoise && (!corrA || !corrB || !maxabs)))
     return uwc_fail("uwc_noisy_gemm_many: the flags need key / corrA, corrB, maxabs arrays");
   bool split = count >= 2 && hash && denoise && out_mode == OUT_I32 && !(flags & FLAG_TILE128) && m % 256 == 0 &&
-               n % 256 == 0 && k % 128 == 0 && k <= (1 << 24);
+               n % 256 == 0 && k % 128 == 0 && k <= (1 << 24) && n <= (1 << 24);
   for (int i = 0; i < count; i++) {
     if (int st = gemm_check(A[i], B, m, n, k, r, denoise ? corrA[i] : nullptr, denoise ? corrB[i] : nullptr,
                             denoise ? maxabs[i] : nullptr, lmax, hash ? key[i] : nullptr, target,

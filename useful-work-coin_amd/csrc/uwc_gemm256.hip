@@ -808,15 +808,25 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
         u8* base = reinterpret_cast<u8*>(I.out) + ((long)row0 * p.ldc + col) * ES;
         float4 sw{};
         if constexpr (OUT != OUT_I32) sw = float4{p.b_scale[col], p.b_scale[col + 1], p.b_scale[col + 2], p.b_scale[col + 3]};
+        // the four LDS reads first, then the stores: read, wait, store in turn put an LDS round
+        // trip in front of every one of a storer's 64 stores per item
+        v4i xs[4];
+        float ascs[4];
 #pragma unroll
         for (int jj = 0; jj < 4; jj++) {
           const int rr = 8 * jj + (lane >> 3);
-          const v4i x = *reinterpret_cast<const v4i*>(slot + ((4 * i + j) * 64 + hh * 32 + (rr ^ (2 * (2 * j + hh)))) * 16);
-          u8* dst = base + (long)rr * p.ldc * ES;
+          xs[jj] = *reinterpret_cast<const v4i*>(slot + ((4 * i + j) * 64 + hh * 32 + (rr ^ (2 * (2 * j + hh)))) * 16);
+          if constexpr (OUT != OUT_I32) ascs[jj] = p.a_scale[row0 + rr];
+        }
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) {
+          const int rr = 8 * jj + (lane >> 3);
+          const v4i x = xs[jj];
+          u8* dst = base + (u32)(rr * p.ldc * ES);  // < 2^32: 32 rows of at most 2^24 elements
           if constexpr (OUT == OUT_I32) {
             *reinterpret_cast<v4i*>(dst) = x;
           } else {
-            const float asc = p.a_scale[row0 + rr];
+            const float asc = ascs[jj];
             const float y0 = __fmul_rn(__fmul_rn((float)x[0], asc), sw.x);
             const float y1 = __fmul_rn(__fmul_rn((float)x[1], asc), sw.y);
             const float y2 = __fmul_rn(__fmul_rn((float)x[2], asc), sw.z);

@@ -268,15 +268,25 @@ __global__ void __launch_bounds__(P_THREADS) plain_gemm_kernel(PlainParams p) {
           u8* base = reinterpret_cast<u8*>(p.out) + ((long)row0 * p.ldc + col) * ES;
           float4 sw{};
           if constexpr (OUT != P_OUT_I32) sw = *reinterpret_cast<const float4*>(p.b_scale + col);
+          // the four LDS reads (and row scales) first, then the stores: read, wait, store in turn
+          // put an LDS round trip (and a scale load) in front of every store
+          v4i xs[4];
+          float ascs[4];
 #pragma unroll
           for (int jj = 0; jj < 4; jj++) {
             const int r = 8 * jj + (lane >> 3);
-            const v4i x = *reinterpret_cast<const v4i*>(slot + ((4 * b + rj) * 64 + rh * 32 + (r ^ (2 * (2 * rj + rh)))) * 16);
+            xs[jj] = *reinterpret_cast<const v4i*>(slot + ((4 * b + rj) * 64 + rh * 32 + (r ^ (2 * (2 * rj + rh)))) * 16);
+            if constexpr (OUT != P_OUT_I32) ascs[jj] = p.a_scale[row0 + r];
+          }
+#pragma unroll
+          for (int jj = 0; jj < 4; jj++) {
+            const int r = 8 * jj + (lane >> 3);
+            const v4i x = xs[jj];
             u8* dst = base + (long)r * p.ldc * ES;
             if constexpr (OUT == P_OUT_I32) {
               *reinterpret_cast<v4i*>(dst) = x;
             } else {
-              const float asc = p.a_scale[row0 + r];
+              const float asc = ascs[jj];
               const float y0 = __fmul_rn(__fmul_rn((float)x[0], asc), sw.x);
               const float y1 = __fmul_rn(__fmul_rn((float)x[1], asc), sw.y);
               const float y2 = __fmul_rn(__fmul_rn((float)x[2], asc), sw.z);
