@@ -19,8 +19,13 @@
 //     group g), so P never leaves registers; V^T is stored with its keys in that order
 //     (qkv_post / v_transpose write it so), one 16-byte load per lane and dim block;
 //   * the three row statistics (max, exact sum, max of the scaled probabilities) each need the
-//     previous one over the whole causal row, so the kernel sweeps the keys four times and
-//     recomputes the scores (cheap on the matrix cores) instead of storing T x T rows;
+//     previous one over the whole causal row: sweep 1 finds the max, sweep 2 the exact sum and,
+//     from per-lane candidates, the third statistic (sweep 3, a pass over the keys of its own,
+//     runs only for waves with a near tie), sweep 4 quantizes P and runs P x V; the scores are
+//     recomputed on the matrix cores rather than stored as T x T rows, and the exponentials of
+//     sweep 2 are kept in a scratch for sweep 4 (uwc_attention_ws);
+//   * workgroups are mapped so that each XCD owns whole kv heads, whose K and V then stay in its
+//     L2 (at_block);
 //   * exp rows have max exactly det_exp(0) = 1 and every term below 2, so exact_rowsum's
 //     scale is the constant 2^41 (L = 20 for MAX_KEYS = 2^20): a term is rint(e * 2^41) < 2^42;
 //   * the divisions by the row constants den and sp are products with their float64
