@@ -628,6 +628,116 @@ def traffic_probe(args, torch, ops, O, np):
     log("traffic probe: done")
 
 
+def linear_traffic_cases():
+    """The kernels whose HBM traffic --linears-traffic-probe measures, in order: (case name, m, n, k,
+    what, algorithmic bytes). what: "gemm" = exact GEMM with the fused fp32 dequant
+    (uwc_igemm_dequant_f32: X int8 m x k, W int8 n x k, fp32 out and scales), "quant" = quant_act of
+    an fp32 m x k input (bs 512: int8 out and one scale per row)."""
+    cases = [("configs[0] mlp_up", 64, 6144, 2048, "gemm")]
+    for m in (1, 8, 32):
+        cases += [(f"decode M={m} {nm}", m, n, k, "gemm") for nm, (n, k) in LLAMA_LINEARS.items()]
+    cases += [("configs[1] quant_act 2048x2048", 2048, 0, 2048, "quant"),
+              ("configs[1] quant_act 2048x6144", 2048, 0, 6144, "quant")]
+    cases += [(f"configs[1] {nm}", 2048, n, k, "gemm") for nm, (n, k) in
+              (("qkv", (4096, 2048)), ("o", (2048, 2048)), ("gu", (12288, 2048)), ("down", (2048, 6144)))]
+    out = []
+    for name, m, n, k, what in cases:
+        byt = (n * k + m * k + 4 * m * n + 4 * (m + n)) if what == "gemm" else (m * k * 5 + 4 * m)
+        out.append((name, m, n, k, what, byt))
+    return out
+
+
+LT_REPS = 3
+
+
+def linears_traffic_probe(torch):
+    """What the rocprofv3 --pmc passes over the linears profile: every case of linear_traffic_cases()
+    LT_REPS times (a distinct weight buffer each time), each case preceded by one tiny
+    mfma_rate_kernel dispatch that marks where it starts, then the calibration copy."""
+    from uwc_amd import _lib, detrt
+    dev = "cuda"
+    st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+    sink = torch.zeros(1 << 20, dtype=torch.int32, device=dev)
+    for name, m, n, k, what, _ in linear_traffic_cases():
+        if what == "gemm":
+            Ws = [torch.randint(-64, 65, (n, k), dtype=torch.int8, device=dev) for _ in range(LT_REPS)]
+            X = torch.randint(-64, 65, (m, k), dtype=torch.int8, device=dev)
+            sx, sw = torch.rand(m, device=dev) + 0.5, torch.rand(n, device=dev) * 1e-3
+            Y = torch.empty((m, n), dtype=torch.float32, device=dev)
+        else:
+            xs = [torch.randn((m, k), device=dev) for _ in range(LT_REPS)]
+        torch.cuda.synchronize()
+        _lib.call("uwc_mfma_rate_probe", 1, 0, sink.data_ptr(), sink.numel(), st())  # the case marker
+        for i in range(LT_REPS):
+            if what == "gemm":
+                _lib.call("uwc_igemm_dequant_f32", X.data_ptr(), Ws[i].data_ptr(), m, n, k, sx.data_ptr(),
+                          sw.data_ptr(), Y.data_ptr(), st())
+            else:
+                detrt.quant_act(xs[i], 512)
+        torch.cuda.synchronize()
+        log(f"linears traffic probe: {name}")
+    x = torch.empty(COPY_BYTES, dtype=torch.int8, device=dev).fill_(1)
+    y = torch.empty_like(x)
+    torch.cuda.synchronize()
+    _lib.call("uwc_mfma_rate_probe", 1, 0, sink.data_ptr(), sink.numel(), st())
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    log("linears traffic probe: done")
+
+
+def summarize_linears_traffic(fetch_csv, write_csv, out_path, cmd):
+    """FETCH_SIZE / WRITE_SIZE per dispatch of every case of linears_traffic_probe, calibrated by the
+    256 MiB copy, against the case's algorithmic bytes, into out_path."""
+    import csv
+    import statistics
+
+    def segments(path, counter):
+        rows = [r for r in csv.DictReader(open(path)) if r["Counter_Name"].startswith(counter)]
+        rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+        segs, cur = [], None
+        for r in rows:
+            if "mfma_rate_kernel" in r["Kernel_Name"]:
+                cur = []
+                segs.append(cur)
+            elif cur is not None and not r["Kernel_Name"].startswith("void at::"):
+                # torch's own kernels are the next case's tensor set-up, not this case's work
+                cur.append((r["Kernel_Name"].replace("(anonymous namespace)::", ""), float(r["Counter_Value"])))
+        return segs
+
+    cases = linear_traffic_cases()
+    res = {}
+    for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        segs = segments(path, counter)
+        assert len(segs) == len(cases) + 1, f"{counter}: {len(segs)} marked segments for {len(cases)} cases + copy"
+        copy = [v for nm, v in segs[-1] if "copy" in nm.lower() and v > 0.5 * COPY_BYTES / 1024]
+        assert copy, f"{counter}: no calibration copy after the last marker"
+        factor = COPY_BYTES / (statistics.median(copy) * 1024.0)
+        for c, seg in zip(cases, segs[:-1]):
+            per = {}
+            for nm, v in seg:
+                per.setdefault(nm.split("(")[0], []).append(v)
+            res.setdefault(c[0], {})[counter] = (factor, {nm: statistics.median(vs) * 1024.0 * factor
+                                                          for nm, vs in per.items()})
+    with open(out_path, "w") as f:
+        f.write("HBM traffic (rocprofv3 FETCH_SIZE, WRITE_SIZE) of the configs[0], decode and configs[1] kernels, "
+                f"median per dispatch over {LT_REPS} (distinct weight buffers), calibrated by a {COPY_BYTES} B copy\n")
+        f.write(f"commands: {cmd}\n")
+        f.write(f"calibration factors: FETCH_SIZE {res[cases[0][0]]['FETCH_SIZE'][0]:.4f}, WRITE_SIZE "
+                f"{res[cases[0][0]]['WRITE_SIZE'][0]:.4f}\n\n")
+        f.write(f"{'case':34s} {'kernel':44s} {'read MB':>9s} {'write MB':>9s} {'total MB':>9s} {'algo MB':>9s} {'ratio':>6s}\n")
+        for name, m, n, k, what, byt in cases:
+            fr, wr = res[name]["FETCH_SIZE"][1], res[name]["WRITE_SIZE"][1]
+            for kn in sorted(set(fr) | set(wr)):
+                rd, wt = fr.get(kn, 0.0), wr.get(kn, 0.0)
+                f.write(f"{name:34s} {kn[:44]:44s} {rd / 1e6:9.2f} {wt / 1e6:9.2f} {(rd + wt) / 1e6:9.2f} "
+                        f"{byt / 1e6:9.2f} {(rd + wt) / byt:6.2f}\n")
+        f.write("\nalgo MB: W + X + fp32 out + scales for the GEMMs (uwc_igemm_dequant_f32); fp32 in + int8 out + "
+                "scales for quant_act. ratio > 1: bytes fetched or written beyond the algorithmic ones (e.g. the "
+                "skinny kernels' X broadcast to every workgroup, or W rows read twice through L2).\n")
+    print(open(out_path).read())
+
+
 def summarize_pmc(fetch_csv, write_csv, cmd, nonces):
     """Per-dispatch FETCH_SIZE / WRITE_SIZE of the noisy GEMM, each scaled by COPY_BYTES over the
     counter's reading for the calibration copy, into TRAFFIC_FILE."""
@@ -964,6 +1074,10 @@ def main():
     ap.add_argument("--e2e-cpu-tokens", type=int, default=256)
     ap.add_argument("--traffic-probe", action="store_true", help="the workload of the FETCH_SIZE / WRITE_SIZE passes")
     ap.add_argument("--linears-only", action="store_true", help="run only configs[1], configs[0] and the decode linears")
+    ap.add_argument("--linears-traffic-probe", action="store_true",
+                    help="the workload of the FETCH_SIZE / WRITE_SIZE passes over the configs[0], decode and configs[1] kernels")
+    ap.add_argument("--summarize-linears-traffic", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "OUT", "CMD"),
+                    help="write the HBM-traffic summary of a --linears-traffic-probe pair of counter runs")
     ap.add_argument("--summarize-linears-trace", nargs=3, metavar=("TRACE_CSV", "OUT", "CMD"),
                     help="write the graph-timed linears' kernel-trace summary under profiles/")
     ap.add_argument("--summarize-pmc", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "CMD", "NONCES"),
@@ -996,6 +1110,9 @@ def main():
     if args.summarize_counters:
         summarize_counters(*args.summarize_counters)
         return
+    if args.summarize_linears_traffic:
+        summarize_linears_traffic(*args.summarize_linears_traffic)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the multi-GPU layout "
               "is a design in DESIGN.md, not a measured path", file=sys.stderr)
@@ -1013,6 +1130,9 @@ def main():
         args.gemm_group = min(args.group, ops.GEMM_GROUP)
     if args.traffic_probe:
         traffic_probe(args, torch, ops, O, np)
+        return
+    if args.linears_traffic_probe:
+        linears_traffic_probe(torch)
         return
     if args.e2e_only:
         print(json.dumps(qwen3_e2e(args, torch, np)))
