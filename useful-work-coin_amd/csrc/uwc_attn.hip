@@ -63,7 +63,9 @@ __device__ __forceinline__ float at_exp(float z) {
   p = __fadd_rn(__fmul_rn(p, f), DX_E2);
   p = __fadd_rn(__fmul_rn(p, f), DX_E1);
   p = __fadd_rn(__fmul_rn(p, f), DX_E0);
-  const float r = __fmul_rn(p, __int_as_float(((int)n + 127) << 23));
+  // p * 2^n with -126 <= n <= 0 and p >= 1 is a normal number, so the product is exact and
+  // equals ldexp(p, n), one instruction instead of building 2^n and multiplying
+  const float r = __builtin_amdgcn_ldexpf(p, (int)n);
   return under ? 0.0f : r;
 }
 
@@ -256,8 +258,8 @@ __global__ void __launch_bounds__(256, HD == 128 ? 2 : 3) attention_kernel(const
     t.vs = vs[sc_base + (u32)min(kt * 64 + lane, T - 1) * (u32)Hkv];
   };
   // scores(kt, ...) from a fetched tile: the same MFMAs, scales and mask
-  auto scores_t = [&](int kt, const KTile& t, float S[4][4], auto mask) AT_AI {
-    constexpr bool MASK = decltype(mask)::value;
+  auto scores_t = [&](int kt, const KTile& t, float S[4][4], auto mask, auto noinv) AT_AI {
+    constexpr bool MASK = decltype(mask)::value, NOINV = decltype(noinv)::value;
     float4 skv[4];
     sk_slot[lane] = t.ks;
     __builtin_amdgcn_wave_barrier();
@@ -271,7 +273,8 @@ __global__ void __launch_bounds__(256, HD == 128 ? 2 : 3) attention_kernel(const
       for (int c = 0; c < NC; c++) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(t.kf[b][c], qf[c], acc, 0, 0, 0);
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const float sv = __fmul_rn(__fmul_rn(__fmul_rn((float)acc[i], my_qs), at_get(skv[b], i)), inv_sqrt);
+        const float y = __fmul_rn(__fmul_rn((float)acc[i], my_qs), at_get(skv[b], i));
+        const float sv = NOINV ? y : __fmul_rn(y, inv_sqrt);
         if constexpr (MASK) {
           const int j = kt * 64 + 16 * b + 4 * g + i;
           S[b][i] = (j <= qi && j < T) ? sv : -__int_as_float(0x7f800000);
@@ -281,27 +284,29 @@ __global__ void __launch_bounds__(256, HD == 128 ? 2 : 3) attention_kernel(const
       }
     }
   };
-  // a sweep over the key tiles with the tiles fetched two ahead; full tiles unmasked
-  auto ksweep = [&](auto body) AT_AI {
+  // a sweep over the key tiles with the tiles fetched two ahead; full tiles unmasked. With noinv
+  // the scores are left without the final factor 1 / sqrt(hd) (sweep 1's max needs no more)
+  auto ksweep = [&](auto body, auto noinv) AT_AI {
     KTile kb[2];
     pipelined([&](int kt, auto sl) AT_AI { kfetch(kt, kb[decltype(sl)::value]); },
               [&](int kt, auto sl) AT_AI {
                 float S[4][4];
-                if (kt < nfull) scores_t(kt, kb[decltype(sl)::value], S, std::false_type{});
-                else scores_t(kt, kb[decltype(sl)::value], S, std::true_type{});
+                if (kt < nfull) scores_t(kt, kb[decltype(sl)::value], S, std::false_type{}, noinv);
+                else scores_t(kt, kb[decltype(sl)::value], S, std::true_type{}, noinv);
                 body(kt, S, kb[decltype(sl)::value]);
               });
   };
 
-  // sweep 1: row max
+  // sweep 1: row max. A score is fl(y * inv) with y = fl(fl(acc * qs) * ks) and inv > 0, a
+  // monotone function of y, so the max score is fl(max_j y_j * inv) (-inf for an empty row too)
   float mx = -__int_as_float(0x7f800000);
-  ksweep([&](int kt, const float (&S)[4][4], const KTile&) AT_AI {
+  ksweep([&](int kt, const float (&Y)[4][4], const KTile&) AT_AI {
 #pragma unroll
     for (int b = 0; b < 4; b++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) mx = fmaxf(mx, S[b][i]);
-  });
-  mx = at_max_groups(mx);
+      for (int i = 0; i < 4; i++) mx = fmaxf(mx, Y[b][i]);
+  }, std::true_type{});
+  mx = __fmul_rn(at_max_groups(mx), inv_sqrt);
 
   // sweep 2: exact denominator (fixed point at 2^41); masked entries give det_exp(-inf) = 0.
   // A tile's 16 terms per lane sum exactly in float64 (< 2^46), then join a u64 total.
@@ -343,7 +348,7 @@ __global__ void __launch_bounds__(256, HD == 128 ? 2 : 3) attention_kernel(const
       if constexpr (ES) *reinterpret_cast<float4*>(ewave + kt * 1024 + b * 256) = float4{e[0], e[1], e[2], e[3]};
     }
     dsum += (u64)part;
-  });
+  }, std::false_type{});
   dsum = at_sum_groups(dsum);
   const float den = (float)ldexp((double)dsum, -41);
   const double rden = 1.0 / (double)den;
