@@ -12,6 +12,23 @@ typedef uint8_t u8;
 typedef uint64_t u64;
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+// 16-byte stores and loads with the non-temporal hint (the nt bit: streamed through the caches
+// rather than kept), for data written once and read once much later, e.g. a scratch larger than
+// the caches, so that it does not evict what the kernel rereads from L2.
+typedef u32 u2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void uwc_store_nt(void* p, float4 v) {
+  __builtin_nontemporal_store(f4v{v.x, v.y, v.z, v.w}, reinterpret_cast<f4v*>(p));
+}
+__device__ __forceinline__ void uwc_store_nt(void* p, v4i v) { __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(p)); }
+__device__ __forceinline__ void uwc_store_nt(void* p, uint2 v) {
+  __builtin_nontemporal_store(u2v{v.x, v.y}, reinterpret_cast<u2v*>(p));
+}
+__device__ __forceinline__ float4 uwc_load_nt(const float* p) {
+  const f4v t = __builtin_nontemporal_load(reinterpret_cast<const f4v*>(p));
+  return float4{t.x, t.y, t.z, t.w};
+}
 
 #define UWC_OK 0
 

@@ -21,7 +21,9 @@
 //     global side (each lane of a DMA writes a fixed LDS slot and fetches the bytes that belong
 //     there).
 //   * Transposed C: the B fragment is the MFMA's A operand, so lane l holds row l & 31 of a
-//     block and four consecutive columns per register group (16-byte epilogue stores).
+//     block and four consecutive columns per register group (16-byte epilogue stores, with the
+//     non-temporal hint: the output is written once and would otherwise evict the A and B panels
+//     the XCD's other tiles read from L2; 77.5 -> 76.9 us per nonce in the batched mining launch).
 //   * Transcript fold every r along k: a lane XORs its accumulators into 4 partials (hash block
 //     x bit 0 of the tile index) with 3-input v_bitop3 XORs, spread over a chunk's last pass
 //     (blocks folded three MFMAs after their last MFMA of the chunk) and the next chunk's first
@@ -513,17 +515,17 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
       for (int j = 0; j < 4; j++) {
         u8* dst = base + loff + 8 * j * ES;
         if constexpr (OUT == OUT_I32) {
-          *reinterpret_cast<v4i*>(dst) = v4i{v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]};
+          uwc_store_nt(dst, v4i{v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]});
         } else {
           float y[4];
 #pragma unroll
           for (int i = 0; i < 4; i++)
             y[i] = __fmul_rn(__fmul_rn((float)v[4 * j + i], asc), p.b_scale[col0 + 8 * j + lc + i]);
           if constexpr (OUT == OUT_F32) {
-            *reinterpret_cast<float4*>(dst) = float4{y[0], y[1], y[2], y[3]};
+            uwc_store_nt(dst, float4{y[0], y[1], y[2], y[3]});
           } else {
             const uint2 w{bf16_rne(y[0]) | (bf16_rne(y[1]) << 16), bf16_rne(y[2]) | (bf16_rne(y[3]) << 16)};
-            *reinterpret_cast<uint2*>(dst) = w;
+            uwc_store_nt(dst, w);
           }
         }
       }
@@ -824,7 +826,7 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
           const v4i x = xs[jj];
           u8* dst = base + (u32)(rr * p.ldc * ES);  // < 2^32: 32 rows of at most 2^24 elements
           if constexpr (OUT == OUT_I32) {
-            *reinterpret_cast<v4i*>(dst) = x;
+            uwc_store_nt(dst, x);
           } else {
             const float asc = ascs[jj];
             const float y0 = __fmul_rn(__fmul_rn((float)x[0], asc), sw.x);
@@ -832,10 +834,9 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
             const float y2 = __fmul_rn(__fmul_rn((float)x[2], asc), sw.z);
             const float y3 = __fmul_rn(__fmul_rn((float)x[3], asc), sw.w);
             if constexpr (OUT == OUT_F32) {
-              *reinterpret_cast<float4*>(dst) = float4{y0, y1, y2, y3};
+              uwc_store_nt(dst, float4{y0, y1, y2, y3});
             } else {
-              *reinterpret_cast<uint2*>(dst) =
-                  uint2{bf16_rne(y0) | (bf16_rne(y1) << 16), bf16_rne(y2) | (bf16_rne(y3) << 16)};
+              uwc_store_nt(dst, uint2{bf16_rne(y0) | (bf16_rne(y1) << 16), bf16_rne(y2) | (bf16_rne(y3) << 16)});
             }
           }
         }

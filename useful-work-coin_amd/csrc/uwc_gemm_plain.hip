@@ -242,7 +242,9 @@ __global__ void __launch_bounds__(P_THREADS) plain_gemm_kernel(PlainParams p) {
   // columns 4 (l % 8) .. + 3 of a block: 8 whole row segments per instruction instead of 32 rows
   // of 16 bytes (the output burst at the end of a launch drains faster). The XOR keeps the 16
   // lanes of each write (16 rows) and of each read (2 rows x 8 pieces) on distinct 16-byte bank
-  // groups.
+  // groups. The stores carry the non-temporal hint, so that the output stream does not evict the
+  // operand panels other workgroups of the XCD still read from L2 (the M = 2048 Qwen3-1.7B
+  // linears 4-8% faster).
   if constexpr (OUT != P_OUT_NONE) {
     constexpr int ES = OUT == P_OUT_BF16 ? 2 : 4;
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -284,7 +286,7 @@ __global__ void __launch_bounds__(P_THREADS) plain_gemm_kernel(PlainParams p) {
             const v4i x = xs[jj];
             u8* dst = base + (long)r * p.ldc * ES;
             if constexpr (OUT == P_OUT_I32) {
-              *reinterpret_cast<v4i*>(dst) = x;
+              uwc_store_nt(dst, x);
             } else {
               const float asc = ascs[jj];
               const float y0 = __fmul_rn(__fmul_rn((float)x[0], asc), sw.x);
@@ -292,10 +294,9 @@ __global__ void __launch_bounds__(P_THREADS) plain_gemm_kernel(PlainParams p) {
               const float y2 = __fmul_rn(__fmul_rn((float)x[2], asc), sw.z);
               const float y3 = __fmul_rn(__fmul_rn((float)x[3], asc), sw.w);
               if constexpr (OUT == P_OUT_F32) {
-                *reinterpret_cast<float4*>(dst) = float4{y0, y1, y2, y3};
+                uwc_store_nt(dst, float4{y0, y1, y2, y3});
               } else {
-                *reinterpret_cast<uint2*>(dst) =
-                    uint2{p_bf16_rne(y0) | (p_bf16_rne(y1) << 16), p_bf16_rne(y2) | (p_bf16_rne(y3) << 16)};
+                uwc_store_nt(dst, uint2{p_bf16_rne(y0) | (p_bf16_rne(y1) << 16), p_bf16_rne(y2) | (p_bf16_rne(y3) << 16)});
               }
             }
           }

@@ -377,7 +377,7 @@ static void sk_mt(int mt, int out_mode, dim3 grid, dim3 block, size_t lds, hipSt
 //   * requests of a CU return in issue order: an L2 hit issued after HBM misses waits for them.
 //     X (a few KB to 64 KB, L2-resident) is therefore requested before any W;
 //   * X replicated into every CU costs more than streaming W when m k is large (64 x 2048 bytes
-//     per workgroup against 48 KB of W each at configs[0]). Above one group's LDS budget the
+//     per workgroup against 48 KB of W each at 64 x 6144 x 2048). Above one group's LDS budget the
 //     tokens are split into ts = 2 groups: each workgroup holds half of X and reads its W rows,
 //     and the two workgroups of a row block run in the same round on one XCD (round-robin
 //     dispatch puts workgroup b on XCD b % 8) so the second read of W is served by that XCD's
