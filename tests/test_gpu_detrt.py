@@ -86,6 +86,26 @@ def test_linear_fixtures(dev, name):
             assert torch.equal(y, y2)
 
 
+@pytest.mark.parametrize("rows,k", [(2048, 1024), (1024, 1536)])
+@pytest.mark.parametrize("bs", [0, 2, 16, 32, 64, 128, 256, 512])
+def test_quant_act_double_group_kernel(dev, rows, k, bs):
+    """The one-wave-per-1024-elements quantizer (taken from 2048 double groups on): every Hadamard
+    block size, so that every count of cross-lane stages (and with it every sign the lanes end with)
+    runs; k = 1536 leaves the second wave of a row half empty. Tiny, huge, zero and subnormal rows,
+    against the oracle bit for bit."""
+    _, detrt = _mods()
+    rng = np.random.default_rng(rows + k + bs)
+    x = rng.standard_normal((rows, k)).astype(np.float32) * np.exp(rng.uniform(-30, 30, size=(rows, 1))).astype(np.float32)
+    x[0] = 0.0
+    x[1] *= np.float32(1e-38)
+    x[2, 7] = 3.0e38
+    x[3, :] = np.float32(-2.5)  # equal values: the transform concentrates them in few lanes
+    q, s = detrt.quant_act(torch.from_numpy(x).to(dev), bs)
+    wq, ws = O.quant_act(x, bs)
+    assert np.array_equal(q.cpu().numpy(), wq)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), ws.view(np.uint32))
+
+
 @pytest.mark.parametrize("k,bs", [(2048, 512), (6144, 512), (4096, 128), (14336, 128), (2048, 0), (128, 64),
                                   (4096, 512), (4608, 512), (1536, 1), (512, 8), (640, 128), (4096, 1024)])
 def test_quant_act_random_rows(dev, k, bs):

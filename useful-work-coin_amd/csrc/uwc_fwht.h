@@ -97,18 +97,45 @@ __device__ __forceinline__ void fwht512_rows(float y[NG][8], int G, int lane, in
 // holds the 16 consecutive elements 16 i .. 16 i + 15 with i = b0 + 2 b1 + 4 b3 + 8 b4 + 16 b5
 // (b = the bits of L). Stages h = 1, 2, 4, 8 then pair elements inside a lane, and stages
 // h = 16 .. 256 pair lane L with L ^ 1, ^ 2, ^ 8, ^ 16, ^ 32: lane bit 2, the one exchange the
-// VALU cannot do in one DPP operand, is never crossed. A cross-lane stage is one sign flip and
-// one add per element: the lower lane of a pair computes o + v = v + o (a + b), the upper one
-// o + (-v) = o - v (a - b), the same single rounded IEEE operation on the same two operands as
-// the reference's pair (a + b, a - b), with the partner's value o read through a DPP operand of
-// the add (or exchanged by v_permlane16/32_swap).
+// VALU cannot do in one DPP operand, is never crossed.
+//
+// A cross-lane stage is one VALU operation per element. Each lane holds its values times a sign
+// s (+1 or -1, the same for all 16 of them and for both lanes of every pair still to be
+// exchanged), so that the one operation w' = w + c o (w the lane's value, o the partner's, c = +1
+// in the lower lane of the pair, -1 in the upper) serves both lanes: the lower lane gets
+// s (a + b), the upper s (b - a) = -s (a - b), i.e. the pair (a + b, a - b) of the reference with
+// the upper lane's sign flipped. c o is exact and rounding to nearest is symmetric, so each value
+// is the reference's single rounded a + b or a - b, up to sign. For h = 16, 32, 64 the operation
+// is v_fmac_f32 with the partner read through a DPP operand (quad_perm [1,0,3,2], [2,3,0,1],
+// row_ror:8); for h = 128, 256 v_permlane16/32_swap hands every lane the pair's lower value a
+// and upper value b, and every lane takes a + c b (no sign change). The sign is returned: the
+// caller quantizes with a signed reciprocal (y / s = w * (sign / s) exactly) and takes |w| = |y|.
 __device__ __forceinline__ int fw16_index(int lane) {
   return (lane & 3) | ((lane >> 1) & 0x1C);  // b0 + 2 b1 + 4 b3 + 8 b4 + 16 b5
 }
 
+// y[j] += c * y[j] of the DPP partner lane, for the 16 values of a lane. One asm block per stage:
+// s_nop 4 covers the wait states a DPP read needs after a VALU write of its source (and after an
+// EXEC write) whatever the compiler scheduled before the block; inside it every instruction reads
+// and writes its own register only.
+#define FW16_DPP_STAGE(DPP)                                                                                 \
+  asm("s_nop 4\n\t"                                                                                         \
+      "v_fmac_f32_dpp %0, %0, %16 " DPP "\n\tv_fmac_f32_dpp %1, %1, %16 " DPP "\n\t"                       \
+      "v_fmac_f32_dpp %2, %2, %16 " DPP "\n\tv_fmac_f32_dpp %3, %3, %16 " DPP "\n\t"                       \
+      "v_fmac_f32_dpp %4, %4, %16 " DPP "\n\tv_fmac_f32_dpp %5, %5, %16 " DPP "\n\t"                       \
+      "v_fmac_f32_dpp %6, %6, %16 " DPP "\n\tv_fmac_f32_dpp %7, %7, %16 " DPP "\n\t"                       \
+      "v_fmac_f32_dpp %8, %8, %16 " DPP "\n\tv_fmac_f32_dpp %9, %9, %16 " DPP "\n\t"                       \
+      "v_fmac_f32_dpp %10, %10, %16 " DPP "\n\tv_fmac_f32_dpp %11, %11, %16 " DPP "\n\t"                   \
+      "v_fmac_f32_dpp %12, %12, %16 " DPP "\n\tv_fmac_f32_dpp %13, %13, %16 " DPP "\n\t"                   \
+      "v_fmac_f32_dpp %14, %14, %16 " DPP "\n\tv_fmac_f32_dpp %15, %15, %16 " DPP                          \
+      : "+v"(y[0]), "+v"(y[1]), "+v"(y[2]), "+v"(y[3]), "+v"(y[4]), "+v"(y[5]), "+v"(y[6]), "+v"(y[7]),     \
+        "+v"(y[8]), "+v"(y[9]), "+v"(y[10]), "+v"(y[11]), "+v"(y[12]), "+v"(y[13]), "+v"(y[14]),          \
+        "+v"(y[15])                                                                                         \
+      : "v"(c))
+
 // y[0..15]: the lane's elements of one double group; lbs = log2(bs), bs <= 512. Every lane of the
-// wave must be active.
-__device__ __forceinline__ void fwht16(float y[16], int lane, int lbs) {
+// wave must be active. Returns true when the lane holds the negated transform.
+__device__ __forceinline__ bool fwht16(float y[16], int lane, int lbs) {
 #pragma unroll
   for (int lh = 0; lh < 4; lh++) {
     if (lh < lbs) {
@@ -122,34 +149,32 @@ __device__ __forceinline__ void fwht16(float y[16], int lane, int lbs) {
         }
     }
   }
-  // stages h = 16, 32, 64 (lane bits 0, 1, 3): DPP quad_perm [1,0,3,2], [2,3,0,1], row_ror:8
+  bool neg = false;
+  // stages h = 16, 32, 64 (lane bits 0, 1, 3)
 #pragma unroll
   for (int lh = 4; lh < 7; lh++) {
     if (lh < lbs) {
-      const int bit = lh == 4 ? 0 : lh == 5 ? 1 : 3;
-      const u32 sgn = (lane >> bit) & 1 ? 0x80000000u : 0u;
-#pragma unroll
-      for (int j = 0; j < 16; j++) {
-        const float v = y[j];
-        const float sv = __uint_as_float(__float_as_uint(v) ^ sgn);
-        const float o = lh == 4 ? qa_dpp<0xB1>(v) : lh == 5 ? qa_dpp<0x4E>(v) : qa_dpp<0x128>(v);
-        y[j] = __fadd_rn(o, sv);
-      }
+      const int bit = (lane >> (lh == 4 ? 0 : lh == 5 ? 1 : 3)) & 1;
+      const float c = bit ? -1.0f : 1.0f;
+      if (lh == 4) FW16_DPP_STAGE("quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf");
+      else if (lh == 5) FW16_DPP_STAGE("quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf");
+      else FW16_DPP_STAGE("row_ror:8 row_mask:0xf bank_mask:0xf");
+      neg ^= bit;
     }
   }
-  // stages h = 128, 256 (lane bits 4, 5): the swap hands every lane both values of its pair
+  // stages h = 128, 256 (lane bits 4, 5): both lanes of a pair hold the same sign here
 #pragma unroll
   for (int lh = 7; lh < 9; lh++) {
     if (lh < lbs) {
-      const u32 sgn = (lane >> (lh - 3)) & 1 ? 0x80000000u : 0u;
+      const float c = (lane >> (lh - 3)) & 1 ? -1.0f : 1.0f;
 #pragma unroll
       for (int j = 0; j < 16; j++) {
         const u32 v = __float_as_uint(y[j]);
         const auto ab = lh == 7 ? __builtin_amdgcn_permlane16_swap(v, v, false, false)
                                 : __builtin_amdgcn_permlane32_swap(v, v, false, false);
-        // lower lane: a + b; upper lane: a + (-b)
-        y[j] = __fadd_rn(__uint_as_float(ab[0]), __uint_as_float(ab[1] ^ sgn));
+        y[j] = __builtin_fmaf(__uint_as_float(ab[1]), c, __uint_as_float(ab[0]));
       }
     }
   }
+  return neg;
 }

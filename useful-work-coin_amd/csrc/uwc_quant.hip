@@ -255,7 +255,7 @@ __global__ void __launch_bounds__(64 * QD_MAX) quant_act_dgroup_kernel(const T* 
 #pragma unroll
     for (int j = 0; j < 16; j++) y[j] = 0.f;
   }
-  fwht16(y, lane, lbs);
+  const bool neg = fwht16(y, lane, lbs);
   float mx = 0.f;
 #pragma unroll
   for (int j = 0; j < 16; j++) mx = fmaxf(mx, fabsf(y[j]));
@@ -267,7 +267,8 @@ __global__ void __launch_bounds__(64 * QD_MAX) quant_act_dgroup_kernel(const T* 
   for (int i = 1; i < D; i++) mx = fmaxf(mx, wmax[i]);
   const float fq = (float)qmax;
   const float s = __fdiv_rn(fmaxf(mx, 1e-8f), fq);
-  const double rs = 1.0 / (double)s;
+  // the lane holds y or -y: y / s = w * (+-1 / s), the sign exact in the float64 product
+  const double rs = neg ? -1.0 / (double)s : 1.0 / (double)s;
   u32 w[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) {
