@@ -3,24 +3,65 @@
 // quantizing row kernels (uwc_rows.h): stages h = 1, 2, 4 pair elements inside a lane, stages
 // h = 8 .. 256 pair lane L with lane L ^ (h / 8). Each output of a stage is one rounded add or
 // subtract of the same two inputs, in the same stage order, as the LDS form (pairs (i, i + h) ->
-// (a + b, a - b)), so the results are the same bits.
+// (a + b, a - b)), so the results are the same bits up to a per-lane sign the transforms return.
 #pragma once
 #include "uwc_common.h"
 
 // The transform of G (<= NG) groups held as y[g][0..7], stage-major over the groups so that every
 // stage's cross-lane exchanges are independent of each other; every lane of the wave must be
-// active. The exchanges run on the VALU:
-// DPP quad_perm for lane ^ 1 and ^ 2, DPP row rotations for ^ 4 (row_ror:12 reads lane + 4,
-// row_ror:4 lane - 4, inside 16-lane rows) and ^ 8 (row_ror:8), and v_permlane16_swap /
-// v_permlane32_swap for ^ 16 and ^ 32, which hand every lane both values of its pair (the lower
-// lane's in the first result, the upper's in the second).
+// active. Cross-lane stages, by lane bit (the pair of lanes L < U, a the value of L, b of U):
+//   * bits 0, 1, 3 (h = 8, 16, 64): one v_fmac_f32 per element, w += c o with the partner's value
+//     o through a DPP operand (quad_perm [1,0,3,2], [2,3,0,1], row_ror:8) and c = +1 in L, -1 in
+//     U, under a per-lane sign as in the 16-per-lane form below: L gets s (a + b), U
+//     s (b - a) = -s (a - b), and U's sign flips;
+//   * bit 2 (h = 32): a DPP add in L (partner L + 4: row_ror:12, banks 0 and 2 of each row) and a
+//     DPP subtract in U (partner U - 4: row_ror:4, banks 1 and 3) writing one new register, the
+//     bank mask leaving the other lanes' value: a + b and a - b with no sign change;
+//   * bits 4, 5 (h = 128, 256): v_permlane16/32_swap hands every lane a and b, then a + c b.
+// The pair of every stage shares its sign (the sign depends on bits 0, 1, 3 only), c o is exact,
+// and rounding to nearest is symmetric: every value is the reference's single rounded a + b or
+// a - b, up to the lane's sign, which is returned (true: the lane holds the negated transform).
 template <int CTRL>
 __device__ __forceinline__ float qa_dpp(float x) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
 }
 
+// w[j] += c * w[j] of the DPP partner lane for the 8 values of one group; s_nop 4 covers the wait
+// states of a DPP read after a VALU (or EXEC) write of its source, whatever precedes the block
+#define FW8_FMAC_STAGE(w, DPP)                                                                              \
+  asm("s_nop 4\n\t"                                                                                         \
+      "v_fmac_f32_dpp %0, %0, %8 " DPP "\n\tv_fmac_f32_dpp %1, %1, %8 " DPP "\n\t"                         \
+      "v_fmac_f32_dpp %2, %2, %8 " DPP "\n\tv_fmac_f32_dpp %3, %3, %8 " DPP "\n\t"                         \
+      "v_fmac_f32_dpp %4, %4, %8 " DPP "\n\tv_fmac_f32_dpp %5, %5, %8 " DPP "\n\t"                         \
+      "v_fmac_f32_dpp %6, %6, %8 " DPP "\n\tv_fmac_f32_dpp %7, %7, %8 " DPP                                \
+      : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(w[4]), "+v"(w[5]), "+v"(w[6]), "+v"(w[7])      \
+      : "v"(c))
+
+// n[j] = w[j] + w[j + 4 lanes] in banks 0, 2 and w[j - 4 lanes] - w[j] in banks 1, 3 of every row
+__device__ __forceinline__ void fw8_lane4(const float w[8], float n[8]) {
+  asm("s_nop 4\n\t"
+      "v_add_f32_dpp %0, %8, %8 row_ror:12 row_mask:0xf bank_mask:0x5\n\t"
+      "v_sub_f32_dpp %0, %8, %8 row_ror:4 row_mask:0xf bank_mask:0xa\n\t"
+      "v_add_f32_dpp %1, %9, %9 row_ror:12 row_mask:0xf bank_mask:0x5\n\t"
+      "v_sub_f32_dpp %1, %9, %9 row_ror:4 row_mask:0xf bank_mask:0xa\n\t"
+      "v_add_f32_dpp %2, %10, %10 row_ror:12 row_mask:0xf bank_mask:0x5\n\t"
+      "v_sub_f32_dpp %2, %10, %10 row_ror:4 row_mask:0xf bank_mask:0xa\n\t"
+      "v_add_f32_dpp %3, %11, %11 row_ror:12 row_mask:0xf bank_mask:0x5\n\t"
+      "v_sub_f32_dpp %3, %11, %11 row_ror:4 row_mask:0xf bank_mask:0xa\n\t"
+      "v_add_f32_dpp %4, %12, %12 row_ror:12 row_mask:0xf bank_mask:0x5\n\t"
+      "v_sub_f32_dpp %4, %12, %12 row_ror:4 row_mask:0xf bank_mask:0xa\n\t"
+      "v_add_f32_dpp %5, %13, %13 row_ror:12 row_mask:0xf bank_mask:0x5\n\t"
+      "v_sub_f32_dpp %5, %13, %13 row_ror:4 row_mask:0xf bank_mask:0xa\n\t"
+      "v_add_f32_dpp %6, %14, %14 row_ror:12 row_mask:0xf bank_mask:0x5\n\t"
+      "v_sub_f32_dpp %6, %14, %14 row_ror:4 row_mask:0xf bank_mask:0xa\n\t"
+      "v_add_f32_dpp %7, %15, %15 row_ror:12 row_mask:0xf bank_mask:0x5\n\t"
+      "v_sub_f32_dpp %7, %15, %15 row_ror:4 row_mask:0xf bank_mask:0xa"
+      : "=&v"(n[0]), "=&v"(n[1]), "=&v"(n[2]), "=&v"(n[3]), "=&v"(n[4]), "=&v"(n[5]), "=&v"(n[6]), "=&v"(n[7])
+      : "v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3]), "v"(w[4]), "v"(w[5]), "v"(w[6]), "v"(w[7]));
+}
+
 template <int NG>
-__device__ __forceinline__ void fwht512_rows(float y[NG][8], int G, int lane, int lbs) {
+__device__ __forceinline__ bool fwht512_rows(float y[NG][8], int G, int lane, int lbs) {
 #pragma unroll
   for (int lh = 0; lh < 3; lh++) {
     if (lh < lbs) {
@@ -38,42 +79,37 @@ __device__ __forceinline__ void fwht512_rows(float y[NG][8], int G, int lane, in
         }
     }
   }
-  // lane ^ 1, 2, 4, 8: the partner's value o; the lower lane keeps v + o, the upper o - v
+  bool neg = false;
 #pragma unroll
   for (int lh = 3; lh < 7; lh++) {
     if (lh < lbs) {
-      const int d = 1 << (lh - 3);
-      const bool hi = lane & d;
+      if (lh == 5) {
 #pragma unroll
-      for (int g = 0; g < NG; g++)
-        if (g < G) {
+        for (int g = 0; g < NG; g++)
+          if (g < G) {
+            float n[8];
+            fw8_lane4(y[g], n);
 #pragma unroll
-          for (int j = 0; j < 8; j++) {
-            // every lane runs every exchange (a DPP read of a lane outside EXEC returns the bound
-            // value, not the lane's), then selects: no branch may depend on hi before this point
-            const float v = y[g][j];
-            float o;
-            if (d == 1) {
-              o = qa_dpp<0xB1>(v);  // quad_perm [1,0,3,2]
-            } else if (d == 2) {
-              o = qa_dpp<0x4E>(v);  // quad_perm [2,3,0,1]
-            } else if (d == 4) {
-              const float up = qa_dpp<0x12C>(v), down = qa_dpp<0x124>(v);  // row_ror:12 / row_ror:4
-              o = hi ? down : up;
-            } else {
-              o = qa_dpp<0x128>(v);  // row_ror:8
-            }
-            const float sum = __fadd_rn(v, o), dif = __fsub_rn(o, v);
-            y[g][j] = hi ? dif : sum;
+            for (int j = 0; j < 8; j++) y[g][j] = n[j];
           }
-        }
+      } else {
+        const int bit = (lane >> (lh - 3)) & 1;
+        const float c = bit ? -1.0f : 1.0f;
+#pragma unroll
+        for (int g = 0; g < NG; g++)
+          if (g < G) {
+            if (lh == 3) FW8_FMAC_STAGE(y[g], "quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf");
+            else if (lh == 4) FW8_FMAC_STAGE(y[g], "quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf");
+            else FW8_FMAC_STAGE(y[g], "row_ror:8 row_mask:0xf bank_mask:0xf");
+          }
+        neg ^= bit;
+      }
     }
   }
-  // lane ^ 16, 32: the swap gives the pair's lower value a and upper value b in every lane
 #pragma unroll
   for (int lh = 7; lh < 9; lh++) {
     if (lh < lbs) {
-      const bool hi = lane & (1 << (lh - 3));
+      const float c = (lane >> (lh - 3)) & 1 ? -1.0f : 1.0f;
 #pragma unroll
       for (int g = 0; g < NG; g++)
         if (g < G) {
@@ -82,13 +118,12 @@ __device__ __forceinline__ void fwht512_rows(float y[NG][8], int G, int lane, in
             const u32 v = __float_as_uint(y[g][j]);
             const auto ab = lh == 7 ? __builtin_amdgcn_permlane16_swap(v, v, false, false)
                                     : __builtin_amdgcn_permlane32_swap(v, v, false, false);
-            const float a = __uint_as_float(ab[0]), b = __uint_as_float(ab[1]);
-            const float sum = __fadd_rn(a, b), dif = __fsub_rn(a, b);
-            y[g][j] = hi ? dif : sum;
+            y[g][j] = __builtin_fmaf(__uint_as_float(ab[1]), c, __uint_as_float(ab[0]));
           }
         }
     }
   }
+  return neg;
 }
 
 

@@ -68,32 +68,9 @@ __global__ void __launch_bounds__(256) quant_act_kernel(const T* __restrict__ x,
 // quantizing pass reloads and transforms again.
 #define QA_GMAX 16
 
-__device__ __forceinline__ void fwht512(float v[8], int lane, int lbs) {
-#pragma unroll
-  for (int lh = 0; lh < 3; lh++) {
-    if (lh < lbs) {
-      const int h = 1 << lh;
-#pragma unroll
-      for (int j = 0; j < 8; j++)
-        if (!(j & h)) {
-          const float a = v[j], b = v[j + h];
-          v[j] = __fadd_rn(a, b);
-          v[j + h] = __fsub_rn(a, b);
-        }
-    }
-  }
-#pragma unroll
-  for (int lh = 3; lh < 9; lh++) {
-    if (lh < lbs) {
-      const int d = 1 << (lh - 3);
-      const bool hi = lane & d;
-#pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const float o = __shfl_xor(v[j], d, 64);
-        v[j] = hi ? __fsub_rn(o, v[j]) : __fadd_rn(v[j], o);
-      }
-    }
-  }
+// one group: the lane's sign is returned as by fwht512_rows
+__device__ __forceinline__ bool fwht512(float v[8], int lane, int lbs) {
+  return fwht512_rows<1>(reinterpret_cast<float(*)[8]>(v), 1, lane, lbs);
 }
 
 __device__ __forceinline__ void load8(const float* p, float v[8]) {
@@ -121,11 +98,12 @@ __global__ void __launch_bounds__(256) quant_act_wave_kernel(const T* __restrict
   const T* xr = x + (u64)row * k + lane * 8;
   float y[STASH ? QA_GMAX : 1][8];
   float mx = 0.f;
+  bool neg = false;  // the lane holds the negated transform (the same for every group)
   if constexpr (STASH) {
 #pragma unroll
     for (int g = 0; g < QA_GMAX; g++)
       if (g < G) load8(xr + g * 512, y[g]);
-    fwht512_rows<QA_GMAX>(y, G, lane, lbs);
+    neg = fwht512_rows<QA_GMAX>(y, G, lane, lbs);
 #pragma unroll
     for (int g = 0; g < QA_GMAX; g++)
       if (g < G) {
@@ -135,7 +113,7 @@ __global__ void __launch_bounds__(256) quant_act_wave_kernel(const T* __restrict
   } else {
     for (int g = 0; g < G; g++) {
       load8(xr + g * 512, y[0]);
-      fwht512(y[0], lane, lbs);
+      neg = fwht512(y[0], lane, lbs);
 #pragma unroll
       for (int j = 0; j < 8; j++) mx = fmaxf(mx, fabsf(y[0][j]));
     }
@@ -144,7 +122,7 @@ __global__ void __launch_bounds__(256) quant_act_wave_kernel(const T* __restrict
   for (int s = 32; s > 0; s >>= 1) mx = fmaxf(mx, __shfl_xor(mx, s, 64));
   const float fq = (float)qmax;
   const float s = __fdiv_rn(fmaxf(mx, 1e-8f), fq);
-  const double rs = 1.0 / (double)s;
+  const double rs = neg ? -1.0 / (double)s : 1.0 / (double)s;  // y / s = w * (+-1 / s)
   i8* qr = q + (u64)row * k + lane * 8;
   auto emit = [&](const float v[8], int g) {
     u64 packed = 0;
@@ -184,7 +162,7 @@ __global__ void __launch_bounds__(64 * QA_GMAX) quant_act_group_kernel(const T* 
   const u64 row = blockIdx.x;
   float y[1][8];
   load8(x + row * k + g * 512 + lane * 8, y[0]);
-  fwht512_rows<1>(y, 1, lane, lbs);
+  const bool neg = fwht512_rows<1>(y, 1, lane, lbs);
   float mx = 0.f;
 #pragma unroll
   for (int j = 0; j < 8; j++) mx = fmaxf(mx, fabsf(y[0][j]));
@@ -196,7 +174,7 @@ __global__ void __launch_bounds__(64 * QA_GMAX) quant_act_group_kernel(const T* 
   for (int i = 1; i < G; i++) mx = fmaxf(mx, wmax[i]);
   const float fq = (float)qmax;
   const float s = __fdiv_rn(fmaxf(mx, 1e-8f), fq);
-  const double rs = 1.0 / (double)s;
+  const double rs = neg ? -1.0 / (double)s : 1.0 / (double)s;  // y / s = w * (+-1 / s)
   u64 packed = 0;
 #pragma unroll
   for (int j = 0; j < 8; j++) {

@@ -140,11 +140,12 @@ __device__ __forceinline__ void dx_quant_lds_g(float* row, int k, int lbs, int q
                                                float* __restrict__ scale, DxRed& red) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, G = k >> 9;
   float mx = 0.f;
+  bool neg = false;  // the lane holds its groups' transform negated (the same sign for each)
   for (int g = wave; g < G; g += 4) {
     float4* p = reinterpret_cast<float4*>(row + g * 512 + lane * 8);
     const float4 a = p[0], b = p[1];
     float y[1][8] = {{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w}};
-    fwht512_rows<1>(y, 1, lane, lbs);
+    neg = fwht512_rows<1>(y, 1, lane, lbs);
 #pragma unroll
     for (int j = 0; j < 8; j++) mx = fmaxf(mx, fabsf(y[0][j]));
     p[0] = float4{y[0][0], y[0][1], y[0][2], y[0][3]};
@@ -153,7 +154,8 @@ __device__ __forceinline__ void dx_quant_lds_g(float* row, int k, int lbs, int q
   mx = block_max256(mx, red);
   const float fq = (float)qmax;
   const float s = __fdiv_rn(fmaxf(mx, 1e-8f), fq);
-  const double rs = 1.0 / (double)s;
+  // the lane reads back what it wrote: y / s = w * (+-1 / s)
+  const double rs = neg ? -1.0 / (double)s : 1.0 / (double)s;
   for (int g = wave; g < G; g += 4) {
     const float4* p = reinterpret_cast<const float4*>(row + g * 512 + lane * 8);
     const float4 a = p[0], b = p[1];
