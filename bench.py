@@ -312,6 +312,7 @@ def detrt_layer(args, torch, np):
     # GEMM-only device time per linear
     stream_of = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
     gemm_us, per = 0.0, {}
+    vend = dict(ours=0.0, blas=0.0, equal=True)
     for name, (nn, kk) in shapes.items():
         q, sx = detrt.quant_act(xs[name], lays[name].bs)
         y = torch.empty((M, nn), dtype=torch.float32, device=dev)
@@ -319,8 +320,13 @@ def detrt_layer(args, torch, np):
         f = lambda q=q, sx=sx, y=y, lay=lay, nn=nn, kk=kk: L.uwc_igemm_dequant_f32(  # noqa: E731
             q.data_ptr(), lay.Wq.data_ptr(), M, nn, kk, sx.data_ptr(), lay.sw.data_ptr(), y.data_ptr(), stream_of())
         us = _graph_time_us(torch, [f] * 8)
-        per[name] = dict(us=round(us, 2), tops=round(2.0 * M * nn * kk / us / 1e6, 1))
+        o_us, b_us, same = vendor_i32(torch, L, q, lay.Wq)
+        per[name] = dict(us=round(us, 2), tops=round(2.0 * M * nn * kk / us / 1e6, 1), i32_us=round(o_us, 2),
+                         hipblaslt_i32_us=round(b_us, 2), hipblaslt_equal=same)
         gemm_us += us
+        vend["ours"] += o_us
+        vend["blas"] += b_us
+        vend["equal"] &= same
     import oracle as O
     ctops, ct, ran, cores = cpu_linears(torch, np, O, M, shapes, budget_s=3.0)
     out = dict(workload="Qwen3-1.7B layer linears (qkv, o, gu, down) at M=2048, quant_act + exact GEMM + dequant",
@@ -330,6 +336,10 @@ def detrt_layer(args, torch, np):
                gemm_only=dict(us_per_layer=round(gemm_us, 2), tops=round(2.0 * macs / gemm_us / 1e6, 1),
                               frac_of_peak=round(2.0 * macs / gemm_us / 1e6 / PEAK_INT8_TOPS, 4), per_linear=per,
                               kernel="uwc_igemm_dequant_f32 (exact int8 GEMM, fused fp32 dequant), graph-replayed"),
+               vs_hipblaslt=dict(ours_i32_us_per_layer=round(vend["ours"], 2),
+                                 hipblaslt_i32_us_per_layer=round(vend["blas"], 2), outputs_equal=vend["equal"],
+                                 note="the four GEMMs on the same int8 operands, int32 out: uwc_igemm_i32 against "
+                                      "torch._int_mm (hipBLASLt), graph-replayed on this box"),
                host_ms_per_layer=round(host_dt * 1e3, 4),
                cpu_baseline=dict(value=round(ctops, 4), unit="TOPS", cores=cores, kind="port", **host_cpu(),
                                  sample=f"quant_act + fp64 matmul + dequant, {ran}, {ct:.2f} s"))
@@ -360,6 +370,24 @@ def _graph_time_us(torch, launches, reps=3):
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) * 1e3 / (reps * len(launches))
+
+
+def vendor_i32(torch, L, A, W):
+    """The same int8 GEMM on the same operands, int32 out, two ways, graph-replayed: this library's
+    uwc_igemm_i32 and the vendor's (torch._int_mm, hipBLASLt on ROCm). Returns (ours_us, blas_us,
+    outputs_equal)."""
+    m, k = A.shape
+    n = W.shape[0]
+    C = torch.empty((m, n), dtype=torch.int32, device=A.device)
+    Wt = W.t()  # k x n, column-major: the layout _int_mm takes for A W^T
+    ours = lambda: L.uwc_igemm_i32(A.data_ptr(), W.data_ptr(), m, n, k, C.data_ptr(),  # noqa: E731
+                                   torch.cuda.current_stream().cuda_stream)
+    ours_us = _graph_time_us(torch, [ours] * 4)
+    blas_us = _graph_time_us(torch, [lambda: (torch._int_mm(A, Wt), 0)[1]] * 4)
+    torch.cuda.synchronize()
+    same = bool(torch.equal(torch._int_mm(A, Wt), C))
+    del C
+    return ours_us, blas_us, same
 
 
 def cpu_linears(torch, np, O, m, shapes, budget_s=3.0):
@@ -472,6 +500,7 @@ def llama_prefill(args, torch, np):
     M = 8192
     shapes = {"qkv": (6144, 4096), "o": (4096, 4096), "gu": (28672, 4096), "down": (4096, 14336)}
     per, total_us, ops = {}, 0.0, 0.0
+    vend = dict(ours=0.0, blas=0.0, equal=True)
     for name, (n, k) in shapes.items():
         X = torch.randint(-64, 65, (M, k), dtype=torch.int8, device=dev)
         W = torch.randint(-64, 65, (n, k), dtype=torch.int8, device=dev)
@@ -480,15 +509,25 @@ def llama_prefill(args, torch, np):
         f = lambda: L.uwc_igemm_dequant_f32(X.data_ptr(), W.data_ptr(), M, n, k, sx.data_ptr(), sw.data_ptr(),  # noqa: E731
                                             Y.data_ptr(), torch.cuda.current_stream().cuda_stream)
         us = _graph_time_us(torch, [f] * 4)
-        per[name] = dict(us=round(us, 2), tops=round(2.0 * M * n * k / us / 1e6, 1))
+        del Y
+        o_us, b_us, same = vendor_i32(torch, L, X, W)
+        per[name] = dict(us=round(us, 2), tops=round(2.0 * M * n * k / us / 1e6, 1), i32_us=round(o_us, 2),
+                         hipblaslt_i32_us=round(b_us, 2), hipblaslt_equal=same)
         total_us += us
         ops += 2.0 * M * n * k
-        del X, W, Y
+        vend["ours"] += o_us
+        vend["blas"] += b_us
+        vend["equal"] &= same
+        del X, W
         torch.cuda.empty_cache()
     import oracle as O
     ctops, ct, ran, cores = cpu_linears(torch, np, O, 2048, {"o": (4096, 4096)}, budget_s=1.0)
     out = dict(us_per_layer=round(total_us, 1), tops=round(ops / total_us / 1e6, 1),
                frac_of_peak=round(ops / total_us / 1e6 / PEAK_INT8_TOPS, 4), per_linear=per,
+               vs_hipblaslt=dict(ours_i32_us_per_layer=round(vend["ours"], 1),
+                                 hipblaslt_i32_us_per_layer=round(vend["blas"], 1), outputs_equal=vend["equal"],
+                                 note="the same int8 operands, int32 out: uwc_igemm_i32 against torch._int_mm "
+                                      "(hipBLASLt), graph-replayed on this box"),
                cpu_baseline=dict(value=round(ctops, 4), unit="TOPS", cores=cores, kind="port", **host_cpu(),
                                  sample=f"quant_act + fp64 matmul + dequant of the o linear at M=2048 "
                                         f"(a quarter of the prefill rows), {ct:.2f} s"))
@@ -1073,7 +1112,7 @@ def main():
     ap.add_argument("--e2e-layers", type=int, default=28)
     ap.add_argument("--e2e-cpu-tokens", type=int, default=256)
     ap.add_argument("--traffic-probe", action="store_true", help="the workload of the FETCH_SIZE / WRITE_SIZE passes")
-    ap.add_argument("--linears-only", action="store_true", help="run only configs[1], configs[0] and the decode linears")
+    ap.add_argument("--linears-only", action="store_true", help="run only configs[1], configs[0], the decode and the prefill linears")
     ap.add_argument("--linears-traffic-probe", action="store_true",
                     help="the workload of the FETCH_SIZE / WRITE_SIZE passes over the configs[0], decode and configs[1] kernels")
     ap.add_argument("--summarize-linears-traffic", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "OUT", "CMD"),
@@ -1138,7 +1177,8 @@ def main():
         print(json.dumps(qwen3_e2e(args, torch, np)))
         return
     if args.linears_only:
-        print(json.dumps({"detrt_layer": detrt_layer(args, torch, np), "detrt_skinny": skinny_linears(args, torch, np)}))
+        print(json.dumps({"detrt_layer": detrt_layer(args, torch, np), "detrt_skinny": skinny_linears(args, torch, np),
+                          "llama_prefill": llama_prefill(args, torch, np)}))
         return
     ceiling = mfma_ceiling(torch)
     res = mining(args, torch, np, ops)
