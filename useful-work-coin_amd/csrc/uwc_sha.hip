@@ -115,29 +115,40 @@ __device__ __forceinline__ void sha_load16(const u32* __restrict__ p, int n, int
 // H(0x00 || block) of n little-endian data words at p (n <= 256); VEC: p is 16-byte aligned.
 // The next 64-byte piece's words are loaded before the current one is compressed, so the load
 // latency hides behind a compression (one wave per SIMD runs these chains: the leaves of a
-// 8192 x 2048 stage output are 65,536 chains).
+// 8192 x 2048 stage output are 65,536 chains). Message word j of the prefixed stream is
+// (Z[j-1] << 24) | (Z[j] >> 8) with Z[j] = bswap(d[j]): bytes d[j-1].3, d[j].0, d[j].1, d[j].2,
+// one v_perm_b32 of the raw words (selector 0x07000102) for every piece whose 16 words are all
+// data; the last piece (the tail, the 0x80 terminator and the length) takes the general form.
 template <bool VEC>
 __device__ void sha_block_leaf(const u32* __restrict__ p, int n, u32 out[8]) {
   const int nb = (4 * n + 1 + 1 + 8 + 63) / 64;
   sha_init(out);
-  u32 prev = 0;  // the 0x00 prefix
+  u32 prevraw = 0;  // the raw word before the piece: the top byte of the first is the 0x00 prefix
   u32 d[16];
   sha_load16<VEC>(p, n, 0, d);
   for (int b = 0; b < nb; b++) {
     u32 nxt[16];
     if (b + 1 < nb) sha_load16<VEC>(p, n, b + 1, nxt);
     u32 w[16];
+    if (16 * b + 16 <= n) {
 #pragma unroll
-    for (int t = 0; t < 16; t++) {
-      const int j = 16 * b + t;
-      u32 cur;
-      if (j < n) cur = __builtin_bswap32(d[t]) >> 8;
-      else if (j == n) cur = 0x00800000u;
-      else cur = 0;
-      w[t] = (j <= n ? (prev << 24) : 0u) | cur;
-      prev = j < n ? __builtin_bswap32(d[t]) : 0u;
+      for (int t = 0; t < 16; t++) w[t] = __builtin_amdgcn_perm(t ? d[t - 1] : prevraw, d[t], 0x07000102u);
+      prevraw = d[15];
+    } else {
+      u32 prev = __builtin_bswap32(prevraw);
+#pragma unroll
+      for (int t = 0; t < 16; t++) {
+        const int j = 16 * b + t;
+        u32 cur;
+        if (j < n) cur = __builtin_bswap32(d[t]) >> 8;
+        else if (j == n) cur = 0x00800000u;
+        else cur = 0;
+        w[t] = (j <= n ? (prev << 24) : 0u) | cur;
+        prev = j < n ? __builtin_bswap32(d[t]) : 0u;
+      }
+      prevraw = __builtin_bswap32(prev);
+      if (b == nb - 1) w[15] = (u32)((4 * n + 1) * 8);
     }
-    if (b == nb - 1) w[15] = (u32)((4 * n + 1) * 8);
     sha_compress(out, w);
 #pragma unroll
     for (int t = 0; t < 16; t++) d[t] = nxt[t];
