@@ -104,6 +104,15 @@ int uwc_igemm_i32(const int8_t* A, const int8_t* B, int m, int n, int k, int32_t
 int uwc_igemm_dequant_f32(const int8_t* A, const int8_t* B, int m, int n, int k, const float* sx, const float* sw,
                           float* Y, hipStream_t stream);
 
+/* Y = fadd(x, fmul(fmul(f32(A * B^T), sx[i]), sw[j])) (fp32 m x n, rows of stride n): the exact
+ * GEMM with the dequant and the residual add in its epilogue where the 256 x 256 tiles take the
+ * shape, else the dequantized product followed by the residual pass; the same bits either way.
+ * Y must not overlap x.
+ * Replaces DetLinear.int_gemm + detgpu kernels.dequant_residual of the o and down projections:
+ * runtime/detrt/qwen3.py:106-126, runtime/detgpu/kernels.py:805-813, runtime/detrt/stage.py:217, 224. */
+int uwc_igemm_dequant_residual_f32(const int8_t* A, const int8_t* B, int m, int n, int k, const float* sx,
+                                   const float* sw, const float* x, float* Y, hipStream_t stream);
+
 /* Scratch words uwc_b3_root_and_seed needs for an input of nbytes (host-side, no GPU work). */
 int uwc_b3_scratch_words(uint64_t nbytes);
 

@@ -120,6 +120,11 @@ def test_other_entry_points_reject_bad_arguments():
     assert L.uwc_quant_rows_had(fake, 4, 100, 0, fake, fake, None) == -1
     assert "multiple of 8" in L.uwc_last_error().decode()
     assert L.uwc_quant_rows_had(fake, 4, 96, 64, fake, fake, None) == -1
+    # the fused GEMM + residual: the output may not overlap the residual
+    assert L.uwc_igemm_dequant_residual_f32(fake, fake, 256, 256, 128, fake, fake, fake, fake, None) == -1
+    assert "overlaps" in L.uwc_last_error().decode()
+    assert L.uwc_igemm_dequant_residual_f32(fake, fake, 256, 256, 128, fake, fake, None, fake, None) == -1
+    assert "null" in L.uwc_last_error().decode()
 
 
 def test_python_surface_matches_reference_names():

@@ -125,6 +125,32 @@ def test_dequant_residual_and_embed(dev):
         detgpu.embed(_t(table, dev), _t(np.array([50]), dev))
 
 
+@pytest.mark.parametrize("m,n,k", [(8192, 2048, 256), (8192, 2048, 2048), (2048, 2048, 512), (384, 256, 128)])
+def test_linear_residual_fused(dev, m, n, k):
+    """uwc_igemm_dequant_residual_f32 (the 256 x 256 GEMM with the dequant and the residual add in
+    its epilogue where its tiles fill the CUs, 8192 x 2048; else the dequantized product and the
+    residual pass) equals dequant_residual of the int32 product bit for bit, and the oracle on
+    sampled rows."""
+    from uwc_amd import detgpu, detrt, ops
+    g = torch.Generator(device=dev)
+    g.manual_seed(m + n + k)
+    q = torch.randint(-127, 128, (m, k), dtype=torch.int8, device=dev, generator=g)
+    W = torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev, generator=g)
+    s = torch.rand(m, device=dev, generator=g) * 1e-3 + 1e-6
+    sw = torch.rand(n, device=dev, generator=g) * 1e-2 + 1e-6
+    x = torch.randn((m, n), device=dev, generator=g)
+    lin = detrt.DetLinear.from_quantized(W, sw, 0)
+    y = detgpu.linear_residual(lin, q, s, x)
+    ref = detgpu.dequant_residual(ops.igemm_i32(q, W), s, sw, x)
+    assert torch.equal(y.view(torch.int32), ref.view(torch.int32))
+    rows = [0, 1, m // 2 + 3, m - 1]
+    acc = (q[rows].cpu().numpy().astype(np.int64) @ W.cpu().numpy().astype(np.int64).T).astype(np.int32)
+    want = x[rows].cpu().numpy() + S.dequant(acc, s[rows].cpu().numpy(), sw.cpu().numpy())
+    assert np.array_equal(_u32(y[rows]), _u32(want))
+    out = torch.empty_like(x)
+    assert detgpu.linear_residual(lin, q, s, x, out=out) is out and torch.equal(out, y)
+
+
 def _qkv_ref(acc, s1, sw, qnw, knw, cos, sin, B, T, H, Hkv, hd, eps, qknorm):
     qkv = S.dequant(acc, s1, sw)
     N = B * T

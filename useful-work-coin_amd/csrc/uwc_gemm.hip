@@ -459,6 +459,33 @@ extern "C" int uwc_igemm_dequant_f32(const int8_t* A, const int8_t* B, int m, in
                         OUT_F32, 0, nullptr, stream);
 }
 
+int uwc_gemm256_residual(const int8_t* A, const int8_t* B, int m, int n, int k, const float* sx, const float* sw,
+                         const float* x, float* Y, hipStream_t stream);
+extern "C" int uwc_dequant_residual(const void* acc, const float* s, const float* sw, const float* x, int rows, int n,
+                                    float* out, hipStream_t stream);
+
+extern "C" int uwc_igemm_dequant_residual_f32(const int8_t* A, const int8_t* B, int m, int n, int k, const float* sx,
+                                              const float* sw, const float* x, float* Y, hipStream_t stream) {
+  const char* fn = "uwc_igemm_dequant_residual_f32";
+  if (!x || !Y) return uwc_fail("%s: null x or Y", fn);
+  if (int st = gemm_check(A, B, m, n, k, 0, nullptr, nullptr, nullptr, 0, nullptr, nullptr, nullptr, 0, sx, sw, Y,
+                          OUT_F32, 0))
+    return st;
+  const uintptr_t xa = (uintptr_t)x, ya = (uintptr_t)Y, bytes = (uintptr_t)m * (uintptr_t)n * 4;
+  if (xa < ya + bytes && ya < xa + bytes) return uwc_fail("%s: Y overlaps x", fn);
+  // the shapes uwc_noisy_gemm puts on 256 x 256 tiles with one workgroup per tile (at least one
+  // tile per CU, the last round at least 90% full); their epilogue adds the residual
+  const int cus = uwc_cu_count();
+  const long t256 = (long)(m / 256) * (n / 256), rounds256 = (t256 + cus - 1) / cus;
+  const bool fills = t256 >= cus && t256 * 10 >= rounds256 * cus * 9;
+  const bool k256 = k % 128 == 0 && k <= (1 << 24) && n <= (1 << 24);
+  if (m % 256 == 0 && n % 256 == 0 && k256 && fills && aligned16(Y) && aligned16(x) && n % 4 == 0)
+    return uwc_gemm256_residual(A, B, m, n, k, sx, sw, x, Y, stream);
+  // elsewhere: the dequantized product, then Y = fadd(x, Y) in place (each element read, then written)
+  if (int st = uwc_igemm_dequant_f32(A, B, m, n, k, sx, sw, Y, stream)) return st;
+  return uwc_dequant_residual(Y, nullptr, nullptr, x, m, n, Y, stream);
+}
+
 int uwc_noisy_gemm256_many(int count, const int8_t* const* A, const int8_t* B, int m, int n, int k, int r,
                            const int8_t* const* corrA, const int8_t* const* corrB, const int32_t* const* maxabs,
                            int lmax, const uint32_t* const* key, const uint32_t* target, uint32_t* const* wins,

@@ -82,6 +82,7 @@ static_assert(W_LDS + W_LDS_HANDOFF <= 160 * 1024, "LDS exceeds 160 KiB (gfx950 
 #define OUT_I32 1
 #define OUT_BF16 2
 #define OUT_F32 3
+#define OUT_F32R 4  // OUT_F32 plus an fp32 residual of the same layout (plain GEMMs only)
 #define WIN_WORDS 10
 #define DUMP_WORDS 24
 
@@ -108,6 +109,7 @@ struct Gemm256Params {
   int max_wins;
   const float* a_scale;
   const float* b_scale;
+  const float* res;  // OUT_F32R: the residual rows, row stride ldc
   int ldc;  // output row stride in elements
   int count;
   int tiles;  // > 0: the plain multi-tile form (item i is tile blockIdx.x + i * gridDim.x of it[0])
@@ -510,7 +512,7 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
       u8* base = reinterpret_cast<u8*>(out) + ((long)row0 * p.ldc + col0) * ES;
       const u32 loff = (u32)(lr * p.ldc + lc) * ES;
       float asc = 0.f;
-      if constexpr (OUT == OUT_BF16 || OUT == OUT_F32) asc = p.a_scale[row0 + lr];
+      if constexpr (OUT == OUT_BF16 || OUT == OUT_F32 || OUT == OUT_F32R) asc = p.a_scale[row0 + lr];
 #pragma unroll
       for (int j = 0; j < 4; j++) {
         u8* dst = base + loff + 8 * j * ES;
@@ -523,6 +525,10 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
             y[i] = __fmul_rn(__fmul_rn((float)v[4 * j + i], asc), p.b_scale[col0 + 8 * j + lc + i]);
           if constexpr (OUT == OUT_F32) {
             uwc_store_nt(dst, float4{y[0], y[1], y[2], y[3]});
+          } else if constexpr (OUT == OUT_F32R) {
+            const float4 x = uwc_load_nt(p.res + ((long)(row0 + lr) * p.ldc + col0 + 8 * j + lc));
+            uwc_store_nt(dst, float4{__fadd_rn(x.x, y[0]), __fadd_rn(x.y, y[1]), __fadd_rn(x.z, y[2]),
+                                     __fadd_rn(x.w, y[3])});
           } else {
             const uint2 w{bf16_rne(y[0]) | (bf16_rne(y[1]) << 16), bf16_rne(y[2]) | (bf16_rne(y[3]) << 16)};
             uwc_store_nt(dst, w);
@@ -814,6 +820,11 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
         // trip in front of every one of a storer's 64 stores per item
         v4i xs[4];
         float ascs[4];
+        float4 rs[4];  // OUT_F32R: the residual of the four row segments, loaded first
+        if constexpr (OUT == OUT_F32R) {
+#pragma unroll
+          for (int jj = 0; jj < 4; jj++) rs[jj] = uwc_load_nt(p.res + ((long)(row0 + 8 * jj + (lane >> 3)) * p.ldc + col));
+        }
 #pragma unroll
         for (int jj = 0; jj < 4; jj++) {
           const int rr = 8 * jj + (lane >> 3);
@@ -835,6 +846,9 @@ __global__ void __launch_bounds__(W_THREADS) noisy_gemm256_kernel(Gemm256Params 
             const float y3 = __fmul_rn(__fmul_rn((float)x[3], asc), sw.w);
             if constexpr (OUT == OUT_F32) {
               uwc_store_nt(dst, float4{y0, y1, y2, y3});
+            } else if constexpr (OUT == OUT_F32R) {
+              uwc_store_nt(dst, float4{__fadd_rn(rs[jj].x, y0), __fadd_rn(rs[jj].y, y1), __fadd_rn(rs[jj].z, y2),
+                                       __fadd_rn(rs[jj].w, y3)});
             } else {
               uwc_store_nt(dst, uint2{bf16_rne(y0) | (bf16_rne(y1) << 16), bf16_rne(y2) | (bf16_rne(y3) << 16)});
             }
@@ -1084,6 +1098,25 @@ int uwc_noisy_gemm256(const int8_t* A, const int8_t* B, int m, int n, int k, int
   else if (denoise) out256<false, true>(out_mode, grid, stream, p);
   else out256<false, false>(out_mode, grid, stream, p);
   return uwc_launch_status("noisy_gemm256");
+}
+
+// Y = x + fmul(fmul(f32(A B^T), sx[i]), sw[j]) on 256 x 256 tiles, one workgroup per tile: the
+// fp32 dequant epilogue with the residual added before the store (the same two roundings and the
+// same add as a separate residual pass, without writing and rereading the dequantized rows).
+// Called by uwc_igemm_dequant_residual_f32 for the shapes uwc_noisy_gemm puts on these tiles.
+int uwc_gemm256_residual(const int8_t* A, const int8_t* B, int m, int n, int k, const float* sx, const float* sw,
+                         const float* x, float* Y, hipStream_t stream) {
+  Gemm256Params p{};
+  p.B = B;
+  p.m = m, p.n = n, p.k = k;
+  p.a_scale = sx;
+  p.b_scale = sw;
+  p.res = x;
+  p.ldc = n;
+  p.count = 1;
+  p.it[0] = Gemm256Item{A, nullptr, nullptr, nullptr, nullptr, nullptr, Y, nullptr};
+  go256<false, false, OUT_F32R>(dim3((m / W_BM) * (n / W_BN)), stream, p);
+  return uwc_launch_status("noisy_gemm256 (dequant + residual)");
 }
 
 // `count` (1 .. G256_MAXB) hashed, denoised GEMMs with int32 outputs sharing B in one launch, each

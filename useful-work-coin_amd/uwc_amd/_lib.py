@@ -29,6 +29,7 @@ SIGNATURES = {
     "uwc_noisy_gemm_many": [i32, vp, vp, i32, i32, i32, i32, vp, vp, vp, i32, vp, vp, vp, i32, vp, vp, vp, i32, i32, vp, vp],
     "uwc_igemm_i32": [vp, vp, i32, i32, i32, vp, vp],
     "uwc_igemm_dequant_f32": [vp, vp, i32, i32, i32, vp, vp, vp, vp],
+    "uwc_igemm_dequant_residual_f32": [vp, vp, i32, i32, i32, vp, vp, vp, vp, vp],
     "uwc_b3_scratch_words": [u64],
     "uwc_b3_root_and_seed": [vp, u64, vp, vp, vp, u32, vp, vp, vp, u64, vp],
     "uwc_b3_root_and_seed_static": [vp, u64, vp, vp, vp, u32, vp, vp, vp],

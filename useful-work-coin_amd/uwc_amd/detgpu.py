@@ -176,6 +176,27 @@ def dequant_residual(acc, s, sw, x, out=None):
     return out
 
 
+def linear_residual(lin, q, s, x, out=None):
+    """x + fmul(fmul(f32(q @ lin.Wq^T), s), lin.sw): a DetLinear's exact GEMM on pre-quantized rows
+    q (N, k) with the dequant and the residual x (N, n) added in one call
+    (uwc_igemm_dequant_residual_f32: in the GEMM's epilogue where its 256 x 256 tiles take the
+    shape), the same bits as dequant_residual(lin.int_gemm(q), s, lin.sw, x). out: an optional
+    contiguous (N, n) float32 destination that does not overlap x."""
+    if lin.mine and lin.mw is not None:
+        return dequant_residual(lin.int_gemm(q), s, lin.sw, x, out=out)
+    q, x = q.contiguous(), x.contiguous()
+    N = q.shape[0]
+    if out is None:
+        out = torch.empty((N, lin.n), dtype=F32, device=q.device)
+    elif out.shape != (N, lin.n) or out.dtype != F32 or not out.is_contiguous():
+        raise AssertionError(f"linear_residual: out must be a contiguous float32 {N} x {lin.n} tensor")
+    if x.shape != (N, lin.n) or x.dtype != F32:
+        raise AssertionError(f"linear_residual: x must be float32 {N} x {lin.n}")
+    _lib.call("uwc_igemm_dequant_residual_f32", q.data_ptr(), lin.Wq.data_ptr(), N, lin.n, lin.k, s.data_ptr(),
+              lin.sw.data_ptr(), x.data_ptr(), out.data_ptr(), _stream())
+    return out
+
+
 def swiglu_quant(acc, s3, sw, bs: int):
     """quant_act(silu(g) * u, bs) from the gate_up GEMM's int32 rows (detgpu/kernels.py:816-826),
     or from float32 GU rows (s3 = sw = None)."""
@@ -414,10 +435,10 @@ def layer_fused(m, L, x: torch.Tensor, B: int, T: int, out: torch.Tensor | None 
                                              L["cos"][:T], L["sin"][:T], T, H, Hkv, m.eps, m.qk_norm)
     oc = attention(qq, qs, kq, ks, vq, vs, B, T, H, Hkv, m.inv_sqrt_hd, vt=vt)
     q2, s2 = quant_act(oc, L["o"].bs)
-    r1 = dequant_residual(L["o"].int_gemm(q2), s2, L["o"].sw, x)
+    r1 = linear_residual(L["o"], q2, s2, x)
     q3, s3 = rmsnorm_quant(r1, L["post_norm"], m.eps, L["gu"].bs)
     q4, s4 = swiglu_quant(L["gu"].int_gemm(q3), s3, L["gu"].sw, L["down"].bs)
-    return dequant_residual(L["down"].int_gemm(q4), s4, L["down"].sw, r1, out=out)
+    return linear_residual(L["down"], q4, s4, r1, out=out)
 
 
 @torch.no_grad()
