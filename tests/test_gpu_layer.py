@@ -75,8 +75,11 @@ def test_fp32_ops_match_ieee_and_detrt(dev):
         assert same.all(), (op, np.nonzero(~same)[0][:5], got[~same][:3], r[~same][:3])
 
 
-@pytest.mark.parametrize("k,bs", [(128, 64), (2048, 512), (6144, 512), (1024, 64), (512, 1), (1536, 0), (1000, 8), (96, 0)])
+@pytest.mark.parametrize("k,bs", [(128, 64), (2048, 512), (6144, 512), (1024, 64), (512, 1), (1536, 0), (1000, 8), (96, 0),
+                                  (4096, 128), (2560, 256), (3584, 32), (2048, 2)])
 def test_rmsnorm_quant_and_rmsnorm(dev, k, bs):
+    """k = 512 G up to 4096 run on the one-wave-per-row kernel (every G from 1 to 8 at some bs),
+    the rest on the LDS row kernel."""
     from uwc_amd import detgpu
     rng = np.random.default_rng(k + bs)
     x = _rows(rng, 37, k)
