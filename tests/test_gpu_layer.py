@@ -94,8 +94,10 @@ def test_rmsnorm_quant_and_rmsnorm(dev, k, bs):
     assert np.array_equal(_u32(y), _u32(ref_h))
 
 
-@pytest.mark.parametrize("I,bs", [(256, 64), (6144, 512), (1024, 8), (512, 2), (300, 4)])
+@pytest.mark.parametrize("I,bs", [(256, 64), (6144, 512), (1024, 8), (512, 2), (300, 4), (2560, 128), (3584, 256),
+                                  (5632, 512), (4096, 1)])
 def test_swiglu_quant(dev, I, bs):
+    """I = 512 G up to 6144 run on the one-wave-per-row kernel, the rest on the LDS row kernel."""
     from uwc_amd import detgpu
     rng = np.random.default_rng(I)
     n = 19

@@ -40,6 +40,36 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const float* __restrict__ 
   }
 }
 
+// quant_act (qmax 64, dx_quant_lds_g's ops) of one row held by a wave in the 8-per-lane layout of
+// fwht512_rows (lane L: elements 8 L .. 8 L + 7 of each 512-element group): the transform, the
+// row's max |y| by a wave reduction, one 8-byte store per group and lane, the scale by lane 0.
+template <int G>
+__device__ __forceinline__ void wave_quant_row(float (&y)[G][8], int lane, int lbs, i8* __restrict__ qrow,
+                                               float* __restrict__ srow) {
+  const bool neg = fwht512_rows<G>(y, G, lane, lbs);
+  float m2 = 0.f;
+#pragma unroll
+  for (int g = 0; g < G; g++)
+#pragma unroll
+    for (int j = 0; j < 8; j++) m2 = fmaxf(m2, fabsf(y[g][j]));
+  m2 = wave_max(m2);
+  const float fq = 64.0f;
+  const float sc = __fdiv_rn(fmaxf(m2, 1e-8f), fq);
+  const double rs = neg ? -1.0 / (double)sc : 1.0 / (double)sc;  // the lane holds y or -y
+  i8* qr = qrow + lane * 8;
+#pragma unroll
+  for (int g = 0; g < G; g++) {
+    u64 packed = 0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const float t = fminf(fmaxf(rintf(uwc_div_rd(y[g][j], rs)), -fq), fq);
+      packed |= (u64)(u8)(i8)(int)t << (8 * j);
+    }
+    *reinterpret_cast<u64*>(qr + g * 512) = packed;
+  }
+  if (lane == 0) *srow = lbs > 0 ? __fmul_rn(sc, __fdiv_rn(1.0f, uwc_sqrt_rn((float)(1 << lbs)))) : sc;
+}
+
 // rmsnorm + quant_act with one wave per row and the row in registers, for k = 512 G (G <= 8) and
 // bs = 2^lbs <= 512: lane L holds elements 8 L .. 8 L + 7 of each 512-element group (the layout of
 // fwht512_rows), the max square and the exact fixed-point sum are wave reductions (a max and an
@@ -85,31 +115,42 @@ __global__ void __launch_bounds__(256) rmsnorm_quant_wave_kernel(const float* __
 #pragma unroll
     for (int j = 0; j < 8; j++) y[g][j] = __fmul_rn(__fmul_rn(y[g][j], rr), wv[j]);
   }
-  const bool neg = fwht512_rows<G>(y, G, lane, lbs);
-  float m2 = 0.f;
-#pragma unroll
-  for (int g = 0; g < G; g++)
-#pragma unroll
-    for (int j = 0; j < 8; j++) m2 = fmaxf(m2, fabsf(y[g][j]));
-  m2 = wave_max(m2);
-  const float fq = 64.0f;
-  const float sc = __fdiv_rn(fmaxf(m2, 1e-8f), fq);
-  const double rs = neg ? -1.0 / (double)sc : 1.0 / (double)sc;  // the lane holds y or -y
-  i8* qr = q + r * K + lane * 8;
-#pragma unroll
-  for (int g = 0; g < G; g++) {
-    u64 packed = 0;
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-      const float t = fminf(fmaxf(rintf(uwc_div_rd(y[g][j], rs)), -fq), fq);
-      packed |= (u64)(u8)(i8)(int)t << (8 * j);
-    }
-    *reinterpret_cast<u64*>(qr + g * 512) = packed;
-  }
-  if (lane == 0) scale[r] = lbs > 0 ? __fmul_rn(sc, __fdiv_rn(1.0f, uwc_sqrt_rn((float)(1 << lbs)))) : sc;
+  wave_quant_row<G>(y, lane, lbs, q + r * K, scale + r);
 }
 
 // ------------------------------------------------------------------ swiglu + quant_act
+// swiglu_quant from int32 gate | up rows with one wave per row and the row in registers, for
+// I = 512 G (G <= 12) and bs <= 512: element i = fmul(silu(deq(g_i)), deq(u_i)) as in the row
+// kernel below, then wave_quant_row. No LDS and no barrier.
+template <int G>
+__global__ void __launch_bounds__(256) swiglu_quant_wave_kernel(const i32* __restrict__ acc, const float* __restrict__ s3,
+                                                                const float* __restrict__ sw, int rows, int lbs,
+                                                                i8* __restrict__ q, float* __restrict__ scale) {
+  constexpr int I = 512 * G;
+  const int lane = threadIdx.x & 63;
+  const long r = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;  // whole waves only; no barriers below
+  const i32* ar = acc + r * 2L * I + lane * 8;
+  const float* swr = sw + lane * 8;
+  const float sx = s3[r];
+  float y[G][8];
+#pragma unroll
+  for (int g = 0; g < G; g++) {
+    const v4i g0 = *reinterpret_cast<const v4i*>(ar + g * 512), g1 = *reinterpret_cast<const v4i*>(ar + g * 512 + 4);
+    const v4i u0 = *reinterpret_cast<const v4i*>(ar + I + g * 512), u1 = *reinterpret_cast<const v4i*>(ar + I + g * 512 + 4);
+    const float4 wg0 = *reinterpret_cast<const float4*>(swr + g * 512), wg1 = *reinterpret_cast<const float4*>(swr + g * 512 + 4);
+    const float4 wu0 = *reinterpret_cast<const float4*>(swr + I + g * 512),
+                 wu1 = *reinterpret_cast<const float4*>(swr + I + g * 512 + 4);
+    const int gv[8] = {g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
+    const int uv[8] = {u0[0], u0[1], u0[2], u0[3], u1[0], u1[1], u1[2], u1[3]};
+    const float wgv[8] = {wg0.x, wg0.y, wg0.z, wg0.w, wg1.x, wg1.y, wg1.z, wg1.w};
+    const float wuv[8] = {wu0.x, wu0.y, wu0.z, wu0.w, wu1.x, wu1.y, wu1.z, wu1.w};
+#pragma unroll
+    for (int j = 0; j < 8; j++) y[g][j] = __fmul_rn(dx_silu(dx_deq(gv[j], sx, wgv[j])), dx_deq(uv[j], sx, wuv[j]));
+  }
+  wave_quant_row<G>(y, lane, lbs, q + r * (long)I, scale + r);
+}
+
 // acc: rows x 2I (gate | up), int32 accumulators dequantized with s3[row], sw[col], or with FP
 // already fp32; row value i = fmul(silu(g_i), u_i) (stage.py:220-221).
 template <bool FP>
@@ -398,6 +439,21 @@ extern "C" int uwc_swiglu_quant(const void* acc, const float* s3, const float* s
   int st = check_bs(fn, bs, I);
   if (st) return st;
   if (rows == 0) return UWC_OK;
+  const int bse = bs > 1 ? bs : 1;
+  if (s3 && I % 512 == 0 && I <= 512 * 12 && bse <= 512 && ((uintptr_t)acc & 15) == 0 && ((uintptr_t)sw & 15) == 0 &&
+      ((uintptr_t)q & 7) == 0) {
+    const int lbs = __builtin_ctz((unsigned)bse);
+    const dim3 grid((unsigned)((rows + 3) / 4));
+    const i32* a = static_cast<const i32*>(acc);
+#define SWQ(G)                                                                                                        \
+  case G: hipLaunchKernelGGL(swiglu_quant_wave_kernel<G>, grid, dim3(256), 0, stream, a, s3, sw, rows, lbs, q, scale); break;
+    switch (I / 512) {
+      SWQ(1) SWQ(2) SWQ(3) SWQ(4) SWQ(5) SWQ(6) SWQ(7) SWQ(8) SWQ(9) SWQ(10) SWQ(11)
+      default: hipLaunchKernelGGL(swiglu_quant_wave_kernel<12>, grid, dim3(256), 0, stream, a, s3, sw, rows, lbs, q, scale); break;
+    }
+#undef SWQ
+    return uwc_launch_status(fn);
+  }
   size_t smem;
   if (s3) {
     if ((st = row_lds(fn, (const void*)swiglu_quant_kernel<false>, I, smem))) return st;
