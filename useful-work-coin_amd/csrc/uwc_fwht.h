@@ -26,6 +26,23 @@ __device__ __forceinline__ float qa_dpp(float x) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
 }
 
+// The max over a fully active wave, in every lane: DPP partners inside each 16-lane row
+// (quad_perm [1,0,3,2], [2,3,0,1], then row_ror:4 and :8 over the quads), v_permlane16_swap and
+// v_permlane32_swap across rows; VALU operations only (a __shfl_xor step is an LDS round trip).
+// A max is the same in any order.
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, qa_dpp<0xB1>(v));
+  v = fmaxf(v, qa_dpp<0x4E>(v));
+  v = fmaxf(v, qa_dpp<0x124>(v));
+  v = fmaxf(v, qa_dpp<0x128>(v));
+  u32 u = __float_as_uint(v);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  u = __float_as_uint(v);
+  const auto b = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 // w[j] += c * w[j] of the DPP partner lane for the 8 values of one group; s_nop 4 covers the wait
 // states of a DPP read after a VALU (or EXEC) write of its source, whatever precedes the block
 #define FW8_FMAC_STAGE(w, DPP)                                                                              \

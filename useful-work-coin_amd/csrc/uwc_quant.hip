@@ -39,8 +39,7 @@ __global__ void __launch_bounds__(256) quant_act_kernel(const T* __restrict__ x,
   }
   float mx = 0.f;
   for (int i = tid; i < k; i += 256) mx = fmaxf(mx, fabsf(rowf[i]));
-#pragma unroll
-  for (int s = 32; s > 0; s >>= 1) mx = fmaxf(mx, __shfl_xor(mx, s));
+  mx = wave_max(mx);
   if ((tid & 63) == 0) red[tid >> 6] = mx;
   __syncthreads();
   const float amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
@@ -118,8 +117,7 @@ __global__ void __launch_bounds__(256) quant_act_wave_kernel(const T* __restrict
       for (int j = 0; j < 8; j++) mx = fmaxf(mx, fabsf(y[0][j]));
     }
   }
-#pragma unroll
-  for (int s = 32; s > 0; s >>= 1) mx = fmaxf(mx, __shfl_xor(mx, s, 64));
+  mx = wave_max(mx);
   const float fq = (float)qmax;
   const float s = __fdiv_rn(fmaxf(mx, 1e-8f), fq);
   const double rs = neg ? -1.0 / (double)s : 1.0 / (double)s;  // y / s = w * (+-1 / s)
@@ -166,8 +164,7 @@ __global__ void __launch_bounds__(64 * QA_GMAX) quant_act_group_kernel(const T* 
   float mx = 0.f;
 #pragma unroll
   for (int j = 0; j < 8; j++) mx = fmaxf(mx, fabsf(y[0][j]));
-#pragma unroll
-  for (int s = 32; s > 0; s >>= 1) mx = fmaxf(mx, __shfl_xor(mx, s, 64));
+  mx = wave_max(mx);
   if (lane == 0) wmax[g] = mx;
   __syncthreads();
   mx = wmax[0];
@@ -237,8 +234,7 @@ __global__ void __launch_bounds__(64 * QD_MAX) quant_act_dgroup_kernel(const T* 
   float mx = 0.f;
 #pragma unroll
   for (int j = 0; j < 16; j++) mx = fmaxf(mx, fabsf(y[j]));
-#pragma unroll
-  for (int s = 32; s > 0; s >>= 1) mx = fmaxf(mx, __shfl_xor(mx, s, 64));
+  mx = wave_max(mx);
   if (lane == 0) wmax[d] = mx;
   __syncthreads();
   mx = wmax[0];

@@ -76,17 +76,32 @@ __device__ __forceinline__ long long dx_fix(float v, int sh) {
 __device__ __forceinline__ float dx_unfix(long long s, int sh) { return (float)ldexp((double)s, -sh); }
 
 // ------------------------------------------------------------------ wave reductions (wave64)
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int s = 32; s > 0; s >>= 1) v = fmaxf(v, __shfl_xor(v, s, 64));
-  return v;
+// Every lane gets the wave's max / sum; the wave must be fully active. Inside each 16-lane row the
+// partners come through DPP operands (quad_perm [1,0,3,2], [2,3,0,1]: the quad; row_ror:4, 8: the
+// four quads), across rows from v_permlane16_swap and v_permlane32_swap (each lane receives its
+// pair's lower and upper value): VALU operations only, where __shfl_xor went through the LDS
+// crossbar (ds_bpermute) with an LDS round trip per step. A max and an integer sum are the same
+// in any order.
+// wave_max: uwc_fwht.h
+
+template <int CTRL>
+__device__ __forceinline__ long long dpp64(long long x) {
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)(unsigned)x, CTRL, 0xF, 0xF, true);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(x >> 32), CTRL, 0xF, 0xF, true);
+  return (long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo);
 }
 
 __device__ __forceinline__ long long wave_sum64(long long v) {
+  v += dpp64<0xB1>(v);
+  v += dpp64<0x4E>(v);
+  v += dpp64<0x124>(v);
+  v += dpp64<0x128>(v);
 #pragma unroll
-  for (int s = 32; s > 0; s >>= 1) {
-    const int lo = __shfl_xor((int)(unsigned)v, s, 64), hi = __shfl_xor((int)(v >> 32), s, 64);
-    v += (long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo);
+  for (int s = 0; s < 2; s++) {
+    const u32 lo = (u32)v, hi = (u32)((unsigned long long)v >> 32);
+    const auto l = s ? __builtin_amdgcn_permlane32_swap(lo, lo, false, false) : __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+    const auto h = s ? __builtin_amdgcn_permlane32_swap(hi, hi, false, false) : __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    v = (long long)(((unsigned long long)h[0] << 32) | l[0]) + (long long)(((unsigned long long)h[1] << 32) | l[1]);
   }
   return v;
 }
