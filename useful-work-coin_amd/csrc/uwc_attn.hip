@@ -23,7 +23,8 @@
 //     from per-lane candidates, the third statistic (sweep 3, a pass over the keys of its own,
 //     runs only for waves with a near tie), sweep 4 quantizes P and runs P x V; the scores are
 //     recomputed on the matrix cores rather than stored as T x T rows, and the exponentials of
-//     sweep 2 are kept in a scratch for sweep 4 (uwc_attention_ws);
+//     sweep 2 are kept in a scratch for sweep 4 (uwc_attention_ws), which also runs sweep 1 as
+//     a kernel of its own whose workgroups share each key tile through LDS (attn_rowmax_kernel);
 //   * workgroups are mapped so that each XCD owns whole kv heads, whose K and V then stay in its
 //     L2 (at_block);
 //   * exp rows have max exactly det_exp(0) = 1 and every term below 2, so exact_rowsum's
@@ -40,6 +41,7 @@
 // lambdas are always inlined: an out-of-line call would take the address of the register arrays
 // they capture (private memory)
 #define AT_AI __attribute__((always_inline))
+typedef void __attribute__((address_space(3)))* s2_lptr_at;
 
 __device__ __forceinline__ v4i at_zero4() { return v4i{0, 0, 0, 0}; }
 
@@ -143,12 +145,16 @@ __host__ __device__ constexpr u64 at_tiles(u64 Tp) { return at_tile0(Tp / 16); }
 // the same bits. The scratch (2.2 GB at T = 8192, 16 heads) is written and read with the
 // non-temporal hint: cached normally, its stream evicted the XCD's K and V from L2
 // (2.087 -> 1.960 ms per Qwen3-1.7B layer at T = 8192).
-template <int HD, bool ES>
-__global__ void __launch_bounds__(256, HD == 128 ? 2 : 3) attention_kernel(const i8* __restrict__ qq, const float* __restrict__ qs,
-                                                        const i8* __restrict__ kq, const float* __restrict__ ks,
-                                                        const i8* __restrict__ vt, const float* __restrict__ vs, int T,
-                                                        int Tp, int H, int Hkv, float inv_sqrt, float* __restrict__ o,
-                                                        float* __restrict__ escr) {
+//
+// RM: the row maxima of sweep 1 come from rmax (attn_rowmax_kernel, y = fl(fl(acc qs) ks) per
+// query and head at rmax[(b T + q) H + h]) and the kernel starts at sweep 2. A max over the same
+// values in another order is the same number, so both forms give the same bits.
+template <int HD, bool ES, bool RM>
+__global__ void __launch_bounds__(256, HD == 128 ? 2 : 3)
+    attention_kernel(const i8* __restrict__ qq, const float* __restrict__ qs, const i8* __restrict__ kq,
+                     const float* __restrict__ ks, const i8* __restrict__ vt, const float* __restrict__ vs, int T,
+                     int Tp, int H, int Hkv, float inv_sqrt, float* __restrict__ o, float* __restrict__ escr,
+                     const float* __restrict__ rmax) {
   constexpr int NC = (HD + 63) / 64;  // 64-dim chunks of the score product
   constexpr int ND = HD / 16;         // 16-dim blocks of the output
   __shared__ __attribute__((aligned(16))) float at_slot[4][2][64];
@@ -302,13 +308,18 @@ __global__ void __launch_bounds__(256, HD == 128 ? 2 : 3) attention_kernel(const
   // sweep 1: row max. A score is fl(y * inv) with y = fl(fl(acc * qs) * ks) and inv > 0, a
   // monotone function of y, so the max score is fl(max_j y_j * inv) (-inf for an empty row too)
   float mx = -__int_as_float(0x7f800000);
-  ksweep([&](int kt, const float (&Y)[4][4], const KTile&) AT_AI {
+  if constexpr (RM) {
+    // a padding query (qi >= T) sees keys 0 .. T - 1, as query T - 1 does
+    mx = __fmul_rn(rmax[(nb + qc) * (u32)H + h], inv_sqrt);
+  } else {
+    ksweep([&](int kt, const float (&Y)[4][4], const KTile&) AT_AI {
 #pragma unroll
-    for (int b = 0; b < 4; b++)
+      for (int b = 0; b < 4; b++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) mx = fmaxf(mx, Y[b][i]);
-  }, std::true_type{});
-  mx = __fmul_rn(at_max_groups(mx), inv_sqrt);
+        for (int i = 0; i < 4; i++) mx = fmaxf(mx, Y[b][i]);
+    }, std::true_type{});
+    mx = __fmul_rn(at_max_groups(mx), inv_sqrt);
+  }
 
   // sweep 2: exact denominator (fixed point at 2^41); masked entries give det_exp(-inf) = 0.
   // A tile's 16 terms per lane sum exactly in float64 (< 2^46), then join a u64 total.
@@ -492,10 +503,132 @@ __global__ void __launch_bounds__(256, HD == 128 ? 2 : 3) attention_kernel(const
   }
 }
 
-extern "C" uint64_t uwc_attention_scratch_bytes(int B, int T, int H) {
-  if (B <= 0 || T <= 0 || H <= 0) return 0;
+// ------------------------------------------------------------------ sweep 1 alone
+// The row max of y = fl(fl(acc qs) ks) over each query's causal keys, for the stored-exp form.
+// Inside the full kernel (two waves per SIMD) this sweep waited on its K loads most of the time:
+// every wave fetched each 64-key tile itself, 16 half-used 128-byte lines per load instruction.
+// Here the four waves of a workgroup (64 queries of one head, the same key tiles) share each tile:
+// it is DMA'd once into an LDS ring of NS tiles (global_load_lds_dwordx4, each lane 16 bytes,
+// eight consecutive lanes one whole 128-byte key row), every wave issuing the same number of DMAs
+// per tile so that its wait counts are static, and read back in the MFMA operand layout. The
+// 16-byte pieces of key row m sit at piece p ^ swz(m) so that the 16 lanes of a read (rows
+// 16 b .. + 15, one piece) hit 16 distinct bank groups.
+__device__ __forceinline__ void at_dma16(const void* g, u32 lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ void at_dma4(const void* g, u32 lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+template <int N>
+__device__ __forceinline__ void at_waitv() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// LDS barrier: this wave's LDS operations done, then every wave's (global memory is not fenced)
+__device__ __forceinline__ void at_lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+template <int HD>
+__host__ __device__ constexpr int at_swz(int m) {
+  return (m / (16 / (HD / 16))) & (HD / 16 - 1);
+}
+
+template <int HD, int NS>
+__global__ void __launch_bounds__(256) attn_rowmax_kernel(const i8* __restrict__ qq, const float* __restrict__ qs,
+                                                          const i8* __restrict__ kq, const float* __restrict__ ks,
+                                                          int T, int Tp, int H, int Hkv, float* __restrict__ rmax) {
+  constexpr int NC = (HD + 63) / 64;
+  constexpr int PR = HD / 16;                     // 16-byte pieces per key row
+  constexpr int TILE = 64 * HD;                   // bytes of one 64-key tile
+  constexpr int KD = TILE >= 4096 ? TILE / 4096 : 1;  // K DMAs per wave and tile
+  constexpr int KL = TILE >= 4096 ? 64 : TILE / 64;   // lanes active in each (HD 32: 32)
+  constexpr int NW = (NS - 2) * (KD + 1);         // DMAs of the tiles a wait leaves in flight
+  __shared__ __attribute__((aligned(16))) u8 kring[NS][TILE];
+  __shared__ __attribute__((aligned(16))) float sring[NS][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int ql = lane & 15, g = lane >> 4;
+  int qt, h, bseq;
+  at_block((int)blockIdx.x, Tp / 64, H, Hkv, (int)(gridDim.x / (u32)(Tp / 64 * H)), qt, h, bseq);
+  // every wave runs every tile and barrier (a wave past T computes clamped rows and stores nothing)
+  const int q0 = qt * 64 + wave * 16;
+  const int hk = h / (H / Hkv);
+  const u32 nb = (u32)(bseq * T);
+  const int qi = q0 + ql, qc = min(qi, T - 1);
+  const float my_qs = qs[(nb + qc) * (u32)H + h];
+  v4i qf[NC];
+#pragma unroll
+  for (int c = 0; c < NC; c++) {
+    const int d0 = 64 * c + 16 * g;
+    qf[c] = d0 < HD ? *reinterpret_cast<const v4i*>(qq + ((nb + qc) * (u32)H + h) * HD + d0) : at_zero4();
+  }
+  // the compiler waits for these loads here (asm inputs), so that it places no vmcnt wait for them
+  // inside the tile loop, where any vmcnt wait would also drain the ring's DMAs
+#pragma unroll
+  for (int c = 0; c < NC; c++) asm volatile("" ::"v"(qf[c]));
+  asm volatile("" ::"v"(my_qs));
+  const int nkt = qt + 1;  // key tiles 0 .. qt; tile qt holds the diagonal
+  const i8* kbase = kq + (size_t)hk * HD;
+  const u32 sc_base = nb * (u32)Hkv + hk;
+  const u32 kr0 = (u32)(uintptr_t)(s2_lptr_at)kring[0], sr0 = (u32)(uintptr_t)(s2_lptr_at)sring[0];
+  auto issue = [&](int kt) AT_AI {
+    const int st = kt % NS;
+#pragma unroll
+    for (int u = 0; u < KD; u++) {
+      const int s16 = (wave * KD + u) * KL + lane;  // 16-byte slot of the tile
+      const int m = s16 / PR, p = (s16 % PR) ^ at_swz<HD>(m);
+      const i8* src = kbase + (nb + (u32)min(kt * 64 + m, T - 1)) * (u32)(Hkv * HD) + 16 * p;
+      const u32 dst = __builtin_amdgcn_readfirstlane(kr0 + (u32)(st * TILE + (wave * KD + u) * KL * 16));
+      if (KL == 64 || lane < KL) at_dma16(src, dst);
+    }
+    const float* ssrc = ks + sc_base + (u32)min(kt * 64 + wave * 16 + (lane & 15), T - 1) * (u32)Hkv;
+    const u32 sdst = __builtin_amdgcn_readfirstlane(sr0 + (u32)(st * 256 + wave * 64));
+    if (lane < 16) at_dma4(ssrc, sdst);
+  };
+#pragma unroll
+  for (int t = 0; t < NS - 1; t++)
+    if (t < nkt) issue(t);
+  float mx = -__int_as_float(0x7f800000);
+  for (int kt = 0; kt < nkt; kt++) {
+    if (kt + NS - 2 < nkt) at_waitv<NW>();
+    else at_waitv<0>();
+    at_lds_barrier();  // tile kt is in LDS; every wave is done with tile kt - 1's stage
+    if (kt + NS - 1 < nkt) issue(kt + NS - 1);
+    const int st = kt % NS;
+    const u8* tile = kring[st];
+    float4 skv[4];
+#pragma unroll
+    for (int b = 0; b < 4; b++) skv[b] = *reinterpret_cast<const float4*>(&sring[st][16 * b + 4 * g]);
+    const bool diag = kt == qt;
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+      v4i acc = at_zero4();
+      const int m = 16 * b + ql;
+#pragma unroll
+      for (int c = 0; c < NC; c++) {
+        const int p = 4 * c + g;
+        const v4i kf = p < PR ? *reinterpret_cast<const v4i*>(tile + 16 * (m * PR + (p ^ at_swz<HD>(m)))) : at_zero4();
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf, qf[c], acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float y = __fmul_rn(__fmul_rn((float)acc[i], my_qs), at_get(skv[b], i));
+        const int j = kt * 64 + 16 * b + 4 * g + i;
+        mx = fmaxf(mx, (!diag || (j <= qi && j < T)) ? y : -__int_as_float(0x7f800000));
+      }
+    }
+  }
+  mx = at_max_groups(mx);
+  if (g == 0 && qi < T) rmax[(nb + qi) * (u32)H + h] = mx;
+}
+
+// The scratch of uwc_attention_ws: the exponentials' tiles, then the row maxima of sweep 1
+// (one float per query and head, from a 256-byte boundary).
+static u64 at_exp_bytes(int B, int T, int H) {
   const u64 Tp = ((u64)T + 63) / 64 * 64;
   return (u64)B * (u64)H * at_tiles(Tp) * 4096;
+}
+
+extern "C" uint64_t uwc_attention_scratch_bytes(int B, int T, int H) {
+  if (B <= 0 || T <= 0 || H <= 0) return 0;
+  return at_exp_bytes(B, T, H) + ((u64)B * (u64)T * (u64)H * 4 + 255) / 256 * 256;
 }
 
 static int attention_go(const char* fn, const int8_t* qq, const float* qs, const int8_t* kq, const float* ks,
@@ -519,9 +652,19 @@ static int attention_go(const char* fn, const int8_t* qq, const float* qs, const
                       (unsigned long long)uwc_attention_scratch_bytes(B, T, H));
     if ((uintptr_t)escratch & 15) return uwc_fail("%s: escratch must be 16-byte aligned", fn);
   }
+  // with the scratch: the row maxima first (sweep 1 alone), then the full kernel reading them
+  float* rmax = escratch ? escratch + at_exp_bytes(B, T, H) / 4 : nullptr;
   auto go = [&](auto hdc, auto esc) {
-    hipLaunchKernelGGL((attention_kernel<decltype(hdc)::value, decltype(esc)::value>), grid, dim3(256), 0, stream, qq,
-                       qs, kq, ks, vt, vs, T, Tp, H, Hkv, inv_sqrt_hd, o, escratch);
+    constexpr int HDV = decltype(hdc)::value;
+    if constexpr (decltype(esc)::value) {
+      hipLaunchKernelGGL((attn_rowmax_kernel<HDV, 4>), grid, dim3(256), 0, stream, qq, qs, kq, ks, T, Tp, H, Hkv,
+                         rmax);
+      hipLaunchKernelGGL((attention_kernel<HDV, true, true>), grid, dim3(256), 0, stream, qq, qs, kq, ks, vt, vs, T,
+                         Tp, H, Hkv, inv_sqrt_hd, o, escratch, rmax);
+    } else {
+      hipLaunchKernelGGL((attention_kernel<HDV, false, false>), grid, dim3(256), 0, stream, qq, qs, kq, ks, vt, vs, T,
+                         Tp, H, Hkv, inv_sqrt_hd, o, nullptr, nullptr);
+    }
   };
   auto go_hd = [&](auto esc) {
     if (hd == 32) go(std::integral_constant<int, 32>{}, esc);
