@@ -204,3 +204,92 @@ def test_block_mapping_is_a_bijection_and_xcd_local(ntiles, H, Hkv, B):
             assert {(b, h // G) for _, h, b in mine} == {((u // Hkv), u % Hkv) for u in range(x, B * Hkv, 8)}
             qts = [qt for qt, _, _ in mine]
             assert qts == sorted(qts, reverse=True)
+
+
+def _rowmax_tile_maps(hd: int):
+    """attn_rowmax_kernel's ring tile of 64 key rows x hd bytes in 16-byte slots: the DMA map
+    (wave, DMA u, lane) -> (key row m, piece p) at slot s, and the read map (lane, block b,
+    chunk c) -> slot. swz(m) = (m / (16 / PR)) & (PR - 1), PR = hd / 16 pieces per row."""
+    PR = hd // 16
+    TILE = 64 * hd
+    KD = TILE // 4096 if TILE >= 4096 else 1
+    KL = 64 if TILE >= 4096 else TILE // 64
+    swz = lambda m: (m // (16 // PR)) & (PR - 1)
+    written = {}
+    for wave in range(4):
+        for u in range(KD):
+            for lane in range(KL):
+                s = (wave * KD + u) * KL + lane
+                m = s // PR
+                p = (s % PR) ^ swz(m)
+                assert s not in written
+                written[s] = (m, p)
+    reads = {}
+    NC = (hd + 63) // 64
+    for lane in range(64):
+        ql, g = lane & 15, lane >> 4
+        for b in range(4):
+            for c in range(NC):
+                p = 4 * c + g
+                if p < PR:
+                    m = 16 * b + ql
+                    reads[(lane, b, c)] = m * PR + (p ^ swz(m))
+    return PR, written, reads
+
+
+@pytest.mark.parametrize("hd", [32, 64, 128])
+def test_rowmax_ring_dma_and_reads(hd):
+    """Every 16-byte piece of the 64 key rows is DMA'd exactly once, the slots of one DMA
+    instruction are contiguous (lane l at slot base + l, as global_load_lds writes them), eight
+    (hd 128) consecutive lanes read one whole key row, the lane that reads (block b, chunk c)
+    finds key row 16 b + (lane & 15) at dims 64 c + 16 (lane >> 4), and the 16 lanes of one lane
+    group hit 16 distinct 16-byte bank groups (no LDS bank conflict)."""
+    PR, written, reads = _rowmax_tile_maps(hd)
+    assert sorted(written) == list(range(64 * PR))
+    assert sorted(written.values()) == [(m, p) for m in range(64) for p in range(PR)]
+    if hd == 128:
+        for s0 in range(0, 64 * PR, 8):
+            assert {written[s][0] for s in range(s0, s0 + 8)} == {s0 // 8}
+    for (lane, b, c), s in reads.items():
+        assert written[s] == (16 * b + (lane & 15), 4 * c + (lane >> 4))
+    for b in range(4):
+        for c in range((hd + 63) // 64):
+            for g in range(4):
+                slots = [reads[(g * 16 + ql, b, c)] for ql in range(16) if (g * 16 + ql, b, c) in reads]
+                if slots:
+                    assert len({s % 16 for s in slots}) == len(slots)
+
+
+@pytest.mark.parametrize("T,hd", [(1, 128), (100, 64), (300, 32), (2048, 128)])
+def test_rowmax_ring_schedule(T, hd):
+    """The ring schedule of attn_rowmax_kernel (NS = 4 stages): tiles 0 .. NS - 2 issued up
+    front, tile kt + NS - 1 issued after the barrier of iteration kt into tile kt - 1's stage;
+    the wait before iteration kt leaves at most NW = (NS - 2)(KD + 1) of the wave's DMAs
+    pending, or none. Emulated per wave: the tile a wait covers has landed, and a stage is
+    overwritten only after every wave has read it."""
+    NS = 4
+    TILE = 64 * hd
+    KD = TILE // 4096 if TILE >= 4096 else 1
+    per_tile = KD + 1
+    NW = (NS - 2) * per_tile
+    for qt in range((T + 63) // 64):
+        nkt = qt + 1
+        issued = []        # tile per DMA, in issue order
+        stage_of = {}
+        last_read = {}     # stage -> last tile read from it
+        for t in range(NS - 1):
+            if t < nkt:
+                issued += [t] * per_tile
+                stage_of[t] = t % NS
+        done = 0           # DMAs known complete
+        for kt in range(nkt):
+            allowed = NW if kt + NS - 2 < nkt else 0
+            done = max(done, len(issued) - allowed)
+            assert all(x != kt for x in issued[done:]), "tile read before its DMA completed"
+            if kt + NS - 1 < nkt:
+                st = (kt + NS - 1) % NS
+                assert last_read.get(st, -1) <= kt - 1 and st == (kt - 1) % NS
+                issued += [kt + NS - 1] * per_tile
+                stage_of[kt + NS - 1] = st
+            assert stage_of[kt] == kt % NS
+            last_read[kt % NS] = kt
