@@ -146,15 +146,20 @@ __host__ __device__ constexpr u64 at_tiles(u64 Tp) { return at_tile0(Tp / 16); }
 // non-temporal hint: cached normally, its stream evicted the XCD's K and V from L2
 // (2.087 -> 1.960 ms per Qwen3-1.7B layer at T = 8192).
 //
-// RM: the row maxima of sweep 1 come from rmax (attn_rowmax_kernel, y = fl(fl(acc qs) ks) per
-// query and head at rmax[(b T + q) H + h]) and the kernel starts at sweep 2. A max over the same
-// values in another order is the same number, so both forms give the same bits.
-template <int HD, bool ES, bool RM>
-__global__ void __launch_bounds__(256, HD == 128 ? 2 : 3)
+// MODE 0 runs the four sweeps. The stored form splits them over launches whose per-row
+// results sit in rows (three arrays of nq = B T H floats, index (b T + q) H + h): the row max
+// of y = fl(fl(acc qs) ks) (attn_rowmax_kernel), the exact denominator den and the
+// probabilities' scale sp. MODE 1 reads the row max and runs sweeps 2-4; MODE 2 reads the row
+// max, runs sweeps 2-3 and writes den and sp; MODE 3 reads den and sp and runs sweep 4 alone, so
+// that every wave of the launch streams its stored exponentials at once instead of beside other
+// waves' exponential work. Each statistic is the same number however it is split (a max in
+// any order, an exact integer sum, values passed as floats), so every form gives the same bits.
+template <int HD, bool ES, int MODE>
+__global__ void __launch_bounds__(256, MODE == 2 ? 3 : HD == 128 ? 2 : 3)
     attention_kernel(const i8* __restrict__ qq, const float* __restrict__ qs, const i8* __restrict__ kq,
                      const float* __restrict__ ks, const i8* __restrict__ vt, const float* __restrict__ vs, int T,
                      int Tp, int H, int Hkv, float inv_sqrt, float* __restrict__ o, float* __restrict__ escr,
-                     const float* __restrict__ rmax) {
+                     float* __restrict__ rows, u32 nq) {
   constexpr int NC = (HD + 63) / 64;  // 64-dim chunks of the score product
   constexpr int ND = HD / 16;         // 16-dim blocks of the output
   __shared__ __attribute__((aligned(16))) float at_slot[4][2][64];
@@ -308,9 +313,11 @@ __global__ void __launch_bounds__(256, HD == 128 ? 2 : 3)
   // sweep 1: row max. A score is fl(y * inv) with y = fl(fl(acc * qs) * ks) and inv > 0, a
   // monotone function of y, so the max score is fl(max_j y_j * inv) (-inf for an empty row too)
   float mx = -__int_as_float(0x7f800000);
-  if constexpr (RM) {
-    // a padding query (qi >= T) sees keys 0 .. T - 1, as query T - 1 does
-    mx = __fmul_rn(rmax[(nb + qc) * (u32)H + h], inv_sqrt);
+  // a padding query (qi >= T) sees keys 0 .. T - 1, as query T - 1 does
+  const u32 ridx = (nb + qc) * (u32)H + h;
+  if constexpr (MODE == 3) {
+  } else if constexpr (MODE >= 1) {
+    mx = __fmul_rn(rows[ridx], inv_sqrt);
   } else {
     ksweep([&](int kt, const float (&Y)[4][4], const KTile&) AT_AI {
 #pragma unroll
@@ -321,6 +328,25 @@ __global__ void __launch_bounds__(256, HD == 128 ? 2 : 3)
     mx = __fmul_rn(at_max_groups(mx), inv_sqrt);
   }
 
+  // stored form: tile loads for sweeps 3 and 4, and the V scales of a tile (lane's key
+  // 64 kt + lane, staged through the wave's LDS slot as at_stage_scales does)
+  auto eload = [&](int kt, float4 (&ev)[4]) AT_AI {
+#pragma unroll
+    for (int b = 0; b < 4; b++) ev[b] = uwc_load_nt(ewave + kt * 1024 + b * 256);
+  };
+  auto vsload = [&](int kt) AT_AI { return vs[sc_base + (u32)min(kt * 64 + lane, T - 1) * (u32)Hkv]; };
+  auto vsstage = [&](float v, float4 out[4]) AT_AI {
+    sv_slot[lane] = v;
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int b = 0; b < 4; b++) out[b] = *reinterpret_cast<const float4*>(sv_slot + 16 * b + 4 * g);
+    __builtin_amdgcn_wave_barrier();
+  };
+  float den, sp;
+  if constexpr (MODE == 3) {
+    den = rows[nq + ridx];
+    sp = rows[2 * nq + ridx];
+  } else {
   // sweep 2: exact denominator (fixed point at 2^41); masked entries give det_exp(-inf) = 0.
   // A tile's 16 terms per lane sum exactly in float64 (< 2^46), then join a u64 total.
   //
@@ -363,23 +389,9 @@ __global__ void __launch_bounds__(256, HD == 128 ? 2 : 3)
     dsum += (u64)part;
   }, std::false_type{});
   dsum = at_sum_groups(dsum);
-  const float den = (float)ldexp((double)dsum, -41);
+  den = (float)ldexp((double)dsum, -41);
   const double rden = 1.0 / (double)den;
 
-  // stored form: tile loads for sweeps 3 and 4, and the V scales of a tile (lane's key
-  // 64 kt + lane, staged through the wave's LDS slot as at_stage_scales does)
-  auto eload = [&](int kt, float4 (&ev)[4]) AT_AI {
-#pragma unroll
-    for (int b = 0; b < 4; b++) ev[b] = uwc_load_nt(ewave + kt * 1024 + b * 256);
-  };
-  auto vsload = [&](int kt) AT_AI { return vs[sc_base + (u32)min(kt * 64 + lane, T - 1) * (u32)Hkv]; };
-  auto vsstage = [&](float v, float4 out[4]) AT_AI {
-    sv_slot[lane] = v;
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (int b = 0; b < 4; b++) out[b] = *reinterpret_cast<const float4*>(sv_slot + 16 * b + 4 * g);
-    __builtin_amdgcn_wave_barrier();
-  };
   // sweep 3: max of the V-scaled probabilities, only for waves with a near tie (see sweep 2)
   float pm = 0.f;
   const bool near_tie = p2 > __fmul_rn(p1, 0x1.fffep-1f);
@@ -416,8 +428,16 @@ __global__ void __launch_bounds__(256, HD == 128 ? 2 : 3)
       }
   });
   pm = at_max_groups(pm);
-  const float sp = __fdiv_rn(fmaxf(pm, 1e-30f), AT_PLEVELS);
-  const double rsp = 1.0 / (double)sp;
+  sp = __fdiv_rn(fmaxf(pm, 1e-30f), AT_PLEVELS);
+  if constexpr (MODE == 2) {
+    if (g == 0 && qi < T) {
+      rows[nq + ridx] = den;
+      rows[2 * nq + ridx] = sp;
+    }
+    return;
+  }
+  }
+  const double rden = 1.0 / (double)den, rsp = 1.0 / (double)sp;
 
   // sweep 4: 14-bit probabilities as two 7-bit limbs, O^T = V^T P^T on the matrix cores
   v4i ohi[ND], olo[ND];
@@ -619,8 +639,8 @@ __global__ void __launch_bounds__(256) attn_rowmax_kernel(const i8* __restrict__
   if (g == 0 && qi < T) rmax[(nb + qi) * (u32)H + h] = mx;
 }
 
-// The scratch of uwc_attention_ws: the exponentials' tiles, then the row maxima of sweep 1
-// (one float per query and head, from a 256-byte boundary).
+// The scratch of uwc_attention_ws: the exponentials' tiles, then the per-row statistics (row
+// max, den, sp: three arrays of one float per query and head) from a 256-byte boundary.
 static u64 at_exp_bytes(int B, int T, int H) {
   const u64 Tp = ((u64)T + 63) / 64 * 64;
   return (u64)B * (u64)H * at_tiles(Tp) * 4096;
@@ -628,7 +648,7 @@ static u64 at_exp_bytes(int B, int T, int H) {
 
 extern "C" uint64_t uwc_attention_scratch_bytes(int B, int T, int H) {
   if (B <= 0 || T <= 0 || H <= 0) return 0;
-  return at_exp_bytes(B, T, H) + ((u64)B * (u64)T * (u64)H * 4 + 255) / 256 * 256;
+  return at_exp_bytes(B, T, H) + ((u64)B * (u64)T * (u64)H * 12 + 255) / 256 * 256;
 }
 
 static int attention_go(const char* fn, const int8_t* qq, const float* qs, const int8_t* kq, const float* ks,
@@ -652,18 +672,21 @@ static int attention_go(const char* fn, const int8_t* qq, const float* qs, const
                       (unsigned long long)uwc_attention_scratch_bytes(B, T, H));
     if ((uintptr_t)escratch & 15) return uwc_fail("%s: escratch must be 16-byte aligned", fn);
   }
-  // with the scratch: the row maxima first (sweep 1 alone), then the full kernel reading them
-  float* rmax = escratch ? escratch + at_exp_bytes(B, T, H) / 4 : nullptr;
+  // with the scratch: sweep 1 (the row maxima), sweeps 2-3 (den, sp), sweep 4, each a launch
+  float* rows = escratch ? escratch + at_exp_bytes(B, T, H) / 4 : nullptr;
+  const u32 nq = (u32)B * (u32)T * (u32)H;
   auto go = [&](auto hdc, auto esc) {
     constexpr int HDV = decltype(hdc)::value;
     if constexpr (decltype(esc)::value) {
       hipLaunchKernelGGL((attn_rowmax_kernel<HDV, 4>), grid, dim3(256), 0, stream, qq, qs, kq, ks, T, Tp, H, Hkv,
-                         rmax);
-      hipLaunchKernelGGL((attention_kernel<HDV, true, true>), grid, dim3(256), 0, stream, qq, qs, kq, ks, vt, vs, T,
-                         Tp, H, Hkv, inv_sqrt_hd, o, escratch, rmax);
+                         rows);
+      hipLaunchKernelGGL((attention_kernel<HDV, true, 2>), grid, dim3(256), 0, stream, qq, qs, kq, ks, vt, vs, T, Tp,
+                         H, Hkv, inv_sqrt_hd, o, escratch, rows, nq);
+      hipLaunchKernelGGL((attention_kernel<HDV, true, 3>), grid, dim3(256), 0, stream, qq, qs, kq, ks, vt, vs, T, Tp,
+                         H, Hkv, inv_sqrt_hd, o, escratch, rows, nq);
     } else {
-      hipLaunchKernelGGL((attention_kernel<HDV, false, false>), grid, dim3(256), 0, stream, qq, qs, kq, ks, vt, vs, T,
-                         Tp, H, Hkv, inv_sqrt_hd, o, nullptr, nullptr);
+      hipLaunchKernelGGL((attention_kernel<HDV, false, 0>), grid, dim3(256), 0, stream, qq, qs, kq, ks, vt, vs, T,
+                         Tp, H, Hkv, inv_sqrt_hd, o, nullptr, nullptr, 0u);
     }
   };
   auto go_hd = [&](auto esc) {
