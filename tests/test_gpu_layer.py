@@ -198,6 +198,9 @@ def test_qkv_post(dev, B, T, H, Hkv, hd, qknorm):
         j = (pos & ~63) | (((pos >> 2) & 3) << 4) | (((pos >> 4) & 3) << 2) | (pos & 3)
         assert np.array_equal(vt[bseq, :, :, j], rv[n]), n
     assert Tp % 64 == 0
+    for pos in range(T, Tp):  # pad keys: zero
+        j = (pos & ~63) | (((pos >> 2) & 3) << 4) | (((pos >> 4) & 3) << 2) | (pos & 3)
+        assert not vt[:, :, :, j].any(), pos
 
 
 @pytest.mark.parametrize("stored", [False, True])

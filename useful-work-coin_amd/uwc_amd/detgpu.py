@@ -95,7 +95,12 @@ def qkv_post_vt(acc, s1, sw, qnw, knw, cos, sin, T: int, H: int, Hkv: int, eps: 
     dev = acc.device
     e = lambda *shape, dt=torch.int8: torch.empty(shape, dtype=dt, device=dev)
     qq, qs, kq, ks, vq, vs = e(N, H, hd), e(N, H, 1, dt=F32), e(N, Hkv, hd), e(N, Hkv, 1, dt=F32), e(N, Hkv, hd), e(N, Hkv, 1, dt=F32)
-    vt = torch.zeros((B, Hkv, hd, vt_tokens(T)), dtype=torch.int8, device=dev)
+    # qkv_post writes every key below T; the pad keys T .. Tp - 1 (their positions are spread over
+    # the last 64-key tile, which vt_pos permutes) only meet zero probabilities in attention, and
+    # that tile is zeroed first so that vt is defined everywhere
+    vt = torch.empty((B, Hkv, hd, vt_tokens(T)), dtype=torch.int8, device=dev)
+    if T % 64:
+        vt[..., T // 64 * 64:].zero_()
     qn = qnw.contiguous() if qknorm else None
     kn = knw.contiguous() if qknorm else None
     cos, sin = cos.contiguous(), sin.contiguous()
