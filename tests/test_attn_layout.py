@@ -206,17 +206,20 @@ def test_block_mapping_is_a_bijection_and_xcd_local(ntiles, H, Hkv, B):
             assert qts == sorted(qts, reverse=True)
 
 
-def _rowmax_tile_maps(hd: int):
-    """attn_rowmax_kernel's ring tile of 64 key rows x hd bytes in 16-byte slots: the DMA map
-    (wave, DMA u, lane) -> (key row m, piece p) at slot s, and the read map (lane, block b,
-    chunk c) -> slot. swz(m) = (m / (16 / PR)) & (PR - 1), PR = hd / 16 pieces per row."""
+def _rowmax_tile_maps(hd: int, W: int = 4):
+    """attn_rowmax_kernel's ring tile of 64 key rows x hd bytes in 16-byte slots, DMA'd by the W
+    waves of a workgroup: the DMA map (wave, DMA u, lane) -> (key row m, piece p) at slot s, and
+    the read map (lane, block b, chunk c) -> slot. swz(m) = (m / (16 / PR)) & (PR - 1), PR = hd / 16
+    pieces per row."""
     PR = hd // 16
     TILE = 64 * hd
-    KD = TILE // 4096 if TILE >= 4096 else 1
-    KL = 64 if TILE >= 4096 else TILE // 64
+    KS = TILE // 16 // W
+    KD = KS // 64 if KS >= 64 else 1
+    KL = 64 if KS >= 64 else KS
+    assert KD * KL * W * 16 == TILE
     swz = lambda m: (m // (16 // PR)) & (PR - 1)
     written = {}
-    for wave in range(4):
+    for wave in range(W):
         for u in range(KD):
             for lane in range(KL):
                 s = (wave * KD + u) * KL + lane
@@ -238,13 +241,15 @@ def _rowmax_tile_maps(hd: int):
 
 
 @pytest.mark.parametrize("hd", [32, 64, 128])
-def test_rowmax_ring_dma_and_reads(hd):
-    """Every 16-byte piece of the 64 key rows is DMA'd exactly once, the slots of one DMA
-    instruction are contiguous (lane l at slot base + l, as global_load_lds writes them), eight
-    (hd 128) consecutive lanes read one whole key row, the lane that reads (block b, chunk c)
-    finds key row 16 b + (lane & 15) at dims 64 c + 16 (lane >> 4), and the 16 lanes of one lane
-    group hit 16 distinct 16-byte bank groups (no LDS bank conflict)."""
-    PR, written, reads = _rowmax_tile_maps(hd)
+@pytest.mark.parametrize("W", [4, 8, 16])
+def test_rowmax_ring_dma_and_reads(hd, W):
+    """Every 16-byte piece of the 64 key rows is DMA'd exactly once by the W waves (4 per head of
+    the workgroup), the slots of one DMA instruction are contiguous (lane l at slot base + l, as
+    global_load_lds writes them), eight (hd 128) consecutive lanes read one whole key row, the
+    lane that reads (block b, chunk c) finds key row 16 b + (lane & 15) at dims 64 c + 16 (lane >> 4),
+    and the 16 lanes of one lane group hit 16 distinct 16-byte bank groups (no LDS bank
+    conflict). The key scales: 64 / W lanes of each wave, every key once."""
+    PR, written, reads = _rowmax_tile_maps(hd, W)
     assert sorted(written) == list(range(64 * PR))
     assert sorted(written.values()) == [(m, p) for m in range(64) for p in range(PR)]
     if hd == 128:
@@ -258,6 +263,8 @@ def test_rowmax_ring_dma_and_reads(hd):
                 slots = [reads[(g * 16 + ql, b, c)] for ql in range(16) if (g * 16 + ql, b, c) in reads]
                 if slots:
                     assert len({s % 16 for s in slots}) == len(slots)
+    SL = 64 // W
+    assert sorted(w * SL + l for w in range(W) for l in range(SL)) == list(range(64))
 
 
 @pytest.mark.parametrize("T,hd", [(1, 128), (100, 64), (300, 32), (2048, 128)])
@@ -269,7 +276,8 @@ def test_rowmax_ring_schedule(T, hd):
     overwritten only after every wave has read it."""
     NS = 4
     TILE = 64 * hd
-    KD = TILE // 4096 if TILE >= 4096 else 1
+    KS = TILE // 16 // 4
+    KD = KS // 64 if KS >= 64 else 1
     per_tile = KD + 1
     NW = (NS - 2) * per_tile
     for qt in range((T + 63) // 64):

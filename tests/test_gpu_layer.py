@@ -205,10 +205,12 @@ def test_qkv_post(dev, B, T, H, Hkv, hd, qknorm):
 
 @pytest.mark.parametrize("stored", [False, True])
 @pytest.mark.parametrize("B,T,H,Hkv,hd", [(1, 1, 1, 1, 32), (1, 12, 4, 2, 32), (2, 70, 4, 2, 64),
-                                          (1, 300, 2, 1, 128), (1, 129, 16, 8, 128)])
+                                          (1, 300, 2, 1, 128), (1, 129, 16, 8, 128), (1, 100, 8, 2, 64),
+                                          (2, 70, 8, 1, 128)])
 def test_attention(dev, B, T, H, Hkv, hd, stored):
     """Both forms of the kernel (exponentials recomputed per pass, or kept in the scratch of
-    uwc_attention_ws) against the oracle's attention, bit for bit."""
+    uwc_attention_ws) against the oracle's attention, bit for bit; 1, 2, 4 and 8 heads per kv
+    head (the stored form's row max takes 1, 2 or 4 heads per workgroup)."""
     from uwc_amd import detgpu
     rng = np.random.default_rng(T * 7 + hd)
     N = B * T
@@ -252,7 +254,8 @@ def test_attention_repeated_keys(dev, period, T, hd, stored):
     np.testing.assert_array_equal(_u32(o), _u32(ref.transpose(1, 0, 2).reshape(T, H * hd)))
 
 
-@pytest.mark.parametrize("B,T,H,Hkv,hd", [(1, 2048, 16, 8, 128), (2, 1000, 4, 4, 64), (1, 777, 8, 2, 32)])
+@pytest.mark.parametrize("B,T,H,Hkv,hd", [(1, 2048, 16, 8, 128), (2, 1000, 4, 4, 64), (1, 777, 8, 2, 32),
+                                          (1, 1500, 16, 2, 128)])
 def test_attention_stored_equals_recomputed(dev, B, T, H, Hkv, hd):
     """The stored-exponentials form equals the recomputing one bit for bit at sizes the oracle
     would take minutes for (the oracle comparison above covers both at small T)."""

@@ -527,12 +527,15 @@ __global__ void __launch_bounds__(256, MODE == 2 ? 3 : HD == 128 ? 2 : 3)
 // The row max of y = fl(fl(acc qs) ks) over each query's causal keys, for the stored-exp form.
 // Inside the full kernel (two waves per SIMD) this sweep waited on its K loads most of the time:
 // every wave fetched each 64-key tile itself, 16 half-used 128-byte lines per load instruction.
-// Here the four waves of a workgroup (64 queries of one head, the same key tiles) share each tile:
-// it is DMA'd once into an LDS ring of NS tiles (global_load_lds_dwordx4, each lane 16 bytes,
-// eight consecutive lanes one whole 128-byte key row), every wave issuing the same number of DMAs
-// per tile so that its wait counts are static, and read back in the MFMA operand layout. The
-// 16-byte pieces of key row m sit at piece p ^ swz(m) so that the 16 lanes of a read (rows
-// 16 b .. + 15, one piece) hit 16 distinct bank groups.
+// Here the 4 HPW waves of a workgroup (64 queries of each of HPW heads that share one kv head,
+// so the same key tiles) share each tile: it is DMA'd once into an LDS ring of NS tiles
+// (global_load_lds_dwordx4, each lane 16 bytes, eight consecutive lanes one whole 128-byte key
+// row), every wave issuing the same number of DMAs per tile so that its wait counts are static,
+// and read back in the MFMA operand layout. The 16-byte pieces of key row m sit at piece
+// p ^ swz(m) so that the 16 lanes of a read (rows 16 b .. + 15, one piece) hit 16 distinct bank
+// groups. The tiles' DMAs from L2 bound this kernel (one head per workgroup ran no faster with
+// a third less VALU work), so the heads of a kv head share them: Qwen3-1.7B (2 heads per kv
+// head) moves half the key bytes per score.
 __device__ __forceinline__ void at_dma16(const void* g, u32 lds) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
 }
@@ -551,24 +554,29 @@ __host__ __device__ constexpr int at_swz(int m) {
   return (m / (16 / (HD / 16))) & (HD / 16 - 1);
 }
 
-template <int HD, int NS>
-__global__ void __launch_bounds__(256) attn_rowmax_kernel(const i8* __restrict__ qq, const float* __restrict__ qs,
-                                                          const i8* __restrict__ kq, const float* __restrict__ ks,
-                                                          int T, int Tp, int H, int Hkv, float* __restrict__ rmax) {
+template <int HD, int NS, int HPW>
+__global__ void __launch_bounds__(256 * HPW) attn_rowmax_kernel(const i8* __restrict__ qq, const float* __restrict__ qs,
+                                                                const i8* __restrict__ kq, const float* __restrict__ ks,
+                                                                int T, int Tp, int H, int Hkv, float* __restrict__ rmax) {
   constexpr int NC = (HD + 63) / 64;
   constexpr int PR = HD / 16;                     // 16-byte pieces per key row
   constexpr int TILE = 64 * HD;                   // bytes of one 64-key tile
-  constexpr int KD = TILE >= 4096 ? TILE / 4096 : 1;  // K DMAs per wave and tile
-  constexpr int KL = TILE >= 4096 ? 64 : TILE / 64;   // lanes active in each (HD 32: 32)
+  constexpr int W = 4 * HPW;                      // waves of the workgroup
+  constexpr int KS = TILE / 16 / W;               // 16-byte slots of a tile per wave
+  constexpr int KD = KS >= 64 ? KS / 64 : 1;      // K DMAs per wave and tile
+  constexpr int KL = KS >= 64 ? 64 : KS;          // lanes active in each
+  constexpr int SL = 64 / W;                      // key scales per wave and tile
   constexpr int NW = (NS - 2) * (KD + 1);         // DMAs of the tiles a wait leaves in flight
+  static_assert(KS >= 1 && SL >= 1 && KD * KL * W * 16 == TILE, "tile split over the waves");
   __shared__ __attribute__((aligned(16))) u8 kring[NS][TILE];
   __shared__ __attribute__((aligned(16))) float sring[NS][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int ql = lane & 15, g = lane >> 4;
-  int qt, h, bseq;
-  at_block((int)blockIdx.x, Tp / 64, H, Hkv, (int)(gridDim.x / (u32)(Tp / 64 * H)), qt, h, bseq);
+  int qt, hg, bseq;
+  at_block((int)blockIdx.x, Tp / 64, H / HPW, Hkv, (int)(gridDim.x / (u32)(Tp / 64 * (H / HPW))), qt, hg, bseq);
   // every wave runs every tile and barrier (a wave past T computes clamped rows and stores nothing)
-  const int q0 = qt * 64 + wave * 16;
+  const int h = hg * HPW + (wave >> 2);
+  const int q0 = qt * 64 + (wave & 3) * 16;
   const int hk = h / (H / Hkv);
   const u32 nb = (u32)(bseq * T);
   const int qi = q0 + ql, qc = min(qi, T - 1);
@@ -598,9 +606,9 @@ __global__ void __launch_bounds__(256) attn_rowmax_kernel(const i8* __restrict__
       const u32 dst = __builtin_amdgcn_readfirstlane(kr0 + (u32)(st * TILE + (wave * KD + u) * KL * 16));
       if (KL == 64 || lane < KL) at_dma16(src, dst);
     }
-    const float* ssrc = ks + sc_base + (u32)min(kt * 64 + wave * 16 + (lane & 15), T - 1) * (u32)Hkv;
-    const u32 sdst = __builtin_amdgcn_readfirstlane(sr0 + (u32)(st * 256 + wave * 64));
-    if (lane < 16) at_dma4(ssrc, sdst);
+    const float* ssrc = ks + sc_base + (u32)min(kt * 64 + wave * SL + (lane & (SL - 1)), T - 1) * (u32)Hkv;
+    const u32 sdst = __builtin_amdgcn_readfirstlane(sr0 + (u32)(st * 256 + wave * SL * 4));
+    if (lane < SL) at_dma4(ssrc, sdst);
   };
 #pragma unroll
   for (int t = 0; t < NS - 1; t++)
@@ -616,24 +624,33 @@ __global__ void __launch_bounds__(256) attn_rowmax_kernel(const i8* __restrict__
     float4 skv[4];
 #pragma unroll
     for (int b = 0; b < 4; b++) skv[b] = *reinterpret_cast<const float4*>(&sring[st][16 * b + 4 * g]);
-    const bool diag = kt == qt;
+    // tiles below qt hold only keys below the wave's first query: no mask; tile qt masks
+    auto tile_max = [&](auto mask) AT_AI {
 #pragma unroll
-    for (int b = 0; b < 4; b++) {
-      v4i acc = at_zero4();
-      const int m = 16 * b + ql;
+      for (int b = 0; b < 4; b++) {
+        v4i acc = at_zero4();
+        const int m = 16 * b + ql;
 #pragma unroll
-      for (int c = 0; c < NC; c++) {
-        const int p = 4 * c + g;
-        const v4i kf = p < PR ? *reinterpret_cast<const v4i*>(tile + 16 * (m * PR + (p ^ at_swz<HD>(m)))) : at_zero4();
-        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf, qf[c], acc, 0, 0, 0);
+        for (int c = 0; c < NC; c++) {
+          const int p = 4 * c + g;
+          const v4i kf =
+              p < PR ? *reinterpret_cast<const v4i*>(tile + 16 * (m * PR + (p ^ at_swz<HD>(m)))) : at_zero4();
+          acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf, qf[c], acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const float y = __fmul_rn(__fmul_rn((float)acc[i], my_qs), at_get(skv[b], i));
+          if constexpr (decltype(mask)::value) {
+            const int j = kt * 64 + 16 * b + 4 * g + i;
+            mx = fmaxf(mx, (j <= qi && j < T) ? y : -__int_as_float(0x7f800000));
+          } else {
+            mx = fmaxf(mx, y);
+          }
+        }
       }
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const float y = __fmul_rn(__fmul_rn((float)acc[i], my_qs), at_get(skv[b], i));
-        const int j = kt * 64 + 16 * b + 4 * g + i;
-        mx = fmaxf(mx, (!diag || (j <= qi && j < T)) ? y : -__int_as_float(0x7f800000));
-      }
-    }
+    };
+    if (kt < qt) tile_max(std::false_type{});
+    else tile_max(std::true_type{});
   }
   mx = at_max_groups(mx);
   if (g == 0 && qi < T) rmax[(nb + qi) * (u32)H + h] = mx;
@@ -675,11 +692,20 @@ static int attention_go(const char* fn, const int8_t* qq, const float* qs, const
   // with the scratch: sweep 1 (the row maxima), sweeps 2-3 (den, sp), sweep 4, each a launch
   float* rows = escratch ? escratch + at_exp_bytes(B, T, H) / 4 : nullptr;
   const u32 nq = (u32)B * (u32)T * (u32)H;
+  // the row max's workgroups take HPW heads of one kv head (4, 2 or 1 of its G = H / Hkv)
+  const int G = H / Hkv, hpw = G % 4 == 0 ? 4 : G % 2 == 0 ? 2 : 1;
   auto go = [&](auto hdc, auto esc) {
     constexpr int HDV = decltype(hdc)::value;
     if constexpr (decltype(esc)::value) {
-      hipLaunchKernelGGL((attn_rowmax_kernel<HDV, 4>), grid, dim3(256), 0, stream, qq, qs, kq, ks, T, Tp, H, Hkv,
-                         rows);
+      auto rowmax = [&](auto hp) {
+        constexpr int HP = decltype(hp)::value;
+        const dim3 rgrid((unsigned)((long)(Tp / 64) * (H / HP) * B));
+        hipLaunchKernelGGL((attn_rowmax_kernel<HDV, 4, HP>), rgrid, dim3(256 * HP), 0, stream, qq, qs, kq, ks, T, Tp,
+                           H, Hkv, rows);
+      };
+      if (hpw == 4) rowmax(std::integral_constant<int, 4>{});
+      else if (hpw == 2) rowmax(std::integral_constant<int, 2>{});
+      else rowmax(std::integral_constant<int, 1>{});
       hipLaunchKernelGGL((attention_kernel<HDV, true, 2>), grid, dim3(256), 0, stream, qq, qs, kq, ks, vt, vs, T, Tp,
                          H, Hkv, inv_sqrt_hd, o, escratch, rows, nq);
       hipLaunchKernelGGL((attention_kernel<HDV, true, 3>), grid, dim3(256), 0, stream, qq, qs, kq, ks, vt, vs, T, Tp,
