@@ -149,11 +149,10 @@ __host__ __device__ constexpr u64 at_tiles(u64 Tp) { return at_tile0(Tp / 16); }
 // MODE 0 runs the four sweeps. The stored form splits them over launches whose per-row
 // results sit in rows (three arrays of nq = B T H floats, index (b T + q) H + h): the row max
 // of y = fl(fl(acc qs) ks) (attn_rowmax_kernel), the exact denominator den and the
-// probabilities' scale sp. MODE 1 reads the row max and runs sweeps 2-4; MODE 2 reads the row
-// max, runs sweeps 2-3 and writes den and sp; MODE 3 reads den and sp and runs sweep 4 alone, so
-// that every wave of the launch streams its stored exponentials at once instead of beside other
-// waves' exponential work. Each statistic is the same number however it is split (a max in
-// any order, an exact integer sum, values passed as floats), so every form gives the same bits.
+// probabilities' scale sp. MODE 2 reads the row max, runs sweeps 2-3 (at three waves per SIMD:
+// they need fewer registers than sweep 4) and writes den and sp; MODE 3 reads den and sp and
+// runs sweep 4 alone. Each statistic is the same number however it is split (a max in any order,
+// an exact integer sum, values passed as floats), so every form gives the same bits.
 template <int HD, bool ES, int MODE>
 __global__ void __launch_bounds__(256, MODE == 2 ? 3 : HD == 128 ? 2 : 3)
     attention_kernel(const i8* __restrict__ qq, const float* __restrict__ qs, const i8* __restrict__ kq,
@@ -316,7 +315,7 @@ __global__ void __launch_bounds__(256, MODE == 2 ? 3 : HD == 128 ? 2 : 3)
   // a padding query (qi >= T) sees keys 0 .. T - 1, as query T - 1 does
   const u32 ridx = (nb + qc) * (u32)H + h;
   if constexpr (MODE == 3) {
-  } else if constexpr (MODE >= 1) {
+  } else if constexpr (MODE == 2) {
     mx = __fmul_rn(rows[ridx], inv_sqrt);
   } else {
     ksweep([&](int kt, const float (&Y)[4][4], const KTile&) AT_AI {
