@@ -125,12 +125,14 @@ def test_large_tile_plain_odd_k_steps(dev, k):
                            Yr.view(torch.int16) if mode == ops.OUT_BF16 else Yr.view(torch.int32))
 
 
-@pytest.mark.parametrize("m,n,k", [(2048, 32768, 256), (2560, 30720, 384), (4096, 16384, 128)])
+@pytest.mark.parametrize("m,n,k", [(2048, 32768, 256), (2560, 30720, 384), (4096, 16384, 128), (8192, 4096, 2048),
+                                   (2560, 16384, 128), (4096, 8192, 640)])
 def test_plain_multi_tile(dev, m, n, k):
-    """Plain int32 GEMMs of at least four 256 x 256 tiles per CU run on the persistent split-role
-    kernel (each workgroup takes tiles b, b + grid, ...; 1024, 1200 and 1024 tiles here, so some
-    workgroups take one more tile than others; 2, 3 and 1 k steps): the output equals the generic
-    128 x 128 kernel's, and a sample of rows equals the oracle's exact product."""
+    """Plain int32 GEMMs of at least two 256 x 256 tiles per CU run on the persistent split-role
+    kernel (each workgroup takes tiles b, b + grid, ...; 1024, 1200, 1024, 512, 640 and 512 tiles
+    here, so at some shapes some workgroups take one more tile than others; 2, 3, 1, 16, 1 and 5 k
+    steps): the output equals the generic 128 x 128 kernel's, and a sample of rows equals the
+    oracle's exact product."""
     from uwc_amd import ops
     A, B = _rand(dev, m + k, m, k), _rand(dev, n + 3 * k, n, k)
     C = _gemm(A, B, ops.OUT_I32)

@@ -51,7 +51,7 @@
 #define W_BK 128
 #endif
 #ifndef W_MULTI
-#define W_MULTI 4  // plain int32 GEMMs of >= W_MULTI tiles per CU take the persistent multi-tile form
+#define W_MULTI 2  // plain int32 GEMMs of >= W_MULTI tiles per CU take the persistent multi-tile form
 #endif
 #ifndef W_STAGES
 #define W_STAGES (W_BK == 64 ? 4 : 2)
@@ -1082,8 +1082,11 @@ int uwc_noisy_gemm256(const int8_t* A, const int8_t* B, int m, int n, int k, int
   // its tiles in turn on the split-role kernel, so a tile's output stores drain while the next
   // one computes and the next tile's first k steps load during the hand-off. Measured against one
   // workgroup per tile: 8192 x 151808 x 2048 (74 tiles per CU) 2942 -> 2813 us, 8192 x 12288 x
-  // 2048 (6) 240 -> 233 us, but 2 tiles per CU 74 -> 78 us, and the fp32 dequant epilogue, which
-  // only the 4 storer waves run in this form, was 3-10% slower at every prefill shape.
+  // 2048 (6) 240 -> 233 us, and at 2-3 tiles per CU (graph-replayed, interleaved, outputs equal)
+  // 8192 x 4096 x 2048 83.7 -> 77.9 us, 8192 x 4096 x 4096 130.0 -> 126.0, 8192 x 6144 x 4096
+  // 184.3 -> 182.0, 8192 x 4096 x 14336 375.5 -> 369.0 (an earlier build of this form had been
+  // slower at 2 tiles per CU). The fp32 dequant epilogue, which only the 4 storer waves run in this
+  // form, was 3-10% slower at every prefill shape, so it keeps one workgroup per tile.
   const int G = uwc_cu_count() & ~7;
   const long tiles = (long)(m / W_BM) * (n / W_BN);
   if (W_MULTI > 0 && !hash && !denoise && out_mode == OUT_I32 && G >= 8 && tiles >= (long)W_MULTI * G &&
