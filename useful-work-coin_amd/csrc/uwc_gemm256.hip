@@ -1086,7 +1086,8 @@ int uwc_noisy_gemm256(const int8_t* A, const int8_t* B, int m, int n, int k, int
   // 8192 x 4096 x 2048 83.7 -> 77.9 us, 8192 x 4096 x 4096 130.0 -> 126.0, 8192 x 6144 x 4096
   // 184.3 -> 182.0, 8192 x 4096 x 14336 375.5 -> 369.0 (an earlier build of this form had been
   // slower at 2 tiles per CU). The fp32 dequant epilogue, which only the 4 storer waves run in this
-  // form, was 3-10% slower at every prefill shape, so it keeps one workgroup per tile.
+  // form, is 1.5-3% slower at the prefill shapes (8192 x 28672 x 4096 802 -> 815 us), so it keeps
+  // one workgroup per tile.
   const int G = uwc_cu_count() & ~7;
   const long tiles = (long)(m / W_BM) * (n / W_BN);
   if (W_MULTI > 0 && !hash && !denoise && out_mode == OUT_I32 && G >= 8 && tiles >= (long)W_MULTI * G &&
