@@ -161,3 +161,17 @@ def test_column_split_gemm_all_out_modes(dev, m, n, k):
     _lib.call("uwc_igemm_dequant_f32", At.data_ptr(), Bt.data_ptr(), m, n, k, sxt.data_ptr(), swt.data_ptr(),
               Y.data_ptr(), torch.cuda.current_stream().cuda_stream)
     assert np.array_equal(Y.cpu().numpy().view(np.uint32), O.dequant(ref, sx, sw).view(np.uint32))
+
+
+@pytest.mark.parametrize("m,n", [(1, 1), (3, 4), (7, 6), (5, 151936), (70000, 8), (65537, 12)])
+def test_dequant_every_layout(dev, m, n):
+    """uwc_dequant_f32 equals the oracle's (f32(acc) * sx[row]) * sw[col] bit for bit: the
+    four-column form (n % 4 == 0, rows on grid y, more rows than the grid's 65535 taking the row
+    loop) and the element form (n % 4 != 0)."""
+    _, detrt = _mods()
+    rng = np.random.default_rng(m * 7 + n)
+    acc = rng.integers(-2**31, 2**31 - 1, size=(m, n), dtype=np.int64).astype(np.int32)
+    sx = rng.uniform(1e-6, 1e-2, m).astype(np.float32)
+    sw = rng.uniform(1e-6, 1e-2, n).astype(np.float32)
+    y = detrt.dequant(torch.from_numpy(acc).to(dev), torch.from_numpy(sx).to(dev), torch.from_numpy(sw).to(dev))
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), O.dequant(acc, sx, sw).view(np.uint32))
