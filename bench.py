@@ -973,14 +973,14 @@ def summarize_e2e_trace(stats_csv, out_path, cmd):
             name = re.sub(r"\(.*", "", r["Name"].replace("(anonymous namespace)::", ""))[:58]
             f.write(f"{name:58s} {int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:9.2f} "
                     f"{float(r['TotalDurationNs']) / 3e6:8.2f} {float(r['Percentage']):5.1f}%\n")
-        f.write("\nPer forward: 28 x (rmsnorm_quant_wave_kernel x 2, noisy_gemm256_kernel<false, false, 1> for qkv "
-                "and gate_up (the multi-tile split form for gate_up), noisy_gemm256_kernel<false, false, 4, false> for "
+        f.write("\nPer forward: 28 x (rmsnorm_quant_wave_kernel x 2, noisy_gemm256_kernel<false, false, 1, true> "
+                "(the persistent multi-tile form) for qkv and gate_up, noisy_gemm256_kernel<false, false, 4, false> for "
                 "o and down (dequant and residual add in the epilogue), qkv_post_kernel, the stored-exponentials "
                 "attention in three launches (attn_rowmax_kernel: the row maxima; attention_kernel<128, true, 2>: the "
                 "exact sums, exponentials stored; attention_kernel<128, true, 3>: P x V), quant_act_dgroup_kernel, "
                 "swiglu_quant_wave_kernel), then one batched set of sha_* launches for all 28 layers' stage-output "
                 "roots (sha_block_leaves, sha_row_leaf_quad, sha_group, sha_tree), rmsnorm_quant + the lm_head GEMM "
-                "(256x256 tiles + a 128-wide column tail) + its fp32 dequant + the logits' Merkle root "
+                "(256x256 tiles + a 128-wide column tail) + its fp32 dequant (dequant4_kernel) + the logits' Merkle root "
                 "(sha_block_leaves, sha_row_tree, sha_group, sha_tree); ms/fwd = total / 3 (the buffer copies and "
                 "the random-number and scaling kernels are model set-up and the oracle's weight copies, outside the "
                 "timed forwards; the T = 64 parity run adds the few small-shape kernels).\n")
