@@ -231,6 +231,30 @@ def test_attention(dev, B, T, H, Hkv, hd, stored):
 
 
 @pytest.mark.parametrize("stored", [False, True])
+@pytest.mark.parametrize("lo,hi,T,hd", [(0.1, 0.4, 300, 64), (0.5, 2.0, 200, 128), (0.2, 1.0, 150, 32),
+                                        (0.05, 0.1, 260, 64), (0.03, 0.08, 260, 128)])
+def test_attention_underflowing_exponentials(dev, lo, hi, T, hd, stored):
+    """Large q and k scales spread the scores over hundreds of nats, so exponentials underflow
+    (det_exp's t < -126 rule; 96-97% of them at the first three scale ranges, 38% and 7% at the
+    last two): in tiles without masked keys the kernel leaves that rule out (a subnormal instead
+    of 0), which no output can show; both forms against the oracle bit for bit."""
+    from uwc_amd import detgpu
+    rng = np.random.default_rng(int(hi * 100) + T)
+    H, Hkv = 4, 2
+    qq = rng.integers(-127, 128, (T, H, hd)).astype(np.int8)
+    kq = rng.integers(-127, 128, (T, Hkv, hd)).astype(np.int8)
+    vq = rng.integers(-127, 128, (T, Hkv, hd)).astype(np.int8)
+    qs = rng.uniform(lo, hi, (T, H, 1)).astype(np.float32)
+    ks = rng.uniform(lo, hi, (T, Hkv, 1)).astype(np.float32)
+    vs = rng.uniform(1e-3, 3e-2, (T, Hkv, 1)).astype(np.float32)
+    inv = S.inv_sqrt_hd(hd)
+    o = detgpu.attention(_t(qq, dev), _t(qs, dev), _t(kq, dev), _t(ks, dev), _t(vq, dev), _t(vs, dev), 1, T, H, Hkv,
+                         float(inv), stored_exp=stored).cpu().numpy()
+    _, _, _, ref = S.attention(qq.astype(np.int64), qs, kq.astype(np.int64), ks, vq.astype(np.int64), vs, inv)
+    np.testing.assert_array_equal(_u32(o), _u32(ref.transpose(1, 0, 2).reshape(T, H * hd)))
+
+
+@pytest.mark.parametrize("stored", [False, True])
 @pytest.mark.parametrize("period,T,hd", [(7, 300, 64), (3, 200, 128), (64, 260, 32)])
 def test_attention_repeated_keys(dev, period, T, hd, stored):
     """Keys, values and their scales repeating every `period` positions give exact ties in e * vs
