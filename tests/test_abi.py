@@ -127,6 +127,17 @@ def test_other_entry_points_reject_bad_arguments():
     assert "overlaps" in L.uwc_last_error().decode()
     assert L.uwc_igemm_dequant_residual_f32(fake, fake, 256, 256, 128, fake, fake, None, fake, None) == -1
     assert "null" in L.uwc_last_error().decode()
+    # the stored-exp attention: a scratch one byte short of the exponentials and the per-row
+    # statistics (row max, den, sp) is refused before any launch; so is a missing one
+    need = L.uwc_attention_scratch_bytes(1, 300, 4)
+    inv = ctypes.c_float(0.125)
+    assert L.uwc_attention_ws(fake, fake, fake, fake, fake, fake, 1, 300, 4, 2, 64, inv, fake, fake, need - 1,
+                              None) == -1
+    assert "escratch holds" in L.uwc_last_error().decode()
+    assert L.uwc_attention_ws(fake, fake, fake, fake, fake, fake, 1, 300, 4, 2, 64, inv, fake, None, need, None) == -1
+    assert "null escratch" in L.uwc_last_error().decode()
+    assert L.uwc_attention(fake, fake, fake, fake, fake, fake, 1, 300, 4, 3, 64, inv, fake, None) == -1
+    assert "H % Hkv" in L.uwc_last_error().decode() or "Hkv" in L.uwc_last_error().decode()
 
 
 def test_python_surface_matches_reference_names():
