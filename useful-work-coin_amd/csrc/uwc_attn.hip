@@ -43,6 +43,27 @@
 #define AT_AI __attribute__((always_inline))
 typedef void __attribute__((address_space(3)))* s2_lptr_at;
 
+// One wave-wide DMA into LDS at lds + 16 lane (dwordx4) or lds + 4 lane (dword); lds is
+// wave-uniform (M0). Such loads count in vmcnt only, so the kernels wait for them with explicit
+// vmcnt counts and a workgroup barrier before another wave reads the data.
+__device__ __forceinline__ void at_dma16(const void* g, u32 lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+// the same with the non-temporal hint (data read once: the stored exponentials)
+__device__ __forceinline__ void at_dma16_nt(const void* g, u32 lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ void at_dma4(const void* g, u32 lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+template <int N>
+__device__ __forceinline__ void at_waitv() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// LDS barrier: this wave's LDS operations done, then every wave's (global memory is not fenced)
+__device__ __forceinline__ void at_lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+
 __device__ __forceinline__ v4i at_zero4() { return v4i{0, 0, 0, 0}; }
 
 // round_half_even(e * 2^41) for 0 <= e < 2, as a float64 integer (exact: e * 2^41 is a float32
@@ -178,7 +199,9 @@ __global__ void __launch_bounds__(256, MODE == 2 ? 3 : HD == 128 ? 2 : 3)
   int qt, h, bseq;
   at_block((int)blockIdx.x, Tp / 64, H, Hkv, (int)(gridDim.x / (u32)(Tp / 64 * H)), qt, h, bseq);
   const int q0 = qt * 64 + wave * 16;
-  if (q0 >= T) return;  // whole waves only; the kernel has no workgroup barriers
+  // whole waves only (MODE 3 keeps every wave: its loop has workgroup barriers; a wave past T
+  // computes clamped rows and stores nothing)
+  if (MODE != 3 && q0 >= T) return;
   const int hk = h / (H / Hkv);
   // 32-bit offsets: the host checks B * T * max(H, Hkv) * HD < 2^31
   const u32 nb = (u32)(bseq * T);
@@ -485,7 +508,70 @@ __global__ void __launch_bounds__(256, MODE == 2 ? 3 : HD == 128 ? 2 : 3)
     for (int d = 0; d < ND; d++)
       vf[d] = *reinterpret_cast<const v4i*>(vbase + (u32)(16 * d + ql) * (u32)Tp + kt * 64 + 16 * g);
   };
-  if constexpr (ES) {
+  if constexpr (MODE == 3) {
+    // Sweep 4 with every load a DMA into LDS: the wave's own exponentials (4 KiB a tile) into
+    // its slot of a 3-stage ring, the tile's V^T rows (64 keys of every dim, the same for the
+    // four waves: each DMAs a quarter) and V scales (a quarter each) into shared rings. Loaded per
+    // wave into registers, as the other forms do, the 13 vector-memory instructions of a wave
+    // and tile (8 of them for V tiles the workgroup's four waves all read) bound the sweep at the
+    // CU's rate for such instructions; here a wave issues 7 DMAs a tile. No compiler-issued
+    // global load remains in the loop, so every wait count is static. A V row of a tile is 64
+    // bytes, four 16-byte pieces, piece p of row r stored at p ^ ((r >> 2) & 3) so that the 16
+    // rows of an MFMA fragment read (one piece) hit 16 distinct bank groups.
+    constexpr int VT = HD * 64;                   // bytes of a V tile
+    constexpr int VS = VT / 16 / 4;               // its 16-byte slots per wave
+    constexpr int VD = VS >= 64 ? VS / 64 : 1;    // V DMAs per wave and tile
+    constexpr int VL = VS >= 64 ? 64 : VS;        // lanes active in each
+    constexpr int PER = 4 + VD + 1;               // DMAs per wave and tile: exponentials, V, V scales
+    static_assert(VD * VL * 4 * 16 == VT && PER < 32, "V tile split over the four waves");
+    __shared__ __attribute__((aligned(16))) u8 ering[3][4][4096];
+    __shared__ __attribute__((aligned(16))) u8 vring[3][VT];
+    __shared__ __attribute__((aligned(16))) float sring[3][64];
+    const u32 er0 = (u32)(uintptr_t)(s2_lptr_at)ering[0][0], vr0 = (u32)(uintptr_t)(s2_lptr_at)vring[0];
+    const u32 sr0 = (u32)(uintptr_t)(s2_lptr_at)sring[0];
+    // the row constants are final before the loop: the compiler's waits for their loads stay here
+    asm volatile("" ::"v"(rden), "v"(rsp));
+    auto issue = [&](int kt) AT_AI {
+      const int st = kt % 3;
+#pragma unroll
+      for (int b = 0; b < 4; b++)
+        at_dma16_nt(ewave + kt * 1024 + b * 256,
+                    __builtin_amdgcn_readfirstlane(er0 + (u32)((st * 4 + wave) * 4096 + b * 1024)));
+#pragma unroll
+      for (int u = 0; u < VD; u++) {
+        const int s16 = (wave * VD + u) * VL + lane, row = s16 >> 2, p = (s16 & 3) ^ ((row >> 2) & 3);
+        const i8* src = vbase + (u32)row * (u32)Tp + kt * 64 + 16 * p;
+        const u32 dst = __builtin_amdgcn_readfirstlane(vr0 + (u32)(st * VT + (wave * VD + u) * VL * 16));
+        if (VL == 64 || lane < VL) at_dma16(src, dst);
+      }
+      const float* ssrc = vs + sc_base + (u32)min(kt * 64 + wave * 16 + (lane & 15), T - 1) * (u32)Hkv;
+      if (lane < 16) at_dma4(ssrc, __builtin_amdgcn_readfirstlane(sr0 + (u32)(st * 256 + wave * 64)));
+    };
+    if (nkt > 0) issue(0);
+    if (nkt > 1) issue(1);
+    for (int kt = 0; kt < nkt; kt++) {
+      if (kt + 1 < nkt) at_waitv<PER>();  // tile kt + 1's DMAs may still be in flight
+      else at_waitv<0>();
+      at_lds_barrier();  // tile kt is in LDS; every wave is done with tile kt - 1's stage
+      if (kt + 2 < nkt) issue(kt + 2);
+      const int st = kt % 3;
+      float e[4][4];
+      float4 svv[4];
+#pragma unroll
+      for (int b = 0; b < 4; b++) {
+        const float4 x = *reinterpret_cast<const float4*>(ering[st][wave] + b * 1024 + lane * 16);
+        e[b][0] = x.x, e[b][1] = x.y, e[b][2] = x.z, e[b][3] = x.w;
+        svv[b] = *reinterpret_cast<const float4*>(&sring[st][16 * b + 4 * g]);
+      }
+      v4i vf[ND];
+#pragma unroll
+      for (int d = 0; d < ND; d++) {
+        const int row = 16 * d + ql;
+        vf[d] = *reinterpret_cast<const v4i*>(vring[st] + 16 * (row * 4 + (g ^ ((row >> 2) & 3))));
+      }
+      pv_tile(e, svv, vf);
+    }
+  } else if constexpr (ES) {
     float4 eb[2][4];
     float vb[2];
     v4i vfb[2][ND];  // the tile's V rows, fetched two tiles ahead with its exponentials and scales
@@ -550,19 +636,6 @@ __global__ void __launch_bounds__(256, MODE == 2 ? 3 : HD == 128 ? 2 : 3)
 // groups. The tiles' DMAs from L2 bound this kernel (one head per workgroup ran no faster with
 // a third less VALU work), so the heads of a kv head share them: Qwen3-1.7B (2 heads per kv
 // head) moves half the key bytes per score.
-__device__ __forceinline__ void at_dma16(const void* g, u32 lds) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
-}
-__device__ __forceinline__ void at_dma4(const void* g, u32 lds) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
-}
-template <int N>
-__device__ __forceinline__ void at_waitv() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-// LDS barrier: this wave's LDS operations done, then every wave's (global memory is not fenced)
-__device__ __forceinline__ void at_lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
 template <int HD>
 __host__ __device__ constexpr int at_swz(int m) {
   return (m / (16 / (HD / 16))) & (HD / 16 - 1);
