@@ -976,8 +976,8 @@ def summarize_e2e_trace(stats_csv, out_path, cmd):
         f.write("\nPer forward: 28 x (rmsnorm_quant_wave_kernel x 2, noisy_gemm256_kernel<false, false, 1, true> "
                 "(the persistent multi-tile form) for qkv and gate_up, noisy_gemm256_kernel<false, false, 4, false> for "
                 "o and down (dequant and residual add in the epilogue), qkv_post_kernel, the stored-exponentials "
-                "attention in three launches (attn_rowmax_kernel: the row maxima; attention_kernel<128, true, 2>: the "
-                "exact sums, exponentials stored; attention_kernel<128, true, 3>: P x V), quant_act_dgroup_kernel, "
+                "attention in two launches (attn_rowmax_kernel: the row maxima; attention_kernel<128, true>: the "
+                "exact sums with the exponentials stored, then P x V from them), quant_act_dgroup_kernel, "
                 "swiglu_quant_wave_kernel), then one batched set of sha_* launches for all 28 layers' stage-output "
                 "roots (sha_block_leaves, sha_row_leaf_quad, sha_group, sha_tree), rmsnorm_quant + the lm_head GEMM "
                 "(256x256 tiles + a 128-wide column tail) + its fp32 dequant (dequant4_kernel) + the logits' Merkle root "

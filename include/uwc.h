@@ -297,17 +297,16 @@ int uwc_attention(const int8_t* qq, const float* qs, const int8_t* kq, const flo
 
 /* Bytes of the scratch of uwc_attention_ws for B sequences of T tokens and H heads: the
  * exponentials, 4 KiB per 16 queries x 64 keys of the causal triangle (2.2 GB at B = 1,
- * T = 8192, H = 16), then the per-row statistics (row max, denominator, probability scale),
- * 12 bytes per query and head from a 256-byte boundary; 0
- * for empty shapes. Host-side, no GPU work. No counterpart in the reference (its kernel keeps
+ * T = 8192, H = 16), then the row maxima, 4 bytes per query and head from a 256-byte boundary;
+ * 0 for empty shapes. Host-side, no GPU work. No counterpart in the reference (its kernel keeps
  * nothing between passes). */
 uint64_t uwc_attention_scratch_bytes(int B, int T, int H);
 
 /* uwc_attention that keeps every e_ij = det_exp(s_ij - max) it computes for the exact row sum in
  * escratch (at least uwc_attention_scratch_bytes(B, T, H) bytes, 16-byte aligned) and reads it
- * back for the probability maximum and the P x V pass instead of recomputing scores and
- * exponentials, the sweeps split over three launches (row maxima; sums; P x V) that pass their
- * per-row statistics through the same scratch: identical output, about half the VALU work, 12 bytes of HBM traffic per score.
+ * back for the P x V pass instead of recomputing scores and exponentials, in two launches: the
+ * row maxima (left in the same scratch), then the sums and P x V. Identical output, about half
+ * the VALU work, 8 bytes of HBM traffic per score (each exponential written and read once).
  * Replaces the same reference as uwc_attention. */
 int uwc_attention_ws(const int8_t* qq, const float* qs, const int8_t* kq, const float* ks, const int8_t* vt,
                      const float* vs, int B, int T, int H, int Hkv, int hd, float inv_sqrt_hd, float* o,

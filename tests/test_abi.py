@@ -58,20 +58,20 @@ def test_scratch_words_host_only():
 
 def test_attention_scratch_bytes_host_only():
     """The stored-exp attention's scratch: 4 KiB per (16-query block, 64-key tile) pair of the
-    causal triangle, per sequence and head, then three floats per query and head (row max, den,
-    sp) from a 256-byte boundary."""
+    causal triangle, per sequence and head, then one float per query and head (the row max) from
+    a 256-byte boundary."""
     from uwc_amd import _lib
     L = _lib.lib()
-    rows = lambda B, T, H: (B * T * H * 12 + 255) // 256 * 256
+    rows = lambda B, T, H: (B * T * H * 4 + 255) // 256 * 256
     assert L.uwc_attention_scratch_bytes(0, 8, 1) == 0
     assert L.uwc_attention_scratch_bytes(1, 1, 1) == 4 * 4096 + 256       # 4 blocks of 16 in one 64-key tile
-    assert L.uwc_attention_scratch_bytes(1, 65, 1) == 12 * 4096 + 1024    # 4 blocks x 1 tile + 4 x 2
+    assert L.uwc_attention_scratch_bytes(1, 65, 1) == 12 * 4096 + 512     # 4 blocks x 1 tile + 4 x 2
     # brute force over the blocks of 16 queries: block wq sees key tiles 0 .. wq / 4
     for T in (64, 100, 1000, 8192):
         Tp = (T + 63) // 64 * 64
         tiles = sum(wq // 4 + 1 for wq in range(Tp // 16))
         assert L.uwc_attention_scratch_bytes(3, T, 5) == 3 * 5 * tiles * 4096 + rows(3, T, 5)
-    assert L.uwc_attention_scratch_bytes(1, 8192, 16) == 2164260864 + 8192 * 16 * 12
+    assert L.uwc_attention_scratch_bytes(1, 8192, 16) == 2164260864 + 8192 * 16 * 4
 
 
 @pytest.mark.parametrize("kwargs,msg", [
@@ -127,8 +127,8 @@ def test_other_entry_points_reject_bad_arguments():
     assert "overlaps" in L.uwc_last_error().decode()
     assert L.uwc_igemm_dequant_residual_f32(fake, fake, 256, 256, 128, fake, fake, None, fake, None) == -1
     assert "null" in L.uwc_last_error().decode()
-    # the stored-exp attention: a scratch one byte short of the exponentials and the per-row
-    # statistics (row max, den, sp) is refused before any launch; so is a missing one
+    # the stored-exp attention: a scratch one byte short of the exponentials and the row maxima
+    # is refused before any launch; so is a missing one
     need = L.uwc_attention_scratch_bytes(1, 300, 4)
     inv = ctypes.c_float(0.125)
     assert L.uwc_attention_ws(fake, fake, fake, fake, fake, fake, 1, 300, 4, 2, 64, inv, fake, fake, need - 1,

@@ -267,37 +267,114 @@ def test_rowmax_ring_dma_and_reads(hd, W):
     assert sorted(w * SL + l for w in range(W) for l in range(SL)) == list(range(64))
 
 
+def _ring_schedule(nkt: int, NS: int, per_tile: int):
+    """One wave's DMA ring of NS stages as the attention kernels run it: tiles 0 .. NS - 2 issued
+    up front, tile kt + NS - 1 issued after the barrier of iteration kt into tile kt - 1's stage;
+    the wait before iteration kt leaves at most (NS - 2) per_tile of the wave's DMAs pending, or
+    none when no later tile is in flight. Checks that the tile a wait covers has landed and that
+    a stage is overwritten only after the iteration that read it (every wave passed the barrier
+    of the next one)."""
+    NW = (NS - 2) * per_tile
+    issued = []        # tile per DMA, in issue order
+    stage_of = {}
+    last_read = {}     # stage -> last tile read from it
+    for t in range(NS - 1):
+        if t < nkt:
+            issued += [t] * per_tile
+            stage_of[t] = t % NS
+    done = 0           # DMAs known complete
+    for kt in range(nkt):
+        allowed = NW if kt + NS - 2 < nkt else 0
+        done = max(done, len(issued) - allowed)
+        assert all(x != kt for x in issued[done:]), "tile read before its DMA completed"
+        if kt + NS - 1 < nkt:
+            st = (kt + NS - 1) % NS
+            assert last_read.get(st, -1) <= kt - 1 and st == (kt - 1) % NS
+            issued += [kt + NS - 1] * per_tile
+            stage_of[kt + NS - 1] = st
+        assert stage_of[kt] == kt % NS
+        last_read[kt % NS] = kt
+
+
 @pytest.mark.parametrize("T,hd", [(1, 128), (100, 64), (300, 32), (2048, 128)])
 def test_rowmax_ring_schedule(T, hd):
-    """The ring schedule of attn_rowmax_kernel (NS = 4 stages): tiles 0 .. NS - 2 issued up
-    front, tile kt + NS - 1 issued after the barrier of iteration kt into tile kt - 1's stage;
-    the wait before iteration kt leaves at most NW = (NS - 2)(KD + 1) of the wave's DMAs
-    pending, or none. Emulated per wave: the tile a wait covers has landed, and a stage is
-    overwritten only after every wave has read it."""
-    NS = 4
+    """attn_rowmax_kernel's ring: NS = 4 stages, KD + 1 DMAs per wave and tile (key rows, key
+    scales)."""
     TILE = 64 * hd
     KS = TILE // 16 // 4
     KD = KS // 64 if KS >= 64 else 1
-    per_tile = KD + 1
-    NW = (NS - 2) * per_tile
     for qt in range((T + 63) // 64):
-        nkt = qt + 1
-        issued = []        # tile per DMA, in issue order
-        stage_of = {}
-        last_read = {}     # stage -> last tile read from it
-        for t in range(NS - 1):
-            if t < nkt:
-                issued += [t] * per_tile
-                stage_of[t] = t % NS
-        done = 0           # DMAs known complete
-        for kt in range(nkt):
-            allowed = NW if kt + NS - 2 < nkt else 0
-            done = max(done, len(issued) - allowed)
-            assert all(x != kt for x in issued[done:]), "tile read before its DMA completed"
-            if kt + NS - 1 < nkt:
-                st = (kt + NS - 1) % NS
-                assert last_read.get(st, -1) <= kt - 1 and st == (kt - 1) % NS
-                issued += [kt + NS - 1] * per_tile
-                stage_of[kt + NS - 1] = st
-            assert stage_of[kt] == kt % NS
-            last_read[kt % NS] = kt
+        _ring_schedule(qt + 1, 4, KD + 1)
+
+
+def _vchunk(r: int) -> int:
+    """Chunk (four 16-byte slots) of row r of a 16-row block in the P x V ring."""
+    return 4 * ((r >> 1) & 3) + 2 * (r & 1) + (r >> 3)
+
+
+def _pv_maps(hd: int):
+    """The P x V sweep's (attention_kernel MODES 3 and 4) V ring tile: hd / 16 blocks of 16 V^T
+    rows x 64 key bytes, row r of block d in chunk _vchunk(r) (slots 64 d + 4 chunk .. + 3), its
+    piece p at slot p ^ ((r >> 1) & 3) of the chunk; the four waves DMA the tile in VD
+    instructions of VL lanes each, lane l of an instruction writing slot base + l. Returns the
+    DMAs per wave and tile, the DMA map slot -> (row, piece, instruction) and the read map
+    (lane, fragment d) -> slot."""
+    VT = hd * 64
+    VS = VT // 16 // 4
+    VD = VS // 64 if VS >= 64 else 1
+    VL = 64 if VS >= 64 else VS
+    assert VD * VL * 4 * 16 == VT
+    inv = {_vchunk(r): r for r in range(16)}
+    written = {}
+    for wave in range(4):
+        for u in range(VD):
+            base = (wave * VD + u) * VL
+            for lane in range(VL):
+                s16 = base + lane
+                r = inv[(s16 >> 2) & 15]
+                row = 16 * (s16 >> 6) + r
+                p = (s16 & 3) ^ ((r >> 1) & 3)
+                assert s16 not in written
+                written[s16] = (row, p, (wave, u))
+    reads = {}
+    for lane in range(64):
+        ql, g = lane & 15, lane >> 4
+        for d in range(hd // 16):
+            reads[(lane, d)] = 64 * d + 4 * _vchunk(ql) + (g ^ ((ql >> 1) & 3))
+    return VD + 5, written, reads
+
+
+@pytest.mark.parametrize("hd", [32, 64, 128])
+def test_pv_ring_dma_and_reads(hd):
+    """Every 16-byte piece of the tile's hd V^T rows is DMA'd exactly once by the four waves;
+    four consecutive lanes of one DMA read one row's 64 contiguous bytes; the lane that reads
+    fragment d finds dim 16 d + (lane & 15) at keys 16 (lane >> 4) .. + 15 (the MFMA B operand).
+    Banks: every lane's slot residue mod 16 equals the one attn_rowmax_kernel's ring read gives
+    the same lane (chunk c = 0, whose pattern rocprofv3 counts free of bank conflicts), so the
+    two reads spread over the banks alike; the 16 lanes of a lane group hit 16 distinct 16-byte
+    bank groups. The V scales: lanes 0-15 of wave w DMA keys 16 w .. + 15."""
+    _, written, reads = _pv_maps(hd)
+    assert sorted(written) == list(range(hd * 4))
+    assert sorted((r, p) for r, p, _ in written.values()) == [(r, p) for r in range(hd) for p in range(4)]
+    for s0 in range(0, hd * 4, 4):
+        rows = {written[s][0] for s in range(s0, s0 + 4)}
+        assert len(rows) == 1 and {written[s][1] for s in range(s0, s0 + 4)} == {0, 1, 2, 3}
+        assert len({written[s][2] for s in range(s0, s0 + 4)}) == 1
+    for (lane, d), s in reads.items():
+        assert written[s][:2] == (16 * d + (lane & 15), lane >> 4)
+    _, _, rm_reads = _rowmax_tile_maps(128)
+    for (lane, d), s in reads.items():
+        assert s % 16 == rm_reads[(lane, 0, 0)] % 16, (lane, d)
+    for d in range(hd // 16):
+        for g in range(4):
+            assert len({reads[(g * 16 + ql, d)] % 16 for ql in range(16)}) == 16
+    assert sorted(w * 16 + l for w in range(4) for l in range(16)) == list(range(64))
+
+
+@pytest.mark.parametrize("T,hd", [(1, 128), (100, 64), (300, 32), (2048, 128)])
+def test_pv_ring_schedule(T, hd):
+    """The P x V ring: NS = 3 stages, 4 + VD + 1 DMAs per wave and tile (exponentials, V, V
+    scales); the kernel waits for vmcnt(PER) while tile kt + 1 is in flight, else vmcnt(0)."""
+    per, _, _ = _pv_maps(hd)
+    for qt in range((T + 63) // 64):
+        _ring_schedule(qt + 1, 3, per)

@@ -66,6 +66,10 @@ __device__ __forceinline__ void at_lds_barrier() { asm volatile("s_waitcnt lgkmc
 
 __device__ __forceinline__ v4i at_zero4() { return v4i{0, 0, 0, 0}; }
 
+// The chunk (four 16-byte slots) of row r (0..15) in a 16-row block of the P x V sweep's V ring:
+// 4 ((r >> 1) & 3) + 2 (r & 1) + (r >> 3)
+__host__ __device__ constexpr int at_vchunk(int r) { return 4 * ((r >> 1) & 3) + 2 * (r & 1) + (r >> 3); }
+
 // round_half_even(e * 2^41) for 0 <= e < 2, as a float64 integer (exact: e * 2^41 is a float32
 // scaled by a power of two, its rounding to an integer is a float32 integer below 2^42).
 __device__ __forceinline__ double at_fix41(float e) { return (double)rintf(__fmul_rn(e, 0x1p41f)); }
@@ -170,27 +174,24 @@ __device__ __forceinline__ void at_block(int id, int ntiles, int H, int Hkv, int
 __host__ __device__ constexpr u64 at_tile0(u64 wq) { return (wq / 4 + 1) * (2 * (wq / 4) + wq % 4); }
 __host__ __device__ constexpr u64 at_tiles(u64 Tp) { return at_tile0(Tp / 16); }
 
-// ES (exp stored): sweep 2 writes every e_ij it computes to escr (one 4 KiB tile per wave and key
-// tile, 16 floats per lane as four float4 at lane and piece offsets), and sweeps 3 and 4 read them
-// back instead of recomputing the scores and det_exp (about two thirds of the VALU work per score
-// element), two tiles ahead. The same values go through the same operations, so both forms give
+// Without ES the kernel runs the four sweeps, recomputing the scores and det_exp in each.
+// ES (exp stored, uwc_attention_ws) runs after attn_rowmax_kernel, which leaves each row's max
+// of y = fl(fl(acc qs) ks) in rows (B T H floats, index (b T + q) H + h; a max in any order is
+// the same number). Sweep 2 writes every e_ij it computes to escr (one 4 KiB tile per wave and
+// key tile, 16 floats per lane as four float4 at lane and piece offsets), and sweeps 3 and 4
+// read them back instead of recomputing the scores and det_exp (about two thirds of the VALU
+// work per score element); the same values go through the same operations, so both forms give
 // the same bits. The scratch (2.2 GB at T = 8192, 16 heads) is written and read with the
-// non-temporal hint: cached normally, its stream evicted the XCD's K and V from L2
-// (2.087 -> 1.960 ms per Qwen3-1.7B layer at T = 8192).
-//
-// MODE 0 runs the four sweeps. The stored form splits them over launches whose per-row
-// results sit in rows (three arrays of nq = B T H floats, index (b T + q) H + h): the row max
-// of y = fl(fl(acc qs) ks) (attn_rowmax_kernel), the exact denominator den and the
-// probabilities' scale sp. MODE 2 reads the row max, runs sweeps 2-3 (at three waves per SIMD:
-// they need fewer registers than sweep 4) and writes den and sp; MODE 3 reads den and sp and
-// runs sweep 4 alone. Each statistic is the same number however it is split (a max in any order,
-// an exact integer sum, values passed as floats), so every form gives the same bits.
-template <int HD, bool ES, int MODE>
-__global__ void __launch_bounds__(256, MODE == 2 ? 3 : HD == 128 ? 2 : 3)
+// non-temporal hint: cached normally, its stream evicted the XCD's K and V from L2. Sweep 4 of
+// the stored form feeds every operand through LDS (DMA rings, see there). The workgroups of
+// one launch are at different sweeps at any time (their causal rows differ in length), so one
+// workgroup's VALU-bound sums overlap another's memory-bound P x V on the same CU.
+template <int HD, bool ES>
+__global__ void __launch_bounds__(256, ES ? 3 : HD == 128 ? 2 : 3)
     attention_kernel(const i8* __restrict__ qq, const float* __restrict__ qs, const i8* __restrict__ kq,
                      const float* __restrict__ ks, const i8* __restrict__ vt, const float* __restrict__ vs, int T,
                      int Tp, int H, int Hkv, float inv_sqrt, float* __restrict__ o, float* __restrict__ escr,
-                     float* __restrict__ rows, u32 nq) {
+                     const float* __restrict__ rows) {
   constexpr int NC = (HD + 63) / 64;  // 64-dim chunks of the score product
   constexpr int ND = HD / 16;         // 16-dim blocks of the output
   __shared__ __attribute__((aligned(16))) float at_slot[4][2][64];
@@ -199,9 +200,9 @@ __global__ void __launch_bounds__(256, MODE == 2 ? 3 : HD == 128 ? 2 : 3)
   int qt, h, bseq;
   at_block((int)blockIdx.x, Tp / 64, H, Hkv, (int)(gridDim.x / (u32)(Tp / 64 * H)), qt, h, bseq);
   const int q0 = qt * 64 + wave * 16;
-  // whole waves only (MODE 3 keeps every wave: its loop has workgroup barriers; a wave past T
-  // computes clamped rows and stores nothing)
-  if (MODE != 3 && q0 >= T) return;
+  // whole waves only (the stored form keeps every wave: its sweep 4 has workgroup barriers; a
+  // wave past T computes clamped rows and stores nothing)
+  if (!ES && q0 >= T) return;
   const int hk = h / (H / Hkv);
   // 32-bit offsets: the host checks B * T * max(H, Hkv) * HD < 2^31
   const u32 nb = (u32)(bseq * T);
@@ -352,8 +353,7 @@ __global__ void __launch_bounds__(256, MODE == 2 ? 3 : HD == 128 ? 2 : 3)
   float mx = -__int_as_float(0x7f800000);
   // a padding query (qi >= T) sees keys 0 .. T - 1, as query T - 1 does
   const u32 ridx = (nb + qc) * (u32)H + h;
-  if constexpr (MODE == 3) {
-  } else if constexpr (MODE == 2) {
+  if constexpr (ES) {
     mx = __fmul_rn(rows[ridx], inv_sqrt);
   } else {
     ksweep([&](int kt, const float (&Y)[4][4], const KTile&, auto) AT_AI {
@@ -379,11 +379,6 @@ __global__ void __launch_bounds__(256, MODE == 2 ? 3 : HD == 128 ? 2 : 3)
     for (int b = 0; b < 4; b++) out[b] = *reinterpret_cast<const float4*>(sv_slot + 16 * b + 4 * g);
     __builtin_amdgcn_wave_barrier();
   };
-  float den, sp;
-  if constexpr (MODE == 3) {
-    den = rows[nq + ridx];
-    sp = rows[2 * nq + ridx];
-  } else {
   // sweep 2: exact denominator (fixed point at 2^41); masked entries give det_exp(-inf) = 0.
   // A tile's 16 terms per lane sum exactly in float64 (< 2^46), then join a u64 total.
   //
@@ -426,7 +421,7 @@ __global__ void __launch_bounds__(256, MODE == 2 ? 3 : HD == 128 ? 2 : 3)
     dsum += (u64)part;
   }, std::false_type{});
   dsum = at_sum_groups(dsum);
-  den = (float)ldexp((double)dsum, -41);
+  const float den = (float)ldexp((double)dsum, -41);
   const double rden = 1.0 / (double)den;
 
   // sweep 3: max of the V-scaled probabilities, only for waves with a near tie (see sweep 2)
@@ -465,16 +460,8 @@ __global__ void __launch_bounds__(256, MODE == 2 ? 3 : HD == 128 ? 2 : 3)
       }
   });
   pm = at_max_groups(pm);
-  sp = __fdiv_rn(fmaxf(pm, 1e-30f), AT_PLEVELS);
-  if constexpr (MODE == 2) {
-    if (g == 0 && qi < T) {
-      rows[nq + ridx] = den;
-      rows[2 * nq + ridx] = sp;
-    }
-    return;
-  }
-  }
-  const double rden = 1.0 / (double)den, rsp = 1.0 / (double)sp;
+  const float sp = __fdiv_rn(fmaxf(pm, 1e-30f), AT_PLEVELS);
+  const double rsp = 1.0 / (double)sp;
 
   // sweep 4: 14-bit probabilities as two 7-bit limbs, O^T = V^T P^T on the matrix cores
   v4i ohi[ND], olo[ND];
@@ -508,38 +495,50 @@ __global__ void __launch_bounds__(256, MODE == 2 ? 3 : HD == 128 ? 2 : 3)
     for (int d = 0; d < ND; d++)
       vf[d] = *reinterpret_cast<const v4i*>(vbase + (u32)(16 * d + ql) * (u32)Tp + kt * 64 + 16 * g);
   };
-  if constexpr (MODE == 3) {
+  if constexpr (ES) {
     // Sweep 4 with every load a DMA into LDS: the wave's own exponentials (4 KiB a tile) into
-    // its slot of a 3-stage ring, the tile's V^T rows (64 keys of every dim, the same for the
+    // its slot of a 2-stage ring, the tile's V^T rows (64 keys of every dim, the same for the
     // four waves: each DMAs a quarter) and V scales (a quarter each) into shared rings. Loaded per
-    // wave into registers, as the other forms do, the 13 vector-memory instructions of a wave
-    // and tile (8 of them for V tiles the workgroup's four waves all read) bound the sweep at the
-    // CU's rate for such instructions; here a wave issues 7 DMAs a tile. No compiler-issued
-    // global load remains in the loop, so every wait count is static. A V row of a tile is 64
-    // bytes, four 16-byte pieces, piece p of row r stored at p ^ ((r >> 2) & 3) so that the 16
-    // rows of an MFMA fragment read (one piece) hit 16 distinct bank groups.
+    // wave into registers, the 13 vector-memory instructions of a wave and tile (8 of them for
+    // V tiles the workgroup's four waves all read) bound the sweep at the CU's rate for such
+    // instructions; here a wave issues 7 DMAs a tile. No compiler-issued global load remains in
+    // the loop, so every wait count is static. The V tile is HD / 16
+    // blocks of 16 rows x 64 key bytes (1 KiB, 64 slots of 16 bytes); row r of block d sits in
+    // chunk at_vchunk(r) of four slots (its 64 bytes, so four consecutive DMA lanes read one
+    // row segment), piece p at slot p ^ ((r >> 1) & 3) of the chunk. A fragment read (lane
+    // group g reads piece g of the block's 16 rows) then gives every lane the slot residue
+    // (mod 16) the row-max ring's reads give it, a pattern measured free of bank conflicts
+    // (the earlier slot 4 r + (p ^ ((r >> 2) & 3)), distinct residues in each 16-lane group,
+    // measured 2-way).
     constexpr int VT = HD * 64;                   // bytes of a V tile
     constexpr int VS = VT / 16 / 4;               // its 16-byte slots per wave
     constexpr int VD = VS >= 64 ? VS / 64 : 1;    // V DMAs per wave and tile
     constexpr int VL = VS >= 64 ? 64 : VS;        // lanes active in each
-    constexpr int PER = 4 + VD + 1;               // DMAs per wave and tile: exponentials, V, V scales
-    static_assert(VD * VL * 4 * 16 == VT && PER < 32, "V tile split over the four waves");
-    __shared__ __attribute__((aligned(16))) u8 ering[3][4][4096];
-    __shared__ __attribute__((aligned(16))) u8 vring[3][VT];
-    __shared__ __attribute__((aligned(16))) float sring[3][64];
+    static_assert(VD * VL * 4 * 16 == VT, "V tile split over the four waves");
+    // two ring stages, so that three workgroups (at three waves per SIMD) fit a CU's LDS
+    constexpr int NS = 2;
+    static_assert(NS == 2, "the loop's wait assumes one tile in flight");
+    __shared__ __attribute__((aligned(16))) u8 ering[NS][4][4096];
+    __shared__ __attribute__((aligned(16))) u8 vring[NS][VT];
+    __shared__ __attribute__((aligned(16))) float sring[NS][64];
     const u32 er0 = (u32)(uintptr_t)(s2_lptr_at)ering[0][0], vr0 = (u32)(uintptr_t)(s2_lptr_at)vring[0];
     const u32 sr0 = (u32)(uintptr_t)(s2_lptr_at)sring[0];
-    // the row constants are final before the loop: the compiler's waits for their loads stay here
+    // the row constants are final before the loop (the compiler's waits for the loads they
+    // come from stay out of it)
     asm volatile("" ::"v"(rden), "v"(rsp));
+    // the wave's stores of its exponentials (sweep 2) are done before its DMAs read them
+    at_waitv<0>();
     auto issue = [&](int kt) AT_AI {
-      const int st = kt % 3;
+      const int st = kt % NS;
 #pragma unroll
       for (int b = 0; b < 4; b++)
         at_dma16_nt(ewave + kt * 1024 + b * 256,
                     __builtin_amdgcn_readfirstlane(er0 + (u32)((st * 4 + wave) * 4096 + b * 1024)));
 #pragma unroll
       for (int u = 0; u < VD; u++) {
-        const int s16 = (wave * VD + u) * VL + lane, row = s16 >> 2, p = (s16 & 3) ^ ((row >> 2) & 3);
+        const int s16 = (wave * VD + u) * VL + lane, c = (s16 >> 2) & 15;
+        const int r = ((c & 1) << 3) | ((c >> 2) << 1) | ((c >> 1) & 1);  // at_vchunk(r) = c
+        const int row = 16 * (s16 >> 6) + r, p = (s16 & 3) ^ ((r >> 1) & 3);
         const i8* src = vbase + (u32)row * (u32)Tp + kt * 64 + 16 * p;
         const u32 dst = __builtin_amdgcn_readfirstlane(vr0 + (u32)(st * VT + (wave * VD + u) * VL * 16));
         if (VL == 64 || lane < VL) at_dma16(src, dst);
@@ -547,14 +546,13 @@ __global__ void __launch_bounds__(256, MODE == 2 ? 3 : HD == 128 ? 2 : 3)
       const float* ssrc = vs + sc_base + (u32)min(kt * 64 + wave * 16 + (lane & 15), T - 1) * (u32)Hkv;
       if (lane < 16) at_dma4(ssrc, __builtin_amdgcn_readfirstlane(sr0 + (u32)(st * 256 + wave * 64)));
     };
-    if (nkt > 0) issue(0);
-    if (nkt > 1) issue(1);
+    for (int t = 0; t < NS - 1; t++)
+      if (t < nkt) issue(t);
     for (int kt = 0; kt < nkt; kt++) {
-      if (kt + 1 < nkt) at_waitv<PER>();  // tile kt + 1's DMAs may still be in flight
-      else at_waitv<0>();
+      at_waitv<0>();  // tile kt's DMAs done (with two stages no other tile is in flight)
       at_lds_barrier();  // tile kt is in LDS; every wave is done with tile kt - 1's stage
-      if (kt + 2 < nkt) issue(kt + 2);
-      const int st = kt % 3;
+      if (kt + NS - 1 < nkt) issue(kt + NS - 1);
+      const int st = kt % NS;
       float e[4][4];
       float4 svv[4];
 #pragma unroll
@@ -565,34 +563,10 @@ __global__ void __launch_bounds__(256, MODE == 2 ? 3 : HD == 128 ? 2 : 3)
       }
       v4i vf[ND];
 #pragma unroll
-      for (int d = 0; d < ND; d++) {
-        const int row = 16 * d + ql;
-        vf[d] = *reinterpret_cast<const v4i*>(vring[st] + 16 * (row * 4 + (g ^ ((row >> 2) & 3))));
-      }
+      for (int d = 0; d < ND; d++)
+        vf[d] = *reinterpret_cast<const v4i*>(vring[st] + 16 * (64 * d + 4 * at_vchunk(ql) + (g ^ ((ql >> 1) & 3))));
       pv_tile(e, svv, vf);
     }
-  } else if constexpr (ES) {
-    float4 eb[2][4];
-    float vb[2];
-    v4i vfb[2][ND];  // the tile's V rows, fetched two tiles ahead with its exponentials and scales
-    pipelined(
-        [&](int kt, auto sl) AT_AI {
-          eload(kt, eb[decltype(sl)::value]);
-          vb[decltype(sl)::value] = vsload(kt);
-          vload(kt, vfb[decltype(sl)::value]);
-        },
-        [&](int kt, auto sl) AT_AI {
-          constexpr int L = decltype(sl)::value;
-          const v4i (&vf)[ND] = vfb[L];
-          float4 svv[4];
-          vsstage(vb[L], svv);
-          float e[4][4];
-#pragma unroll
-          for (int b = 0; b < 4; b++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) e[b][i] = at_get(eb[L][b], i);
-          pv_tile(e, svv, vf);
-        });
   } else sweep([&](int kt, auto mask) {
     float S[4][4];
     float4 skv[4], svv[4];
@@ -743,8 +717,8 @@ __global__ void __launch_bounds__(256 * HPW) attn_rowmax_kernel(const i8* __rest
   if (g == 0 && qi < T) rmax[(nb + qi) * (u32)H + h] = mx;
 }
 
-// The scratch of uwc_attention_ws: the exponentials' tiles, then the per-row statistics (row
-// max, den, sp: three arrays of one float per query and head) from a 256-byte boundary.
+// The scratch of uwc_attention_ws: the exponentials' tiles, then the row maxima (one float per
+// query and head) from a 256-byte boundary.
 static u64 at_exp_bytes(int B, int T, int H) {
   const u64 Tp = ((u64)T + 63) / 64 * 64;
   return (u64)B * (u64)H * at_tiles(Tp) * 4096;
@@ -752,7 +726,7 @@ static u64 at_exp_bytes(int B, int T, int H) {
 
 extern "C" uint64_t uwc_attention_scratch_bytes(int B, int T, int H) {
   if (B <= 0 || T <= 0 || H <= 0) return 0;
-  return at_exp_bytes(B, T, H) + ((u64)B * (u64)T * (u64)H * 12 + 255) / 256 * 256;
+  return at_exp_bytes(B, T, H) + ((u64)B * (u64)T * (u64)H * 4 + 255) / 256 * 256;
 }
 
 static int attention_go(const char* fn, const int8_t* qq, const float* qs, const int8_t* kq, const float* ks,
@@ -776,9 +750,8 @@ static int attention_go(const char* fn, const int8_t* qq, const float* qs, const
                       (unsigned long long)uwc_attention_scratch_bytes(B, T, H));
     if ((uintptr_t)escratch & 15) return uwc_fail("%s: escratch must be 16-byte aligned", fn);
   }
-  // with the scratch: sweep 1 (the row maxima), sweeps 2-3 (den, sp), sweep 4, each a launch
+  // with the scratch: sweep 1 (the row maxima) a launch, sweeps 2-4 another
   float* rows = escratch ? escratch + at_exp_bytes(B, T, H) / 4 : nullptr;
-  const u32 nq = (u32)B * (u32)T * (u32)H;
   // the row max's workgroups take HPW heads of one kv head (4, 2 or 1 of its G = H / Hkv)
   const int G = H / Hkv, hpw = G % 4 == 0 ? 4 : G % 2 == 0 ? 2 : 1;
   auto go = [&](auto hdc, auto esc) {
@@ -793,13 +766,11 @@ static int attention_go(const char* fn, const int8_t* qq, const float* qs, const
       if (hpw == 4) rowmax(std::integral_constant<int, 4>{});
       else if (hpw == 2) rowmax(std::integral_constant<int, 2>{});
       else rowmax(std::integral_constant<int, 1>{});
-      hipLaunchKernelGGL((attention_kernel<HDV, true, 2>), grid, dim3(256), 0, stream, qq, qs, kq, ks, vt, vs, T, Tp,
-                         H, Hkv, inv_sqrt_hd, o, escratch, rows, nq);
-      hipLaunchKernelGGL((attention_kernel<HDV, true, 3>), grid, dim3(256), 0, stream, qq, qs, kq, ks, vt, vs, T, Tp,
-                         H, Hkv, inv_sqrt_hd, o, escratch, rows, nq);
+      hipLaunchKernelGGL((attention_kernel<HDV, true>), grid, dim3(256), 0, stream, qq, qs, kq, ks, vt, vs, T, Tp, H,
+                         Hkv, inv_sqrt_hd, o, escratch, rows);
     } else {
-      hipLaunchKernelGGL((attention_kernel<HDV, false, 0>), grid, dim3(256), 0, stream, qq, qs, kq, ks, vt, vs, T,
-                         Tp, H, Hkv, inv_sqrt_hd, o, nullptr, nullptr, 0u);
+      hipLaunchKernelGGL((attention_kernel<HDV, false>), grid, dim3(256), 0, stream, qq, qs, kq, ks, vt, vs, T, Tp,
+                         H, Hkv, inv_sqrt_hd, o, nullptr, nullptr);
     }
   };
   auto go_hd = [&](auto esc) {
