@@ -224,27 +224,64 @@ __host__ __device__ __forceinline__ int vt_pos(int j) {
   return (j & ~63) | (((j >> 2) & 3) << 4) | (((j >> 4) & 3) << 2) | (j & 3);
 }
 
+// One workgroup takes QP_TOKENS consecutive tokens; wave w the heads w, w + 4, ... of each, QH
+// heads at a time, the tokens inside that loop. Loaded once per workgroup instead of per head
+// and token: the rope's cos and sin rows (per token), the q/k norm weights, the heads' column
+// scales (per head group, for all its tokens). A V head's quantized bytes of the 4 tokens are in
+// one wave's registers, so when the tokens are positions 4a .. 4a + 3 of one sequence (vt_pos
+// keeps those 4 adjacent) each transposed row gets one 4-byte store instead of 4 byte stores to
+// rows Tp bytes apart. About half the vector-memory instructions per token of a
+// one-token-per-workgroup form, which measured only 4% slower (90.5 against 87.2 us at T = 8192,
+// Qwen3-1.7B): the per-head chain (three wave reductions, a square root, two divisions, a
+// float64 reciprocal, the per-element ops) is the larger cost.
+#define QP_TOKENS 4
 template <int HD, bool FP>
 __global__ void __launch_bounds__(256) qkv_post_kernel(
     const void* __restrict__ acc, const float* __restrict__ s1, const float* __restrict__ sw,
     const float* __restrict__ qnw, const float* __restrict__ knw, const float* __restrict__ cosb,
-    const float* __restrict__ sinb, int T, int H, int Hkv, float inv_hd, float eps, int qknorm, i8* __restrict__ qq,
-    float* __restrict__ qs, i8* __restrict__ kq, float* __restrict__ ks, i8* __restrict__ vq, float* __restrict__ vs,
-    i8* __restrict__ vt, int Tp) {
+    const float* __restrict__ sinb, long N, int T, int H, int Hkv, float inv_hd, float eps, int qknorm,
+    i8* __restrict__ qq, float* __restrict__ qs, i8* __restrict__ kq, float* __restrict__ ks, i8* __restrict__ vq,
+    float* __restrict__ vs, i8* __restrict__ vt, int Tp) {
   constexpr int NV = HD >= 64 ? HD / 64 : 1;
   constexpr int L = HD == 32 ? 5 : HD == 64 ? 6 : 7;  // ceil(log2(HD))
-  const int n = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int pos = n % T, bseq = n / T;
+  constexpr int TK = QP_TOKENS;
+  static_assert(TK == 4, "a transposed row's 4-byte store holds the bytes of exactly 4 tokens");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const long n0 = (long)blockIdx.x * TK;
+  const int nt = (int)min((long)TK, N - n0);  // tokens of this workgroup (>= 1)
   const int NH = H + 2 * Hkv;
   const long W = (long)NH * HD;
   const bool act = HD >= 64 || lane < HD;
-  const float sx = FP ? 1.0f : s1[n];
-  // One head of the token (wave-uniform hh) from its dequantized values v.
-  auto head = [&](int hh, float (&v)[NV]) {
+  // per token: scale, position, sequence, rope rows (a missing token repeats the last one's)
+  float sx[TK], cs[TK][NV], sn[TK][NV];
+  int pos[TK], bs[TK];
+#pragma unroll
+  for (int t = 0; t < TK; t++) {
+    const long n = n0 + min(t, nt - 1);
+    pos[t] = (int)(n % T);
+    bs[t] = (int)(n / T);
+    sx[t] = FP ? 1.0f : s1[n];
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+      const int d = act ? lane + 64 * j : 0;
+      cs[t][j] = cosb[(long)pos[t] * HD + d];
+      sn[t][j] = sinb[(long)pos[t] * HD + d];
+    }
+  }
+  const bool packed = nt == TK && bs[0] == bs[TK - 1] && (pos[0] & 3) == 0 && ((uintptr_t)vt & 3) == 0;
+  float qn[NV], kn[NV];
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    qn[j] = qknorm && act ? qnw[lane + 64 * j] : 0.0f;
+    kn[j] = qknorm && act ? knw[lane + 64 * j] : 0.0f;
+  }
+  // One head hh of token t (wave-uniform) from its dequantized values v; the quantized values
+  // are left in qv
+  auto head = [&](int hh, int t, float (&v)[NV], i8 (&qv)[NV]) {
+    const long n = n0 + t;
     const bool isq = hh < H, isv = hh >= H + Hkv;
     if (!isv) {
       if (qknorm) {  // det_rmsnorm over the head (qwen3.py:214-216)
-        const float* wn = isq ? qnw : knw;
         float mx = 0.f;
 #pragma unroll
         for (int j = 0; j < NV; j++) mx = fmaxf(mx, __fmul_rn(v[j], v[j]));
@@ -255,7 +292,7 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(
         const float ss = dx_unfix(wave_sum64(s), sh);
         const float r = __fdiv_rn(1.0f, uwc_sqrt_rn(__fadd_rn(__fmul_rn(ss, inv_hd), eps)));
 #pragma unroll
-        for (int j = 0; j < NV; j++) v[j] = act ? __fmul_rn(__fmul_rn(v[j], r), wn[lane + 64 * j]) : 0.0f;
+        for (int j = 0; j < NV; j++) v[j] = act ? __fmul_rn(__fmul_rn(v[j], r), isq ? qn[j] : kn[j]) : 0.0f;
       }
       // rope: fadd(fmul(z, cos), fmul(rot(z), sin)), rot(z) = cat(-z[half:], z[:half])
       float rot[NV];
@@ -266,13 +303,8 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(
         const float o = __shfl_xor(v[0], HD / 2, 64);
         rot[0] = (lane & (HD / 2)) ? o : -o;
       }
-      const float* cr = cosb + (long)pos * HD;
-      const float* sr = sinb + (long)pos * HD;
 #pragma unroll
-      for (int j = 0; j < NV; j++) {
-        const int d = lane + 64 * j;
-        v[j] = act ? __fadd_rn(__fmul_rn(v[j], cr[d]), __fmul_rn(rot[j], sr[d])) : 0.0f;
-      }
+      for (int j = 0; j < NV; j++) v[j] = act ? __fadd_rn(__fmul_rn(v[j], cs[t][j]), __fmul_rn(rot[j], sn[t][j])) : 0.0f;
     }
     // quant_sym(qmax = 127) over the head (core.py:160-166)
     float am = 0.f;
@@ -280,53 +312,80 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(
     for (int j = 0; j < NV; j++) am = fmaxf(am, fabsf(v[j]));
     const float s = __fdiv_rn(fmaxf(wave_max(am), 1e-8f), 127.0f);
     const double rs = 1.0 / (double)s;
-    i8 qv[NV];
 #pragma unroll
     for (int j = 0; j < NV; j++) qv[j] = (i8)(int)fminf(fmaxf(rintf(uwc_div_rd(v[j], rs)), -127.f), 127.f);
     i8* qo;
     float* so;
     if (isq) {
-      qo = qq + ((long)n * H + hh) * HD;
-      so = qs + (long)n * H + hh;
+      qo = qq + (n * H + hh) * HD;
+      so = qs + n * H + hh;
     } else if (!isv) {
-      qo = kq + ((long)n * Hkv + (hh - H)) * HD;
-      so = ks + (long)n * Hkv + (hh - H);
+      qo = kq + (n * Hkv + (hh - H)) * HD;
+      so = ks + n * Hkv + (hh - H);
     } else {
-      qo = vq + ((long)n * Hkv + (hh - H - Hkv)) * HD;
-      so = vs + (long)n * Hkv + (hh - H - Hkv);
+      qo = vq + (n * Hkv + (hh - H - Hkv)) * HD;
+      so = vs + n * Hkv + (hh - H - Hkv);
     }
     if (act) {
 #pragma unroll
       for (int j = 0; j < NV; j++) qo[lane + 64 * j] = qv[j];
     }
     if (lane == 0) *so = s;
-    if (isv && vt && act) {
-      const int hk = hh - H - Hkv;
-      i8* col = vt + ((long)(bseq * Hkv + hk) * HD) * Tp + vt_pos(pos);
-#pragma unroll
-      for (int j = 0; j < NV; j++) col[(long)(lane + 64 * j) * Tp] = qv[j];
-    }
   };
-  // A wave takes heads wave, wave + 4, ...: the loads of QH of its heads are issued together
-  // (indices clamped in range, values of heads past NH unused), so the wave waits for memory once
-  // per QH heads instead of once per head.
-  constexpr int QH = 4;
+  // QH heads per pass, their loads for all the tokens issued together (indices clamped in
+  // range, values of heads past NH unused) so that the wave waits for memory once per pass
+  // (2 measured faster than 4: fewer registers)
+  constexpr int QH = 2;
   for (int h0 = wave; h0 < NH; h0 += 4 * QH) {
-    float vv[QH][NV];
+    float swv[QH][NV];
+    float vv[TK][QH][NV];
 #pragma unroll
     for (int c = 0; c < QH; c++) {
       const int col0 = min(h0 + 4 * c, NH - 1) * HD;
 #pragma unroll
-      for (int j = 0; j < NV; j++) {
-        const int d = act ? lane + 64 * j : 0;
-        if constexpr (FP) vv[c][j] = static_cast<const float*>(acc)[n * W + col0 + d];
-        else vv[c][j] = dx_deq(static_cast<const i32*>(acc)[n * W + col0 + d], sx, sw[col0 + d]);
-        if (!act) vv[c][j] = 0.0f;
+      for (int j = 0; j < NV; j++) swv[c][j] = FP ? 1.0f : sw[col0 + (act ? lane + 64 * j : 0)];
+    }
+#pragma unroll
+    for (int t = 0; t < TK; t++) {
+      const long n = n0 + min(t, nt - 1);
+#pragma unroll
+      for (int c = 0; c < QH; c++) {
+        const int col0 = min(h0 + 4 * c, NH - 1) * HD;
+#pragma unroll
+        for (int j = 0; j < NV; j++) {
+          const int d = act ? lane + 64 * j : 0;
+          if constexpr (FP) vv[t][c][j] = static_cast<const float*>(acc)[n * W + col0 + d];
+          else vv[t][c][j] = dx_deq(static_cast<const i32*>(acc)[n * W + col0 + d], sx[t], swv[c][j]);
+          if (!act) vv[t][c][j] = 0.0f;
+        }
       }
     }
 #pragma unroll
-    for (int c = 0; c < QH; c++)
-      if (h0 + 4 * c < NH) head(h0 + 4 * c, vv[c]);
+    for (int c = 0; c < QH; c++) {
+      const int hh = h0 + 4 * c;
+      if (hh >= NH) break;
+      const bool tv = vt && hh >= H + Hkv;  // a V head with the transposed copy wanted
+      const int hk = hh - H - Hkv;
+      u32 pk[NV] = {};
+#pragma unroll
+      for (int t = 0; t < TK; t++) {
+        if (t >= nt) break;
+        i8 qv[NV];
+        head(hh, t, vv[t][c], qv);
+        if (tv && act) {
+#pragma unroll
+          for (int j = 0; j < NV; j++) {
+            if (packed) pk[j] |= (u32)(u8)qv[j] << (8 * t);
+            else vt[((long)(bs[t] * Hkv + hk) * HD + lane + 64 * j) * Tp + vt_pos(pos[t])] = qv[j];
+          }
+        }
+      }
+      if (tv && act && packed) {
+#pragma unroll
+        for (int j = 0; j < NV; j++)
+          *reinterpret_cast<u32*>(vt + ((long)(bs[0] * Hkv + hk) * HD + lane + 64 * j) * Tp + vt_pos(pos[0])) = pk[j];
+      }
+    }
   }
 }
 
@@ -507,14 +566,15 @@ extern "C" int uwc_qkv_post(const void* acc, const float* s1, const float* sw, c
   if (N > 0x7fffffff) return uwc_fail("%s: too many tokens", fn);
   const float inv_hd = (float)(1.0 / (double)hd);
   const int Tp = uwc_vt_tokens(T);
+  const dim3 grid((unsigned)((N + QP_TOKENS - 1) / QP_TOKENS));
 #define QKV_LAUNCH(HD)                                                                                               \
   do {                                                                                                               \
     if (s1)                                                                                                          \
-      hipLaunchKernelGGL((qkv_post_kernel<HD, false>), dim3((unsigned)N), dim3(256), 0, stream, acc, s1, sw, qnw,    \
-                         knw, cosb, sinb, T, H, Hkv, inv_hd, eps, qknorm, qq, qs, kq, ks, vq, vs, vt, Tp);            \
+      hipLaunchKernelGGL((qkv_post_kernel<HD, false>), grid, dim3(256), 0, stream, acc, s1, sw, qnw, knw, cosb,      \
+                         sinb, N, T, H, Hkv, inv_hd, eps, qknorm, qq, qs, kq, ks, vq, vs, vt, Tp);                    \
     else                                                                                                             \
-      hipLaunchKernelGGL((qkv_post_kernel<HD, true>), dim3((unsigned)N), dim3(256), 0, stream, acc, s1, sw, qnw,     \
-                         knw, cosb, sinb, T, H, Hkv, inv_hd, eps, qknorm, qq, qs, kq, ks, vq, vs, vt, Tp);            \
+      hipLaunchKernelGGL((qkv_post_kernel<HD, true>), grid, dim3(256), 0, stream, acc, s1, sw, qnw, knw, cosb,       \
+                         sinb, N, T, H, Hkv, inv_hd, eps, qknorm, qq, qs, kq, ks, vq, vs, vt, Tp);                    \
   } while (0)
   if (hd == 32) QKV_LAUNCH(32);
   else if (hd == 64) QKV_LAUNCH(64);
