@@ -686,6 +686,97 @@ def linear_traffic_cases():
     return out
 
 
+ATTN_FILE = os.path.join(ROOT, "profiles", "attention_8192_counters.txt")
+ATTN_SHAPE = (8192, 16, 8, 128)  # configs[4]'s attention: T, heads, kv heads, head_dim (Qwen3-1.7B)
+ATTN_REPS = 4
+
+
+def attention_probe(torch):
+    """What the attention profile's passes run: configs[4]'s attention in the stored-exponentials
+    form (v_transpose_kernel, attn_rowmax_kernel, then attention_kernel<128, true>) ATTN_REPS times
+    on random int8 heads, then the calibration copy of COPY_BYTES three times."""
+    from uwc_amd import detgpu
+    T, H, Hkv, hd = ATTN_SHAPE
+    dev = "cuda"
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    qq = torch.randint(-127, 128, (T, H, hd), dtype=torch.int8, device=dev, generator=g)
+    kq = torch.randint(-127, 128, (T, Hkv, hd), dtype=torch.int8, device=dev, generator=g)
+    vq = torch.randint(-127, 128, (T, Hkv, hd), dtype=torch.int8, device=dev, generator=g)
+    qs, ks, vs = (torch.rand((T, h, 1), device=dev, generator=g) * 3e-2 + 1e-3 for h in (H, Hkv, Hkv))
+    for _ in range(ATTN_REPS):
+        detgpu.attention(qq, qs, kq, ks, vq, vs, 1, T, H, Hkv, float(1.0 / hd ** 0.5), stored_exp=True)
+    x = torch.empty(COPY_BYTES, dtype=torch.int8, device=dev).fill_(1)
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    log("attention probe: done")
+
+
+def summarize_attention(stats_csv, sq_csv, fetch_csv, write_csv, cmd):
+    """The attention profile from four passes over `bench.py --attention-probe` (a kernel trace
+    with --stats, one --pmc pass of SQ counters with GRBM_GUI_ACTIVE, one of FETCH_SIZE, one of
+    WRITE_SIZE), per kernel: average duration, VALU instructions per score element, VALU busy,
+    the waves' wait share, LDS bank conflicts and HBM bytes (KiB counters scaled by the
+    calibration copy), into ATTN_FILE. GRBM_GUI_ACTIVE sums the 8 XCDs' active cycles, so one XCD's
+    are a dispatch's cycles; VALU busy = SQ_ACTIVE_INST_VALU x 4 cycles / (1024 SIMDs x one XCD's
+    active cycles)."""
+    import csv
+    import statistics
+    T, H, Hkv, hd = ATTN_SHAPE
+    scores = H * T * (T + 1) // 2
+    kernels = {"attention_kernel<128, true>": "attention_kernel<128, true> (sums, then P x V)",
+               "attn_rowmax_kernel<128, 4, 2>": "attn_rowmax_kernel<128, 4, 2> (row maxima)"}
+
+    def per_kernel(path):
+        vals = {}
+        for row in csv.DictReader(open(path)):
+            vals.setdefault((row["Kernel_Name"], row["Counter_Name"]), []).append(float(row["Counter_Value"]))
+        return vals
+
+    sq, fetch, write = per_kernel(sq_csv), per_kernel(fetch_csv), per_kernel(write_csv)
+    durs = {r["Name"]: float(r["AverageNs"]) for r in csv.DictReader(open(stats_csv))}
+
+    def med(vals, key, counter):
+        xs = [x for (n, c), v in vals.items() if key in n and c.startswith(counter) for x in v]
+        return statistics.median(xs), len(xs)
+
+    def calib(vals, counter):
+        xs = [x for (n, c), v in vals.items() if "copy" in n.lower() and c.startswith(counter) for x in v]
+        return COPY_BYTES / (statistics.median([x for x in xs if x > 0.5 * COPY_BYTES / 1024]) * 1024.0)
+
+    ff, wf = calib(fetch, "FETCH_SIZE"), calib(write, "WRITE_SIZE")
+    exp_bytes = 4096 * H * sum(wq // 4 + 1 for wq in range(T // 16))
+    with open(ATTN_FILE, "w") as f:
+        f.write(f"rocprofv3 profile of configs[4]'s attention (Qwen3-1.7B: T = {T}, {H} heads, {Hkv} kv heads, head_dim "
+                f"{hd}; stored-exponentials form), medians per dispatch over the probe's {ATTN_REPS} calls\n")
+        f.write(f"commands: {cmd}\n")
+        f.write(f"score elements per call: {scores} (causal triangle x heads); exponentials stored: {exp_bytes} B, "
+                f"written once and read once\n")
+        f.write(f"calibration factors: FETCH_SIZE {ff:.4f}, WRITE_SIZE {wf:.4f} (a {COPY_BYTES} B device copy)\n\n")
+        for key, label in kernels.items():
+            dur = next((v for n, v in durs.items() if key in n), float("nan")) / 1e3
+            insts, n = med(sq, key, "SQ_INSTS_VALU")
+            act, _ = med(sq, key, "SQ_ACTIVE_INST_VALU")
+            gui, _ = med(sq, key, "GRBM_GUI_ACTIVE")
+            wcyc, _ = med(sq, key, "SQ_WAVE_CYCLES")
+            wait, _ = med(sq, key, "SQ_WAIT_INST_ANY")
+            lds, _ = med(sq, key, "SQ_INSTS_LDS")
+            bank, _ = med(sq, key, "SQ_LDS_BANK_CONFLICT")
+            fb = med(fetch, key, "FETCH_SIZE")[0] * 1024.0 * ff
+            wb = med(write, key, "WRITE_SIZE")[0] * 1024.0 * wf
+            f.write(f"{label}\n")
+            f.write(f"  average duration: {dur:.1f} us (kernel trace); dispatches counted: {n}\n")
+            f.write(f"  VALU wave-instructions: {insts:.0f} = {insts * 64 / scores:.1f} per score element\n")
+            f.write(f"  VALU busy: {4 * act / (1024 * gui / 8):.3f}; waves waiting on an instruction's inputs: "
+                    f"{wait / wcyc:.3f} of their cycles\n")
+            f.write(f"  LDS instructions: {lds:.0f}; LDS bank conflict cycles: {bank:.0f}\n")
+            f.write(f"  HBM: read {fb / 1e9:.3f} GB, written {wb / 1e9:.3f} GB = {(fb + wb) / 1e9:.3f} GB, "
+                    f"{(fb + wb) / (dur * 1e-6) / 1e12:.2f} TB/s over the average duration\n\n")
+    print(open(ATTN_FILE).read())
+
+
 LT_REPS = 3
 
 
@@ -1116,6 +1207,10 @@ def main():
     ap.add_argument("--e2e-layers", type=int, default=28)
     ap.add_argument("--e2e-cpu-tokens", type=int, default=256)
     ap.add_argument("--traffic-probe", action="store_true", help="the workload of the FETCH_SIZE / WRITE_SIZE passes")
+    ap.add_argument("--attention-probe", action="store_true",
+                    help="configs[4]'s attention a few times, then the calibration copy (the attention profile's workload)")
+    ap.add_argument("--summarize-attention", nargs=5, metavar=("STATS_CSV", "SQ_CSV", "FETCH_CSV", "WRITE_CSV", "CMD"),
+                    help="write profiles/attention_8192_counters.txt from the attention probe's passes")
     ap.add_argument("--linears-only", action="store_true", help="run only configs[1], configs[0], the decode and the prefill linears")
     ap.add_argument("--linears-traffic-probe", action="store_true",
                     help="the workload of the FETCH_SIZE / WRITE_SIZE passes over the configs[0], decode and configs[1] kernels")
@@ -1156,6 +1251,9 @@ def main():
     if args.summarize_linears_traffic:
         summarize_linears_traffic(*args.summarize_linears_traffic)
         return
+    if args.summarize_attention:
+        summarize_attention(*args.summarize_attention)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the multi-GPU layout "
               "is a design in DESIGN.md, not a measured path", file=sys.stderr)
@@ -1176,6 +1274,9 @@ def main():
         return
     if args.linears_traffic_probe:
         linears_traffic_probe(torch)
+        return
+    if args.attention_probe:
+        attention_probe(torch)
         return
     if args.e2e_only:
         print(json.dumps(qwen3_e2e(args, torch, np)))
