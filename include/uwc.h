@@ -273,7 +273,8 @@ int uwc_rmsnorm_f32(const float* x, const float* w, int rows, int k, float inv_d
  * tables (max_pos x hd, row = position), and quant_sym(127) per head: qq (N, H, hd) int8, qs
  * (N, H), kq / vq (N, Hkv, hd), ks / vs (N, Hkv). vt (optional, NULL to skip) receives V
  * transposed per (sequence, kv head) in the attention kernel's key order, (B, Hkv, hd,
- * uwc_vt_tokens(T)) int8. hd in {32, 64, 128}.
+ * uwc_vt_tokens(T)) int8. hd in {32, 64, 128}; acc, sw, qnw, knw, the tables, qq, kq, vq 16-byte
+ * aligned.
  * Replaces detgpu kernels.qkv_post: runtime/detgpu/kernels.py:788-802, :356-398. */
 int uwc_qkv_post(const void* acc, const float* s1, const float* sw, const float* qnw, const float* knw,
                  const float* cos_tab, const float* sin_tab, int B, int T, int H, int Hkv, int hd, float eps, int qknorm,

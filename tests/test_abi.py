@@ -138,6 +138,15 @@ def test_other_entry_points_reject_bad_arguments():
     assert "null escratch" in L.uwc_last_error().decode()
     assert L.uwc_attention(fake, fake, fake, fake, fake, fake, 1, 300, 4, 3, 64, inv, fake, None) == -1
     assert "H % Hkv" in L.uwc_last_error().decode() or "Hkv" in L.uwc_last_error().decode()
+    # qkv_post loads and stores whole vectors: a base off a 16-byte boundary is refused
+    odd = ctypes.c_void_p((1 << 20) + 4)
+    eps = ctypes.c_float(1e-6)
+    assert L.uwc_qkv_post(odd, fake, fake, fake, fake, fake, fake, 1, 64, 4, 2, 128, eps, 1, fake, fake, fake, fake,
+                          fake, fake, None, None) == -1
+    assert "16-byte aligned" in L.uwc_last_error().decode()
+    assert L.uwc_qkv_post(fake, fake, fake, fake, fake, fake, odd, 1, 64, 4, 2, 128, eps, 1, fake, fake, fake, fake,
+                          fake, fake, None, None) == -1
+    assert "16-byte aligned" in L.uwc_last_error().decode()
 
 
 def test_python_surface_matches_reference_names():

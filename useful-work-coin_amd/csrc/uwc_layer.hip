@@ -224,16 +224,20 @@ __host__ __device__ __forceinline__ int vt_pos(int j) {
   return (j & ~63) | (((j >> 2) & 3) << 4) | (((j >> 4) & 3) << 2) | (j & 3);
 }
 
-// One workgroup takes QP_TOKENS consecutive tokens; wave w the heads w, w + 4, ... of each, QH
-// heads at a time, the tokens inside that loop. Loaded once per workgroup instead of per head
-// and token: the rope's cos and sin rows (per token), the q/k norm weights, the heads' column
-// scales (per head group, for all its tokens). A V head's quantized bytes of the 4 tokens are in
-// one wave's registers, so when the tokens are positions 4a .. 4a + 3 of one sequence (vt_pos
-// keeps those 4 adjacent) each transposed row gets one 4-byte store instead of 4 byte stores to
-// rows Tp bytes apart. About half the vector-memory instructions per token of a
-// one-token-per-workgroup form, which measured only 4% slower (90.5 against 87.2 us at T = 8192,
-// Qwen3-1.7B): the per-head chain (three wave reductions, a square root, two divisions, a
-// float64 reciprocal, the per-element ops) is the larger cost.
+// Four heads per wave: each 16-lane row of a wave holds one head, a lane NV = HD / 16 adjacent
+// dims, so the per-head work that does not grow with the head's size (the row maxima and the
+// exact sum of squares as 4-step DPP reductions inside the row, the shift, the correctly rounded
+// square root and divisions, the float64 reciprocal) runs once per four heads, and every load
+// and store of a lane is one contiguous vector. The rope's partner of dim d is d +- HD / 2, the
+// same register of lane l ^ 8 in the row (DPP row_ror:8); rot's sign rides on sin (fl(-a b) is
+// -fl(a b)). Heads 16 p + 4 w + r for pass p, wave w, row r, so a row's head is one kind (q, k
+// or v) and a branch on it splits rows, never a row.
+//
+// One workgroup takes QP_TOKENS consecutive tokens, each pass of a wave its tokens in turn; the
+// column scales of a pass are loaded once for the four. A V head's quantized bytes of the 4
+// tokens stay in the row's registers, so when the tokens are positions 4a .. 4a + 3 of one
+// sequence (vt_pos keeps those 4 adjacent) each transposed row gets one 4-byte store instead of 4
+// byte stores to rows Tp bytes apart.
 #define QP_TOKENS 4
 template <int HD, bool FP>
 __global__ void __launch_bounds__(256) qkv_post_kernel(
@@ -242,149 +246,153 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(
     const float* __restrict__ sinb, long N, int T, int H, int Hkv, float inv_hd, float eps, int qknorm,
     i8* __restrict__ qq, float* __restrict__ qs, i8* __restrict__ kq, float* __restrict__ ks, i8* __restrict__ vq,
     float* __restrict__ vs, i8* __restrict__ vt, int Tp) {
-  constexpr int NV = HD >= 64 ? HD / 64 : 1;
-  constexpr int L = HD == 32 ? 5 : HD == 64 ? 6 : 7;  // ceil(log2(HD))
+  constexpr int NV = HD / 16;  // dims per lane
+  constexpr int L = HD == 32 ? 5 : HD == 64 ? 6 : 7;  // log2(HD)
   constexpr int TK = QP_TOKENS;
   static_assert(TK == 4, "a transposed row's 4-byte store holds the bytes of exactly 4 tokens");
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, row = lane >> 4, sl = lane & 15;
+  const int d0 = NV * sl;
   const long n0 = (long)blockIdx.x * TK;
   const int nt = (int)min((long)TK, N - n0);  // tokens of this workgroup (>= 1)
   const int NH = H + 2 * Hkv;
   const long W = (long)NH * HD;
-  const bool act = HD >= 64 || lane < HD;
-  // per token: scale, position, sequence, rope rows (a missing token repeats the last one's)
-  float sx[TK], cs[TK][NV], sn[TK][NV];
   int pos[TK], bs[TK];
+  float sx[TK];
 #pragma unroll
   for (int t = 0; t < TK; t++) {
     const long n = n0 + min(t, nt - 1);
     pos[t] = (int)(n % T);
     bs[t] = (int)(n / T);
     sx[t] = FP ? 1.0f : s1[n];
-#pragma unroll
-    for (int j = 0; j < NV; j++) {
-      const int d = act ? lane + 64 * j : 0;
-      cs[t][j] = cosb[(long)pos[t] * HD + d];
-      sn[t][j] = sinb[(long)pos[t] * HD + d];
-    }
   }
   const bool packed = nt == TK && bs[0] == bs[TK - 1] && (pos[0] & 3) == 0 && ((uintptr_t)vt & 3) == 0;
-  float qn[NV], kn[NV];
+  // NV consecutive floats, 16-byte aligned for NV >= 4 (8-byte for NV = 2): the host checks the
+  // bases, and every offset used here is a multiple of NV
+  auto ldv = [](const float* p, float (&v)[NV]) {
+    if constexpr (NV % 4 == 0) {
 #pragma unroll
-  for (int j = 0; j < NV; j++) {
-    qn[j] = qknorm && act ? qnw[lane + 64 * j] : 0.0f;
-    kn[j] = qknorm && act ? knw[lane + 64 * j] : 0.0f;
-  }
-  // One head hh of token t (wave-uniform) from its dequantized values v; the quantized values
-  // are left in qv
-  auto head = [&](int hh, int t, float (&v)[NV], i8 (&qv)[NV]) {
-    const long n = n0 + t;
-    const bool isq = hh < H, isv = hh >= H + Hkv;
-    if (!isv) {
-      if (qknorm) {  // det_rmsnorm over the head (qwen3.py:214-216)
-        float mx = 0.f;
-#pragma unroll
-        for (int j = 0; j < NV; j++) mx = fmaxf(mx, __fmul_rn(v[j], v[j]));
-        const int sh = dx_shift(wave_max(mx), L);
-        long long s = 0;
-#pragma unroll
-        for (int j = 0; j < NV; j++) s += act ? dx_fix(__fmul_rn(v[j], v[j]), sh) : 0;
-        const float ss = dx_unfix(wave_sum64(s), sh);
-        const float r = __fdiv_rn(1.0f, uwc_sqrt_rn(__fadd_rn(__fmul_rn(ss, inv_hd), eps)));
-#pragma unroll
-        for (int j = 0; j < NV; j++) v[j] = act ? __fmul_rn(__fmul_rn(v[j], r), isq ? qn[j] : kn[j]) : 0.0f;
+      for (int j = 0; j < NV; j += 4) {
+        const float4 x = *reinterpret_cast<const float4*>(p + j);
+        v[j] = x.x, v[j + 1] = x.y, v[j + 2] = x.z, v[j + 3] = x.w;
       }
-      // rope: fadd(fmul(z, cos), fmul(rot(z), sin)), rot(z) = cat(-z[half:], z[:half])
-      float rot[NV];
-      if constexpr (NV >= 2) {
-#pragma unroll
-        for (int j = 0; j < NV; j++) rot[j] = j < NV / 2 ? -v[j + NV / 2] : v[j - NV / 2];
-      } else {
-        const float o = __shfl_xor(v[0], HD / 2, 64);
-        rot[0] = (lane & (HD / 2)) ? o : -o;
-      }
-#pragma unroll
-      for (int j = 0; j < NV; j++) v[j] = act ? __fadd_rn(__fmul_rn(v[j], cs[t][j]), __fmul_rn(rot[j], sn[t][j])) : 0.0f;
-    }
-    // quant_sym(qmax = 127) over the head (core.py:160-166)
-    float am = 0.f;
-#pragma unroll
-    for (int j = 0; j < NV; j++) am = fmaxf(am, fabsf(v[j]));
-    const float s = __fdiv_rn(fmaxf(wave_max(am), 1e-8f), 127.0f);
-    const double rs = 1.0 / (double)s;
-#pragma unroll
-    for (int j = 0; j < NV; j++) qv[j] = (i8)(int)fminf(fmaxf(rintf(uwc_div_rd(v[j], rs)), -127.f), 127.f);
-    i8* qo;
-    float* so;
-    if (isq) {
-      qo = qq + (n * H + hh) * HD;
-      so = qs + n * H + hh;
-    } else if (!isv) {
-      qo = kq + (n * Hkv + (hh - H)) * HD;
-      so = ks + n * Hkv + (hh - H);
     } else {
-      qo = vq + (n * Hkv + (hh - H - Hkv)) * HD;
-      so = vs + n * Hkv + (hh - H - Hkv);
+      const float2 x = *reinterpret_cast<const float2*>(p);
+      v[0] = x.x, v[1] = x.y;
     }
-    if (act) {
-#pragma unroll
-      for (int j = 0; j < NV; j++) qo[lane + 64 * j] = qv[j];
-    }
-    if (lane == 0) *so = s;
   };
-  // QH heads per pass, their loads for all the tokens issued together (indices clamped in
-  // range, values of heads past NH unused) so that the wave waits for memory once per pass
-  // (2 measured faster than 4: fewer registers)
-  constexpr int QH = 2;
-  for (int h0 = wave; h0 < NH; h0 += 4 * QH) {
-    float swv[QH][NV];
-    float vv[TK][QH][NV];
+  float qn[NV], kn[NV];
+  if (qknorm) {
+    ldv(qnw + d0, qn);
+    ldv(knw + d0, kn);
+  }
+  const bool low = sl < 8;  // the row's lanes holding the first half of the head
+  for (int p = 0; p * 16 < NH; p++) {
+    const int hh = 16 * p + 4 * wave + row;  // this row's head
+    const bool live = hh < NH;
+    const int hc = min(hh, NH - 1);
+    const bool isq = hc < H, isv = hc >= H + Hkv;
+    const int col = hc * HD + d0;
+    float swv[NV];
+    if constexpr (!FP) ldv(sw + col, swv);
+    u32 pk[NV];
 #pragma unroll
-    for (int c = 0; c < QH; c++) {
-      const int col0 = min(h0 + 4 * c, NH - 1) * HD;
-#pragma unroll
-      for (int j = 0; j < NV; j++) swv[c][j] = FP ? 1.0f : sw[col0 + (act ? lane + 64 * j : 0)];
-    }
+    for (int j = 0; j < NV; j++) pk[j] = 0;
 #pragma unroll
     for (int t = 0; t < TK; t++) {
-      const long n = n0 + min(t, nt - 1);
+      if (t >= nt) break;
+      const long n = n0 + t;
+      float v[NV];
+      if constexpr (FP) {
+        ldv(static_cast<const float*>(acc) + n * W + col, v);
+      } else {
+        const i32* a = static_cast<const i32*>(acc) + n * W + col;
+        int av[NV];
+        if constexpr (NV % 4 == 0) {
 #pragma unroll
-      for (int c = 0; c < QH; c++) {
-        const int col0 = min(h0 + 4 * c, NH - 1) * HD;
+          for (int j = 0; j < NV; j += 4) {
+            const int4 x = *reinterpret_cast<const int4*>(a + j);
+            av[j] = x.x, av[j + 1] = x.y, av[j + 2] = x.z, av[j + 3] = x.w;
+          }
+        } else {
+          const int2 x = *reinterpret_cast<const int2*>(a);
+          av[0] = x.x, av[1] = x.y;
+        }
 #pragma unroll
-        for (int j = 0; j < NV; j++) {
-          const int d = act ? lane + 64 * j : 0;
-          if constexpr (FP) vv[t][c][j] = static_cast<const float*>(acc)[n * W + col0 + d];
-          else vv[t][c][j] = dx_deq(static_cast<const i32*>(acc)[n * W + col0 + d], sx[t], swv[c][j]);
-          if (!act) vv[t][c][j] = 0.0f;
+        for (int j = 0; j < NV; j++) v[j] = dx_deq(av[j], sx[t], swv[j]);
+      }
+      if (!isv) {
+        if (qknorm) {  // det_rmsnorm over the head (qwen3.py:214-216)
+          float mx = 0.f;
+#pragma unroll
+          for (int j = 0; j < NV; j++) mx = fmaxf(mx, __fmul_rn(v[j], v[j]));
+          const int sh = dx_shift(row16_max(mx), L);
+          long long sq = 0;
+#pragma unroll
+          for (int j = 0; j < NV; j++) sq += dx_fix(__fmul_rn(v[j], v[j]), sh);
+          const float ss = dx_unfix(row16_sum64(sq), sh);
+          const float r = __fdiv_rn(1.0f, uwc_sqrt_rn(__fadd_rn(__fmul_rn(ss, inv_hd), eps)));
+#pragma unroll
+          for (int j = 0; j < NV; j++) v[j] = __fmul_rn(__fmul_rn(v[j], r), isq ? qn[j] : kn[j]);
+        }
+        // rope: fadd(fmul(z, cos), fmul(rot(z), sin)), rot(z) = cat(-z[half:], z[:half])
+        float cs[NV], sn[NV];
+        ldv(cosb + (long)pos[t] * HD + d0, cs);
+        ldv(sinb + (long)pos[t] * HD + d0, sn);
+        float part[NV];
+#pragma unroll
+        for (int j = 0; j < NV; j++) part[j] = qa_dpp<0x128>(v[j]);  // row_ror:8: lane l ^ 8 of the row
+#pragma unroll
+        for (int j = 0; j < NV; j++) v[j] = __fadd_rn(__fmul_rn(v[j], cs[j]), __fmul_rn(part[j], low ? -sn[j] : sn[j]));
+      }
+      // quant_sym(qmax = 127) over the head (core.py:160-166)
+      float am = 0.f;
+#pragma unroll
+      for (int j = 0; j < NV; j++) am = fmaxf(am, fabsf(v[j]));
+      const float s = __fdiv_rn(fmaxf(row16_max(am), 1e-8f), 127.0f);
+      const double rs = 1.0 / (double)s;
+      u32 qb[NV / 2];  // the lane's NV quantized bytes, 2 per 16-bit half (NV >= 2)
+#pragma unroll
+      for (int j = 0; j < NV; j++) {
+        const int qv = (int)fminf(fmaxf(rintf(uwc_div_rd(v[j], rs)), -127.f), 127.f);
+        const u32 b = (u32)qv & 0xffu;
+        if (j % 2 == 0) qb[j / 2] = b;
+        else qb[j / 2] |= b << 8;
+        if (packed) pk[j] |= b << (8 * t);
+      }
+      if (live) {
+        i8* qo;
+        float* so;
+        if (isq) {
+          qo = qq + (n * H + hh) * HD;
+          so = qs + n * H + hh;
+        } else if (!isv) {
+          qo = kq + (n * Hkv + (hh - H)) * HD;
+          so = ks + n * Hkv + (hh - H);
+        } else {
+          qo = vq + (n * Hkv + (hh - H - Hkv)) * HD;
+          so = vs + n * Hkv + (hh - H - Hkv);
+        }
+        if constexpr (NV == 2) {
+          *reinterpret_cast<unsigned short*>(qo + d0) = (unsigned short)qb[0];
+        } else {
+#pragma unroll
+          for (int j = 0; j < NV / 4; j++)
+            *reinterpret_cast<u32*>(qo + d0 + 4 * j) = qb[2 * j] | (qb[2 * j + 1] << 16);
+        }
+        if (sl == 0) *so = s;
+        if (vt && isv && !packed) {
+          const int hk = hh - H - Hkv;
+#pragma unroll
+          for (int j = 0; j < NV; j++)
+            vt[((long)(bs[t] * Hkv + hk) * HD + d0 + j) * Tp + vt_pos(pos[t])] = (i8)((qb[j / 2] >> (8 * (j % 2))) & 0xff);
         }
       }
     }
-#pragma unroll
-    for (int c = 0; c < QH; c++) {
-      const int hh = h0 + 4 * c;
-      if (hh >= NH) break;
-      const bool tv = vt && hh >= H + Hkv;  // a V head with the transposed copy wanted
+    if (live && vt && isv && packed) {
       const int hk = hh - H - Hkv;
-      u32 pk[NV] = {};
 #pragma unroll
-      for (int t = 0; t < TK; t++) {
-        if (t >= nt) break;
-        i8 qv[NV];
-        head(hh, t, vv[t][c], qv);
-        if (tv && act) {
-#pragma unroll
-          for (int j = 0; j < NV; j++) {
-            if (packed) pk[j] |= (u32)(u8)qv[j] << (8 * t);
-            else vt[((long)(bs[t] * Hkv + hk) * HD + lane + 64 * j) * Tp + vt_pos(pos[t])] = qv[j];
-          }
-        }
-      }
-      if (tv && act && packed) {
-#pragma unroll
-        for (int j = 0; j < NV; j++)
-          *reinterpret_cast<u32*>(vt + ((long)(bs[0] * Hkv + hk) * HD + lane + 64 * j) * Tp + vt_pos(pos[0])) = pk[j];
-      }
+      for (int j = 0; j < NV; j++)
+        *reinterpret_cast<u32*>(vt + ((long)(bs[0] * Hkv + hk) * HD + d0 + j) * Tp + vt_pos(pos[0])) = pk[j];
     }
   }
 }
@@ -561,6 +569,9 @@ extern "C" int uwc_qkv_post(const void* acc, const float* s1, const float* sw, c
   if (qknorm && (!qnw || !knw)) return uwc_fail("%s: q/k norm weights are needed with qknorm", fn);
   if (B < 0 || T <= 0 || H <= 0 || Hkv <= 0 || H % Hkv) return uwc_fail("%s: bad B=%d T=%d H=%d Hkv=%d", fn, B, T, H, Hkv);
   if (hd != 32 && hd != 64 && hd != 128) return uwc_fail("%s: head_dim %d not in {32, 64, 128}", fn, hd);
+  if (((uintptr_t)acc | (uintptr_t)sw | (uintptr_t)qnw | (uintptr_t)knw | (uintptr_t)cosb | (uintptr_t)sinb |
+       (uintptr_t)qq | (uintptr_t)kq | (uintptr_t)vq) & 15)
+    return uwc_fail("%s: acc, sw, qnw, knw, cos, sin, qq, kq, vq must be 16-byte aligned", fn);
   const long N = (long)B * T;
   if (N == 0) return UWC_OK;
   if (N > 0x7fffffff) return uwc_fail("%s: too many tokens", fn);

@@ -106,6 +106,22 @@ __device__ __forceinline__ long long wave_sum64(long long v) {
   return v;
 }
 
+// The max and the int64 sum over each 16-lane row (the first four steps of wave_max and
+// wave_sum64), in every lane of the row; rows reduce independently of each other.
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, qa_dpp<0xB1>(v));
+  v = fmaxf(v, qa_dpp<0x4E>(v));
+  v = fmaxf(v, qa_dpp<0x124>(v));
+  return fmaxf(v, qa_dpp<0x128>(v));
+}
+
+__device__ __forceinline__ long long row16_sum64(long long v) {
+  v += dpp64<0xB1>(v);
+  v += dpp64<0x4E>(v);
+  v += dpp64<0x124>(v);
+  return v + dpp64<0x128>(v);
+}
+
 // ------------------------------------------------------------------ workgroup (256 threads) reductions
 struct DxRed {
   float f[4];
