@@ -17,7 +17,8 @@
 //   * the C registers of the four 16x16 score blocks of a 64-key tile are, lane by lane, the
 //     16 keys of one query that the P x V MFMA needs as its k slots (keys 16 b + 4 g + i for lane
 //     group g), so P never leaves registers; V^T is stored with its keys in that order
-//     (qkv_post / v_transpose write it so), one 16-byte load per lane and dim block;
+//     (qkv_post / v_transpose write it so), one 16-byte load (in the stored form one LDS read
+//     from a ring the workgroup fills) per lane and dim block;
 //   * the three row statistics (max, exact sum, max of the scaled probabilities) each need the
 //     previous one over the whole causal row: sweep 1 finds the max, sweep 2 the exact sum and,
 //     from per-lane candidates, the third statistic (sweep 3, a pass over the keys of its own,
