@@ -373,8 +373,9 @@ def test_pv_ring_dma_and_reads(hd):
 
 @pytest.mark.parametrize("T,hd", [(1, 128), (100, 64), (300, 32), (2048, 128)])
 def test_pv_ring_schedule(T, hd):
-    """The P x V ring: NS = 3 stages, 4 + VD + 1 DMAs per wave and tile (exponentials, V, V
-    scales); the kernel waits for vmcnt(PER) while tile kt + 1 is in flight, else vmcnt(0)."""
+    """The P x V ring (after the sums, in the same kernel): NS = 2 stages, 4 + VD + 1 DMAs per wave
+    and tile (exponentials, V, V scales); tile kt + 1 is issued after the barrier of iteration kt
+    and the kernel waits for vmcnt(0) before each iteration, so no other tile is in flight."""
     per, _, _ = _pv_maps(hd)
     for qt in range((T + 63) // 64):
-        _ring_schedule(qt + 1, 3, per)
+        _ring_schedule(qt + 1, 2, per)
