@@ -357,7 +357,7 @@ __global__ void __launch_bounds__(256, ES ? 3 : HD == 128 ? 2 : 3)
   if constexpr (ES) {
     mx = __fmul_rn(rows[ridx], inv_sqrt);
   } else {
-    ksweep([&](int kt, const float (&Y)[4][4], const KTile&, auto) AT_AI {
+    ksweep([&](int, const float (&Y)[4][4], const KTile&, auto) AT_AI {
 #pragma unroll
       for (int b = 0; b < 4; b++)
 #pragma unroll
@@ -438,7 +438,7 @@ __global__ void __launch_bounds__(256, ES ? 3 : HD == 128 ? 2 : 3)
           eload(kt, eb[decltype(sl)::value]);
           vb[decltype(sl)::value] = vsload(kt);
         },
-        [&](int kt, auto sl) AT_AI {
+        [&](int, auto sl) AT_AI {
           constexpr int L = decltype(sl)::value;
           float4 svv[4];
           vsstage(vb[L], svv);
